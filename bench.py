@@ -1,0 +1,167 @@
+"""Benchmark of the paged decode hot path on one MI355X.
+
+One step = one fused KV-append + paged decode-attention launch
+(``mt_paged_decode_batch``) over one batch of BASELINE config 2: B = 64
+requests, contexts L ~ U{128..1024}, 12 heads, head_dim 64, page 16, fp16 K/V
+with fp32 accumulation, an 8192-page pool shuffled from the seed. Inputs are
+resident in HBM before the timed region. To measure cold-cache HBM bandwidth,
+steps rotate over ``--pools`` disjoint copies of the pool, tables and Q/K/V
+(6 x ~113 MB touched per cycle, beyond the 256 MB Infinity Cache).
+
+Prints one JSON line: decode tokens/s (B tokens per step / mean step time from
+HIP events around the K timed steps), the roofline of the decode kernel
+(algorithmic bytes per launch / mean launch time vs 8 TB/s) and the CPU
+baseline (the C restatement in oracle/, OpenMP on the host cores, on a
+bounded sample of the same workload).
+"""
+import argparse
+import ctypes as ct
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from minitorch_amd.runtime import runtime, CudaEvent, P, I, Z  # noqa: E402
+from minitorch_amd import paged_ops  # noqa: E402
+from minitorch_amd.workloads import config2_case, DevicePagedCase  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+METRIC = 'decode tokens/s (1 GPU) + paged-attn achieved HBM GB/s as % of MI355X peak'
+
+
+def algorithmic_bytes(case):
+    """Minimum HBM traffic of one append + attention launch.
+
+    bytes_append = B*H*D*2*(s_in + s_kv)
+    bytes_attn   = sum_i 2*L_i*H*D*s_kv + B*H*D*(s_q + s_o) + sum_i 4*ceil(L_i/P) + 4*B
+    """
+    s = 4 if case.dtype == 'float32' else 2
+    B, H, D, Pg = case.batch, case.heads, case.dim, case.page_size
+    L = case.lengths.astype(np.int64)
+    append = B * H * D * 2 * (s + s)
+    attn = int((2 * L * H * D * s).sum()) + B * H * D * (s + s) + int((4 * ((L + Pg - 1) // Pg)).sum()) + 4 * B
+    return append + attn
+
+
+def cpu_baseline(case, seconds):
+    try:
+        from oracle import c_oracle
+        lib = c_oracle.library()
+    except Exception as error:  # the oracle library is optional on the GPU box
+        return dict(value=None, unit='tokens/s', cores=None, kind='port', sample=f'unavailable: {error}')
+    host = c_oracle.HostCase(case)
+    threads = min(os.cpu_count() or 1, 16)
+    host.run(lib, threads)  # warm
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        host.run(lib, threads)
+        steps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    return dict(value=case.batch * steps / elapsed, unit='tokens/s', cores=threads, kind='port',
+                sample=f'{steps} steps of config 2 (B=64, same seed) in {elapsed:.1f} s, fp32 arithmetic '
+                       f'on fp16 pages, OpenMP over (request, head)')
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=200)
+    ap.add_argument('--warmup', type=int, default=20)
+    ap.add_argument('--pools', type=int, default=6)
+    ap.add_argument('--seed', type=int, default=0)
+    ap.add_argument('--split', type=int, default=0, help='split length in tokens (0 = automatic)')
+    ap.add_argument('--unroll', type=int, default=0)
+    ap.add_argument('--cpu-seconds', type=float, default=10.0)
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py measures one GPU only: this build has no multi-GPU path '
+              '(request/head sharding is a design note); run with --gpus 1.', file=sys.stderr)
+        sys.exit(2)
+
+    rt = runtime()
+    case = config2_case(args.seed)
+    devs = [DevicePagedCase(case) for _ in range(args.pools)]
+    kw = devs[0].kwargs()
+    ws_bytes = paged_ops.decode_workspace_bytes(b=case.batch, h=case.heads, page_size=case.page_size,
+                                                columns=case.columns, split_tokens=args.split)
+    from minitorch_amd.runtime import RawDeviceBuffer
+    ws = RawDeviceBuffer(max(ws_bytes, 4))
+    ws.fill_words(0)
+    fn = paged_ops.paged_library().mt_paged_decode_split
+    fn.argtypes, fn.restype = [P] * 7 + [I] * 12 + [P, Z], I
+    from minitorch_amd.dtypes import dtype_code
+    calls = [(d.out.ptr, d.q.ptr, d.k.ptr, d.v.ptr, d.slab_table.ptr, d.block_table.ptr, d.offsets.ptr,
+              kw['b'], kw['h'], kw['d'], kw['page_size'], kw['pages_per_slab'], kw['num_slabs'],
+              kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype']), args.split,
+              args.unroll, ws.ptr, ws_bytes) for d in devs]
+
+    def step(i):
+        status = fn(*calls[i % len(calls)])
+        if status:
+            rt.check(status)
+
+    for i in range(args.warmup):
+        step(i)
+    rt.synchronize()
+    start, end = CudaEvent(), CudaEvent()
+    wall0 = time.perf_counter()
+    start.record()
+    for i in range(args.steps):
+        step(i)
+    end.record()
+    rt.synchronize()
+    wall = time.perf_counter() - wall0
+    gpu_s = end.seconds_since(start)
+    per_step = gpu_s / args.steps
+    nbytes = algorithmic_bytes(case)
+    achieved = nbytes / per_step / 1e9
+    result = {
+        'metric': METRIC,
+        'value': case.batch / per_step,
+        'unit': 'tokens/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': per_step * 1e3,
+        'wall_ms_per_step': wall / args.steps * 1e3,
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'f16',
+        'data': 'synthetic',
+        'config': {
+            'workload': 'config 2: op-level paged decode (fused KV append + attention), B=64, '
+                        'L~U[128,1024], H=12, D=64, page 16, fp16 K/V, fp32 accumulate, 8192-page '
+                        'shuffled pool, cold cache via pool rotation',
+            'global_batch': case.batch,
+            'sum_context_tokens': int(case.lengths.sum()),
+            'pools_rotated': args.pools,
+            'split_tokens': args.split or 'auto',
+            'parallelism': 'single GPU',
+        },
+        'roofline': {
+            'bound': 'hbm',
+            'achieved': achieved,
+            'peak': PEAK_HBM_GBS,
+            'unit': 'GB/s',
+            'frac': achieved / PEAK_HBM_GBS,
+            'traffic': None,
+            'algorithmic_bytes_per_launch': nbytes,
+            'kernel': 'decode_kernel<kF16,64,true,U> (mt_paged_decode_split)',
+        },
+    }
+    if not args.no_cpu_baseline:
+        result['cpu_baseline'] = cpu_baseline(case, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == '__main__':
+    main()

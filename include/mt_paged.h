@@ -1,0 +1,72 @@
+/* Paged KV append and paged decode attention: C-ABI of
+ * minitorch_amd/cuda_kernels/paged_attention_kernel.so (gfx950).
+ *
+ * Conventions (reference minitorch/cuda_resident_ops.py:41-47,
+ * src/paged_attention_kernel.cu): every entry returns an int status, 0 on
+ * success, otherwise a hipError_t value (1 = invalid value, 2 = out of
+ * memory); pointers are device addresses; dtype 0 = float32, 1 = float16,
+ * 2 = bfloat16; launches go to the null stream and never synchronize.
+ *
+ * Slab layout: [layers][2 (K,V)][pages_per_slab][heads][page_size][head_dim];
+ * physical page p is slot p % pages_per_slab of slab p / pages_per_slab, whose
+ * base address is slabs[p / pages_per_slab] (0 = absent). A table entry that
+ * is negative, beyond the pool, or whose slab is absent is a missing page:
+ * appends to it are skipped and attention reads it as NaN.
+ */
+#ifndef MT_PAGED_H
+#define MT_PAGED_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Append n tokens per request at the common position `offset`:
+ * K/V [b, h, n, d] -> pages through table [b, columns].
+ * Replaces reference mt_paged_append (src/paged_attention_kernel.cu:96-106). */
+int mt_paged_append(const void* k, const void* v, const uint64_t* slabs, const int* table, int b,
+                    int h, int n, int d, int page_size, int pages_per_slab, int num_slabs,
+                    int columns, int layer, int layers, int offset, int dtype);
+
+/* Causal paged attention for nq >= 1 queries per request: out/q [b, h, nq, d];
+ * query qi attends keys kj < nk with kj <= offset + qi (nk == offset + nq).
+ * Replaces reference mt_paged_attention (src/paged_attention_kernel.cu:108-117). */
+int mt_paged_attention(void* out, const void* q, const uint64_t* slabs, const int* table, int b,
+                       int h, int nq, int nk, int d, int page_size, int pages_per_slab,
+                       int num_slabs, int columns, int layer, int layers, int offset, int dtype);
+
+/* Ragged batched decode: q/k/v/out [b, h, 1, d]; offsets[b] (device) are the
+ * committed lengths. Appends k/v at position offsets[i] of request i, then
+ * attends its offsets[i] + 1 keys. One fused append + attention launch, plus
+ * a split-reduction launch when the table is longer than one context split;
+ * the split partials live in a library-owned device workspace (allocated on
+ * first need, grown on demand, kept until the process ends).
+ * Replaces reference mt_paged_decode_batch (src/paged_attention_kernel.cu:121-137). */
+int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v,
+                          const uint64_t* slabs, const int* table, const int* offsets, int b,
+                          int h, int d, int page_size, int pages_per_slab, int num_slabs,
+                          int columns, int layer, int layers, int dtype);
+
+/* Bytes of workspace mt_paged_decode_split needs (0 when no row can be split).
+ * split_tokens = 0 selects the automatic split length.
+ * No reference counterpart: the split-context reduction is new in this build. */
+int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, int split_tokens,
+                                    size_t* bytes);
+
+/* mt_paged_decode_batch with a caller-owned workspace and an explicit split
+ * length (a multiple of 64, at most 2048; 0 = automatic) and stream unroll
+ * (1, 2 or 4; 0 = default). The workspace holds per-split partials; launches
+ * that share one workspace must not overlap.
+ * No reference counterpart (split-context variant of
+ * src/paged_attention_kernel.cu:121-137). */
+int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v,
+                          const uint64_t* slabs, const int* table, const int* offsets, int b,
+                          int h, int d, int page_size, int pages_per_slab, int num_slabs,
+                          int columns, int layer, int layers, int dtype, int split_tokens,
+                          int unroll, void* workspace, size_t workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MT_PAGED_H */

@@ -1,0 +1,69 @@
+// Device runtime of the boundary: allocation, copies, synchronization, error
+// strings and events on device 0's null stream, with the reference's symbol
+// names and status convention (src/cuda_runtime.cu:7-21; status 0 = success,
+// otherwise the hipError_t value, whose numbering matches the CUDA codes the
+// reference's Python checks: 1 = invalid value, 2 = out of memory).
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace {
+
+__global__ __launch_bounds__(256) void fill_kernel(float* out, int64_t size, float value) {
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < size;
+       i += int64_t(gridDim.x) * blockDim.x)
+    out[i] = value;
+}
+
+__global__ __launch_bounds__(256) void fill_bytes_kernel(uint32_t* out, int64_t words, uint32_t value) {
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < words;
+       i += int64_t(gridDim.x) * blockDim.x)
+    out[i] = value;
+}
+
+int blocks_for(int64_t n) {
+  const int64_t b = (n + 255) / 256;
+  return int(b < (1 << 20) ? b : (1 << 20));
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_malloc(void** p, size_t bytes) { return hipMalloc(p, bytes); }
+int mt_free(void* p) { return hipFree(p); }
+// kind: 0 host->host, 1 host->device, 2 device->host, 3 device->device, 4 default.
+int mt_copy(void* dst, const void* src, size_t bytes, int kind) {
+  if (kind < 0 || kind > 4) return hipErrorInvalidValue;
+  return hipMemcpy(dst, src, bytes, static_cast<hipMemcpyKind>(kind));
+}
+int mt_copy_async(void* dst, const void* src, size_t bytes, int kind) {
+  if (kind < 0 || kind > 4) return hipErrorInvalidValue;
+  return hipMemcpyAsync(dst, src, bytes, static_cast<hipMemcpyKind>(kind), nullptr);
+}
+int mt_sync() { return hipStreamSynchronize(nullptr); }
+const char* mt_error(int code) { return hipGetErrorString(static_cast<hipError_t>(code)); }
+int mt_event_create(hipEvent_t* e) { return hipEventCreate(e); }
+int mt_event_record(hipEvent_t e) { return hipEventRecord(e, nullptr); }
+int mt_event_elapsed(float* ms, hipEvent_t a, hipEvent_t b) {
+  hipError_t e = hipEventSynchronize(b);
+  return e == hipSuccess ? hipEventElapsedTime(ms, a, b) : e;
+}
+int mt_event_destroy(hipEvent_t e) { return hipEventDestroy(e); }
+int mt_device_count(int* n) { return hipGetDeviceCount(n); }
+
+// out[0:n] = value (reference mt_fill, src/cuda_runtime.cu:33-35,54-57).
+int mt_fill(float* p, int n, float v) {
+  if (n < 0) return hipErrorInvalidValue;
+  if (n) fill_kernel<<<blocks_for(n), 256>>>(p, n, v);
+  return hipGetLastError();
+}
+
+// Fill `words` 32-bit words with a bit pattern: a small kernel rather than a
+// memset node, so callers may capture it in a graph.
+int mt_fill_words(void* p, size_t words, unsigned int value) {
+  if (!p && words) return hipErrorInvalidValue;
+  if (words) fill_bytes_kernel<<<blocks_for(int64_t(words)), 256>>>(static_cast<uint32_t*>(p), int64_t(words), value);
+  return hipGetLastError();
+}
+
+}  // extern "C"

@@ -1,0 +1,172 @@
+// Token I/O kernels of the decode step for gfx950: embedding gather, greedy
+// argmax and last-position copy. Semantics follow the reference
+// src/inference_kernels.cu (cited per kernel); the launch shapes are this
+// build's own.
+#include "mt_device.h"
+#include <climits>
+
+using namespace mt;
+
+namespace {
+
+// dst[t, :] = weights[ids[t], :]; a row whose id is non-finite, negative,
+// >= vocab or not an integer becomes NaN (reference src/inference_kernels.cu:7-14).
+// One thread moves 4 floats when dim % 4 == 0 and the pointers are aligned.
+template <bool VEC>
+__global__ __launch_bounds__(256) void embedding_gather_kernel(float* dst, const float* weights,
+                                                               const float* ids, int tokens,
+                                                               int vocab, int dim) {
+  constexpr int E = VEC ? 4 : 1;
+  const int per_row = dim / E;
+  const int64_t total = int64_t(tokens) * per_row;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t t = i / per_row;
+    const int col = int(i - t * per_row) * E;
+    const float raw = ids[t];
+    const bool bad = !isfinite(raw) || raw < 0.f || raw >= float(vocab) || raw != floorf(raw);
+    float* o = dst + t * dim + col;
+    if constexpr (VEC) {
+      float4 val = bad ? make_float4(NAN, NAN, NAN, NAN)
+                       : *reinterpret_cast<const float4*>(weights + int64_t(raw) * dim + col);
+      *reinterpret_cast<float4*>(o) = val;
+    } else {
+      *o = bad ? NAN : weights[int64_t(raw) * dim + col];
+    }
+  }
+}
+
+// Candidate (value, index) for argmax. Order: a NaN beats any number, a larger
+// number beats a smaller one, and on equal keys (both NaN, or equal values)
+// the lower index wins; index INT_MAX marks "no candidate". This is
+// numpy.argmax's first-maximum rule, as in the reference
+// (src/inference_kernels.cu:37-41,47-48).
+struct Cand {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ bool better(const Cand& b, const Cand& a) {
+  if (b.i == INT_MAX) return false;
+  if (a.i == INT_MAX) return true;
+  const bool na = isnan(a.v), nb = isnan(b.v);
+  if (nb != na) return nb;
+  if (!na && b.v != a.v) return b.v > a.v;
+  return b.i < a.i;
+}
+
+__device__ __forceinline__ void consider(Cand& c, float v, int j) {
+  const Cand n{v, j};
+  if (better(n, c)) c = n;
+}
+
+constexpr int kArgmaxThreads = 512;
+
+// One workgroup of 8 waves per row. The aligned interior of the row is read
+// with 16-byte loads; the unaligned head and tail element by element.
+template <int DT>
+__global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, const void* src,
+                                                                    int width) {
+  using T = typename Elem<DT>::T;
+  constexpr int E = per16<DT>();
+  __shared__ float s_v[kArgmaxThreads / 64];
+  __shared__ int s_i[kArgmaxThreads / 64];
+  const int row = blockIdx.x;
+  const T* p = static_cast<const T*>(src) + int64_t(row) * width;
+  const int tid = threadIdx.x;
+  Cand c{-INFINITY, INT_MAX};
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
+  int head = int(((16 - (addr & 15)) & 15) / sizeof(T));
+  if (head > width) head = width;
+  if ((addr & (sizeof(T) - 1)) != 0) head = width;  // misaligned element type: scalar path
+  const int nvec = (width - head) / E;
+  const int tail = head + nvec * E;
+  if (tid < head) consider(c, to_f32<DT>(p[tid]), tid);
+  const uint4* vp = reinterpret_cast<const uint4*>(p + head);
+  for (int j = tid; j < nvec; j += kArgmaxThreads) {
+    float f[E];
+    unpack16<DT>(vp[j], f);
+#pragma unroll
+    for (int e = 0; e < E; ++e) consider(c, f[e], head + j * E + e);
+  }
+  for (int j = tail + tid; j < width; j += kArgmaxThreads) consider(c, to_f32<DT>(p[j]), j);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    Cand o{__shfl_xor(c.v, off), __shfl_xor(c.i, off)};
+    if (better(o, c)) c = o;
+  }
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) { s_v[wave] = c.v; s_i[wave] = c.i; }
+  __syncthreads();
+  if (tid == 0) {
+    Cand best{s_v[0], s_i[0]};
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) {
+      Cand o{s_v[w], s_i[w]};
+      if (better(o, best)) best = o;
+    }
+    dst[row] = float(best.i);
+  }
+}
+
+// dst[b, :] = src[b, n-1, :] (reference src/inference_kernels.cu:28-30).
+template <class T>
+__global__ __launch_bounds__(256) void last_row_kernel(T* dst, const T* src, int batch, int n,
+                                                       int width) {
+  const int64_t total = int64_t(batch) * width;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t b = i / width;
+    dst[i] = src[(b * n + n - 1) * width + (i - b * width)];
+  }
+}
+
+int blocks_for(int64_t threads) {
+  const int64_t b = (threads + 255) / 256;
+  return int(b < (1 << 20) ? b : (1 << 20));
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_embedding_gather(float* dst, const float* weights, const float* ids, int tokens, int vocab,
+                        int dim) {
+  if (tokens < 1 || vocab < 1 || dim < 1 || int64_t(tokens) * dim > INT32_MAX ||
+      int64_t(vocab) * dim > INT32_MAX)
+    return hipErrorInvalidValue;
+  if (!dst || !weights || !ids) return hipErrorInvalidValue;
+  const bool vec = dim % 4 == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(weights) & 15) == 0;
+  const int64_t threads = int64_t(tokens) * (vec ? dim / 4 : dim);
+  if (vec)
+    embedding_gather_kernel<true><<<blocks_for(threads), 256>>>(dst, weights, ids, tokens, vocab, dim);
+  else
+    embedding_gather_kernel<false><<<blocks_for(threads), 256>>>(dst, weights, ids, tokens, vocab, dim);
+  return hipGetLastError();
+}
+
+int mt_row_argmax(float* dst, const void* src, int rows, int width, int dtype) {
+  if (rows < 1 || width < 1 || width > 16777216 || int64_t(rows) * width > INT32_MAX)
+    return hipErrorInvalidValue;
+  if (!dst || !src) return hipErrorInvalidValue;
+  if (dtype == kF32) row_argmax_kernel<kF32><<<rows, kArgmaxThreads>>>(dst, src, width);
+  else if (dtype == kF16) row_argmax_kernel<kF16><<<rows, kArgmaxThreads>>>(dst, src, width);
+  else if (dtype == kBF16) row_argmax_kernel<kBF16><<<rows, kArgmaxThreads>>>(dst, src, width);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+int mt_last_row(void* dst, const void* src, int b, int n, int w, int dtype) {
+  if (b < 1 || n < 1 || w < 1 || int64_t(b) * n * w > INT32_MAX) return hipErrorInvalidValue;
+  if (!dst || !src) return hipErrorInvalidValue;
+  const int blocks = blocks_for(int64_t(b) * w);
+  if (dtype == kF32)
+    last_row_kernel<float><<<blocks, 256>>>(static_cast<float*>(dst), static_cast<const float*>(src), b, n, w);
+  else if (dtype == kF16 || dtype == kBF16)
+    last_row_kernel<uint16_t><<<blocks, 256>>>(static_cast<uint16_t*>(dst), static_cast<const uint16_t*>(src), b, n, w);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // extern "C"

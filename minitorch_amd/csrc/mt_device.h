@@ -1,0 +1,84 @@
+// Device helpers shared by the gfx950 kernels: element types, fp32 conversion
+// and 16-byte vector access.
+//
+// Element codes follow the reference's dtype codes (minitorch/dtypes.py:11):
+// 0 = float32, 1 = float16, 2 = bfloat16. Low-precision values are read into
+// fp32 registers (src/includes/typed_io.cuh:4-6) and written back with
+// round-to-nearest-even; bfloat16 NaNs stay quiet NaNs as in the reference's
+// host encoder (minitorch/dtypes.py:37-46).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace mt {
+
+enum : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+template <int DT> struct Elem;
+template <> struct Elem<kF32> { using T = float; };
+template <> struct Elem<kF16> { using T = uint16_t; };
+template <> struct Elem<kBF16> { using T = uint16_t; };
+
+template <int DT> constexpr int elem_bytes() { return DT == kF32 ? 4 : 2; }
+
+__device__ __forceinline__ float f16_to_f32(uint16_t x) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, x));
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t x) {
+  return __uint_as_float(static_cast<uint32_t>(x) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float x) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+template <int DT> __device__ __forceinline__ float to_f32(typename Elem<DT>::T x) {
+  if constexpr (DT == kF32) return x;
+  else if constexpr (DT == kF16) return f16_to_f32(x);
+  else return bf16_to_f32(x);
+}
+template <int DT> __device__ __forceinline__ typename Elem<DT>::T from_f32(float x) {
+  if constexpr (DT == kF32) return x;
+  else if constexpr (DT == kF16) return f32_to_f16(x);
+  else return f32_to_bf16(x);
+}
+
+// Unpack one 16-byte register group holding 4 (fp32) or 8 (fp16/bf16) values.
+template <int DT> __device__ __forceinline__ void unpack16(const uint4& r, float* o) {
+  if constexpr (DT == kF32) {
+    o[0] = __uint_as_float(r.x); o[1] = __uint_as_float(r.y);
+    o[2] = __uint_as_float(r.z); o[3] = __uint_as_float(r.w);
+  } else {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = to_f32<DT>(static_cast<uint16_t>(w[i] & 0xffffu));
+      o[2 * i + 1] = to_f32<DT>(static_cast<uint16_t>(w[i] >> 16));
+    }
+  }
+}
+
+// Pack 4 (fp32) or 8 (fp16/bf16) fp32 values into one 16-byte group.
+template <int DT> __device__ __forceinline__ uint4 pack16(const float* v) {
+  uint4 r;
+  if constexpr (DT == kF32) {
+    r.x = __float_as_uint(v[0]); r.y = __float_as_uint(v[1]);
+    r.z = __float_as_uint(v[2]); r.w = __float_as_uint(v[3]);
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(from_f32<DT>(v[2 * i])) |
+             (static_cast<uint32_t>(from_f32<DT>(v[2 * i + 1])) << 16);
+    r.x = w[0]; r.y = w[1]; r.z = w[2]; r.w = w[3];
+  }
+  return r;
+}
+
+template <int DT> constexpr int per16() { return 16 / elem_bytes<DT>(); }
+
+}  // namespace mt

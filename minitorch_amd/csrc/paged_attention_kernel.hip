@@ -1,0 +1,744 @@
+// Paged KV append and paged decode attention for gfx950 (CDNA4, wave64).
+//
+// Slab layout (reference src/paged_attention_kernel.cu:2,18-19 and
+// minitorch/paged_kv_cache.py:30): every slab is
+//   [layers][2 (K,V)][pages_per_slab][heads][page_size][head_dim]
+// and physical page p lives in slab p / pages_per_slab at slot
+// p % pages_per_slab; slab base addresses come from a uint64 device table.
+//
+// Decode attention is a GEMV over paged K/V (about one flop per byte), so it
+// is bound by HBM bandwidth and uses no MFMA. The design:
+//   * one workgroup (4 waves) owns one (request, head, context split);
+//   * a wave covers 16 tokens per step: four lanes per token, each lane owning
+//     head_dim/4 contiguous dims, so one page row-block of one head (2 KiB for
+//     fp16, D = 64) is a single coalesced 16-byte-per-lane load;
+//   * every 4-lane token group keeps its own online-softmax state (running max,
+//     denominator, fp32 accumulator), so the stream needs no cross-lane
+//     reduction except the 4-lane dot-product sum; groups, waves and splits are
+//     merged once at the end with the log-sum-exp rule;
+//   * the page table and slab lookups for a split are resolved once into LDS
+//     before streaming, so the dependent table -> slab -> K/V chain is paid once;
+//   * the KV append of the new token is fused: the workgroup that owns the
+//     last split scores the new token from the K/V inputs and writes it into
+//     its page, so append + attention is a single launch;
+//   * a row longer than one split writes (max, denominator, accumulator)
+//     partials to a workspace and a small reduction kernel merges them. (A
+//     last-arriving-workgroup merge inside the decode kernel needs device-scope
+//     release/acquire fences, which write back and invalidate the XCD's L2 per
+//     workgroup; measured on MI355X that made the decode 10x slower than a
+//     separate launch.)
+#include "mt_device.h"
+#include <climits>
+#include <cmath>
+#include <mutex>
+#include <vector>
+
+using namespace mt;
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kWaves = 4;
+constexpr int kThreads = kWave * kWaves;
+constexpr int kGroup = 4;                    // lanes per token
+constexpr int kRowBlock = kWave / kGroup;    // tokens per wave step
+constexpr int kMaxSplitTokens = 2048;
+constexpr int kMaxSplitPages = kMaxSplitTokens / 8;
+constexpr int kDefaultSplitTokens = 256;
+constexpr int kMaxSplitsPerRow = 8;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct Geometry {
+  int heads, dim, page_size, log2_page, pps, num_slabs, columns, layer;
+  int64_t kind_stride;  // elements between the K and V planes of one layer
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Address of (slot, head, row 0, col 0) in the K plane of `layer`, or nullptr
+// for the cases the reference treats as a missing page
+// (src/paged_attention_kernel.cu:11-16): logical column out of range, negative
+// or out-of-pool physical page, or a null slab.
+template <class T>
+__device__ __forceinline__ const T* page_base(const uint64_t* slabs, const int* table_row,
+                                              int64_t logical, const Geometry& g, int head) {
+  if (logical < 0 || logical >= g.columns) return nullptr;
+  const int physical = table_row[logical];
+  if (physical < 0 || int64_t(physical) >= int64_t(g.num_slabs) * g.pps) return nullptr;
+  const uint64_t address = slabs[physical / g.pps];
+  if (!address) return nullptr;
+  const int slot = physical % g.pps;
+  const int64_t i = ((int64_t(g.layer) * 2 * g.pps + slot) * g.heads + head) *
+                    int64_t(g.page_size) * g.dim;
+  return reinterpret_cast<const T*>(address) + i;
+}
+
+// Online-softmax state of one token group, in base-2 units (scores are
+// pre-multiplied by log2(e)). A missing page contributes a NaN score, which
+// fmaxf drops from the running max and which then poisons the denominator,
+// matching the reference's NaN propagation (src/paged_attention_kernel.cu:53,66-69,84).
+template <int N>
+struct Softmax {
+  float m, l, acc[N];
+  __device__ __forceinline__ void init() {
+    m = -INFINITY; l = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) acc[i] = 0.f;
+  }
+  __device__ __forceinline__ void add(float s, const float* v) {
+    const float mn = fmaxf(m, s);
+    const float alpha = (m == -INFINITY) ? 0.f : fast_exp2(m - mn);
+    const float p = fast_exp2(s - mn);
+    l = fmaf(l, alpha, p);
+#pragma unroll
+    for (int i = 0; i < N; ++i) acc[i] = fmaf(p, v[i], acc[i] * alpha);
+    m = mn;
+  }
+  __device__ __forceinline__ void merge(float mo, float lo, const float* ao) {
+    const float mn = fmaxf(m, mo);
+    const float sa = (m == -INFINITY) ? 0.f : fast_exp2(m - mn);
+    const float sb = (mo == -INFINITY) ? 0.f : fast_exp2(mo - mn);
+    l = l * sa + lo * sb;
+#pragma unroll
+    for (int i = 0; i < N; ++i) acc[i] = acc[i] * sa + ao[i] * sb;
+    m = mn;
+  }
+  // Merge the states of the 16 token groups of a wave (lanes with equal
+  // lane % 4): afterwards lanes 0..3 hold the wave's state for their chunk.
+  __device__ __forceinline__ void wave_merge() {
+#pragma unroll
+    for (int off = kGroup; off < kWave; off <<= 1) {
+      float ao[N];
+      const float mo = __shfl_xor(m, off);
+      const float lo = __shfl_xor(l, off);
+#pragma unroll
+      for (int i = 0; i < N; ++i) ao[i] = __shfl_xor(acc[i], off);
+      merge(mo, lo, ao);
+    }
+  }
+};
+
+__device__ __forceinline__ float finalize(float acc, float l) {
+  return l > 0.f ? acc / l : (isnan(l) ? NAN : 0.f);
+}
+
+// Sum of a value over the 4 lanes of a token group (DPP quad permutes).
+__device__ __forceinline__ float group_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));
+  return x;
+}
+
+// Per-lane chunk of one token row: DL values at `p` (K or V plane), converted
+// to fp32. VEC uses 16-byte loads; otherwise element loads masked to `dim`.
+template <int DT, int DL, bool VEC>
+struct Chunk {
+  using T = typename Elem<DT>::T;
+  static constexpr int NV = VEC ? DL * elem_bytes<DT>() / 16 : 1;
+  uint4 raw[VEC ? NV : 1];
+  float val[VEC ? 1 : DL];
+  __device__ __forceinline__ void load(const T* p, int col0, int dim) {
+    if constexpr (VEC) {
+      const uint4* v = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) raw[i] = v[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < DL; ++i) val[i] = (col0 + i < dim) ? to_f32<DT>(p[i]) : 0.f;
+    }
+  }
+  __device__ __forceinline__ void nan_fill() {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) raw[i] = make_uint4(~0u, ~0u, ~0u, ~0u);
+    } else {
+#pragma unroll
+      for (int i = 0; i < DL; ++i) val[i] = NAN;
+    }
+  }
+  __device__ __forceinline__ void to_float(float* o) const {
+    if constexpr (VEC) {
+      constexpr int E = per16<DT>();
+#pragma unroll
+      for (int i = 0; i < NV; ++i) unpack16<DT>(raw[i], o + i * E);
+    } else {
+#pragma unroll
+      for (int i = 0; i < DL; ++i) o[i] = val[i];
+    }
+  }
+};
+
+// Stream the tokens [t0, t0 + ntok) of one (request, head) whose page bases
+// (K plane) are in s_page (entry j covers tokens t0 + j*P ...). Row-blocks
+// rb = rb_first, rb_first + rb_step, ... are processed, U at a time.
+template <int DT, int D, bool VEC, int U>
+__device__ __forceinline__ void stream_rows(Softmax<D / kGroup>& st, const float* qf,
+                                            typename Elem<DT>::T const* const* s_page,
+                                            int ntok, int rb_first, int rb_step,
+                                            const Geometry& g, int dim) {
+  using T = typename Elem<DT>::T;
+  constexpr int DL = D / kGroup;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int tok = lane >> 2;
+  const int col0 = (lane & 3) * DL;
+  const int nrb = (ntok + kRowBlock - 1) / kRowBlock;
+  const int pmask = g.page_size - 1;
+  for (int rb0 = rb_first; rb0 < nrb; rb0 += rb_step * U) {
+    Chunk<DT, DL, VEC> kc[U], vc[U];
+    bool valid[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int rel = (rb0 + u * rb_step) * kRowBlock + tok;
+      valid[u] = rel < ntok;
+      const T* base = valid[u] ? s_page[rel >> g.log2_page] : nullptr;
+      if (base) {
+        const T* kp = base + (rel & pmask) * dim + col0;
+        kc[u].load(kp, col0, dim);
+        vc[u].load(kp + g.kind_stride, col0, dim);
+      } else {
+        kc[u].nan_fill();
+        vc[u].nan_fill();
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float kf[DL], vf[DL];
+      kc[u].to_float(kf);
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < DL; ++i) part = fmaf(qf[i], kf[i], part);
+      const float s = group_sum(part);
+      if (valid[u]) {
+        vc[u].to_float(vf);
+        st.add(s, vf);
+      }
+    }
+  }
+}
+
+template <int DT, int D, bool VEC>
+__device__ __forceinline__ void load_q(float* qf, const typename Elem<DT>::T* q, int col0, int dim,
+                                       float scale) {
+  constexpr int DL = D / kGroup;
+  Chunk<DT, DL, VEC> c;
+  c.load(q + col0, col0, dim);
+  c.to_float(qf);
+#pragma unroll
+  for (int i = 0; i < DL; ++i) qf[i] *= scale;
+}
+
+struct DecodeArgs {
+  void* out;
+  const void* q;
+  const void* k;
+  const void* v;
+  const uint64_t* slabs;
+  const int* table;
+  const int* offsets;
+  int batch;
+  int split_tokens;
+  int nsplit_max;
+  float qscale;
+  int64_t items;
+  Geometry g;
+  float* partials;
+};
+
+// Fused KV append + decode attention over (request, head, split) items.
+template <int DT, int D, bool VEC, int U>
+__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
+  using T = typename Elem<DT>::T;
+  constexpr int DL = D / kGroup;
+  constexpr int PSTRIDE = D + 2;
+  __shared__ const T* s_page[kMaxSplitPages];
+  __shared__ float s_m[kWaves], s_l[kWaves];
+  __shared__ float s_acc[kWaves][D];
+
+  const Geometry& g = a.g;
+  const int dim = VEC ? D : g.dim;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & (kWave - 1);
+  const int col0 = (lane & 3) * DL;
+  const int64_t bh_count = int64_t(a.batch) * g.heads;
+  const int64_t cap = int64_t(g.columns) * g.page_size;
+  const T* qp = static_cast<const T*>(a.q);
+  const T* kin = static_cast<const T*>(a.k);
+  const T* vin = static_cast<const T*>(a.v);
+  T* out = static_cast<T*>(a.out);
+
+  for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
+    const int split = int(item / bh_count);
+    const int64_t bh = item - int64_t(split) * bh_count;
+    const int b = int(bh / g.heads);
+    const int head = int(bh - int64_t(b) * g.heads);
+    const int offset = a.offsets[b];
+    const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
+    T* orow = out + bh * dim;
+    if (L > cap) {
+      // A token beyond the table's columns reads as a missing page: NaN row.
+      if (split == 0)
+        for (int t = tid; t < dim; t += kThreads) orow[t] = from_f32<DT>(NAN);
+      continue;
+    }
+    const int nsplit = L == 0 ? 1 : int((L + a.split_tokens - 1) / a.split_tokens);
+    if (split >= nsplit) continue;
+    const int64_t t0 = int64_t(split) * a.split_tokens;
+    const int64_t t1 = L < t0 + a.split_tokens ? L : t0 + a.split_tokens;
+    const bool owns_new = L > 0 && split == nsplit - 1;
+    const int ntok_paged = int((owns_new ? t1 - 1 : t1) - t0);  // tokens read from pages
+
+    const int* table_row = a.table + int64_t(b) * g.columns;
+    const int npg = int((t1 - t0 + g.page_size - 1) >> g.log2_page);
+    for (int j = tid; j < npg; j += kThreads)
+      s_page[j] = page_base<T>(a.slabs, table_row, (t0 >> g.log2_page) + j, g, head);
+
+    float qf[DL];
+    load_q<DT, D, VEC>(qf, qp + bh * dim, col0, dim, a.qscale);
+    Softmax<DL> st;
+    st.init();
+    __syncthreads();
+
+    stream_rows<DT, D, VEC, U>(st, qf, s_page, ntok_paged, wave, kWaves, g, dim);
+
+    if (owns_new && wave == 0) {
+      // The new token: read from the K/V inputs, scored by group 0 of wave 0,
+      // and written into its page when the page exists (reference append,
+      // src/paged_attention_kernel.cu:23-33). A missing page reads as NaN.
+      const int64_t pos = L - 1;
+      const T* base = s_page[int((pos - t0) >> g.log2_page)];
+      Chunk<DT, DL, VEC> kc, vc;
+      kc.load(kin + bh * dim + col0, col0, dim);
+      vc.load(vin + bh * dim + col0, col0, dim);
+      if (lane < kGroup && base) {
+        T* kp = const_cast<T*>(base) + (pos & (g.page_size - 1)) * dim + col0;
+        T* vp = kp + g.kind_stride;
+        if constexpr (VEC) {
+#pragma unroll
+          for (int i = 0; i < Chunk<DT, DL, VEC>::NV; ++i) {
+            reinterpret_cast<uint4*>(kp)[i] = kc.raw[i];
+            reinterpret_cast<uint4*>(vp)[i] = vc.raw[i];
+          }
+        } else {
+          for (int i = 0; i < DL && col0 + i < dim; ++i) {
+            kp[i] = kin[bh * dim + col0 + i];
+            vp[i] = vin[bh * dim + col0 + i];
+          }
+        }
+      }
+      if (!base) { kc.nan_fill(); vc.nan_fill(); }
+      float kf[DL], vf[DL];
+      kc.to_float(kf);
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < DL; ++i) part = fmaf(qf[i], kf[i], part);
+      const float s = group_sum(part);
+      if (lane < kGroup) {
+        vc.to_float(vf);
+        st.add(s, vf);
+      }
+    }
+
+    st.wave_merge();
+    if (lane < kGroup) {
+#pragma unroll
+      for (int i = 0; i < DL; ++i) s_acc[wave][col0 + i] = st.acc[i];
+      if (lane == 0) { s_m[wave] = st.m; s_l[wave] = st.l; }
+    }
+    __syncthreads();
+
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w]);
+    float lsum = 0.f, asum = 0.f;
+    const int t = tid;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float sc = (s_m[w] == -INFINITY) ? 0.f : fast_exp2(s_m[w] - M);
+      lsum += s_l[w] * sc;
+      if (t < dim) asum += s_acc[w][t] * sc;
+    }
+
+    if (nsplit == 1) {
+      if (t < dim) orow[t] = from_f32<DT>(finalize(asum, lsum));
+    } else {
+      float* part = a.partials + (bh * a.nsplit_max + split) * PSTRIDE;
+      if (t < dim) part[2 + t] = asum;
+      if (t == 0) { part[0] = M; part[1] = lsum; }
+    }
+    __syncthreads();  // LDS is reused by the next item
+  }
+}
+
+// Split-context reduction: for every (request, head) whose context spans more
+// than one split, merge the per-split (max, denominator, accumulator) partials
+// with the log-sum-exp rule and write the output row. Rows with a single split
+// were written by decode_kernel. The kernel boundary orders it after the
+// partial writes, so no device-scope fences are needed.
+template <int DT, int D>
+__global__ __launch_bounds__(128) void merge_kernel(DecodeArgs a) {
+  using T = typename Elem<DT>::T;
+  constexpr int PSTRIDE = D + 2;
+  const Geometry& g = a.g;
+  const int dim = g.dim;
+  const int64_t bh_count = int64_t(a.batch) * g.heads;
+  const int64_t cap = int64_t(g.columns) * g.page_size;
+  T* out = static_cast<T*>(a.out);
+  for (int64_t bh = blockIdx.x; bh < bh_count; bh += gridDim.x) {
+    const int b = int(bh / g.heads);
+    const int offset = a.offsets[b];
+    const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
+    if (L > cap) continue;
+    const int nsplit = L == 0 ? 1 : int((L + a.split_tokens - 1) / a.split_tokens);
+    if (nsplit == 1) continue;
+    const float* base = a.partials + bh * a.nsplit_max * PSTRIDE;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, base[s * PSTRIDE]);
+    float lsum = 0.f, asum = 0.f;
+    const int t = threadIdx.x;
+    for (int s = 0; s < nsplit; ++s) {
+      const float ms = base[s * PSTRIDE];
+      const float sc = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
+      lsum += base[s * PSTRIDE + 1] * sc;
+      if (t < dim) asum += base[s * PSTRIDE + 2 + t] * sc;
+    }
+    if (t < dim) out[bh * dim + t] = from_f32<DT>(finalize(asum, lsum));
+  }
+}
+
+struct QueryArgs {
+  void* out;
+  const void* q;
+  const uint64_t* slabs;
+  const int* table;
+  int batch, nq, nk, offset;
+  float qscale;
+  int64_t items;
+  Geometry g;
+};
+
+// Causal paged attention for nq >= 1 queries per (request, head)
+// (reference paged_forward with offsets == nullptr, src/paged_attention_kernel.cu:35-85):
+// query qi attends keys kj < nk with kj <= offset + qi. One wave per query,
+// four queries per workgroup; page bases are resolved per 2048-token chunk.
+template <int DT, int D, bool VEC, int U>
+__global__ __launch_bounds__(kThreads) void query_kernel(QueryArgs a) {
+  using T = typename Elem<DT>::T;
+  constexpr int DL = D / kGroup;
+  __shared__ const T* s_page[kMaxSplitPages];
+  const Geometry& g = a.g;
+  const int dim = VEC ? D : g.dim;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & (kWave - 1);
+  const int col0 = (lane & 3) * DL;
+  const int qblocks = (a.nq + kWaves - 1) / kWaves;
+  const T* qp = static_cast<const T*>(a.q);
+  T* out = static_cast<T*>(a.out);
+  for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
+    const int64_t bh = item / qblocks;
+    const int qb = int(item - bh * qblocks);
+    const int b = int(bh / g.heads), head = int(bh - int64_t(b) * g.heads);
+    const int qi = qb * kWaves + wave;
+    const bool has_q = qi < a.nq;
+    const int64_t klen = has_q ? (int64_t(a.offset) + qi + 1 < a.nk ? int64_t(a.offset) + qi + 1 : a.nk) : 0;
+    const int qlast = (qb * kWaves + kWaves - 1 < a.nq ? qb * kWaves + kWaves - 1 : a.nq - 1);
+    const int64_t kmax = int64_t(a.offset) + qlast + 1 < a.nk ? int64_t(a.offset) + qlast + 1 : a.nk;
+    const int* table_row = a.table + int64_t(b) * g.columns;
+    float qf[DL];
+    load_q<DT, D, VEC>(qf, qp + (bh * a.nq + (has_q ? qi : 0)) * dim, col0, dim, a.qscale);
+    Softmax<DL> st;
+    st.init();
+    for (int64_t c0 = 0; c0 < kmax; c0 += kMaxSplitTokens) {
+      const int64_t c1 = c0 + kMaxSplitTokens < kmax ? c0 + kMaxSplitTokens : kmax;
+      const int npg = int((c1 - c0 + g.page_size - 1) >> g.log2_page);
+      __syncthreads();
+      for (int j = tid; j < npg; j += kThreads)
+        s_page[j] = page_base<T>(a.slabs, table_row, (c0 >> g.log2_page) + j, g, head);
+      __syncthreads();
+      const int64_t mine = klen - c0 < c1 - c0 ? klen - c0 : c1 - c0;
+      if (mine > 0) stream_rows<DT, D, VEC, U>(st, qf, s_page, int(mine), 0, 1, g, dim);
+    }
+    st.wave_merge();
+    if (has_q && lane < kGroup) {
+      T* orow = out + (bh * a.nq + qi) * dim;
+      for (int i = 0; i < DL; ++i)
+        if (col0 + i < dim) orow[col0 + i] = from_f32<DT>(finalize(st.acc[i], st.l));
+    }
+    __syncthreads();
+  }
+}
+
+struct AppendArgs {
+  const void* k;
+  const void* v;
+  const uint64_t* slabs;
+  const int* table;
+  int batch, n, offset;
+  int64_t vectors;  // number of per-thread units
+  Geometry g;
+};
+
+// Multi-token append at a common offset (reference paged_append with
+// offsets == nullptr, src/paged_attention_kernel.cu:23-33): K/V[b,h,pos,:]
+// goes to token offset + pos of request b; rows whose page is missing are
+// skipped. VEC moves 16 bytes per thread.
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+  using T = typename Elem<DT>::T;
+  constexpr int E = VEC ? per16<DT>() : 1;
+  const Geometry& g = a.g;
+  const int dim = g.dim;
+  const int per_row = dim / E;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < a.vectors;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t row = i / per_row;  // (b*h + head)*n + pos
+    const int col = int(i - row * per_row) * E;
+    const int64_t bhh = row / a.n;
+    const int pos_in = int(row - bhh * a.n);
+    const int b = int(bhh / g.heads), head = int(bhh - int64_t(b) * g.heads);
+    const int64_t pos = int64_t(a.offset) + pos_in;
+    const T* base = page_base<T>(a.slabs, a.table + int64_t(b) * g.columns, pos >> g.log2_page, g, head);
+    if (!base) continue;
+    T* kp = const_cast<T*>(base) + (pos & (g.page_size - 1)) * dim + col;
+    T* vp = kp + g.kind_stride;
+    const int64_t src = row * dim + col;
+    if constexpr (VEC) {
+      *reinterpret_cast<uint4*>(kp) = *reinterpret_cast<const uint4*>(static_cast<const T*>(a.k) + src);
+      *reinterpret_cast<uint4*>(vp) = *reinterpret_cast<const uint4*>(static_cast<const T*>(a.v) + src);
+    } else {
+      *kp = static_cast<const T*>(a.k)[src];
+      *vp = static_cast<const T*>(a.v)[src];
+    }
+  }
+}
+
+// Shape guard of the reference (src/paged_attention_kernel.cu:87-94 and
+// src/includes/flash_common.cuh:17-20): the same inputs are rejected.
+bool paged_shape(int b, int h, int nq, int nk, int d, int page_size, int pps, int num_slabs,
+                 int columns, int layer, int layers, int offset) {
+  return b > 0 && h > 0 && nq > 0 && nk > 0 && d > 0 && d <= 128 &&
+         int64_t(b) * h * nq * d <= INT32_MAX && int64_t(b) * h * nk * d <= INT32_MAX &&
+         int64_t(b) * h <= 65535 && (page_size == 8 || page_size == 16 || page_size == 32) &&
+         pps > 0 && num_slabs > 0 && int64_t(pps) * num_slabs <= INT32_MAX && columns > 0 &&
+         int64_t(b) * columns <= INT32_MAX && nk <= int64_t(columns) * page_size && layers > 0 &&
+         layer >= 0 && layer < layers && offset >= 0 && int64_t(offset) + nq == nk;
+}
+
+Geometry make_geometry(int h, int d, int page_size, int pps, int num_slabs, int columns, int layer) {
+  Geometry g;
+  g.heads = h; g.dim = d; g.page_size = page_size;
+  g.log2_page = page_size == 8 ? 3 : page_size == 16 ? 4 : 5;
+  g.pps = pps; g.num_slabs = num_slabs; g.columns = columns; g.layer = layer;
+  g.kind_stride = int64_t(pps) * h * page_size * d;
+  return g;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int64_t kMaxGrid = int64_t(1) << 30;
+
+int grid_for(int64_t items) { return int(items < kMaxGrid ? items : kMaxGrid); }
+
+// Split length for a decode launch: kDefaultSplitTokens unless the longest
+// possible context (columns * page_size) would need more than
+// kMaxSplitsPerRow splits, then longer splits (multiple of 64, at most 2048).
+int choose_split(int64_t cap, int requested) {
+  if (requested > 0) return requested;
+  int64_t s = kDefaultSplitTokens;
+  if ((cap + s - 1) / s > kMaxSplitsPerRow) {
+    s = (cap + kMaxSplitsPerRow - 1) / kMaxSplitsPerRow;
+    s = (s + 63) / 64 * 64;
+    if (s > kMaxSplitTokens) s = kMaxSplitTokens;
+  }
+  return int(s);
+}
+
+size_t workspace_bytes_for(int64_t bh, int nsplit_max) {
+  // (max, denominator, accumulator[128]) per (row, head, split)
+  return size_t(bh) * nsplit_max * (128 + 2) * sizeof(float);
+}
+
+template <int DT, int D, bool VEC>
+hipError_t launch_decode_t(const DecodeArgs& a, int64_t blocks, int unroll) {
+  if (unroll >= 4)
+    decode_kernel<DT, D, VEC, 4><<<grid_for(blocks), kThreads>>>(a);
+  else if (unroll == 2)
+    decode_kernel<DT, D, VEC, 2><<<grid_for(blocks), kThreads>>>(a);
+  else
+    decode_kernel<DT, D, VEC, 1><<<grid_for(blocks), kThreads>>>(a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.nsplit_max == 1) return e;
+  merge_kernel<DT, (D > 64 ? 128 : 64)><<<grid_for(int64_t(a.batch) * a.g.heads), 128>>>(a);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_decode_dt(const DecodeArgs& a, int64_t blocks, bool vec, int d, int unroll) {
+  if (vec && d == 64) return launch_decode_t<DT, 64, true>(a, blocks, unroll);
+  if (vec && d == 128) return launch_decode_t<DT, 128, true>(a, blocks, unroll);
+  return launch_decode_t<DT, 128, false>(a, blocks, 1);
+}
+
+int decode_common(void* out, const void* q, const void* k, const void* v, const uint64_t* slabs,
+                  const int* table, const int* offsets, int b, int h, int d, int page_size,
+                  int pps, int num_slabs, int columns, int layer, int layers, int dtype,
+                  int split_tokens, int unroll, void* workspace, size_t workspace_bytes) {
+  const int64_t cap = int64_t(columns) * page_size;
+  const int S = choose_split(cap, split_tokens);
+  if (S < 64 || S % 64 != 0 || S > kMaxSplitTokens) return hipErrorInvalidValue;
+  const int64_t nsplit_max = (cap + S - 1) / S;
+  const int64_t bh = int64_t(b) * h;
+  if (nsplit_max > INT_MAX) return hipErrorInvalidValue;
+  if (nsplit_max > 1 && (!workspace || workspace_bytes < workspace_bytes_for(bh, int(nsplit_max))))
+    return hipErrorInvalidValue;
+  DecodeArgs a;
+  a.out = out; a.q = q; a.k = k; a.v = v; a.slabs = slabs; a.table = table; a.offsets = offsets;
+  a.batch = b; a.split_tokens = S; a.nsplit_max = int(nsplit_max);
+  a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
+  a.items = bh * nsplit_max;
+  a.g = make_geometry(h, d, page_size, pps, num_slabs, columns, layer);
+  a.partials = static_cast<float*>(workspace);
+  const bool vec = (d == 64 || d == 128) && aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v);
+  if (dtype == kF32) return launch_decode_dt<kF32>(a, a.items, vec, d, unroll);
+  if (dtype == kF16) return launch_decode_dt<kF16>(a, a.items, vec, d, unroll);
+  if (dtype == kBF16) return launch_decode_dt<kBF16>(a, a.items, vec, d, unroll);
+  return hipErrorInvalidValue;
+}
+
+// Library-owned decode workspace for the reference entry point, which has no
+// workspace argument: grown on demand, kept per device until the process ends.
+std::mutex g_ws_mutex;
+std::vector<std::pair<void*, size_t>> g_ws;
+
+int library_workspace(size_t bytes, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  if (g_ws.size() <= size_t(dev)) g_ws.resize(dev + 1, {nullptr, 0});
+  auto& slot = g_ws[dev];
+  if (slot.second < bytes) {
+    if (slot.first) {
+      e = hipFree(slot.first);  // synchronizes the device before release
+      if (e != hipSuccess) return e;
+      slot = {nullptr, 0};
+    }
+    void* p = nullptr;
+    e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return e;
+    slot = {p, bytes};
+  }
+  *out = slot.first;
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_paged_append(const void* k, const void* v, const uint64_t* slabs, const int* table, int b,
+                    int h, int n, int d, int page_size, int pages_per_slab, int num_slabs,
+                    int columns, int layer, int layers, int offset, int dtype) {
+  if (!k || !v || !slabs || !table) return hipErrorInvalidValue;
+  if (int64_t(offset) + n > INT32_MAX ||
+      !paged_shape(b, h, n, offset + n, d, page_size, pages_per_slab, num_slabs, columns, layer,
+                   layers, offset))
+    return hipErrorInvalidValue;
+  if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
+  AppendArgs a;
+  a.k = k; a.v = v; a.slabs = slabs; a.table = table; a.batch = b; a.n = n; a.offset = offset;
+  a.g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
+  const int E = dtype == kF32 ? 4 : 8;
+  const bool vec = d % E == 0 && aligned16(k) && aligned16(v);
+  a.vectors = int64_t(b) * h * n * (vec ? d / E : d);
+  const int blocks = int((a.vectors + 255) / 256 < 65536 * 16 ? (a.vectors + 255) / 256 : 65536 * 16);
+#define MT_APPEND(DT)                                                        \
+  if (vec) append_kernel<DT, true><<<blocks, 256>>>(a);                      \
+  else append_kernel<DT, false><<<blocks, 256>>>(a);
+  if (dtype == kF32) { MT_APPEND(kF32) }
+  else if (dtype == kF16) { MT_APPEND(kF16) }
+  else { MT_APPEND(kBF16) }
+#undef MT_APPEND
+  return hipGetLastError();
+}
+
+int mt_paged_attention(void* out, const void* q, const uint64_t* slabs, const int* table, int b,
+                       int h, int nq, int nk, int d, int page_size, int pages_per_slab,
+                       int num_slabs, int columns, int layer, int layers, int offset, int dtype) {
+  if (!out || !q || !slabs || !table) return hipErrorInvalidValue;
+  if (!paged_shape(b, h, nq, nk, d, page_size, pages_per_slab, num_slabs, columns, layer, layers,
+                   offset))
+    return hipErrorInvalidValue;
+  if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
+  QueryArgs a;
+  a.out = out; a.q = q; a.slabs = slabs; a.table = table;
+  a.batch = b; a.nq = nq; a.nk = nk; a.offset = offset;
+  a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
+  a.items = int64_t(b) * h * ((nq + kWaves - 1) / kWaves);
+  a.g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
+  const bool vec = (d == 64 || d == 128) && aligned16(out) && aligned16(q);
+  const int blocks = grid_for(a.items);
+#define MT_QUERY(DT)                                                                   \
+  if (vec && d == 64) query_kernel<DT, 64, true, 2><<<blocks, kThreads>>>(a);          \
+  else if (vec && d == 128) query_kernel<DT, 128, true, 2><<<blocks, kThreads>>>(a);   \
+  else query_kernel<DT, 128, false, 1><<<blocks, kThreads>>>(a);
+  if (dtype == kF32) { MT_QUERY(kF32) }
+  else if (dtype == kF16) { MT_QUERY(kF16) }
+  else { MT_QUERY(kBF16) }
+#undef MT_QUERY
+  return hipGetLastError();
+}
+
+int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v,
+                          const uint64_t* slabs, const int* table, const int* offsets, int b,
+                          int h, int d, int page_size, int pages_per_slab, int num_slabs,
+                          int columns, int layer, int layers, int dtype) {
+  if (!out || !q || !k || !v || !slabs || !table || !offsets ||
+      !paged_shape(b, h, 1, 1, d, page_size, pages_per_slab, num_slabs, columns, layer, layers, 0) ||
+      int64_t(columns) * page_size > INT32_MAX)
+    return hipErrorInvalidValue;
+  if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
+  const int64_t cap = int64_t(columns) * page_size;
+  const int S = choose_split(cap, 0);
+  const int64_t nsplit_max = (cap + S - 1) / S;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  if (nsplit_max > 1) {
+    ws_bytes = workspace_bytes_for(int64_t(b) * h, int(nsplit_max));
+    const int e = library_workspace(ws_bytes, &ws);
+    if (e != hipSuccess) return e;
+  }
+  return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
+                       num_slabs, columns, layer, layers, dtype, S, 2, ws, ws_bytes);
+}
+
+int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, int split_tokens,
+                                    size_t* bytes) {
+  if (!bytes || b < 1 || h < 1 || columns < 1 ||
+      !(page_size == 8 || page_size == 16 || page_size == 32))
+    return hipErrorInvalidValue;
+  const int64_t cap = int64_t(columns) * page_size;
+  const int S = choose_split(cap, split_tokens);
+  if (S < 64 || S % 64 != 0 || S > kMaxSplitTokens) return hipErrorInvalidValue;
+  const int64_t nsplit_max = (cap + S - 1) / S;
+  *bytes = nsplit_max > 1 ? workspace_bytes_for(int64_t(b) * h, int(nsplit_max)) : 0;
+  return hipSuccess;
+}
+
+int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v,
+                          const uint64_t* slabs, const int* table, const int* offsets, int b,
+                          int h, int d, int page_size, int pages_per_slab, int num_slabs,
+                          int columns, int layer, int layers, int dtype, int split_tokens,
+                          int unroll, void* workspace, size_t workspace_bytes) {
+  if (!out || !q || !k || !v || !slabs || !table || !offsets ||
+      !paged_shape(b, h, 1, 1, d, page_size, pages_per_slab, num_slabs, columns, layer, layers, 0) ||
+      int64_t(columns) * page_size > INT32_MAX || split_tokens < 0 || unroll < 0)
+    return hipErrorInvalidValue;
+  if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
+  return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
+                       num_slabs, columns, layer, layers, dtype, split_tokens,
+                       unroll == 0 ? 2 : unroll, workspace, workspace_bytes);
+}
+
+}  // extern "C"

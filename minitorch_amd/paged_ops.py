@@ -1,0 +1,80 @@
+"""Thin Python wrappers over the paged-attention and token-I/O C-ABI.
+
+Argument order and meaning follow the reference's ctypes call sites
+(minitorch/paged_kv_cache.py:205-221, minitorch/paged_decode.py:328-332,
+minitorch/kv_cache.py:35,52, minitorch/pretrained_gpt2.py:30-31). Every call
+goes to ``cuda_kernels/paged_attention_kernel.so`` or
+``cuda_kernels/inference_kernels.so``.
+"""
+import ctypes as ct
+from .runtime import library, call, P, I, Z, DeviceTensor, runtime
+from .dtypes import dtype_code
+
+
+def paged_library():
+    return library('paged_attention_kernel')
+
+
+def inference_library():
+    return library('inference_kernels')
+
+
+def paged_append(k, v, slab_table, block_table, *, b, h, n, d, page_size, pages_per_slab,
+                 num_slabs, columns, layer, layers, offset, dtype):
+    """``mt_paged_append`` (reference src/paged_attention_kernel.cu:96-106)."""
+    call(paged_library(), 'mt_paged_append', [P] * 4 + [I] * 12,
+         k, v, slab_table, block_table, b, h, n, d, page_size, pages_per_slab, num_slabs,
+         columns, layer, layers, offset, dtype_code(dtype))
+
+
+def paged_attention(out, q, slab_table, block_table, *, b, h, nq, nk, d, page_size,
+                    pages_per_slab, num_slabs, columns, layer, layers, offset, dtype):
+    """``mt_paged_attention`` (reference src/paged_attention_kernel.cu:108-117)."""
+    call(paged_library(), 'mt_paged_attention', [P] * 4 + [I] * 13,
+         out, q, slab_table, block_table, b, h, nq, nk, d, page_size, pages_per_slab,
+         num_slabs, columns, layer, layers, offset, dtype_code(dtype))
+
+
+def paged_decode_batch(out, q, k, v, slab_table, block_table, offsets, *, b, h, d, page_size,
+                       pages_per_slab, num_slabs, columns, layer, layers, dtype):
+    """``mt_paged_decode_batch`` (reference src/paged_attention_kernel.cu:121-137)."""
+    call(paged_library(), 'mt_paged_decode_batch', [P] * 7 + [I] * 10,
+         out, q, k, v, slab_table, block_table, offsets, b, h, d, page_size, pages_per_slab,
+         num_slabs, columns, layer, layers, dtype_code(dtype))
+
+
+def decode_workspace_bytes(*, b, h, page_size, columns, split_tokens=0):
+    """Workspace size for ``mt_paged_decode_split`` (0 when no row can split)."""
+    out = ct.c_size_t()
+    call(paged_library(), 'mt_paged_decode_workspace_bytes', [I] * 5 + [ct.POINTER(ct.c_size_t)],
+         b, h, page_size, columns, split_tokens, ct.byref(out))
+    return out.value
+
+
+def paged_decode_split(out, q, k, v, slab_table, block_table, offsets, *, b, h, d, page_size,
+                       pages_per_slab, num_slabs, columns, layer, layers, dtype,
+                       split_tokens=0, unroll=0, workspace=None, workspace_bytes=0):
+    """``mt_paged_decode_split``: the decode of ``mt_paged_decode_batch`` with a
+    caller-owned workspace and an explicit split length (0 = automatic)."""
+    call(paged_library(), 'mt_paged_decode_split', [P] * 7 + [I] * 12 + [P, Z],
+         out, q, k, v, slab_table, block_table, offsets, b, h, d, page_size, pages_per_slab,
+         num_slabs, columns, layer, layers, dtype_code(dtype), split_tokens, unroll,
+         workspace, workspace_bytes)
+
+
+def embedding_gather(dst, weights, ids, tokens, vocab, dim):
+    """``mt_embedding_gather`` (reference src/inference_kernels.cu:15-19)."""
+    call(inference_library(), 'mt_embedding_gather', [P, P, P, I, I, I],
+         dst, weights, ids, tokens, vocab, dim)
+
+
+def row_argmax(dst, src, rows, width, dtype):
+    """``mt_row_argmax`` (reference src/inference_kernels.cu:73-79)."""
+    call(inference_library(), 'mt_row_argmax', [P, P, I, I, I], dst, src, rows, width,
+         dtype_code(dtype))
+
+
+def last_row(dst, src, b, n, w, dtype):
+    """``mt_last_row`` (reference src/inference_kernels.cu:66-72)."""
+    call(inference_library(), 'mt_last_row', [P, P, I, I, I, I], dst, src, b, n, w,
+         dtype_code(dtype))

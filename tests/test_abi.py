@@ -1,0 +1,128 @@
+"""The C-ABI libraries load here (no GPU), export every symbol their header
+declares, and reject the shapes the reference rejects before any device work.
+"""
+import ctypes as ct
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from minitorch_amd.runtime import library, P, I, Z
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = {
+    'mt_paged.h': 'paged_attention_kernel',
+    'mt_inference.h': 'inference_kernels',
+    'mt_runtime.h': 'cuda_runtime',
+    'mt_sched.h': 'sched_kernels',
+    'mt_model.h': 'model_kernels',
+}
+
+
+def declared(header):
+    text = (ROOT / 'include' / header).read_text()
+    return re.findall(r'^\s*(?:int|const char\*|size_t)\s+(mt_\w+)\s*\(', text, re.M)
+
+
+@pytest.mark.parametrize('header', sorted(HEADERS))
+def test_header_symbols_exported(header):
+    path = ROOT / 'include' / header
+    if not path.exists():
+        pytest.skip(f'{header} not present')
+    names = declared(header)
+    assert names, header
+    lib = library(HEADERS[header])
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f'{HEADERS[header]}.so lacks {missing}'
+
+
+def test_headers_compile_as_c_and_cpp():
+    for header in sorted((ROOT / 'include').glob('*.h')):
+        for lang in ('c', 'c++'):
+            r = subprocess.run(['gcc', '-x', lang, '-fsyntax-only', '-Wall', '-Werror', str(header)],
+                               capture_output=True, text=True)
+            assert r.returncode == 0, r.stderr
+
+
+def _decode_batch(**overrides):
+    lib = library('paged_attention_kernel')
+    f = lib.mt_paged_decode_batch
+    f.argtypes, f.restype = [P] * 7 + [I] * 10, I
+    args = dict(out=8, q=8, k=8, v=8, slabs=8, table=8, offsets=8, b=4, h=12, d=64, page_size=16,
+                pps=4, num_slabs=16, columns=8, layer=0, layers=1, dtype=0)
+    args.update(overrides)
+    return f(*args.values())
+
+
+@pytest.mark.parametrize('bad', [
+    dict(b=0), dict(h=0), dict(d=0), dict(d=129), dict(page_size=12), dict(page_size=64),
+    dict(pps=0), dict(num_slabs=0), dict(columns=0), dict(layer=1), dict(layer=-1),
+    dict(layers=0), dict(b=65536, h=1), dict(b=300, h=300), dict(dtype=3), dict(dtype=-1),
+    dict(out=None), dict(offsets=None), dict(table=None),
+    dict(pps=2 ** 30, num_slabs=4), dict(b=2 ** 16 - 1, h=1, columns=2 ** 16),
+])
+def test_decode_rejects_invalid_shapes(bad):
+    assert _decode_batch(**bad) == 1
+
+
+def test_append_and_attention_reject_invalid_shapes():
+    lib = library('paged_attention_kernel')
+    app = lib.mt_paged_append
+    app.argtypes, app.restype = [P] * 4 + [I] * 12, I
+    base = [8, 8, 8, 8, 2, 3, 5, 64, 16, 4, 4, 4, 0, 1, 0, 0]
+    bad_offset = list(base)
+    bad_offset[14] = -1
+    assert app(*bad_offset) == 1                      # offset < 0
+    too_long = list(base)
+    too_long[14] = 60                                  # offset + n > columns * P
+    assert app(*too_long) == 1
+    att = lib.mt_paged_attention
+    att.argtypes, att.restype = [P] * 4 + [I] * 13, I
+    # nq + offset != nk
+    assert att(8, 8, 8, 8, 2, 3, 5, 6, 64, 16, 4, 4, 4, 0, 1, 0, 0) == 1
+    # nk beyond the table
+    assert att(8, 8, 8, 8, 2, 3, 5, 70, 64, 16, 4, 4, 4, 0, 1, 65, 0) == 1
+
+
+def test_split_entry_validation_and_workspace_size():
+    lib = library('paged_attention_kernel')
+    ws = lib.mt_paged_decode_workspace_bytes
+    ws.argtypes, ws.restype = [I] * 5 + [ct.POINTER(ct.c_size_t)], I
+    out = ct.c_size_t()
+    assert ws(64, 12, 16, 64, 0, ct.byref(out)) == 0
+    # 4 splits of 256 tokens: (max, denominator, 128 accumulators) per split
+    assert out.value == 768 * 4 * 130 * 4
+    assert ws(64, 12, 16, 16, 0, ct.byref(out)) == 0 and out.value == 0   # cap 256: one split
+    assert ws(64, 12, 16, 64, 100, ct.byref(out)) == 1                     # not a multiple of 64
+    assert ws(64, 12, 16, 64, 4096, ct.byref(out)) == 1                    # beyond 2048
+    assert ws(64, 12, 12, 64, 0, ct.byref(out)) == 1                       # page size
+    split = lib.mt_paged_decode_split
+    split.argtypes, split.restype = [P] * 7 + [I] * 12 + [P, Z], I
+    # a splitting launch without a workspace is rejected
+    assert split(8, 8, 8, 8, 8, 8, 8, 4, 12, 64, 16, 4, 16, 64, 0, 1, 0, 0, 0, None, 0) == 1
+
+
+def test_inference_entries_reject_invalid_shapes():
+    lib = library('inference_kernels')
+    g = lib.mt_embedding_gather
+    g.argtypes, g.restype = [P, P, P, I, I, I], I
+    assert g(8, 8, 8, 0, 10, 4) == 1
+    assert g(8, 8, 8, 1, 0, 4) == 1
+    assert g(8, 8, 8, 2 ** 20, 10, 2 ** 12) == 1
+    a = lib.mt_row_argmax
+    a.argtypes, a.restype = [P, P, I, I, I], I
+    assert a(8, 8, 1, 2 ** 24 + 1, 0) == 1
+    assert a(8, 8, 0, 10, 0) == 1
+    assert a(8, 8, 1, 10, 5) == 1
+    lr = lib.mt_last_row
+    lr.argtypes, lr.restype = [P, P, I, I, I, I], I
+    assert lr(8, 8, 0, 1, 1, 0) == 1
+    assert lr(8, 8, 1, 1, 1, 7) == 1
+
+
+def test_error_strings():
+    lib = library('cuda_runtime')
+    lib.mt_error.argtypes, lib.mt_error.restype = [I], ct.c_char_p
+    assert lib.mt_error(0)
+    assert lib.mt_error(1)

@@ -1,0 +1,191 @@
+"""GPU parity of the paged append / decode attention C-ABI against the oracle.
+
+Every call goes through ``cuda_kernels/paged_attention_kernel.so``. Inputs are
+seeded (numpy default_rng); tolerances are in tests/tolerances.py. The KV
+append is checked bit-exact on the whole pool image.
+"""
+import numpy as np
+import pytest
+
+from minitorch_amd import paged_ops
+from minitorch_amd.runtime import RawDeviceBuffer, DeviceTensor, runtime
+from minitorch_amd.workloads import (make_decode_case, config1_case, config2_case,
+                                     config5_lengths, DevicePagedCase)
+from oracle import paged_oracle as po
+from tolerances import assert_attention_close
+
+pytestmark = pytest.mark.gpu
+CODES = {'float32': po.F32, 'float16': po.F16, 'bfloat16': po.BF16}
+
+
+def run_decode(dev, entry='batch', **extra):
+    c = dev.case
+    args = (dev.out.ptr, dev.q.ptr, dev.k.ptr, dev.v.ptr, dev.slab_table.ptr, dev.block_table.ptr,
+            dev.offsets.ptr)
+    if entry == 'batch':
+        paged_ops.paged_decode_batch(*args, **dev.kwargs())
+    else:
+        ws_bytes = paged_ops.decode_workspace_bytes(b=c.batch, h=c.heads, page_size=c.page_size,
+                                                    columns=c.columns,
+                                                    split_tokens=extra.get('split_tokens', 0))
+        ws = None
+        if ws_bytes:
+            ws = RawDeviceBuffer(ws_bytes)
+            ws.fill_words(0)
+        paged_ops.paged_decode_split(*args, **dev.kwargs(), workspace=ws.ptr if ws else None,
+                                     workspace_bytes=ws_bytes, **extra)
+    runtime().synchronize()
+    return dev.out.to_numpy()
+
+
+def oracle_decode(case, rows=None, present=None):
+    image = case.image.copy()
+    ref = po.image_decode_batch(image, CODES[case.dtype], case.table, case.columns, case.q, case.k,
+                                case.v, case.offsets, case.layer, present=present, rows=rows)
+    return ref, image
+
+
+def check_case(case, entry='batch', rows=None, check_image=True, **extra):
+    dev = DevicePagedCase(case)
+    out = run_decode(dev, entry, **extra)
+    ref, image = oracle_decode(case, rows=rows)
+    if rows is not None:
+        sel = tuple(np.array(rows).T)
+        out, ref = out[sel], ref[sel]
+    assert_attention_close(out, ref, case.dtype, context=f'{case.dtype} B={case.batch}')
+    if check_image:
+        assert np.array_equal(dev.pool_image().view(np.uint8), image.view(np.uint8)), 'append differs'
+    return dev, out
+
+
+def test_config1_fp32_full():
+    check_case(config1_case(0))
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+def test_config1_shape_low_precision(dtype):
+    case = make_decode_case(1, batch=4, heads=12, dim=64, page_size=16, lengths=[7, 33, 64, 120],
+                            pool_pages=64, pages_per_slab=4, dtype=dtype)
+    check_case(case)
+
+
+def test_config2_full_fp16():
+    check_case(config2_case(0))
+
+
+@pytest.mark.parametrize('page_size', [8, 16, 32])
+@pytest.mark.parametrize('dtype', ['float32', 'float16', 'bfloat16'])
+def test_page_sizes_and_boundaries(page_size, dtype):
+    # contexts on page and split boundaries: 1, P, P+1, 255..257, 512, 513, 1000
+    lengths = [1, page_size, page_size + 1, 255, 256, 257, 512, 513, 1000]
+    case = make_decode_case(2, batch=len(lengths), heads=3, dim=64, page_size=page_size,
+                            lengths=lengths, pool_pages=512, pages_per_slab=8, dtype=dtype)
+    check_case(case)
+
+
+@pytest.mark.parametrize('dim', [128, 48, 80, 32])
+@pytest.mark.parametrize('dtype', ['float32', 'bfloat16'])
+def test_head_dims(dim, dtype):
+    case = make_decode_case(3, batch=5, heads=2, dim=dim, page_size=16,
+                            lengths=[1, 17, 100, 300, 700], pool_pages=96, pages_per_slab=4,
+                            dtype=dtype)
+    check_case(case)
+
+
+def test_multi_layer_slab_addressing():
+    case = make_decode_case(4, batch=3, heads=4, dim=64, page_size=16, lengths=[5, 40, 300],
+                            pool_pages=48, pages_per_slab=3, dtype='float16', layers=3, layer=2)
+    check_case(case)
+
+
+def test_missing_pages_give_nan_rows():
+    case = make_decode_case(5, batch=4, heads=2, dim=64, page_size=16, lengths=[40, 40, 300, 20],
+                            pool_pages=64, pages_per_slab=4, dtype='float32')
+    case.table[0, 1] = -1          # hole inside the context -> NaN
+    case.table[1, 2] = -1          # the new token's page missing -> NaN, no write
+    case.table[2, 5] = 10 ** 6     # out-of-pool physical page -> NaN
+    check_case(case)
+
+
+def test_null_slab_reads_nan():
+    case = make_decode_case(6, batch=2, heads=2, dim=64, page_size=16, lengths=[60, 33],
+                            pool_pages=16, pages_per_slab=4, dtype='float32')
+    dev = DevicePagedCase(case)
+    # null out the slab of request 0's second page
+    phys = int(case.table[0, 1])
+    slabs = np.array([dev.pool.ptr + s * case.slab_bytes for s in range(case.num_slabs)], np.uint64)
+    slabs[phys // case.pages_per_slab] = 0
+    dev.slab_table.upload(slabs)
+    out = run_decode(dev)
+    present = np.ones(case.num_slabs, bool)
+    present[phys // case.pages_per_slab] = False
+    ref, image = oracle_decode(case, present=present)
+    assert_attention_close(out, ref, 'float32')
+    assert np.array_equal(dev.pool_image().view(np.uint8), image.view(np.uint8))
+
+
+@pytest.mark.parametrize('split_tokens', [64, 128, 256, 1024])
+@pytest.mark.parametrize('unroll', [1, 2, 4])
+def test_split_entry_equals_oracle(split_tokens, unroll):
+    case = make_decode_case(7, batch=6, heads=3, dim=64, page_size=16,
+                            lengths=[1, 64, 65, 500, 1024, 777], pool_pages=256, pages_per_slab=8,
+                            dtype='float16')
+    check_case(case, entry='split', split_tokens=split_tokens, unroll=unroll)
+
+
+def test_repeat_calls_are_deterministic():
+    case = config2_case(1, batch=16)
+    dev = DevicePagedCase(case)
+    first = run_decode(dev)
+    for _ in range(3):
+        dev.reset_pool()
+        again = run_decode(dev)
+        assert np.array_equal(first.view(np.uint16), again.view(np.uint16))
+
+
+def test_config5_ragged_bf16_sampled_rows():
+    # Config 5 shape (H=25, bf16, lognormal contexts up to 8192) at B=96 with
+    # the longest contexts forced in, checked on a seeded sample of rows.
+    lengths = config5_lengths(0, 96)
+    lengths[:4] = [8192, 4097, 1025, 1]
+    for page_size in (16, 32):
+        pages = int(((lengths + page_size - 1) // page_size).sum()) + 64
+        pages = (pages + 63) // 64 * 64
+        case = make_decode_case(8, batch=96, heads=25, dim=64, page_size=page_size,
+                                lengths=lengths, pool_pages=pages, pages_per_slab=64,
+                                dtype='bfloat16')
+        rng = np.random.default_rng(9)
+        rows = [(b, int(rng.integers(25))) for b in range(96)]
+        check_case(case, rows=rows)
+
+
+@pytest.mark.parametrize('dtype', ['float32', 'float16', 'bfloat16'])
+def test_multi_token_append_and_causal_attention(dtype):
+    # Prefill-style use (reference minitorch/paged_kv_cache.py:205-221):
+    # append n tokens at a common offset, then causal attention for nq = n.
+    rng = np.random.default_rng(10)
+    b, h, d, page_size, n, offset = 2, 3, 64, 16, 37, 20
+    case = make_decode_case(11, batch=b, heads=h, dim=d, page_size=page_size,
+                            lengths=[offset + n, offset + n], pool_pages=16, pages_per_slab=4,
+                            dtype=dtype)
+    dev = DevicePagedCase(case)
+    k = po.encode(rng.standard_normal((b, h, n, d), dtype=np.float32), CODES[dtype])
+    v = po.encode(rng.standard_normal((b, h, n, d), dtype=np.float32), CODES[dtype])
+    q = po.encode(rng.standard_normal((b, h, n, d), dtype=np.float32), CODES[dtype])
+    kd, vd, qd = (DeviceTensor(x.shape, dtype) for x in (k, v, q))
+    for t, x in ((kd, k), (vd, v), (qd, q)):
+        runtime().h2d(t.ptr, x)
+    out = DeviceTensor(q.shape, dtype)
+    common = dict(page_size=page_size, pages_per_slab=case.pages_per_slab,
+                  num_slabs=case.num_slabs, columns=case.columns, layer=0, layers=1, dtype=dtype)
+    paged_ops.paged_append(kd.ptr, vd.ptr, dev.slab_table.ptr, dev.block_table.ptr, b=b, h=h, n=n,
+                           d=d, offset=offset, **common)
+    paged_ops.paged_attention(out.ptr, qd.ptr, dev.slab_table.ptr, dev.block_table.ptr, b=b, h=h,
+                              nq=n, nk=offset + n, d=d, offset=offset, **common)
+    runtime().synchronize()
+    image = case.image.copy()
+    po.image_append(image, case.table, case.columns, k, v, 0, offset=offset)
+    assert np.array_equal(dev.pool_image().view(np.uint8), image.view(np.uint8))
+    ref = po.image_paged_attention(image, CODES[dtype], case.table, case.columns, q, 0, offset,
+                                   offset + n)
+    assert_attention_close(out.to_numpy(), ref, dtype)
