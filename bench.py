@@ -48,6 +48,19 @@ def algorithmic_bytes(case):
     return append + attn
 
 
+def measured_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a copy of known size), or None."""
+    path = os.path.join(ROOT, 'profiles', 'decode_config2_fp16_hbm_traffic.md')
+    try:
+        for line in open(path):
+            if line.startswith('traffic_bytes_per_launch:'):
+                return int(line.split(':')[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(case, seconds):
     try:
         from oracle import c_oracle
@@ -80,6 +93,8 @@ def main():
     ap.add_argument('--unroll', type=int, default=0)
     ap.add_argument('--cpu-seconds', type=float, default=10.0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--calibrate-copy', type=int, default=0, metavar='MB',
+                    help='only run device-to-device copies of MB MiB (counter calibration) and exit')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: this build has no multi-GPU path '
@@ -87,6 +102,16 @@ def main():
         sys.exit(2)
 
     rt = runtime()
+    if args.calibrate_copy:
+        from minitorch_amd.runtime import RawDeviceBuffer
+        nbytes = args.calibrate_copy << 20
+        src, dst = RawDeviceBuffer(nbytes), RawDeviceBuffer(nbytes)
+        src.fill_words(1)
+        for _ in range(args.steps):
+            rt.d2d(dst.ptr, src.ptr, nbytes)
+        rt.synchronize()
+        print(json.dumps({'calibrate_copy_bytes': nbytes, 'copies': args.steps}), flush=True)
+        return
     case = config2_case(args.seed)
     devs = [DevicePagedCase(case) for _ in range(args.pools)]
     kw = devs[0].kwargs()
@@ -153,7 +178,8 @@ def main():
             'peak': PEAK_HBM_GBS,
             'unit': 'GB/s',
             'frac': achieved / PEAK_HBM_GBS,
-            'traffic': None,
+            'traffic': measured_traffic(),
+            'traffic_source': 'profiles/decode_config2_fp16_hbm_traffic.md (rocprofv3 --pmc)',
             'algorithmic_bytes_per_launch': nbytes,
             'kernel': 'decode_kernel<kF16,64,true,U> (mt_paged_decode_split)',
         },

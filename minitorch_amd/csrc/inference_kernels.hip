@@ -82,10 +82,11 @@ __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, 
   const int nvec = (width - head) / E;
   const int tail = head + nvec * E;
   if (tid < head) consider(c, to_f32<DT>(p[tid]), tid);
-  const uint4* vp = reinterpret_cast<const uint4*>(p + head);
+  const auto* vp = global_view(reinterpret_cast<const u32x4*>(p + head));
   for (int j = tid; j < nvec; j += kArgmaxThreads) {
     float f[E];
-    unpack16<DT>(vp[j], f);
+    const u32x4 x = vp[j];
+    unpack16<DT>(x, f);
 #pragma unroll
     for (int e = 0; e < E; ++e) consider(c, f[e], head + j * E + e);
   }

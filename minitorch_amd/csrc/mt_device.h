@@ -14,6 +14,9 @@ namespace mt {
 
 enum : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
 
+// 16 bytes as a native vector, loadable from any address space.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 template <int DT> struct Elem;
 template <> struct Elem<kF32> { using T = float; };
 template <> struct Elem<kF16> { using T = uint16_t; };
@@ -48,7 +51,7 @@ template <int DT> __device__ __forceinline__ typename Elem<DT>::T from_f32(float
 }
 
 // Unpack one 16-byte register group holding 4 (fp32) or 8 (fp16/bf16) values.
-template <int DT> __device__ __forceinline__ void unpack16(const uint4& r, float* o) {
+template <int DT> __device__ __forceinline__ void unpack16(const u32x4& r, float* o) {
   if constexpr (DT == kF32) {
     o[0] = __uint_as_float(r.x); o[1] = __uint_as_float(r.y);
     o[2] = __uint_as_float(r.z); o[3] = __uint_as_float(r.w);
@@ -63,8 +66,8 @@ template <int DT> __device__ __forceinline__ void unpack16(const uint4& r, float
 }
 
 // Pack 4 (fp32) or 8 (fp16/bf16) fp32 values into one 16-byte group.
-template <int DT> __device__ __forceinline__ uint4 pack16(const float* v) {
-  uint4 r;
+template <int DT> __device__ __forceinline__ u32x4 pack16(const float* v) {
+  u32x4 r;
   if constexpr (DT == kF32) {
     r.x = __float_as_uint(v[0]); r.y = __float_as_uint(v[1]);
     r.z = __float_as_uint(v[2]); r.w = __float_as_uint(v[3]);
@@ -80,5 +83,18 @@ template <int DT> __device__ __forceinline__ uint4 pack16(const float* v) {
 }
 
 template <int DT> constexpr int per16() { return 16 / elem_bytes<DT>(); }
+
+// Global-address-space view of a pointer. Pointers that come from LDS or
+// kernel arguments may be generic, and generic (flat) loads are also counted
+// by the LDS wait counter, so an LDS read placed after them would wait for
+// the HBM load to return; global loads keep the two counters independent.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* global_view(const T* p) {
+  return (const __attribute__((address_space(1))) T*)(p);
+}
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* global_view(T* p) {
+  return (__attribute__((address_space(1))) T*)(p);
+}
 
 }  // namespace mt

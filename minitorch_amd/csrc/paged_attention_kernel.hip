@@ -29,6 +29,10 @@
 //     separate launch.)
 #include "mt_device.h"
 #include <climits>
+
+#ifndef MT_NT_LOADS
+#define MT_NT_LOADS 0
+#endif
 #include <cmath>
 #include <mutex>
 #include <vector>
@@ -44,9 +48,13 @@ constexpr int kGroup = 4;                    // lanes per token
 constexpr int kRowBlock = kWave / kGroup;    // tokens per wave step
 constexpr int kMaxSplitTokens = 2048;
 constexpr int kMaxSplitPages = kMaxSplitTokens / 8;
-constexpr int kDefaultSplitTokens = 256;
+constexpr int kDefaultSplitTokens = 1024;
 constexpr int kMaxSplitsPerRow = 8;
 constexpr float kLog2e = 1.4426950408889634f;
+#ifndef MT_STAGES
+#define MT_STAGES 2
+#endif
+constexpr int kStages = MT_STAGES;  // register stages of the K/V stream
 
 struct Geometry {
   int heads, dim, page_size, log2_page, pps, num_slabs, columns, layer;
@@ -135,22 +143,29 @@ template <int DT, int DL, bool VEC>
 struct Chunk {
   using T = typename Elem<DT>::T;
   static constexpr int NV = VEC ? DL * elem_bytes<DT>() / 16 : 1;
-  uint4 raw[VEC ? NV : 1];
+  u32x4 raw[VEC ? NV : 1];
   float val[VEC ? 1 : DL];
   __device__ __forceinline__ void load(const T* p, int col0, int dim) {
     if constexpr (VEC) {
-      const uint4* v = reinterpret_cast<const uint4*>(p);
+      const auto* v = global_view(reinterpret_cast<const u32x4*>(p));
 #pragma unroll
-      for (int i = 0; i < NV; ++i) raw[i] = v[i];
+      for (int i = 0; i < NV; ++i) {
+#if MT_NT_LOADS
+        raw[i] = __builtin_nontemporal_load(v + i);
+#else
+        raw[i] = v[i];
+#endif
+      }
     } else {
+      const auto* g = global_view(p);
 #pragma unroll
-      for (int i = 0; i < DL; ++i) val[i] = (col0 + i < dim) ? to_f32<DT>(p[i]) : 0.f;
+      for (int i = 0; i < DL; ++i) val[i] = (col0 + i < dim) ? to_f32<DT>(g[i]) : 0.f;
     }
   }
   __device__ __forceinline__ void nan_fill() {
     if constexpr (VEC) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) raw[i] = make_uint4(~0u, ~0u, ~0u, ~0u);
+      for (int i = 0; i < NV; ++i) raw[i] = u32x4{~0u, ~0u, ~0u, ~0u};
     } else {
 #pragma unroll
       for (int i = 0; i < DL; ++i) val[i] = NAN;
@@ -168,11 +183,68 @@ struct Chunk {
   }
 };
 
+// One query vector split over the 4 lanes of a token group. For fp16/bf16
+// with 16-byte access the query stays packed in its input type and q.k uses
+// the fp32-accumulating dot2 instructions (v_dot2c_f32_f16 / _bf16), so no
+// K conversion is needed and the query takes DL/2 registers; the 1/sqrt(D)
+// and log2(e) factors are applied to the summed score. fp32 and the masked
+// path keep a pre-scaled fp32 query.
+template <int DT, int D, bool VEC>
+struct Query {
+  using T = typename Elem<DT>::T;
+  static constexpr int DL = D / kGroup;
+  static constexpr bool PACKED = VEC && DT != kF32;
+  uint32_t qp[PACKED ? DL / 2 : 1];
+  float qf[PACKED ? 1 : DL];
+  float post_scale;
+  __device__ __forceinline__ void load(const T* q, int col0, int dim, float scale) {
+    Chunk<DT, DL, VEC> c;
+    c.load(q + col0, col0, dim);
+    if constexpr (PACKED) {
+#pragma unroll
+      for (int w = 0; w < DL / 2; ++w) qp[w] = c.raw[w / 4][w % 4];
+      post_scale = scale;
+    } else {
+      c.to_float(qf);
+#pragma unroll
+      for (int i = 0; i < DL; ++i) qf[i] *= scale;
+      post_scale = 1.f;
+    }
+  }
+  // This lane's part of q.k (before the group sum and post_scale).
+  __device__ __forceinline__ float partial(const Chunk<DT, DL, VEC>& k) const {
+    float s = 0.f;
+    if constexpr (PACKED) {
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+      for (int w = 0; w < DL / 2; ++w) {
+        const uint32_t kw = k.raw[w / 4][w % 4];
+        if constexpr (DT == kF16)
+          s = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qp[w]), __builtin_bit_cast(h2, kw), s, false);
+        else
+          s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, qp[w]), __builtin_bit_cast(b2, kw), s, false);
+      }
+    } else {
+      float kf[DL];
+      k.to_float(kf);
+#pragma unroll
+      for (int i = 0; i < DL; ++i) s = fmaf(qf[i], kf[i], s);
+    }
+    return s;
+  }
+  __device__ __forceinline__ float score(const Chunk<DT, DL, VEC>& k) const {
+    return group_sum(partial(k)) * post_scale;
+  }
+};
+
 // Stream the tokens [t0, t0 + ntok) of one (request, head) whose page bases
 // (K plane) are in s_page (entry j covers tokens t0 + j*P ...). Row-blocks
-// rb = rb_first, rb_first + rb_step, ... are processed, U at a time.
-template <int DT, int D, bool VEC, int U>
-__device__ __forceinline__ void stream_rows(Softmax<D / kGroup>& st, const float* qf,
+// rb = rb_first, rb_first + rb_step, ... are processed U at a time; with
+// STAGES = 2 the loads of the next U row-blocks are in flight while the
+// current ones are scored and accumulated.
+template <int DT, int D, bool VEC, int U, int STAGES>
+__device__ __forceinline__ void stream_rows(Softmax<D / kGroup>& st, const Query<DT, D, VEC>& q,
                                             typename Elem<DT>::T const* const* s_page,
                                             int ntok, int rb_first, int rb_step,
                                             const Geometry& g, int dim) {
@@ -183,9 +255,8 @@ __device__ __forceinline__ void stream_rows(Softmax<D / kGroup>& st, const float
   const int col0 = (lane & 3) * DL;
   const int nrb = (ntok + kRowBlock - 1) / kRowBlock;
   const int pmask = g.page_size - 1;
-  for (int rb0 = rb_first; rb0 < nrb; rb0 += rb_step * U) {
-    Chunk<DT, DL, VEC> kc[U], vc[U];
-    bool valid[U];
+  using C = Chunk<DT, DL, VEC>;
+  auto issue = [&](int rb0, C* kc, C* vc, bool* valid) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int rel = (rb0 + u * rb_step) * kRowBlock + tok;
@@ -200,31 +271,41 @@ __device__ __forceinline__ void stream_rows(Softmax<D / kGroup>& st, const float
         vc[u].nan_fill();
       }
     }
+  };
+  auto consume = [&](const C* kc, const C* vc, const bool* valid) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      float kf[DL], vf[DL];
-      kc[u].to_float(kf);
-      float part = 0.f;
-#pragma unroll
-      for (int i = 0; i < DL; ++i) part = fmaf(qf[i], kf[i], part);
-      const float s = group_sum(part);
+      const float s = q.score(kc[u]);
       if (valid[u]) {
+        float vf[DL];
         vc[u].to_float(vf);
         st.add(s, vf);
       }
     }
-  }
-}
-
-template <int DT, int D, bool VEC>
-__device__ __forceinline__ void load_q(float* qf, const typename Elem<DT>::T* q, int col0, int dim,
-                                       float scale) {
-  constexpr int DL = D / kGroup;
-  Chunk<DT, DL, VEC> c;
-  c.load(q + col0, col0, dim);
-  c.to_float(qf);
+  };
+  if constexpr (STAGES == 1) {
+    for (int rb0 = rb_first; rb0 < nrb; rb0 += rb_step * U) {
+      C kc[U], vc[U];
+      bool valid[U];
+      issue(rb0, kc, vc, valid);
+      consume(kc, vc, valid);
+    }
+  } else {
+    C kc[U], vc[U];
+    bool valid[U];
+    int rb0 = rb_first;
+    if (rb0 < nrb) issue(rb0, kc, vc, valid);
+    while (rb0 < nrb) {
+      const int nxt = rb0 + rb_step * U;
+      C nk[U], nv[U];
+      bool nvalid[U];
+      if (nxt < nrb) issue(nxt, nk, nv, nvalid);
+      consume(kc, vc, valid);
 #pragma unroll
-  for (int i = 0; i < DL; ++i) qf[i] *= scale;
+      for (int u = 0; u < U; ++u) { kc[u] = nk[u]; vc[u] = nv[u]; valid[u] = nvalid[u]; }
+      rb0 = nxt;
+    }
+  }
 }
 
 struct DecodeArgs {
@@ -245,7 +326,7 @@ struct DecodeArgs {
 };
 
 // Fused KV append + decode attention over (request, head, split) items.
-template <int DT, int D, bool VEC, int U>
+template <int DT, int D, bool VEC, int U, int STAGES>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
   using T = typename Elem<DT>::T;
   constexpr int DL = D / kGroup;
@@ -293,13 +374,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     for (int j = tid; j < npg; j += kThreads)
       s_page[j] = page_base<T>(a.slabs, table_row, (t0 >> g.log2_page) + j, g, head);
 
-    float qf[DL];
-    load_q<DT, D, VEC>(qf, qp + bh * dim, col0, dim, a.qscale);
+    Query<DT, D, VEC> qv;
+    qv.load(qp + bh * dim, col0, dim, a.qscale);
     Softmax<DL> st;
     st.init();
     __syncthreads();
 
-    stream_rows<DT, D, VEC, U>(st, qf, s_page, ntok_paged, wave, kWaves, g, dim);
+    stream_rows<DT, D, VEC, U, STAGES>(st, qv, s_page, ntok_paged, wave, kWaves, g, dim);
 
     if (owns_new && wave == 0) {
       // The new token: read from the K/V inputs, scored by group 0 of wave 0,
@@ -316,8 +397,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
         if constexpr (VEC) {
 #pragma unroll
           for (int i = 0; i < Chunk<DT, DL, VEC>::NV; ++i) {
-            reinterpret_cast<uint4*>(kp)[i] = kc.raw[i];
-            reinterpret_cast<uint4*>(vp)[i] = vc.raw[i];
+            global_view(reinterpret_cast<u32x4*>(kp))[i] = kc.raw[i];
+            global_view(reinterpret_cast<u32x4*>(vp))[i] = vc.raw[i];
           }
         } else {
           for (int i = 0; i < DL && col0 + i < dim; ++i) {
@@ -327,15 +408,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
         }
       }
       if (!base) { kc.nan_fill(); vc.nan_fill(); }
-      float kf[DL], vf[DL];
-      kc.to_float(kf);
-      float part = 0.f;
-#pragma unroll
-      for (int i = 0; i < DL; ++i) part = fmaf(qf[i], kf[i], part);
-      const float s = group_sum(part);
+      const float sc = qv.score(kc);
       if (lane < kGroup) {
+        float vf[DL];
         vc.to_float(vf);
-        st.add(s, vf);
+        st.add(sc, vf);
       }
     }
 
@@ -445,8 +522,8 @@ __global__ __launch_bounds__(kThreads) void query_kernel(QueryArgs a) {
     const int qlast = (qb * kWaves + kWaves - 1 < a.nq ? qb * kWaves + kWaves - 1 : a.nq - 1);
     const int64_t kmax = int64_t(a.offset) + qlast + 1 < a.nk ? int64_t(a.offset) + qlast + 1 : a.nk;
     const int* table_row = a.table + int64_t(b) * g.columns;
-    float qf[DL];
-    load_q<DT, D, VEC>(qf, qp + (bh * a.nq + (has_q ? qi : 0)) * dim, col0, dim, a.qscale);
+    Query<DT, D, VEC> qv;
+    qv.load(qp + (bh * a.nq + (has_q ? qi : 0)) * dim, col0, dim, a.qscale);
     Softmax<DL> st;
     st.init();
     for (int64_t c0 = 0; c0 < kmax; c0 += kMaxSplitTokens) {
@@ -457,7 +534,7 @@ __global__ __launch_bounds__(kThreads) void query_kernel(QueryArgs a) {
         s_page[j] = page_base<T>(a.slabs, table_row, (c0 >> g.log2_page) + j, g, head);
       __syncthreads();
       const int64_t mine = klen - c0 < c1 - c0 ? klen - c0 : c1 - c0;
-      if (mine > 0) stream_rows<DT, D, VEC, U>(st, qf, s_page, int(mine), 0, 1, g, dim);
+      if (mine > 0) stream_rows<DT, D, VEC, U, 2>(st, qv, s_page, int(mine), 0, 1, g, dim);
     }
     st.wave_merge();
     if (has_q && lane < kGroup) {
@@ -504,8 +581,8 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     T* vp = kp + g.kind_stride;
     const int64_t src = row * dim + col;
     if constexpr (VEC) {
-      *reinterpret_cast<uint4*>(kp) = *reinterpret_cast<const uint4*>(static_cast<const T*>(a.k) + src);
-      *reinterpret_cast<uint4*>(vp) = *reinterpret_cast<const uint4*>(static_cast<const T*>(a.v) + src);
+      *global_view(reinterpret_cast<u32x4*>(kp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k) + src));
+      *global_view(reinterpret_cast<u32x4*>(vp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v) + src));
     } else {
       *kp = static_cast<const T*>(a.k)[src];
       *vp = static_cast<const T*>(a.v)[src];
@@ -561,12 +638,16 @@ size_t workspace_bytes_for(int64_t bh, int nsplit_max) {
 
 template <int DT, int D, bool VEC>
 hipError_t launch_decode_t(const DecodeArgs& a, int64_t blocks, int unroll) {
-  if (unroll >= 4)
-    decode_kernel<DT, D, VEC, 4><<<grid_for(blocks), kThreads>>>(a);
-  else if (unroll == 2)
-    decode_kernel<DT, D, VEC, 2><<<grid_for(blocks), kThreads>>>(a);
-  else
-    decode_kernel<DT, D, VEC, 1><<<grid_for(blocks), kThreads>>>(a);
+  // Row bytes per lane bound the useful unroll: register stages beyond it spill.
+  constexpr int kMaxUnroll = !VEC ? 1 : (D * elem_bytes<DT>() >= 256 ? 2 : 4);
+  if (unroll > kMaxUnroll) unroll = kMaxUnroll;
+  if constexpr (kMaxUnroll >= 4) {
+    if (unroll >= 4) decode_kernel<DT, D, VEC, 4, kStages><<<grid_for(blocks), kThreads>>>(a);
+  }
+  if constexpr (kMaxUnroll >= 2) {
+    if (unroll == 2) decode_kernel<DT, D, VEC, 2, kStages><<<grid_for(blocks), kThreads>>>(a);
+  }
+  if (unroll <= 1) decode_kernel<DT, D, VEC, 1, kStages><<<grid_for(blocks), kThreads>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.nsplit_max == 1) return e;
   merge_kernel<DT, (D > 64 ? 128 : 64)><<<grid_for(int64_t(a.batch) * a.g.heads), 128>>>(a);
