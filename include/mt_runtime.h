@@ -28,8 +28,14 @@ int mt_event_create(void** e);
 int mt_event_record(void* e);
 int mt_event_elapsed(float* ms, void* a, void* b);
 int mt_event_destroy(void* e);
+/* Wait for an event. No reference counterpart. */
+int mt_event_synchronize(void* e);
 /* Number of visible devices. No reference counterpart. */
 int mt_device_count(int* n);
+/* Pinned host memory (hipHostMalloc) for asynchronous uploads.
+ * No reference counterpart. */
+int mt_host_alloc(void** p, size_t bytes);
+int mt_host_free(void* p);
 /* p[0:n] = v (fp32). Replaces reference mt_fill (src/cuda_runtime.cu:54-57). */
 int mt_fill(float* p, int n, float v);
 /* Fill `words` 32-bit words with `value` by a kernel (graph-capturable,

@@ -1,0 +1,99 @@
+/* Device-side page allocator and decode-step scheduler metadata: C-ABI of
+ * minitorch_amd/cuda_kernels/sched_kernels.so (gfx950).
+ *
+ * The reference keeps the page free list, per-cache page lists, block tables
+ * and decode offsets on the host (minitorch/paged_kv_cache.py:27-263,
+ * minitorch/paged_decode.py:10-93) and uploads them every step. Here they live
+ * in one device "pool state" blob updated by kernels on the null stream, with
+ * page IDs identical to the reference's allocator: LIFO pops, new slabs'
+ * page IDs pushed in reverse order on top of older free pages before a pop
+ * that finds too few free pages, releases pushed in the given order.
+ *
+ * Every pool entry takes the same geometry arguments (MT_POOL_ARGS below):
+ * state (device blob of the size mt_pool_layout reports), max_pages =
+ * max_slabs * pages_per_slab, max_slots (cache rows the pool can track),
+ * max_cols (page columns per row), pool_base (device address of slab 0;
+ * slab s is at pool_base + s * slab_bytes). Status convention as in
+ * mt_paged.h. Budget checks (MemoryError in the reference) are the caller's:
+ * the host knows how many pages are leased without reading the device.
+ */
+#ifndef MT_SCHED_H
+#define MT_SCHED_H
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Header at offset 0 of the state blob. */
+typedef struct mt_pool_header {
+  int top;          /* free pages on the stack */
+  int slabs_opened; /* slabs whose pages have entered the free list */
+  int leased;       /* pages owned by caches or API owners */
+  int error;        /* nonzero after a release of pages the owner does not hold */
+  long long acquires, releases, reuses;
+} mt_pool_header;
+
+/* Byte offsets inside the state blob: [0] header, [1] free stack (int32
+ * [max_pages]), [2] issued bitmap, [3] page owner (int32 [max_pages]),
+ * [4] slab table (uint64 [max_slabs], 0 until a slab is opened), [5] slot
+ * lengths (int32 [max_slots]), [6] slot page counts, [7] slot pages (int32
+ * [max_slots, max_cols], -1 beyond a row's pages), [8] total bytes.
+ * No reference counterpart (new device-side metadata). */
+int mt_pool_layout(int max_pages, int max_slabs, int max_slots, int max_cols, size_t* offsets);
+
+#define MT_POOL_ARGS                                                                          \
+  void *state, int max_pages, int max_slabs, int max_slots, int max_cols, int pages_per_slab, \
+      unsigned long long pool_base, unsigned long long slab_bytes
+
+/* Empty pool: no slabs opened, every slot row empty.
+ * Replaces the state set up by reference KVPagePool.__init__ (minitorch/paged_kv_cache.py:62-69). */
+int mt_pool_init(MT_POOL_ARGS);
+
+/* Pop `count` pages for `owner` into out_pages (device int32 [count]).
+ * Replaces reference KVPagePool.acquire (minitorch/paged_kv_cache.py:71-94). */
+int mt_pool_pop(MT_POOL_ARGS, int count, int owner, int* out_pages);
+
+/* Push pages (device int32 [count]) held by `owner`, in order; a page the
+ * owner does not hold sets header.error and is skipped.
+ * Replaces reference KVPagePool.release (minitorch/paged_kv_cache.py:96-103). */
+int mt_pool_push(MT_POOL_ARGS, const int* pages, int count, int owner);
+
+/* Append per_row pages to each row slots[0..rows) from one pop of
+ * rows * per_row pages (scratch: device int32 [rows * per_row]).
+ * Replaces the page part of reference PagedKVCache.prepare_append
+ * (minitorch/paged_kv_cache.py:171-186). */
+int mt_pool_acquire_rows(MT_POOL_ARGS, const int* slots, int rows, int per_row, int* scratch);
+
+/* Release the pages [keep:] of each row slots[0..rows), row by row; with
+ * reset_length the rows' lengths become 0. keep = 0 replaces reference
+ * _release_cache / PagedKVCache.close (minitorch/paged_kv_cache.py:125-131);
+ * keep = the page count before an append replaces PagedKVCache.abort_append
+ * (minitorch/paged_kv_cache.py:228-234). */
+int mt_pool_release_rows(MT_POOL_ARGS, const int* slots, int rows, int keep, int reset_length);
+
+/* Decode-step metadata for the rows slots[0..b) (one new token each): every
+ * row whose next token starts a new page takes one page, row by row (at most
+ * `limit` pops); new_page[i] = that page or -1; offsets[i] = committed length;
+ * positions[i] = (float)offsets[i]; cu_seqlens[0..b] = exclusive prefix sum
+ * of offsets[i] + 1; table [b, columns] = each row's pages, -1 beyond them.
+ * Replaces reference PagedDecodeBatch.prepare (minitorch/paged_decode.py:303-317). */
+int mt_sched_decode_prepare(MT_POOL_ARGS, const int* slots, int b, int columns, int page_size,
+                            int limit, int* table, int* offsets, float* positions,
+                            int* cu_seqlens, int* new_page);
+
+/* lengths[slots[i]] += tokens. Replaces the length update of reference
+ * CacheBase.commit_append (minitorch/kv_cache.py:343-348). */
+int mt_sched_add_length(MT_POOL_ARGS, const int* slots, int b, int tokens);
+
+/* Return the pages taken by mt_sched_decode_prepare (new_page >= 0), in row
+ * order. Replaces reference PagedDecodeBatch.__exit__'s aborts
+ * (minitorch/paged_decode.py:351-353). */
+int mt_sched_decode_abort(MT_POOL_ARGS, const int* slots, int b, const int* new_page);
+
+#undef MT_POOL_ARGS
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MT_SCHED_H */

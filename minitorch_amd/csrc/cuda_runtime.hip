@@ -49,7 +49,11 @@ int mt_event_elapsed(float* ms, hipEvent_t a, hipEvent_t b) {
   return e == hipSuccess ? hipEventElapsedTime(ms, a, b) : e;
 }
 int mt_event_destroy(hipEvent_t e) { return hipEventDestroy(e); }
+int mt_event_synchronize(hipEvent_t e) { return hipEventSynchronize(e); }
 int mt_device_count(int* n) { return hipGetDeviceCount(n); }
+// Pinned host memory for asynchronous uploads (allocated, never registered).
+int mt_host_alloc(void** p, size_t bytes) { return hipHostMalloc(p, bytes, hipHostMallocDefault); }
+int mt_host_free(void* p) { return hipHostFree(p); }
 
 // out[0:n] = value (reference mt_fill, src/cuda_runtime.cu:33-35,54-57).
 int mt_fill(float* p, int n, float v) {

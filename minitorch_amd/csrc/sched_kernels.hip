@@ -1,0 +1,467 @@
+// Device-side page allocator and decode-step metadata for gfx950.
+//
+// The reference keeps the page free list, per-cache page lists, block tables
+// and decode offsets on the host and uploads them every step
+// (minitorch/paged_kv_cache.py:71-103,171-189; minitorch/paged_decode.py:303-317).
+// Here they live in one device "pool state" blob and are updated by small
+// single-workgroup kernels on the null stream, so admitting, stepping and
+// finishing requests never reads device memory back. Page IDs follow the
+// reference's host allocator exactly:
+//   * the free list is a LIFO stack; pops take the top;
+//   * when a pop of `count` pages finds fewer than `count` free pages, whole
+//     new slabs are opened first and their IDs pushed in reverse order on top
+//     of the older free pages, then all `count` pages are popped
+//     (paged_kv_cache.py:78-89) -- "bulk" pops, used by prepare_append(n);
+//   * a decode step acquires one page per row that needs it, row by row, each
+//     as its own pop of one page (paged_decode.py:307-309 calling
+//     paged_kv_cache.py:171-186) -- "sequential" pops;
+//   * releases push pages in the given order (paged_kv_cache.py:96-103).
+// The state blob layout is computed by pool_layout() and exported through
+// mt_pool_layout() so the host can address the slab table and slot rows.
+#include "mt_device.h"
+#include <climits>
+
+namespace {
+
+constexpr int kThreads = 1024;
+
+struct Header {           // must match include/mt_sched.h (mt_pool_header)
+  int top;                // free pages on the stack
+  int slabs_opened;
+  int leased;
+  int error;              // nonzero after an invalid release
+  long long acquires, releases, reuses;
+};
+
+struct Layout {
+  size_t header, stack, issued, owner, slab_table, slot_len, slot_npages, slot_pages, total;
+};
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+Layout pool_layout(int max_pages, int max_slabs, int max_slots, int max_cols) {
+  Layout l;
+  size_t o = 0;
+  l.header = o; o = align256(o + sizeof(Header));
+  l.stack = o; o = align256(o + size_t(max_pages) * 4);
+  l.issued = o; o = align256(o + size_t((max_pages + 31) / 32) * 4);
+  l.owner = o; o = align256(o + size_t(max_pages) * 4);
+  l.slab_table = o; o = align256(o + size_t(max_slabs) * 8);
+  l.slot_len = o; o = align256(o + size_t(max_slots) * 4);
+  l.slot_npages = o; o = align256(o + size_t(max_slots) * 4);
+  l.slot_pages = o; o = align256(o + size_t(max_slots) * max_cols * 4);
+  l.total = o;
+  return l;
+}
+
+struct Pool {
+  Header* h;
+  int* stack;
+  unsigned* issued;
+  int* owner;
+  unsigned long long* slab_table;
+  int* slot_len;
+  int* slot_npages;
+  int* slot_pages;
+  int max_pages, max_slabs, max_slots, max_cols, pages_per_slab;
+  unsigned long long pool_base, slab_bytes;
+};
+
+Pool make_pool(void* state, int max_pages, int max_slabs, int max_slots, int max_cols, int pps,
+               unsigned long long pool_base, unsigned long long slab_bytes) {
+  const Layout l = pool_layout(max_pages, max_slabs, max_slots, max_cols);
+  char* s = static_cast<char*>(state);
+  Pool p;
+  p.h = reinterpret_cast<Header*>(s + l.header);
+  p.stack = reinterpret_cast<int*>(s + l.stack);
+  p.issued = reinterpret_cast<unsigned*>(s + l.issued);
+  p.owner = reinterpret_cast<int*>(s + l.owner);
+  p.slab_table = reinterpret_cast<unsigned long long*>(s + l.slab_table);
+  p.slot_len = reinterpret_cast<int*>(s + l.slot_len);
+  p.slot_npages = reinterpret_cast<int*>(s + l.slot_npages);
+  p.slot_pages = reinterpret_cast<int*>(s + l.slot_pages);
+  p.max_pages = max_pages; p.max_slabs = max_slabs; p.max_slots = max_slots;
+  p.max_cols = max_cols; p.pages_per_slab = pps; p.pool_base = pool_base; p.slab_bytes = slab_bytes;
+  return p;
+}
+
+// Record the pop of page `page` for `owner`; returns 1 if it was issued before.
+__device__ __forceinline__ int mark_issued(const Pool& p, int page, int owner) {
+  p.owner[page] = owner;
+  const unsigned bit = 1u << (page & 31);
+  return (atomicOr(&p.issued[page >> 5], bit) & bit) ? 1 : 0;
+}
+
+__device__ __forceinline__ void open_slabs(const Pool& p, int first, int count) {
+  for (int s = threadIdx.x; s < count; s += blockDim.x)
+    p.slab_table[first + s] = p.pool_base + (unsigned long long)(first + s) * p.slab_bytes;
+}
+
+// Block-wide exclusive scan of one int per thread (blockDim.x <= 1024).
+__device__ int block_exclusive_scan(int x, int* total, int* sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = (blockDim.x + 63) >> 6;
+  int incl = x;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63 || tid == int(blockDim.x) - 1) sh[wave] = incl;
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int w = 0; w < nw; ++w) { const int v = sh[w]; sh[w] = run; run += v; }
+    sh[32] = run;
+  }
+  __syncthreads();
+  const int excl = sh[wave] + incl - x;
+  *total = sh[32];
+  __syncthreads();
+  return excl;
+}
+
+// Bulk pop of `count` pages (one reference acquire(count)): opens slabs first
+// when the stack is short, then pops. out[r] is the r-th popped page.
+__device__ void bulk_pop(const Pool& p, int count, int owner, int* out, int* s_red) {
+  const int F = p.h->top, opened = p.h->slabs_opened, pps = p.pages_per_slab;
+  const int nslab = count > F ? (count - F + pps - 1) / pps : 0;
+  const int T = F + nslab * pps;
+  int reused = 0;
+  for (int r = threadIdx.x; r < count; r += blockDim.x) {
+    const int idx = T - 1 - r;
+    int page;
+    if (idx >= F) {
+      const int j = (idx - F) / pps, i = (idx - F) % pps;
+      page = (opened + j) * pps + (pps - 1 - i);
+    } else {
+      page = p.stack[idx];
+    }
+    out[r] = page;
+    reused += mark_issued(p, page, owner);
+  }
+  __syncthreads();  // all reads of old stack entries are done
+  // Materialize the unpopped entries of the new slabs.
+  for (int idx = F + threadIdx.x; idx < T - count; idx += blockDim.x) {
+    const int j = (idx - F) / pps, i = (idx - F) % pps;
+    p.stack[idx] = (opened + j) * pps + (pps - 1 - i);
+  }
+  open_slabs(p, opened, nslab);
+  atomicAdd(s_red, reused);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    p.h->top = T - count;
+    p.h->slabs_opened = opened + nslab;
+    p.h->leased += count;
+    p.h->acquires += count;
+    p.h->reuses += *s_red;
+    *s_red = 0;
+  }
+  __syncthreads();
+}
+
+// Push pages[0..n) (in order) on the free stack.
+__device__ void push_pages(const Pool& p, const int* pages, int n, int expect_owner, bool check) {
+  const int top = p.h->top;
+  int bad = 0;
+  for (int r = threadIdx.x; r < n; r += blockDim.x) {
+    const int page = pages[r];
+    if (check && (page < 0 || page >= p.max_pages || p.owner[page] != expect_owner)) { bad = 1; continue; }
+    p.stack[top + r] = page;
+    p.owner[page] = -1;
+  }
+  if (bad) atomicOr(&p.h->error, 1);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    p.h->top = top + n;
+    p.h->leased -= n;
+    p.h->releases += n;
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kThreads) void init_kernel(Pool p) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    p.h->top = 0; p.h->slabs_opened = 0; p.h->leased = 0; p.h->error = 0;
+    p.h->acquires = 0; p.h->releases = 0; p.h->reuses = 0;
+  }
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  const int64_t t0 = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t i = t0; i < (p.max_pages + 31) / 32; i += stride) p.issued[i] = 0;
+  for (int64_t i = t0; i < p.max_pages; i += stride) p.owner[i] = -1;
+  for (int64_t i = t0; i < p.max_slabs; i += stride) p.slab_table[i] = 0;
+  for (int64_t i = t0; i < p.max_slots; i += stride) { p.slot_len[i] = 0; p.slot_npages[i] = 0; }
+  for (int64_t i = t0; i < int64_t(p.max_slots) * p.max_cols; i += stride) p.slot_pages[i] = -1;
+}
+
+// Reference acquire(count, owner) returning the pages (API path).
+__global__ __launch_bounds__(kThreads) void pop_kernel(Pool p, int count, int owner, int* out) {
+  __shared__ int s_red;
+  if (threadIdx.x == 0) s_red = 0;
+  __syncthreads();
+  bulk_pop(p, count, owner, out, &s_red);
+}
+
+// Reference release(pages, owner) (API path); invalid ownership sets error.
+__global__ __launch_bounds__(kThreads) void push_kernel(Pool p, const int* pages, int n, int owner) {
+  push_pages(p, pages, n, owner, true);
+}
+
+// prepare_append(tokens) of a cache whose rows are slots[0..rows): one bulk
+// pop of rows * per_row pages, distributed row by row.
+__global__ __launch_bounds__(kThreads) void acquire_rows_kernel(Pool p, const int* slots, int rows,
+                                                                int per_row, int* scratch) {
+  __shared__ int s_red;
+  if (threadIdx.x == 0) s_red = 0;
+  __syncthreads();
+  const int count = rows * per_row;
+  // owner of a cache's pages is its first slot
+  bulk_pop(p, count, slots[0], scratch, &s_red);
+  for (int r = threadIdx.x; r < count; r += blockDim.x) {
+    const int row = r / per_row, j = r - row * per_row;
+    const int slot = slots[row];
+    p.slot_pages[int64_t(slot) * p.max_cols + p.slot_npages[slot] + j] = scratch[r];
+  }
+  __syncthreads();
+  for (int row = threadIdx.x; row < rows; row += blockDim.x) p.slot_npages[slots[row]] += per_row;
+}
+
+// Release the pages [keep:] of each row slots[0..rows), row by row, in page
+// order (close: keep = 0; abort of an append: keep = the count before it).
+__global__ __launch_bounds__(kThreads) void release_rows_kernel(Pool p, const int* slots, int rows,
+                                                                int keep, int reset_length) {
+  __shared__ int sh[33];
+  int top = p.h->top;
+  int released = 0;
+  for (int base = 0; base < rows; base += blockDim.x) {
+    const int row = base + threadIdx.x;
+    const int slot = row < rows ? slots[row] : 0;
+    const int n = row < rows ? max(p.slot_npages[slot] - keep, 0) : 0;
+    int total;
+    const int at = block_exclusive_scan(n, &total, sh);
+    for (int j = 0; j < n; ++j) {
+      const int page = p.slot_pages[int64_t(slot) * p.max_cols + keep + j];
+      p.stack[top + at + j] = page;
+      p.owner[page] = -1;
+      p.slot_pages[int64_t(slot) * p.max_cols + keep + j] = -1;
+    }
+    if (row < rows) {
+      if (n) p.slot_npages[slot] = keep;
+      if (reset_length) p.slot_len[slot] = 0;
+    }
+    top += total;
+    released += total;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    p.h->top = top;
+    p.h->leased -= released;
+    p.h->releases += released;
+  }
+}
+
+// Decode-step metadata for a batch of slots (one token per row):
+//   offsets[i] = committed length, positions[i] = float(offsets[i]),
+//   cu_seqlens = exclusive prefix sum of offsets[i] + 1,
+//   rows whose next token starts a new page pop one page each, row by row
+//   (sequential pops, limited to `limit` pops), new_page[i] = popped page or -1,
+//   table[i, :columns] = the row's pages, -1 beyond them.
+__global__ __launch_bounds__(kThreads) void decode_prepare_kernel(Pool p, const int* slots, int b,
+                                                                  int columns, int page_size,
+                                                                  int limit, int* table,
+                                                                  int* offsets, float* positions,
+                                                                  int* cu_seqlens, int* new_page) {
+  __shared__ int sh[33];
+  __shared__ int s_red;
+  if (threadIdx.x == 0) s_red = 0;
+  const int F = p.h->top, opened = p.h->slabs_opened, pps = p.pages_per_slab;
+  __syncthreads();
+  int need_base = 0, seq_base = 0, reused = 0, last_rank = -1;
+  for (int base = 0; base < b; base += blockDim.x) {
+    const int i = base + threadIdx.x;
+    const int slot = i < b ? slots[i] : 0;
+    const int len = i < b ? p.slot_len[slot] : 0;
+    const int have = i < b ? p.slot_npages[slot] : 0;
+    const int need = (i < b && (len + 1 + page_size - 1) / page_size > have) ? 1 : 0;
+    int total_need, total_seq;
+    const int rank = need_base + block_exclusive_scan(need, &total_need, sh);
+    const int seq = seq_base + block_exclusive_scan(i < b ? len + 1 : 0, &total_seq, sh);
+    if (i < b) {
+      offsets[i] = len;
+      positions[i] = float(len);
+      cu_seqlens[i] = seq;
+      int page = -1;
+      if (need && rank < limit) {
+        if (rank < F) {
+          page = p.stack[F - 1 - rank];
+        } else {
+          const int k = rank - F;
+          page = (opened + k / pps) * pps + k % pps;
+        }
+        reused += mark_issued(p, page, slot);
+        p.slot_pages[int64_t(slot) * p.max_cols + have] = page;
+        p.slot_npages[slot] = have + 1;
+        last_rank = rank;
+      }
+      new_page[i] = page;
+    }
+    need_base += total_need;
+    seq_base += total_seq;
+  }
+  if (threadIdx.x == 0) cu_seqlens[b] = seq_base;
+  atomicAdd(&s_red, reused);
+  __syncthreads();
+  const int pops = need_base < limit ? need_base : limit;
+  // Leftover pages of the last slab opened by the sequential pops stay on the
+  // stack, reversed (its unused IDs with the smallest unused on top).
+  int nslab = 0, top = F - pops;
+  if (pops > F) {
+    const int m = pops - F;
+    nslab = (m + pps - 1) / pps;
+    const int used_last = m - (nslab - 1) * pps;
+    const int last = opened + nslab - 1;
+    top = pps - used_last;
+    for (int j = threadIdx.x; j < top; j += blockDim.x) p.stack[j] = last * pps + pps - 1 - j;
+  }
+  (void)last_rank;
+  open_slabs(p, opened, nslab);
+  __syncthreads();
+  for (int64_t e = threadIdx.x; e < int64_t(b) * columns; e += blockDim.x) {
+    const int i = int(e / columns), c = int(e - int64_t(i) * columns);
+    const int slot = slots[i];
+    table[e] = c < p.slot_npages[slot] ? p.slot_pages[int64_t(slot) * p.max_cols + c] : -1;
+  }
+  if (threadIdx.x == 0) {
+    p.h->top = top;
+    p.h->slabs_opened = opened + nslab;
+    p.h->leased += pops;
+    p.h->acquires += pops;
+    p.h->reuses += s_red;
+  }
+}
+
+// Commit: lengths += tokens for every row.
+__global__ __launch_bounds__(kThreads) void add_length_kernel(Pool p, const int* slots, int b, int tokens) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < b; i += gridDim.x * blockDim.x)
+    p.slot_len[slots[i]] += tokens;
+}
+
+// Abort of a decode step: push back the pages popped by decode_prepare_kernel,
+// in row order (the reference aborts every prepared cache in batch order).
+__global__ __launch_bounds__(kThreads) void decode_abort_kernel(Pool p, const int* slots, int b,
+                                                                const int* new_page) {
+  __shared__ int sh[33];
+  int top = p.h->top, released = 0;
+  for (int base = 0; base < b; base += blockDim.x) {
+    const int i = base + threadIdx.x;
+    const int page = i < b ? new_page[i] : -1;
+    int total;
+    const int at = block_exclusive_scan(page >= 0 ? 1 : 0, &total, sh);
+    if (page >= 0) {
+      const int slot = slots[i];
+      p.stack[top + at] = page;
+      p.owner[page] = -1;
+      p.slot_npages[slot] -= 1;
+      p.slot_pages[int64_t(slot) * p.max_cols + p.slot_npages[slot]] = -1;
+    }
+    top += total;
+    released += total;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    p.h->top = top;
+    p.h->leased -= released;
+    p.h->releases += released;
+  }
+}
+
+bool valid_geometry(int max_pages, int max_slabs, int max_slots, int max_cols, int pps) {
+  return max_pages > 0 && max_slabs > 0 && max_slots > 0 && max_cols > 0 && pps > 0 &&
+         int64_t(max_slabs) * pps == max_pages && int64_t(max_slots) * max_cols <= INT32_MAX;
+}
+
+}  // namespace
+
+#define MT_POOL_ARGS                                                                          \
+  void *state, int max_pages, int max_slabs, int max_slots, int max_cols, int pages_per_slab, \
+      unsigned long long pool_base, unsigned long long slab_bytes
+#define MT_POOL make_pool(state, max_pages, max_slabs, max_slots, max_cols, pages_per_slab, pool_base, slab_bytes)
+#define MT_POOL_CHECK                                                                   \
+  if (!state || !valid_geometry(max_pages, max_slabs, max_slots, max_cols, pages_per_slab)) \
+    return hipErrorInvalidValue;
+
+extern "C" {
+
+int mt_pool_layout(int max_pages, int max_slabs, int max_slots, int max_cols, size_t* offsets) {
+  if (!offsets || max_pages < 1 || max_slabs < 1 || max_slots < 1 || max_cols < 1)
+    return hipErrorInvalidValue;
+  const Layout l = pool_layout(max_pages, max_slabs, max_slots, max_cols);
+  const size_t v[9] = {l.header, l.stack, l.issued, l.owner, l.slab_table,
+                       l.slot_len, l.slot_npages, l.slot_pages, l.total};
+  for (int i = 0; i < 9; ++i) offsets[i] = v[i];
+  return hipSuccess;
+}
+
+int mt_pool_init(MT_POOL_ARGS) {
+  MT_POOL_CHECK
+  init_kernel<<<256, 256>>>(MT_POOL);
+  return hipGetLastError();
+}
+
+int mt_pool_pop(MT_POOL_ARGS, int count, int owner, int* out_pages) {
+  MT_POOL_CHECK
+  if (count < 0 || count > max_pages || (count > 0 && !out_pages)) return hipErrorInvalidValue;
+  if (count) pop_kernel<<<1, kThreads>>>(MT_POOL, count, owner, out_pages);
+  return hipGetLastError();
+}
+
+int mt_pool_push(MT_POOL_ARGS, const int* pages, int count, int owner) {
+  MT_POOL_CHECK
+  if (count < 0 || count > max_pages || (count > 0 && !pages)) return hipErrorInvalidValue;
+  if (count) push_kernel<<<1, kThreads>>>(MT_POOL, pages, count, owner);
+  return hipGetLastError();
+}
+
+int mt_pool_acquire_rows(MT_POOL_ARGS, const int* slots, int rows, int per_row, int* scratch) {
+  MT_POOL_CHECK
+  if (!slots || rows < 1 || per_row < 0 || int64_t(rows) * per_row > max_pages ||
+      (per_row > 0 && !scratch))
+    return hipErrorInvalidValue;
+  if (per_row) acquire_rows_kernel<<<1, kThreads>>>(MT_POOL, slots, rows, per_row, scratch);
+  return hipGetLastError();
+}
+
+int mt_pool_release_rows(MT_POOL_ARGS, const int* slots, int rows, int keep, int reset_length) {
+  MT_POOL_CHECK
+  if (!slots || rows < 1 || keep < 0) return hipErrorInvalidValue;
+  release_rows_kernel<<<1, kThreads>>>(MT_POOL, slots, rows, keep, reset_length);
+  return hipGetLastError();
+}
+
+int mt_sched_decode_prepare(MT_POOL_ARGS, const int* slots, int b, int columns, int page_size,
+                            int limit, int* table, int* offsets, float* positions,
+                            int* cu_seqlens, int* new_page) {
+  MT_POOL_CHECK
+  if (!slots || b < 1 || columns < 1 || columns > max_cols || limit < 0 || !table || !offsets ||
+      !positions || !cu_seqlens || !new_page || !(page_size == 8 || page_size == 16 || page_size == 32) ||
+      int64_t(b) * columns > INT32_MAX)
+    return hipErrorInvalidValue;
+  decode_prepare_kernel<<<1, kThreads>>>(MT_POOL, slots, b, columns, page_size, limit, table,
+                                         offsets, positions, cu_seqlens, new_page);
+  return hipGetLastError();
+}
+
+int mt_sched_add_length(MT_POOL_ARGS, const int* slots, int b, int tokens) {
+  MT_POOL_CHECK
+  if (!slots || b < 1) return hipErrorInvalidValue;
+  add_length_kernel<<<(b + kThreads - 1) / kThreads, kThreads>>>(MT_POOL, slots, b, tokens);
+  return hipGetLastError();
+}
+
+int mt_sched_decode_abort(MT_POOL_ARGS, const int* slots, int b, const int* new_page) {
+  MT_POOL_CHECK
+  if (!slots || b < 1 || !new_page) return hipErrorInvalidValue;
+  decode_abort_kernel<<<1, kThreads>>>(MT_POOL, slots, b, new_page);
+  return hipGetLastError();
+}
+
+}  // extern "C"

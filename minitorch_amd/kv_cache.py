@@ -1,0 +1,148 @@
+"""Cache transaction base and token helpers (reference minitorch/kv_cache.py).
+
+``CacheBase`` keeps the reference's transaction state machine
+(prepare_append / commit_append / abort_append, one write per layer,
+validation of model, precision and weight version; kv_cache.py:56-160).
+``greedy_token`` and ``last_position`` run ``mt_row_argmax`` and
+``mt_last_row`` from ``cuda_kernels/inference_kernels.so``
+(kv_cache.py:26-53). This build has no autograd, so the reference's no_grad
+checks have nothing to check.
+"""
+import weakref
+from .amp import autocast_dtype
+from .runtime import DeviceTensor
+from . import paged_ops
+
+
+def last_position(x):
+    """Copy the last sequence position of a device [B, T, C] tensor (reference
+    minitorch/kv_cache.py:26-36)."""
+    if not isinstance(x, DeviceTensor) or x.dims != 3:
+        raise ValueError('last_position requires no_grad and device [B,T,C] input')
+    b, n, w = x.shape
+    if min(b, n, w) < 1:
+        raise ValueError('Empty last-position input')
+    out = DeviceTensor((b, 1, w), x.dtype)
+    paged_ops.last_row(out.ptr, x.ptr, b, n, w, x.dtype)
+    return out
+
+
+def greedy_token(logits):
+    """GPU argmax over [B, 1, V] logits, returning fp32 token IDs [B, 1]; ties
+    and NaNs choose the first index, like numpy.argmax (reference
+    minitorch/kv_cache.py:39-53)."""
+    if not isinstance(logits, DeviceTensor) or logits.dims != 3 or logits.shape[1] != 1:
+        raise ValueError('greedy_token requires no_grad and device logits [B,1,V]')
+    b, _, v = logits.shape
+    if b < 1 or not 1 <= v <= 2 ** 24:
+        raise ValueError('Vocabulary must fit exact FP32 token IDs')
+    out = DeviceTensor((b, 1), 'float32')
+    paged_ops.row_argmax(out.ptr, logits.ptr, b, v, logits.dtype)
+    return out
+
+
+class CacheBase:
+    """Transaction state shared by inference caches (reference minitorch/kv_cache.py:56-160)."""
+
+    def __init__(self, model, batch_size=1, capacity=None):
+        if getattr(model, 'training', False):
+            raise ValueError('Call model.eval() before creating an inference cache')
+        capacity = model.n_positions if capacity is None else capacity
+        if (type(batch_size) is not int or batch_size < 1 or type(capacity) is not int
+                or not 1 <= capacity <= model.n_positions):
+            raise ValueError('Invalid cache batch size or capacity')
+        layers = model.transformer_layers()
+        if any(l.attention.attn_hidden_dim > 128 for l in layers):
+            raise ValueError('Cached inference requires head_dim<=128')
+        self.model = weakref.ref(model)
+        self.batch_size, self.capacity = batch_size, capacity
+        self.dtype = autocast_dtype() or 'float32'
+        self.length, self.valid, self.closed = 0, True, False
+        self.layout = tuple((l.attention.n_head, l.attention.attn_hidden_dim) for l in layers)
+        self._pending_tokens = None
+        self._written_layers = set()
+        self.weights = self._weights()
+        self.last_attention_path = None
+
+    def _weights(self):
+        model = self.model()
+        if model is None:
+            raise ValueError('Cache model no longer exists')
+        return model.weights_version()
+
+    def prefill_attention(self, layer, q, k, v):
+        if self.length != 0:
+            raise ValueError('prefill attention requires empty cache')
+        return self._attention(layer, q, k, v, prefill=True)
+
+    def decode_attention(self, layer, q, k, v):
+        if self.length == 0 or self._pending_tokens != 1:
+            raise ValueError('decode attention requires populated cache and one token')
+        return self._attention(layer, q, k, v, prefill=False)
+
+    def attention(self, layer, q, k, v):
+        return (self.prefill_attention if self.length == 0 else self.decode_attention)(layer, q, k, v)
+
+    def _validate_model(self, model):
+        if self.closed or not self.valid:
+            raise ValueError('Cache is closed or invalid; reset/create a cache')
+        if self.model() is not model:
+            raise ValueError('Cache/model/backend mismatch')
+        if getattr(model, 'training', False):
+            raise ValueError('Cached inference requires eval and no_grad')
+        if self.dtype != (autocast_dtype() or 'float32') or self.weights != self._weights():
+            raise ValueError('Cache precision or model weights changed; reset/create a cache')
+
+    def validate(self, model, idx, prefill):
+        self._validate_model(model)
+        if not isinstance(idx, DeviceTensor):
+            raise ValueError('Cache/model/backend mismatch')
+        if idx.dims != 2 or idx.shape[0] != self.batch_size or idx.dtype != 'float32':
+            raise ValueError('Expected FP32 token IDs [cache_batch, sequence]')
+        if prefill and self.length != 0:
+            raise ValueError('prefill requires an empty cache')
+        if not prefill and (self.length == 0 or idx.shape[1] != 1):
+            raise ValueError('decode_step requires a populated cache and one token per batch')
+        if idx.shape[1] < 1 or self.length + idx.shape[1] > self.capacity:
+            raise ValueError('KV cache capacity exceeded or empty prompt')
+
+    def prepare_append(self, tokens):
+        if self.closed or not self.valid or self._pending_tokens is not None:
+            raise ValueError('Cache closed, invalid, or append already pending')
+        if self.dtype != (autocast_dtype() or 'float32'):
+            raise ValueError('Cache writes require no_grad and matching precision')
+        if type(tokens) is not int or tokens < 1 or self.length + tokens > self.capacity:
+            raise ValueError('Invalid append size or cache capacity exceeded')
+        self._pending_tokens = tokens
+        self._written_layers.clear()
+
+    def _check_attention(self, layer, q, k, v):
+        if (self.closed or not self.valid or self._pending_tokens is None
+                or type(layer) is not int or not 0 <= layer < len(self.layout)
+                or layer in self._written_layers):
+            raise ValueError('Invalid cache append transaction or layer')
+        h, d = self.layout[layer]
+        expected = (self.batch_size, h, self._pending_tokens, d)
+        if any(not isinstance(t, DeviceTensor) or t.shape != expected or t.dtype != self.dtype
+               for t in (q, k, v)):
+            raise ValueError('Cache append shape/dtype/backend mismatch')
+
+    def commit_append(self):
+        if self._pending_tokens is None or len(self._written_layers) != len(self.layout):
+            raise ValueError('Cannot commit an incomplete cache append')
+        self.length += self._pending_tokens
+        self._pending_tokens = None
+        self._written_layers.clear()
+
+    def abort_append(self):
+        self._pending_tokens = None
+        self._written_layers.clear()
+        self.valid = False
+
+    def reset(self):
+        if self.closed:
+            raise ValueError('Cannot reset a closed cache')
+        self.weights = self._weights()
+        self.length, self.valid = 0, True
+        self._pending_tokens = None
+        self._written_layers.clear()

@@ -1,0 +1,294 @@
+"""GPT-2 decoder for the end-to-end decode configurations.
+
+Mirrors the reference model's inference entry points
+(minitorch/modules_transformer.py:355-410: ``create_kv_cache``, ``prefill``,
+``decode_step``, ``decode_batch``) and the GPT-2 layer math of
+``TransformerLayer.forward`` (:258-284) with the pretrained adapter's layout
+(minitorch/pretrained_gpt2.py:52-127): fp32 residual stream, LayerNorm in
+fp32, Q/K/V/out/MLP projections, tanh GELU, tied output head. Weights are a
+seeded random init (N(0, 0.02) matrices and embeddings, zero biases, unit
+LayerNorm gains, as HF GPT-2 initializes them) or a host state dict.
+
+MI355X-first choices: projection weights are kept resident on the device in
+the compute type (the reference re-casts fp32 masters on every matmul,
+minitorch/tensor.py:226-231); every projection is one hipBLASLt call with the
+bias as its epilogue; the decode step's Q/K/V are [B, H, 1, D] views of the
+projection outputs (no permute copies).
+"""
+import ctypes as ct
+import numpy as np
+
+from .amp import autocast_dtype
+from .dtypes import dtype_code
+from .runtime import DeviceTensor, library, call, runtime, P, I, F
+from .kv_cache import last_position
+from . import paged_ops
+
+LL = ct.c_longlong
+
+
+def model_library():
+    return library('model_kernels')
+
+
+class _Attention:
+    def __init__(self, n_head, head_dim):
+        self.n_head = n_head
+        self.attn_hidden_dim = head_dim
+        self.attention_impl = 'flash'
+
+
+class _Layer:
+    def __init__(self, n_head, head_dim):
+        self.attention = _Attention(n_head, head_dim)
+
+
+class _Blas:
+    def __init__(self):
+        self.handle = P()
+        call(model_library(), 'mt_blas_create', [ct.POINTER(P)], ct.byref(self.handle))
+
+    def gemm(self, out, a, b, bias, m, n, k, transb, dtype):
+        call(model_library(), 'mt_gemm_ex', [P] * 5 + [I] * 6, self.handle, out, a, b, bias, m, n, k,
+             transb, dtype_code(dtype), dtype_code(dtype))
+
+
+def init_gpt2_state(*, n_vocab, n_embd, n_layer, n_positions, seed=0, std=0.02):
+    """Seeded HF-style random GPT-2 weights as a dict of fp32 numpy arrays in
+    the GPT-2 checkpoint layout (Conv1D weights are [in, out])."""
+    rng = np.random.default_rng(seed)
+    d = n_embd
+
+    def normal(*shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+    state = {'transformer.wte.weight': normal(n_vocab, d), 'transformer.wpe.weight': normal(n_positions, d),
+             'transformer.ln_f.weight': np.ones(d, np.float32), 'transformer.ln_f.bias': np.zeros(d, np.float32)}
+    for i in range(n_layer):
+        p = f'transformer.h.{i}.'
+        state[p + 'ln_1.weight'] = np.ones(d, np.float32)
+        state[p + 'ln_1.bias'] = np.zeros(d, np.float32)
+        state[p + 'ln_2.weight'] = np.ones(d, np.float32)
+        state[p + 'ln_2.bias'] = np.zeros(d, np.float32)
+        state[p + 'attn.c_attn.weight'] = normal(d, 3 * d)
+        state[p + 'attn.c_attn.bias'] = np.zeros(3 * d, np.float32)
+        state[p + 'attn.c_proj.weight'] = normal(d, d)
+        state[p + 'attn.c_proj.bias'] = np.zeros(d, np.float32)
+        state[p + 'mlp.c_fc.weight'] = normal(d, 4 * d)
+        state[p + 'mlp.c_fc.bias'] = np.zeros(4 * d, np.float32)
+        state[p + 'mlp.c_proj.weight'] = normal(4 * d, d)
+        state[p + 'mlp.c_proj.bias'] = np.zeros(d, np.float32)
+    return state
+
+
+class _DeviceWeights:
+    """Device copies of the weights for one compute type."""
+
+    def __init__(self, state, n_layer, d, dtype):
+        self.dtype = dtype
+
+        def put(name, dt=dtype, array=None):
+            a = state[name] if array is None else array
+            return DeviceTensor.from_numpy(np.ascontiguousarray(a), dt)
+
+        self.wte = put('transformer.wte.weight', 'float32')
+        self.wpe = put('transformer.wpe.weight', 'float32')
+        self.head = put('transformer.wte.weight')          # tied head, [V, d] in the compute type
+        self.ln_f = (put('transformer.ln_f.weight', 'float32'), put('transformer.ln_f.bias', 'float32'))
+        self.layers = []
+        for i in range(n_layer):
+            p = f'transformer.h.{i}.'
+            w = state[p + 'attn.c_attn.weight']
+            b = state[p + 'attn.c_attn.bias']
+            layer = dict(
+                ln_1=(put(p + 'ln_1.weight', 'float32'), put(p + 'ln_1.bias', 'float32')),
+                ln_2=(put(p + 'ln_2.weight', 'float32'), put(p + 'ln_2.bias', 'float32')),
+                q=(put(None, array=w[:, :d]), put(None, array=b[:d])),
+                k=(put(None, array=w[:, d:2 * d]), put(None, array=b[d:2 * d])),
+                v=(put(None, array=w[:, 2 * d:]), put(None, array=b[2 * d:])),
+                o=(put(p + 'attn.c_proj.weight'), put(p + 'attn.c_proj.bias')),
+                fc=(put(p + 'mlp.c_fc.weight'), put(p + 'mlp.c_fc.bias')),
+                proj=(put(p + 'mlp.c_proj.weight'), put(p + 'mlp.c_proj.bias')))
+            self.layers.append(layer)
+
+
+class DecoderLM:
+    """GPT-2-architecture decoder with paged-KV inference entry points."""
+
+    def __init__(self, *, n_vocab=50257, n_embd=768, n_head=12, n_layer=6, n_positions=1024,
+                 ln_eps=1e-5, seed=0, state=None):
+        if n_embd % n_head or n_embd // n_head > 128:
+            raise ValueError('head_dim must divide n_embd and be <= 128')
+        self.n_vocab, self.n_embd, self.n_head, self.n_layer = n_vocab, n_embd, n_head, n_layer
+        self.n_positions, self.ln_eps = n_positions, ln_eps
+        self.head_dim = n_embd // n_head
+        self.state = state if state is not None else init_gpt2_state(
+            n_vocab=n_vocab, n_embd=n_embd, n_layer=n_layer, n_positions=n_positions, seed=seed)
+        self.training = False
+        self._version = 0
+        self._layers = tuple(_Layer(n_head, self.head_dim) for _ in range(n_layer))
+        self._device = {}
+        self._blas = None
+
+    # ---------------------------------------------------------- plumbing ---
+    def transformer_layers(self):
+        return self._layers
+
+    def weights_version(self):
+        return self._version
+
+    def eval(self):
+        self.training = False
+        return self
+
+    def load_state(self, state):
+        """Replace the weights (invalidates caches, like a parameter update)."""
+        self.state = state
+        self._device.clear()
+        self._version += 1
+
+    def _weights(self, dtype):
+        if dtype not in self._device:
+            self._device[dtype] = _DeviceWeights(self.state, self.n_layer, self.n_embd, dtype)
+        return self._device[dtype]
+
+    def blas(self):
+        if self._blas is None:
+            self._blas = _Blas()
+        return self._blas
+
+    def create_kv_cache(self, batch_size=1, capacity=None, *, cache_impl='paged', page_size=16,
+                        page_pool=None, kv_budget_bytes=256 * 1024 ** 2, pages_per_slab=4,
+                        paged_prefill_impl='flash'):
+        if cache_impl != 'paged':
+            raise ValueError('This build provides the paged cache (cache_impl="paged")')
+        from .paged_kv_cache import PagedKVCache
+        return PagedKVCache(self, batch_size, capacity, page_size=page_size, page_pool=page_pool,
+                            kv_budget_bytes=kv_budget_bytes, pages_per_slab=pages_per_slab,
+                            paged_prefill_impl=paged_prefill_impl)
+
+    # -------------------------------------------------------------- ops ---
+    def _embed(self, w, ids, positions):
+        rows = ids.size
+        d = self.n_embd
+        tok = DeviceTensor((rows, d), 'float32')
+        pos = DeviceTensor((rows, d), 'float32')
+        paged_ops.embedding_gather(tok.ptr, w.wte.ptr, ids.ptr, rows, self.n_vocab, d)
+        paged_ops.embedding_gather(pos.ptr, w.wpe.ptr, positions.ptr, rows, self.n_positions, d)
+        call(model_library(), 'mt_add_f32', [P, P, P, LL], tok.ptr, tok.ptr, pos.ptr, rows * d)
+        return tok
+
+    def _layernorm(self, x, gb, dtype):
+        rows, width = x.shape
+        out = DeviceTensor((rows, width), dtype)
+        call(model_library(), 'mt_layernorm_typed', [P, P, P, P, I, I, F, I], out.ptr, x.ptr,
+             gb[0].ptr, gb[1].ptr, rows, width, self.ln_eps, dtype_code(dtype))
+        return out
+
+    def _linear(self, x, wb, out_features, dtype):
+        rows, k = x.shape
+        out = DeviceTensor((rows, out_features), dtype)
+        self.blas().gemm(out.ptr, x.ptr, wb[0].ptr, wb[1].ptr, rows, out_features, k, 0, dtype)
+        return out
+
+    def _residual(self, x, y):
+        call(model_library(), 'mt_residual_add', [P, P, LL, I], x.ptr, y.ptr, x.size, dtype_code(y.dtype))
+
+    def _heads(self, t, b, n, split):
+        h, d = self.n_head, self.head_dim
+        out = DeviceTensor((b, h, n, d) if split else (b, n, h * d), t.dtype)
+        call(model_library(), 'mt_heads', [P, P, I, I, I, I, I, I], out.ptr, t.ptr, b, n, h, d,
+             1 if split else 0, dtype_code(t.dtype))
+        return out
+
+    def _mlp_residual(self, x, layer, dtype):
+        d = self.n_embd
+        h = self._layernorm(x, layer['ln_2'], dtype)
+        f = self._linear(h, layer['fc'], 4 * d, dtype)
+        call(model_library(), 'mt_gelu', [P, LL, I], f.ptr, f.size, dtype_code(dtype))
+        y = self._linear(f, layer['proj'], d, dtype)
+        self._residual(x, y)
+
+    def _head(self, w, x, dtype):
+        """Final LayerNorm and tied head: logits [rows, V] in the compute type."""
+        rows = x.shape[0]
+        h = self._layernorm(x, w.ln_f, dtype)
+        logits = DeviceTensor((rows, 1, self.n_vocab), dtype)
+        self.blas().gemm(logits.ptr, h.ptr, w.head.ptr, None, rows, self.n_vocab, self.n_embd, 1, dtype)
+        return logits
+
+    # ------------------------------------------------- inference entries ---
+    def prefill(self, idx, cache=None):
+        """Evaluate a prompt [B, n] of fp32 token IDs; returns (last-position
+        logits [B, 1, V], cache) (reference modules_transformer.py:355-365)."""
+        owns = cache is None
+        cache = self.create_kv_cache(idx.shape[0]) if owns else cache
+        try:
+            return self._cached_forward(idx, cache, True), cache
+        except Exception:
+            if owns:
+                cache.close()
+            raise
+
+    def decode_step(self, idx, cache):
+        """One new token per batch row of one cache (reference :367-371)."""
+        return self._cached_forward(idx, cache, False)
+
+    def _cached_forward(self, idx, cache, prefill):
+        cache.validate(self, idx, prefill)
+        b, n = idx.shape
+        offset = cache.length
+        dtype = cache.dtype
+        w = self._weights(dtype)
+        try:
+            cache.prepare_append(n)
+            positions = DeviceTensor.from_numpy(
+                np.tile(np.arange(offset, offset + n, dtype=np.float32), (b, 1)), 'float32')
+            x = self._embed(w, idx, positions)                      # [b*n, d] fp32
+            d = self.n_embd
+            for i, layer in enumerate(w.layers):
+                hdn = self._layernorm(x, layer['ln_1'], dtype)
+                q, k, v = (self._heads(self._linear(hdn, layer[name], d, dtype), b, n, True)
+                           for name in ('q', 'k', 'v'))
+                att = cache.prefill_attention(i, q, k, v) if prefill else cache.decode_attention(i, q, k, v)
+                merged = self._heads(att, b, n, False).view(b * n, d)
+                self._residual(x, self._linear(merged, layer['o'], d, dtype))
+                self._mlp_residual(x, layer, dtype)
+            last = last_position(x.view(b, n, d)).view(b, d)
+            logits = self._head(w, last, dtype)
+            cache.commit_append()
+            return logits
+        except Exception:
+            cache.abort_append()
+            raise
+
+    def decode_batch(self, idx, caches):
+        """One token per independent paged request in one model batch; rows
+        may have different context lengths (reference modules_transformer.py:373-390)."""
+        from .paged_decode import PagedDecodeBatch
+        with PagedDecodeBatch(self, idx, caches) as batch:
+            batch.prepare()
+            dtype = batch.dtype
+            w = self._weights(dtype)
+            b, d, h, hd = batch.batch_size, self.n_embd, self.n_head, self.head_dim
+            x = self._embed(w, idx, batch.position_ids)
+            for i, layer in enumerate(w.layers):
+                hdn = self._layernorm(x, layer['ln_1'], dtype)
+                q, k, v = (self._linear(hdn, layer[name], d, dtype).view(b, h, 1, hd)
+                           for name in ('q', 'k', 'v'))
+                att = batch.decode_attention(i, q, k, v).view(b, d)
+                self._residual(x, self._linear(att, layer['o'], d, dtype))
+                self._mlp_residual(x, layer, dtype)
+            logits = self._head(w, x, dtype)
+            batch.commit()
+            return logits
+
+
+def distilgpt2(seed=0):
+    """Config 3 architecture: 6 layers, d 768, 12 heads, vocab 50257, 1024 positions."""
+    return DecoderLM(n_vocab=50257, n_embd=768, n_head=12, n_layer=6, n_positions=1024, seed=seed)
+
+
+def gpt2_medium(seed=0):
+    """Config 4 architecture: 24 layers, d 1024, 16 heads, vocab 50257, 1024 positions."""
+    return DecoderLM(n_vocab=50257, n_embd=1024, n_head=16, n_layer=24, n_positions=1024, seed=seed)

@@ -1,0 +1,160 @@
+"""Transactional ragged decode over independent paged caches (reference
+minitorch/paged_decode.py:10-93).
+
+The reference builds the [B, columns] block table, the offsets and the
+position IDs on the host and uploads them (plus two cudaMallocs) every step.
+Here ``prepare()`` uploads only the batch's slot IDs (asynchronously, from
+pinned memory) and one kernel, ``mt_sched_decode_prepare``, takes each row's
+new page from the device free list and writes the table, offsets, positions
+and cu_seqlens into a workspace the pool keeps. ``decode_attention`` then runs
+the fused append + attention kernel per layer on that metadata.
+"""
+import numpy as np
+
+from .paged_kv_cache import PagedKVCache, _DeviceView
+from .runtime import RawDeviceBuffer, PinnedHostBuffer, DeviceTensor, P, I
+from . import paged_ops
+
+
+class _DecodeWorkspace:
+    """Per-pool device buffers for decode metadata, grown on demand."""
+
+    def __init__(self):
+        self.rows = self.cols = 0
+        self.buffer = None
+        self.staging = None
+
+    def ensure(self, rows, cols):
+        if rows <= self.rows and cols <= self.cols and self.buffer is not None:
+            return
+        self.rows, self.cols = max(rows, self.rows), max(cols, self.cols)
+        r, c = self.rows, self.cols
+        # slots | offsets | positions | cu_seqlens | new_page | table
+        self.sizes = [4 * r, 4 * r, 4 * r, 4 * (r + 1), 4 * r, 4 * r * c]
+        self.offsets = np.cumsum([0] + [(s + 255) // 256 * 256 for s in self.sizes]).tolist()
+        self.buffer = RawDeviceBuffer(int(self.offsets[-1]))
+        self.staging = PinnedHostBuffer(4 * r)
+
+    def ptr(self, index):
+        return self.buffer.ptr + int(self.offsets[index])
+
+
+class PagedDecodeBatch:
+    """Batched projections plus per-row paged attention on the null stream.
+
+    Owns only transient metadata; the child caches keep their pages and
+    committed lengths. A failed execution aborts every participating cache.
+    """
+
+    def __init__(self, model, idx, caches):
+        self.caches = tuple(caches)
+        if not self.caches or len({id(c) for c in self.caches}) != len(self.caches):
+            raise ValueError('Decode batch needs nonempty, unique caches')
+        if any(not isinstance(c, PagedKVCache) for c in self.caches):
+            raise ValueError('Batched decode requires paged caches')
+        self.pool = self.caches[0].pool
+        self.dtype, self.layout = self.pool.dtype, self.pool.layout
+        self.batch_size = len(self.caches)
+        if not isinstance(idx, DeviceTensor) or idx.shape != (self.batch_size, 1) or idx.dtype != 'float32':
+            raise ValueError('Expected FP32 token IDs [request_count,1] on model backend')
+        for cache in self.caches:
+            cache._validate_model(model)
+            if (cache.pool is not self.pool or self.pool.closed or cache.batch_size != 1 or
+                    cache._pending_tokens is not None or not 0 < cache.length < cache.capacity):
+                raise ValueError('Decode caches must share a live pool, have batch=1 and remaining capacity')
+        self.offsets = np.array([c.length for c in self.caches], np.int32)
+        self.columns = max((c.length + 1 + self.pool.page_size - 1) // self.pool.page_size for c in self.caches)
+        self.table = self.device_offsets = self.position_ids = self.cu_seqlens = None
+        self._prepared, self._written_layers = [], set()
+        self._committed = False
+        self._device_prepared = False
+        self.last_attention_path = 'paged_batch_decode'
+
+    def _workspace(self):
+        ws = getattr(self.pool, '_decode_workspace', None)
+        if ws is None:
+            ws = self.pool._decode_workspace = _DecodeWorkspace()
+        ws.ensure(self.batch_size, self.columns)
+        return ws
+
+    def prepare(self):
+        if self._prepared or self._committed:
+            raise ValueError('Decode batch already executed')
+        pool, b = self.pool, self.batch_size
+        ws = self._workspace()
+        slots = np.array([c.slot for c in self.caches], np.int32)
+        needs = (self.offsets % pool.page_size) == 0
+        avail = pool.max_pages - pool._leased_count
+        ws.staging.upload_async(ws.ptr(0), slots)
+        pool._call('mt_sched_decode_prepare', [P, I, I, I, I, P, P, P, P, P],
+                   ws.ptr(0), b, self.columns, pool.page_size, avail, ws.ptr(5), ws.ptr(1),
+                   ws.ptr(2), ws.ptr(3), ws.ptr(4))
+        self._device_prepared = True
+        self._ws = ws
+        self.table = _DeviceView(ws.buffer, int(ws.offsets[5]), 4 * b * self.columns)
+        self.device_offsets = _DeviceView(ws.buffer, int(ws.offsets[1]), 4 * b)
+        self.cu_seqlens = _DeviceView(ws.buffer, int(ws.offsets[3]), 4 * (b + 1))
+        self.position_ids = DeviceTensor((b, 1), 'float32', buffer=ws.buffer, byte_offset=int(ws.offsets[2]))
+        # Host half, row by row like the reference (paged_decode.py:307-309):
+        # the row whose page would exceed the budget raises MemoryError.
+        pops = 0
+        for cache, need in zip(self.caches, needs):
+            self._prepared.append(cache)
+            if need and pops >= avail:
+                CacheBase_prepare_failed(cache)
+                raise MemoryError('KV page budget exhausted')
+            cache._prepare_decode_row(bool(need))
+            if need:
+                pool._mirror_sequential_pops(1)
+                pops += 1
+
+    def decode_attention(self, layer, q, k, v):
+        if self.table is None or layer in self._written_layers or not 0 <= layer < len(self.layout):
+            raise ValueError('Invalid decode batch layer/transaction')
+        h, d = self.layout[layer]
+        if any(not isinstance(t, DeviceTensor) or t.shape != (self.batch_size, h, 1, d) or t.dtype != self.dtype
+               for t in (q, k, v)):
+            raise ValueError('Invalid batched decode Q/K/V')
+        out = DeviceTensor(q.shape, self.dtype)
+        pool = self.pool
+        paged_ops.paged_decode_batch(out.ptr, q.ptr, k.ptr, v.ptr, pool.slab_table.ptr, self.table.ptr,
+                                     self.device_offsets.ptr, b=self.batch_size, h=h, d=d,
+                                     page_size=pool.page_size, pages_per_slab=pool.pages_per_slab,
+                                     num_slabs=pool.num_slabs, columns=self.columns, layer=layer,
+                                     layers=len(self.layout), dtype=self.dtype)
+        self._written_layers.add(layer)
+        for cache in self.caches:
+            cache._written_layers.add(layer)
+            cache.last_attention_path = self.last_attention_path
+        return out
+
+    def commit(self):
+        if len(self._written_layers) != len(self.layout):
+            raise ValueError('Cannot commit incomplete decode batch')
+        if any(c._pending_tokens != 1 or len(c._written_layers) != len(c.layout) for c in self.caches):
+            raise ValueError('Decode transaction modified during execution')
+        self.pool._call('mt_sched_add_length', [P, I, I], self._ws.ptr(0), self.batch_size, 1)
+        for cache in self.caches:
+            cache.commit_append(device=False)
+        self._committed = True
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        if not self._committed:
+            if self._device_prepared:
+                self.pool._call('mt_sched_decode_abort', [P, I, P], self._ws.ptr(0), self.batch_size,
+                                self._ws.ptr(4))
+            for cache in self._prepared:
+                cache.abort_append(device=False)
+        self.position_ids = None
+
+
+def CacheBase_prepare_failed(cache):
+    """State of a cache whose prepare_append(1) failed on the budget: the
+    reference's prepare_append aborts itself (paged_kv_cache.py:187-189)."""
+    from .kv_cache import CacheBase
+    CacheBase.prepare_append(cache, 1)
+    cache._previous_counts = list(cache._counts)
+    cache._new_count = 0

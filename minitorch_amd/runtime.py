@@ -43,7 +43,9 @@ class HipRuntime:
             'mt_fill': [P, I, F], 'mt_fill_words': [P, Z, ct.c_uint],
             'mt_event_create': [ct.POINTER(P)], 'mt_event_record': [P],
             'mt_event_elapsed': [ct.POINTER(F), P, P], 'mt_event_destroy': [P],
+            'mt_event_synchronize': [P],
             'mt_device_count': [ct.POINTER(I)],
+            'mt_host_alloc': [ct.POINTER(P), Z], 'mt_host_free': [P],
         }
         for name, args in signatures.items():
             f = getattr(self.lib, name)
@@ -153,6 +155,113 @@ class RawDeviceBuffer:
         self._release()
 
 
+class CachingAllocator:
+    """Reuses freed device blocks by size class instead of hipFree.
+
+    hipFree synchronizes the device, so per-step tensors must not be freed to
+    the driver. Blocks are rounded up to 256 bytes below 1 MiB and to powers of
+    two above it (the reference's MemoryPool, minitorch/memory_pool.py:24-83,
+    uses powers of two). On the single null stream, a block released by the
+    host may be reused at once: later kernels run after every kernel that used
+    the block before.
+    """
+
+    def __init__(self, rt):
+        self.runtime = rt
+        self.free = {}
+        self.cached_bytes = 0
+
+    @staticmethod
+    def size_class(nbytes):
+        if nbytes <= 1 << 20:
+            return max(256, (nbytes + 255) // 256 * 256)
+        return 1 << (nbytes - 1).bit_length()
+
+    def acquire(self, nbytes):
+        size = self.size_class(nbytes)
+        blocks = self.free.get(size)
+        if blocks:
+            self.cached_bytes -= size
+            return blocks.pop(), size
+        try:
+            return self.runtime.malloc(size).value, size
+        except RuntimeError:
+            self.empty()  # out of memory: return cached blocks and retry once
+            return self.runtime.malloc(size).value, size
+
+    def release(self, pointer, size):
+        self.free.setdefault(size, []).append(pointer)
+        self.cached_bytes += size
+
+    def empty(self):
+        for size, blocks in self.free.items():
+            for pointer in blocks:
+                self.runtime._free(P(pointer), size)
+        self.free.clear()
+        self.cached_bytes = 0
+
+
+class PooledBuffer:
+    """Device bytes from the caching allocator, returned to it when dropped."""
+
+    def __init__(self, nbytes):
+        alloc = allocator()
+        self.pointer, self.nbytes = alloc.acquire(nbytes)
+        self._release = weakref.finalize(self, alloc.release, self.pointer, self.nbytes)
+
+    @property
+    def ptr(self):
+        return self.pointer
+
+    def download(self, dtype, count=None, byte_offset=0):
+        dtype = np.dtype(dtype)
+        count = (self.nbytes - byte_offset) // dtype.itemsize if count is None else count
+        return runtime().d2h(np.empty(count, dtype), self.pointer + byte_offset)
+
+    def fill_words(self, value=0):
+        rt = runtime()
+        rt.check(rt.lib.mt_fill_words(self.pointer, self.nbytes // 4, value))
+
+
+_allocator = None
+
+
+def allocator():
+    global _allocator
+    if _allocator is None:
+        _allocator = CachingAllocator(runtime())
+    return _allocator
+
+
+class PinnedHostBuffer:
+    """Pinned host staging memory for asynchronous host-to-device uploads."""
+
+    def __init__(self, nbytes):
+        self.runtime = runtime()
+        self.nbytes = int(nbytes)
+        self.pointer = P()
+        self.runtime.check(self.runtime.lib.mt_host_alloc(ct.byref(self.pointer), self.nbytes))
+        self._release = weakref.finalize(self, self.runtime.lib.mt_host_free, self.pointer)
+        self.array = np.ctypeslib.as_array((ct.c_uint8 * self.nbytes).from_address(self.pointer.value))
+        self._copied = None  # event recorded after the last enqueued upload
+
+    def upload_async(self, dst, array):
+        """Copy ``array`` into this staging buffer and enqueue its upload to ``dst``
+        on the null stream. Before overwriting the staging memory it waits for
+        the previous upload from it to have run (normally long finished)."""
+        a = np.ascontiguousarray(array)
+        if a.nbytes > self.nbytes:
+            raise ValueError('staging buffer too small')
+        if self._copied is not None:
+            self._copied.synchronize()
+        self.array[:a.nbytes] = a.view(np.uint8).reshape(-1)
+        self.runtime.check(self.runtime.lib.mt_copy_async(dst, self.pointer.value, a.nbytes, 1))
+        self.runtime.stats['h2d_bytes'] += a.nbytes
+        if self._copied is None:
+            self._copied = CudaEvent()
+        self._copied.record()
+
+
 class DeviceTensor:
     """Contiguous typed device array (shape, dtype, pointer).
 
@@ -167,7 +276,7 @@ class DeviceTensor:
         self.size = int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1
         self.nbytes = self.size * itemsize(self.dtype)
         if buffer is None:
-            buffer = RawDeviceBuffer(max(self.nbytes, 1))
+            buffer = PooledBuffer(max(self.nbytes, 1))
             byte_offset = 0
         if byte_offset + self.nbytes > buffer.nbytes:
             raise ValueError('DeviceTensor view exceeds its buffer')
@@ -249,6 +358,9 @@ class CudaEvent:
 
     def record(self):
         self.runtime.check(self.runtime.lib.mt_event_record(self.handle))
+
+    def synchronize(self):
+        self.runtime.check(self.runtime.lib.mt_event_synchronize(self.handle))
 
     def seconds_since(self, start):
         ms = F()

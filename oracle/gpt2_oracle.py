@@ -1,0 +1,67 @@
+"""numpy GPT-2 forward restating the reference's decoder math. TEST INFRASTRUCTURE ONLY.
+
+Follows minitorch/modules_transformer.py:258-284 (pre-LayerNorm residual
+block), :81-107 (Q/K/V projections split into heads), the paged/flash
+attention semantics softmax(q.k / sqrt(D)) with a causal mask, the fused
+LayerNorm's one-pass variance E[x^2] - mean^2 clamped at 0 plus eps
+(src/layernorm_kernel.cu:37-99), tanh GELU (minitorch/nn.py:222-226) and the
+tied head (minitorch/pretrained_gpt2.py:35-49). Weights use the GPT-2
+checkpoint layout (Conv1D [in, out]). Computed in float64 by default.
+
+Pinned against transformers' GPT2LMHeadModel built locally from a GPT2Config
+(no download) with the same weights, in tests/test_gpt2_oracle.py.
+"""
+import math
+import numpy as np
+
+
+def layernorm(x, gamma, beta, eps=1e-5):
+    mean = x.mean(-1, keepdims=True)
+    var = np.maximum((x * x).mean(-1, keepdims=True) - mean * mean, 0) + eps
+    return gamma * ((x - mean) / np.sqrt(var)) + beta
+
+
+def gelu(x):
+    return 0.5 * x * (1 + np.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3)))
+
+
+def forward(state, ids, *, n_head, n_layer, eps=1e-5, dtype=np.float64):
+    """Logits [n, V] for token ids [n] at positions 0..n-1."""
+    g = {k: np.asarray(v, dtype) for k, v in state.items()}
+    ids = np.asarray(ids, np.int64)
+    n = ids.size
+    x = g['transformer.wte.weight'][ids] + g['transformer.wpe.weight'][np.arange(n)]
+    d = x.shape[-1]
+    hd = d // n_head
+    mask = np.triu(np.full((n, n), -np.inf), 1)
+    for i in range(n_layer):
+        p = f'transformer.h.{i}.'
+        h = layernorm(x, g[p + 'ln_1.weight'], g[p + 'ln_1.bias'], eps)
+        qkv = h @ g[p + 'attn.c_attn.weight'] + g[p + 'attn.c_attn.bias']
+        q, k, v = (qkv[:, j * d:(j + 1) * d].reshape(n, n_head, hd).transpose(1, 0, 2) for j in range(3))
+        s = q @ k.transpose(0, 2, 1) / math.sqrt(hd) + mask
+        s = s - s.max(-1, keepdims=True)
+        a = np.exp(s)
+        a = a / a.sum(-1, keepdims=True)
+        o = (a @ v).transpose(1, 0, 2).reshape(n, d)
+        x = x + o @ g[p + 'attn.c_proj.weight'] + g[p + 'attn.c_proj.bias']
+        h = layernorm(x, g[p + 'ln_2.weight'], g[p + 'ln_2.bias'], eps)
+        f = gelu(h @ g[p + 'mlp.c_fc.weight'] + g[p + 'mlp.c_fc.bias'])
+        x = x + f @ g[p + 'mlp.c_proj.weight'] + g[p + 'mlp.c_proj.bias']
+    x = layernorm(x, g['transformer.ln_f.weight'], g['transformer.ln_f.bias'], eps)
+    return x @ g['transformer.wte.weight'].T
+
+
+def greedy(state, prompt, steps, *, n_head, n_layer, eps=1e-5):
+    """Greedy tokens after ``prompt`` (first token from the prompt's last
+    position), and the top-1/top-2 logit margin at each step."""
+    ids = list(int(t) for t in prompt)
+    out, margins = [], []
+    for _ in range(steps):
+        logits = forward(state, ids, n_head=n_head, n_layer=n_layer, eps=eps)[-1]
+        top = np.argsort(logits)[-2:]
+        margins.append(float(logits[top[1]] - logits[top[0]]))
+        token = int(np.argmax(logits))
+        out.append(token)
+        ids.append(token)
+    return out, margins

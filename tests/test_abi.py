@@ -90,17 +90,19 @@ def test_split_entry_validation_and_workspace_size():
     ws = lib.mt_paged_decode_workspace_bytes
     ws.argtypes, ws.restype = [I] * 5 + [ct.POINTER(ct.c_size_t)], I
     out = ct.c_size_t()
-    assert ws(64, 12, 16, 64, 0, ct.byref(out)) == 0
-    # 4 splits of 256 tokens: (max, denominator, 128 accumulators) per split
-    assert out.value == 768 * 4 * 130 * 4
-    assert ws(64, 12, 16, 16, 0, ct.byref(out)) == 0 and out.value == 0   # cap 256: one split
+    assert ws(64, 12, 16, 128, 0, ct.byref(out)) == 0
+    # 2048-token table, automatic 1024-token splits: (max, denominator, 128
+    # accumulators) per (row, head, split)
+    assert out.value == 768 * 2 * 130 * 4
+    assert ws(64, 12, 16, 64, 256, ct.byref(out)) == 0 and out.value == 768 * 4 * 130 * 4
+    assert ws(64, 12, 16, 64, 0, ct.byref(out)) == 0 and out.value == 0   # cap 1024: one split
     assert ws(64, 12, 16, 64, 100, ct.byref(out)) == 1                     # not a multiple of 64
     assert ws(64, 12, 16, 64, 4096, ct.byref(out)) == 1                    # beyond 2048
     assert ws(64, 12, 12, 64, 0, ct.byref(out)) == 1                       # page size
     split = lib.mt_paged_decode_split
     split.argtypes, split.restype = [P] * 7 + [I] * 12 + [P, Z], I
     # a splitting launch without a workspace is rejected
-    assert split(8, 8, 8, 8, 8, 8, 8, 4, 12, 64, 16, 4, 16, 64, 0, 1, 0, 0, 0, None, 0) == 1
+    assert split(8, 8, 8, 8, 8, 8, 8, 4, 12, 64, 16, 4, 16, 128, 0, 1, 0, 0, 0, None, 0) == 1
 
 
 def test_inference_entries_reject_invalid_shapes():

@@ -1,0 +1,68 @@
+"""Embedding gather, greedy argmax and last-position copy on the GPU vs the
+oracle (exact)."""
+import numpy as np
+import pytest
+
+from minitorch_amd import paged_ops
+from minitorch_amd.kv_cache import greedy_token, last_position
+from minitorch_amd.runtime import DeviceTensor, runtime
+from oracle import paged_oracle as po
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize('dim', [768, 1024, 30])
+def test_embedding_gather_valid_and_invalid_ids(dim):
+    rng = np.random.default_rng(dim)
+    vocab = 501
+    w = rng.standard_normal((vocab, dim)).astype(np.float32)
+    ids = rng.integers(0, vocab, 40).astype(np.float32)
+    ids[:7] = [np.nan, np.inf, -1, vocab, 3.5, -0.0, vocab - 1]
+    wd, idd = DeviceTensor.from_numpy(w), DeviceTensor.from_numpy(ids)
+    out = DeviceTensor((ids.size, dim))
+    paged_ops.embedding_gather(out.ptr, wd.ptr, idd.ptr, ids.size, vocab, dim)
+    got = out.to_numpy()
+    ref = po.embedding_gather(w, ids)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.nan_to_num(got), np.nan_to_num(ref))
+
+
+@pytest.mark.parametrize('dtype', ['float32', 'float16', 'bfloat16'])
+@pytest.mark.parametrize('width', [1, 7, 50257, 4096])
+def test_row_argmax_first_max_and_nan(dtype, width):
+    rng = np.random.default_rng(width)
+    rows = 9
+    x = rng.standard_normal((rows, 1, width)).astype(np.float32)
+    if width > 8:
+        x[1, 0, [5, width - 3]] = 100.0          # tie: first index wins
+        x[2, 0, [width // 2, 3]] = np.nan        # NaN wins, first NaN
+        x[3, 0, :] = -np.inf                     # all -inf: index 0
+        x[4, 0, :] = 2.0                         # all equal: index 0
+        x[5, 0, -1] = np.inf
+    stored = po.encode(x, {'float32': 0, 'float16': 1, 'bfloat16': 2}[dtype])
+    t = DeviceTensor(x.shape, dtype)
+    runtime().h2d(t.ptr, stored)
+    got = greedy_token(t).to_numpy()[:, 0]
+    ref = po.row_argmax(po.decode(stored, {'float32': 0, 'float16': 1, 'bfloat16': 2}[dtype]))[:, 0]
+    assert got.tolist() == ref.tolist()
+
+
+def test_row_argmax_unaligned_rows():
+    # width 50257 (odd) makes each fp16 row start at a different alignment
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((16, 1, 50257)).astype(np.float16)
+    for r in range(16):
+        x[r, 0, (r * 3137) % 50257] = 50.0
+    t = DeviceTensor(x.shape, 'float16')
+    runtime().h2d(t.ptr, x)
+    assert greedy_token(t).to_numpy()[:, 0].tolist() == np.argmax(x[:, 0].astype(np.float32), -1).tolist()
+
+
+@pytest.mark.parametrize('dtype', ['float32', 'bfloat16'])
+def test_last_position(dtype):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((3, 5, 70)).astype(np.float32)
+    t = DeviceTensor.from_numpy(x, dtype)
+    got = last_position(t).raw_numpy()
+    ref = po.last_row(t.raw_numpy())
+    assert np.array_equal(got, ref)

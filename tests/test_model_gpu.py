@@ -1,0 +1,164 @@
+"""End-to-end decode on the GPU: fp32 greedy tokens vs the numpy GPT-2 oracle,
+batched ragged decode vs independent per-request decode, and the
+continuous-batching gates of the reference's benchmark
+(project/benchmark_continuous_batching.py:50-66,115,189-191): every completed
+request's tokens equal independent generation, and the pool is drained."""
+import numpy as np
+import pytest
+
+from minitorch_amd.amp import autocast
+from minitorch_amd.model import DecoderLM
+from minitorch_amd.kv_cache import greedy_token
+from minitorch_amd.continuous_batching import ContinuousBatcher
+from minitorch_amd.runtime import DeviceTensor
+from oracle import gpt2_oracle as go
+from oracle.pool_oracle import PoolOracle, BatcherOracle
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny(seed=0, layers=2, d=128, heads=2, vocab=512, positions=160):
+    return DecoderLM(n_vocab=vocab, n_embd=d, n_head=heads, n_layer=layers, n_positions=positions, seed=seed)
+
+
+def generate(model, prompt, steps, page_size=16):
+    """Independent generation: prefill then decode_step, one request."""
+    cache = model.create_kv_cache(1, len(prompt) + steps - 1, page_size=page_size)
+    logits, _ = model.prefill(DeviceTensor.from_numpy(np.array([prompt], np.float32)), cache)
+    out = [int(greedy_token(logits).to_numpy()[0, 0])]
+    for _ in range(steps - 1):
+        logits = model.decode_step(DeviceTensor.from_numpy(np.array([[out[-1]]], np.float32)), cache)
+        out.append(int(greedy_token(logits).to_numpy()[0, 0]))
+    cache.close()
+    return out
+
+
+def test_prefill_logits_match_oracle_fp32():
+    model = tiny()
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(0, model.n_vocab, 37)
+    cache = model.create_kv_cache(1, 64)
+    logits, _ = model.prefill(DeviceTensor.from_numpy(prompt[None].astype(np.float32)), cache)
+    ref = go.forward(model.state, prompt, n_head=model.n_head, n_layer=model.n_layer)[-1]
+    got = logits.to_numpy()[0, 0]
+    assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max()
+    cache.close()
+
+
+@pytest.mark.parametrize('page_size', [8, 16, 32])
+def test_greedy_tokens_match_oracle_fp32(page_size):
+    model = tiny(seed=page_size)
+    rng = np.random.default_rng(page_size)
+    prompt = rng.integers(0, model.n_vocab, 21).tolist()
+    got = generate(model, prompt, 12, page_size)
+    ref, margins = go.greedy(model.state, prompt, 12, n_head=model.n_head, n_layer=model.n_layer)
+    assert got == ref, f'margins {margins}'
+
+
+def test_decode_batch_equals_independent_decode_fp32():
+    model = tiny(seed=7)
+    rng = np.random.default_rng(7)
+    prompts = [rng.integers(0, model.n_vocab, n).tolist() for n in (5, 16, 17, 40, 63)]
+    expect = [generate(model, p, 6) for p in prompts]
+    from minitorch_amd.paged_kv_cache import KVPagePool
+    pool = KVPagePool(model, page_size=16, max_bytes=64 * 1024 ** 2)
+    caches, tokens = [], []
+    for p in prompts:
+        c = model.create_kv_cache(1, len(p) + 5, page_size=16, page_pool=pool)
+        logits, _ = model.prefill(DeviceTensor.from_numpy(np.array([p], np.float32)), c)
+        caches.append(c)
+        tokens.append([int(greedy_token(logits).to_numpy()[0, 0])])
+    for _ in range(5):
+        ids = DeviceTensor.from_numpy(np.array([[t[-1]] for t in tokens], np.float32))
+        nxt = greedy_token(model.decode_batch(ids, caches)).to_numpy()[:, 0]
+        for t, n in zip(tokens, nxt):
+            t.append(int(n))
+    assert tokens == expect
+    for c in caches:
+        c.close()
+    assert pool.memory_stats()['kv_pool_used_pages'] == 0
+
+
+def run_trace(model, trace, precision='fp32', max_batch_size=4, budget_pages=None, page_size=16):
+    """Replay (arrival_step, id, prompt, new_tokens) on a step-indexed clock."""
+    page_bytes = 2 * model.n_layer * model.n_embd * page_size * (4 if precision == 'fp32' else 2)
+    budget = (budget_pages or 4096) * page_bytes
+    batcher = ContinuousBatcher(model, max_batch_size=max_batch_size, page_size=page_size,
+                                kv_budget_bytes=budget, precision=precision)
+    steps, pending = [], sorted(trace)
+    while pending or batcher.has_work:
+        while pending and pending[0][0] <= batcher.iteration:
+            _, rid, prompt, new = pending.pop(0)
+            batcher.submit(rid, np.array(prompt), max_new_tokens=new)
+        batcher.step()
+        steps.append(dict(batcher.last_step))
+    return batcher, steps
+
+
+def make_trace(model, rng, n=10):
+    return [(int(rng.integers(0, 8)), f'r{i}', rng.integers(0, model.n_vocab, int(rng.integers(3, 60))).tolist(),
+             int(rng.integers(1, 12))) for i in range(n)]
+
+
+def test_continuous_batching_gates_fp32():
+    model = tiny(seed=11)
+    rng = np.random.default_rng(11)
+    trace = make_trace(model, rng)
+    batcher, steps = run_trace(model, trace, budget_pages=40)
+    for _, rid, prompt, new in trace:
+        r = batcher.requests[rid]
+        assert r.state == 'completed'
+        assert r.output_ids == generate(model, prompt, new), rid
+        ref, margins = go.greedy(model.state, prompt, new, n_head=model.n_head, n_layer=model.n_layer)
+        assert r.output_ids == ref, (rid, margins)
+    assert steps[-1]['kv_pool_used_pages'] == 0 and batcher.reserved_pages == 0
+    batcher.close()
+
+
+def test_continuous_batching_schedule_and_pages_match_oracle():
+    """Scheduling decisions, KV statistics and every decode step's block table
+    equal the integer restatement, with the tokens the GPU produced."""
+    model = tiny(seed=12)
+    rng = np.random.default_rng(12)
+    trace = make_trace(model, rng, 12)
+    batcher, steps = run_trace(model, trace, max_batch_size=3, budget_pages=30)
+    tokens = {rid: batcher.requests[rid].output_ids for _, rid, _, _ in trace}
+    page_bytes = batcher.pool.page_bytes
+    oracle_pool = PoolOracle(page_bytes=page_bytes, page_size=16, max_bytes=30 * page_bytes, pages_per_slab=4)
+    ob = BatcherOracle(oracle_pool, lambda rid, i: tokens[rid][i], max_batch_size=3,
+                       n_positions=model.n_positions)
+    pending = sorted(trace)
+    ours = iter(steps)
+    while pending or ob.has_work:
+        while pending and pending[0][0] <= ob.iteration:
+            _, rid, prompt, new = pending.pop(0)
+            ob.submit(rid, prompt, new)
+        ob.step()
+        s, o = next(ours), ob.steps[-1]
+        for key in ('decode_request_ids', 'prefill_request_ids', 'logical_reserved_pages', 'peak_used_pages',
+                    'kv_pool_used_pages', 'kv_pool_free_pages', 'kv_pool_reserved_bytes',
+                    'kv_pool_page_acquires', 'kv_pool_page_releases', 'kv_pool_page_reuses'):
+            assert s[key] == o[key], (ob.iteration, key, s[key], o[key])
+    assert next(ours, None) is None
+    assert batcher.pool.free_stack() == oracle_pool.free
+    batcher.close()
+
+
+@pytest.mark.parametrize('precision', ['fp16', 'bf16'])
+def test_low_precision_trace_completes(precision):
+    model = tiny(seed=13)
+    rng = np.random.default_rng(13)
+    trace = make_trace(model, rng, 8)
+    batcher, steps = run_trace(model, trace, precision=precision, budget_pages=64)
+    assert all(batcher.requests[rid].state == 'completed' for _, rid, _, _ in trace)
+    assert steps[-1]['kv_pool_used_pages'] == 0
+    batcher.close()
+
+
+def test_distilgpt2_shape_fp32_tokens_match_oracle():
+    model = DecoderLM(n_vocab=50257, n_embd=768, n_head=12, n_layer=6, n_positions=1024, seed=3)
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, 50257, 48).tolist()
+    got = generate(model, prompt, 4)
+    ref, margins = go.greedy(model.state, prompt, 4, n_head=12, n_layer=6)
+    assert got == ref, margins
