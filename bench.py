@@ -82,6 +82,97 @@ def cpu_baseline(case, seconds):
                        f'on fp16 pages, OpenMP over (request, head)')
 
 
+def time_launches(fn, calls, steps, warmup):
+    """Mean seconds per launch from HIP events around ``steps`` launches."""
+    rt = runtime()
+    for i in range(warmup):
+        rt.check(fn(*calls[i % len(calls)]))
+    rt.synchronize()
+    start, end = CudaEvent(), CudaEvent()
+    start.record()
+    for i in range(steps):
+        rt.check(fn(*calls[i % len(calls)]))
+    end.record()
+    rt.synchronize()
+    return end.seconds_since(start) / steps
+
+
+def bench_config5(args):
+    """Config 5: B=512, H=25, D=64, bf16, contexts lognormal(ln 256, 1.2)
+    clipped to [1, 8192], page 16 and 32; contexts over 1024 tokens take the
+    split-context reduction. The ~1.7 GB of K/V exceeds the Infinity Cache,
+    so back-to-back launches read cold data."""
+    from minitorch_amd.workloads import DeviceRaggedCase, config5_lengths
+    from minitorch_amd.runtime import RawDeviceBuffer
+    from minitorch_amd.dtypes import dtype_code
+    lengths = config5_lengths(args.seed, 512)
+    lines = {}
+    fn = paged_ops.paged_library().mt_paged_decode_split
+    fn.argtypes, fn.restype = [P] * 7 + [I] * 12 + [P, Z], I
+    for page_size in (16, 32):
+        case = DeviceRaggedCase(args.seed, batch=512, heads=25, dim=64, page_size=page_size,
+                                lengths=lengths, dtype='bfloat16')
+        kw = case.kwargs()
+        ws_bytes = paged_ops.decode_workspace_bytes(b=512, h=25, page_size=page_size,
+                                                    columns=case.columns, split_tokens=args.split)
+        ws = RawDeviceBuffer(max(ws_bytes, 4))
+        call = (case.out.ptr, case.q.ptr, case.k.ptr, case.v.ptr, case.slab_table.ptr,
+                case.block_table.ptr, case.offsets.ptr, kw['b'], kw['h'], kw['d'], kw['page_size'],
+                kw['pages_per_slab'], kw['num_slabs'], kw['columns'], kw['layer'], kw['layers'],
+                dtype_code(kw['dtype']), args.split, args.unroll, ws.ptr, ws_bytes)
+        per = time_launches(fn, [call], min(args.steps, 50), min(args.warmup, 5))
+        s = 2
+        L = case.lengths
+        nbytes = (512 * 25 * 64 * 2 * (s + s) + int((2 * L * 25 * 64 * s).sum()) + 512 * 25 * 64 * (s + s)
+                  + int((4 * ((L + page_size - 1) // page_size)).sum()) + 4 * 512)
+        lines[page_size] = dict(ms_per_step=per * 1e3, tokens_per_sec=512 / per,
+                                achieved_gbs=nbytes / per / 1e9, frac=nbytes / per / 1e9 / PEAK_HBM_GBS,
+                                algorithmic_bytes=nbytes, columns=case.columns,
+                                rows_over_1024=int((L > 1024).sum()), max_context=int(L.max()))
+        del case, ws
+    main16 = lines[16]
+    return {
+        'metric': METRIC, 'value': main16['tokens_per_sec'], 'unit': 'tokens/s', 'n_gpus': 1,
+        'steps': min(args.steps, 50), 'warmup': min(args.warmup, 5), 'ms_per_step': main16['ms_per_step'],
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16',
+        'data': 'synthetic (hash-filled K/V)',
+        'config': {'workload': 'config 5: ragged op-level paged decode, B=512, H=25, D=64, bf16, '
+                               'L~lognormal(ln 256, 1.2) clipped [1, 8192], split reduction for L>1024',
+                   'sum_context_tokens': int(lengths.sum()), 'split_tokens': args.split or 'auto'},
+        'roofline': {'bound': 'hbm', 'achieved': main16['achieved_gbs'], 'peak': PEAK_HBM_GBS,
+                     'unit': 'GB/s', 'frac': main16['frac'], 'traffic': None,
+                     'algorithmic_bytes_per_launch': main16['algorithmic_bytes']},
+        'page_size_16': lines[16], 'page_size_32': lines[32],
+    }
+
+
+def bench_e2e(args):
+    from minitorch_amd import model as model_mod, e2e
+    if args.config == 3:
+        model = model_mod.distilgpt2(seed=args.seed)
+        trace = e2e.config3_trace(args.seed)
+        warm = e2e.config3_trace(args.seed + 1, requests=8, rate=1000.0)
+        e2e.run_config3(model, warm, precision='fp16')
+        r = e2e.run_config3(model, trace, precision='fp16')
+        value, workload = r['busy_decode_tokens_per_sec'], (
+            'config 3: continuous batching, random-init DistilGPT-2 (6 layers, d 768, 12 heads, vocab '
+            '50257), fp16, 256 Poisson requests at 32 req/s, prompts U[32,512], outputs geometric mean '
+            '128, greedy, EOS off, 16384 pages of 16 tokens, FIFO, max_batch_size 256')
+        dtype = 'f16'
+    else:
+        model = model_mod.gpt2_medium(seed=args.seed)
+        r = e2e.run_config4(model, seed=args.seed, steps=min(args.steps, 40), warmup=min(args.warmup, 5))
+        value, workload = r['decode_tokens_per_sec'], (
+            'config 4: steady state of 128 requests, random-init GPT-2-medium (24 layers, d 1024, 16 '
+            'heads), bf16, contexts lognormal(median 256, sigma 1.2) clipped [16,1024], page 16, 5% '
+            'replaced per step')
+        dtype = 'bf16'
+    return {'metric': 'decode tokens/s (1 GPU), end to end', 'value': value, 'unit': 'tokens/s',
+            'n_gpus': 1, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+            'dtype': dtype, 'data': 'synthetic (random-init weights, random token ids)',
+            'config': {'workload': workload}, 'measurements': r}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument('--gpus', type=int, default=1)
@@ -95,6 +186,9 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--calibrate-copy', type=int, default=0, metavar='MB',
                     help='only run device-to-device copies of MB MiB (counter calibration) and exit')
+    ap.add_argument('--config', type=int, default=2, choices=(2, 3, 4, 5),
+                    help='2: op-level decode (default, the headline line); 5: ragged op-level '
+                         'decode, bf16, H=25, P=16 and 32; 3 / 4: end-to-end decode')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: this build has no multi-GPU path '
@@ -111,6 +205,12 @@ def main():
             rt.d2d(dst.ptr, src.ptr, nbytes)
         rt.synchronize()
         print(json.dumps({'calibrate_copy_bytes': nbytes, 'copies': args.steps}), flush=True)
+        return
+    if args.config == 5:
+        print(json.dumps(bench_config5(args)), flush=True)
+        return
+    if args.config in (3, 4):
+        print(json.dumps(bench_e2e(args)), flush=True)
         return
     case = config2_case(args.seed)
     devs = [DevicePagedCase(case) for _ in range(args.pools)]

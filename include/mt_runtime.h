@@ -41,6 +41,10 @@ int mt_fill(float* p, int n, float v);
 /* Fill `words` 32-bit words with `value` by a kernel (graph-capturable,
  * unlike a memset node). No reference counterpart. */
 int mt_fill_words(void* p, size_t words, unsigned int value);
+/* n elements of dtype set to a deterministic hash of (seed, index), uniform
+ * in [-2, 2): synthetic data for large pools. No reference counterpart
+ * (stands in for reference mt_random, src/cuda_runtime.cu:37-44,58-61). */
+int mt_fill_random(void* p, long long n, unsigned long long seed, int dtype);
 
 #ifdef __cplusplus
 }

@@ -20,6 +20,29 @@ __global__ __launch_bounds__(256) void fill_bytes_kernel(uint32_t* out, int64_t 
     out[i] = value;
 }
 
+// Counter-based hash (SplitMix64 finalizer) of (seed, i) mapped to [-2, 2).
+__device__ __forceinline__ float hash_uniform(unsigned long long seed, unsigned long long i) {
+  unsigned long long z = seed * 0x9E3779B97F4A7C15ull + i + 0x632BE59BD9B4E019ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return float(z >> 40) * (4.0f / 16777216.0f) - 2.0f;
+}
+
+__global__ __launch_bounds__(256) void fill_random_kernel(void* out, int64_t n, unsigned long long seed, int dtype) {
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    const float v = hash_uniform(seed, (unsigned long long)i);
+    if (dtype == 0) {
+      static_cast<float*>(out)[i] = v;
+    } else if (dtype == 1) {
+      static_cast<_Float16*>(out)[i] = static_cast<_Float16>(v);
+    } else {
+      const unsigned u = __float_as_uint(v);
+      static_cast<unsigned short*>(out)[i] = static_cast<unsigned short>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    }
+  }
+}
+
 int blocks_for(int64_t n) {
   const int64_t b = (n + 255) / 256;
   return int(b < (1 << 20) ? b : (1 << 20));
@@ -67,6 +90,14 @@ int mt_fill(float* p, int n, float v) {
 int mt_fill_words(void* p, size_t words, unsigned int value) {
   if (!p && words) return hipErrorInvalidValue;
   if (words) fill_bytes_kernel<<<blocks_for(int64_t(words)), 256>>>(static_cast<uint32_t*>(p), int64_t(words), value);
+  return hipGetLastError();
+}
+
+// n elements of dtype (0 fp32, 1 fp16, 2 bf16) set to a deterministic
+// hash of (seed, index), uniform in [-2, 2): synthetic K/V for large pools.
+int mt_fill_random(void* p, long long n, unsigned long long seed, int dtype) {
+  if ((!p && n) || n < 0 || dtype < 0 || dtype > 2) return hipErrorInvalidValue;
+  if (n) fill_random_kernel<<<blocks_for(n), 256>>>(p, n, seed, dtype);
   return hipGetLastError();
 }
 

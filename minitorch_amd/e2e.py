@@ -1,0 +1,157 @@
+"""End-to-end decode harnesses for the benchmark configurations 3 and 4.
+
+Config 3 replays the reference's continuous-batching benchmark shape
+(project/benchmark_continuous_batching.py:84-97,122) on a random-init
+DistilGPT-2: requests arrive by wall clock (Poisson), the batcher steps while
+there is work, and throughput is reported both with the reference's formula
+(generated tokens / (end - start), arrival gaps included) and as busy-step
+decode throughput (sum of decode batch sizes / sum of decode seconds).
+
+Config 4 holds a steady state of concurrent requests on a random-init
+GPT-2-medium: every step decodes all of them, then each request is replaced
+with a seeded 5 % probability (or when it reaches its capacity) by a fresh
+prefilled one, exercising page free/reuse. Decode tokens/s counts decode
+steps only.
+"""
+import time
+import numpy as np
+
+from .continuous_batching import ContinuousBatcher
+from .kv_cache import greedy_token
+from .paged_kv_cache import KVPagePool
+from .runtime import DeviceTensor, runtime
+from .amp import autocast
+
+
+def config3_trace(seed=0, requests=256, rate=32.0, vocab=50257, n_positions=1024):
+    """(arrival_seconds, request_id, prompt_ids, max_new_tokens) for config 3:
+    Poisson arrivals, prompts U{32..512}, outputs geometric with mean 128,
+    capped so prompt + output <= n_positions."""
+    rng = np.random.default_rng([seed, 3])
+    arrivals = np.cumsum(rng.exponential(1.0 / rate, requests))
+    arrivals -= arrivals[0]
+    out = []
+    for i in range(requests):
+        n = int(rng.integers(32, 513))
+        prompt = rng.integers(0, vocab, n)
+        new = int(min(rng.geometric(1.0 / 128), n_positions - n + 1))
+        out.append((float(arrivals[i]), f'r{i}', prompt, new))
+    return out
+
+
+def _progress(message):
+    import sys
+    print(message, file=sys.stderr, flush=True)
+
+
+def run_config3(model, trace, *, precision='fp16', max_batch_size=256, page_size=16, kv_pages=16384,
+                max_prefills_per_step=1, prefill_token_budget=512, clock=time.perf_counter,
+                report_every=200):
+    itemsize = 4 if precision == 'fp32' else 2
+    page_bytes = 2 * model.n_layer * model.n_embd * page_size * itemsize
+    batcher = ContinuousBatcher(model, max_batch_size=max_batch_size, page_size=page_size,
+                                kv_budget_bytes=kv_pages * page_bytes, precision=precision,
+                                max_prefills_per_step=max_prefills_per_step,
+                                prefill_token_budget=prefill_token_budget, clock=clock)
+    pending = list(trace)
+    steps = []
+    start = clock()
+    while pending or batcher.has_work:
+        now = clock() - start
+        while pending and pending[0][0] <= now:
+            _, rid, prompt, new = pending.pop(0)
+            batcher.submit(rid, prompt, max_new_tokens=new)
+        if batcher.has_work:
+            batcher.step()
+            steps.append(batcher.last_step)
+            if report_every and len(steps) % report_every == 0:
+                _progress(f'config 3: step {len(steps)}, {clock() - start:.1f} s, '
+                          f'decode batch {steps[-1]["decode_batch_size"]}, queued {steps[-1]["queued_requests"]}')
+        elif pending:
+            time.sleep(max(0.0, pending[0][0] - (clock() - start)))
+    elapsed = clock() - start
+    generated = sum(len(r.output_ids) for r in batcher.requests.values())
+    decode_tokens = sum(s['decode_batch_size'] for s in steps)
+    decode_seconds = sum(s['decode_seconds'] for s in steps if s['decode_batch_size'])
+    ttft = [r.ttft_seconds for r in batcher.requests.values() if r.ttft_seconds is not None]
+    result = dict(
+        generated_tokens=generated, elapsed_seconds=elapsed,
+        output_tokens_per_sec=generated / elapsed,
+        busy_decode_tokens_per_sec=decode_tokens / decode_seconds if decode_seconds else None,
+        decode_tokens=decode_tokens, decode_seconds=decode_seconds, steps=len(steps),
+        max_decode_batch_size=max(s['decode_batch_size'] for s in steps),
+        mean_decode_batch_size=float(np.mean([s['decode_batch_size'] for s in steps if s['decode_batch_size']])),
+        ttft_p50_ms=float(np.median(ttft) * 1e3), ttft_p95_ms=float(np.percentile(ttft, 95) * 1e3),
+        completed=sum(r.state == 'completed' for r in batcher.requests.values()),
+        kv_pool_used_pages_after=steps[-1]['kv_pool_used_pages'],
+        peak_used_pages=batcher.peak_used_pages,
+        page_reuses=steps[-1]['kv_pool_page_reuses'])
+    batcher.close()
+    return result
+
+
+def config4_lengths(rng, n):
+    return np.clip(np.round(np.exp(rng.normal(np.log(256.0), 1.2, n))), 16, 1024).astype(int)
+
+
+def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_rate=0.05,
+                precision='bf16', page_size=16, kv_pages=None):
+    """Steady-state decode throughput; returns a dict of measurements."""
+    dtype = {'fp16': 'float16', 'bf16': 'bfloat16', 'fp32': 'float32'}[precision]
+    rng = np.random.default_rng([seed, 4])
+    rt = runtime()
+    itemsize = 4 if precision == 'fp32' else 2
+    page_bytes = 2 * model.n_layer * model.n_embd * page_size * itemsize
+    kv_pages = kv_pages or concurrent * ((model.n_positions + page_size - 1) // page_size)
+    with autocast(dtype) if precision != 'fp32' else _null():
+        pool = KVPagePool(model, page_size=page_size, max_bytes=kv_pages * page_bytes, pages_per_slab=16)
+        caches, last = [], []
+
+        def admit():
+            # context length L counts the token being decoded: prompt of L - 1
+            length = int(config4_lengths(rng, 1)[0]) - 1
+            prompt = rng.integers(0, model.n_vocab, length)
+            cache = model.create_kv_cache(1, model.n_positions, page_size=page_size, page_pool=pool)
+            logits, _ = model.prefill(DeviceTensor.from_numpy(prompt[None].astype(np.float32)), cache)
+            return cache, int(greedy_token(logits).to_numpy()[0, 0])
+
+        for _ in range(concurrent):
+            c, t = admit()
+            caches.append(c)
+            last.append(t)
+        decode_seconds, tokens, replaced, context = 0.0, 0, 0, []
+        for step in range(warmup + steps):
+            ids = DeviceTensor.from_numpy(np.array(last, np.float32)[:, None])
+            context.append(sum(c.length + 1 for c in caches))
+            rt.synchronize()
+            t0 = time.perf_counter()
+            logits = model.decode_batch(ids, caches)
+            nxt = greedy_token(logits).to_numpy()[:, 0]
+            t1 = time.perf_counter()
+            if step >= warmup:
+                decode_seconds += t1 - t0
+                tokens += len(caches)
+            last = [int(t) for t in nxt]
+            if step % 10 == 0:
+                _progress(f'config 4: step {step}, decode {(t1 - t0) * 1e3:.2f} ms')
+            for i in range(len(caches)):
+                if rng.random() < replace_rate or caches[i].length + 1 >= caches[i].capacity:
+                    caches[i].close()
+                    caches[i], last[i] = admit()
+                    replaced += 1
+        stats = pool.memory_stats()
+        for c in caches:
+            c.close()
+        pool.close()
+    return dict(decode_tokens_per_sec=tokens / decode_seconds, decode_seconds=decode_seconds,
+                steps=steps, concurrent=concurrent, mean_context_tokens=float(np.mean(context) / concurrent),
+                replaced_requests=replaced, page_reuses=stats['kv_pool_page_reuses'],
+                ms_per_step=decode_seconds / steps * 1e3)
+
+
+class _null:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        return False

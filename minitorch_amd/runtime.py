@@ -46,6 +46,7 @@ class HipRuntime:
             'mt_event_synchronize': [P],
             'mt_device_count': [ct.POINTER(I)],
             'mt_host_alloc': [ct.POINTER(P), Z], 'mt_host_free': [P],
+            'mt_fill_random': [P, ct.c_longlong, ct.c_ulonglong, I],
         }
         for name, args in signatures.items():
             f = getattr(self.lib, name)

@@ -147,3 +147,55 @@ class DevicePagedCase:
         return dict(b=c.batch, h=c.heads, d=c.dim, page_size=c.page_size,
                     pages_per_slab=c.pages_per_slab, num_slabs=c.num_slabs, columns=c.columns,
                     layer=c.layer, layers=c.layers, dtype=c.dtype)
+
+
+class DeviceRaggedCase:
+    """A large op-level case built on the device (config 5 sizes): pool pages
+    filled with a deterministic hash of (seed, index) in [-2, 2) instead of
+    N(0, 1) host data, block table from a seeded shuffle of the pool, Q/K/V
+    filled the same way. Used for timing; parity uses host-built cases."""
+
+    def __init__(self, seed, *, batch, heads, dim, page_size, lengths, dtype, pages_per_slab=64,
+                 slack_pages=64):
+        from .dtypes import dtype_code
+        rt = runtime()
+        self.dtype = normalize_dtype(dtype)
+        self.batch, self.heads, self.dim, self.page_size = batch, heads, dim, page_size
+        self.lengths = np.asarray(lengths, np.int64)
+        pages_needed = (self.lengths + page_size - 1) // page_size
+        pool_pages = int(pages_needed.sum()) + slack_pages
+        pool_pages = (pool_pages + pages_per_slab - 1) // pages_per_slab * pages_per_slab
+        self.pages_per_slab, self.num_slabs = pages_per_slab, pool_pages // pages_per_slab
+        self.layers, self.layer = 1, 0
+        self.page_bytes = 2 * heads * dim * page_size * itemsize(self.dtype)
+        self.slab_bytes = self.page_bytes * pages_per_slab
+        self.columns = int(pages_needed.max())
+        rng = np.random.default_rng([seed, 5, page_size])
+        perm = rng.permutation(pool_pages).astype(np.int32)
+        table = np.full((batch, self.columns), -1, np.int32)
+        cursor = 0
+        for b in range(batch):
+            n = int(pages_needed[b])
+            table[b, :n] = perm[cursor:cursor + n]
+            cursor += n
+        self.table_host = table
+        self.pool = RawDeviceBuffer(self.num_slabs * self.slab_bytes)
+        code = dtype_code(self.dtype)
+        rt.check(rt.lib.mt_fill_random(self.pool.ptr, self.num_slabs * self.slab_bytes // itemsize(self.dtype),
+                                       seed, code))
+        self.slab_table = RawDeviceBuffer(8 * self.num_slabs)
+        self.slab_table.upload(np.array([self.pool.ptr + s * self.slab_bytes for s in range(self.num_slabs)],
+                                        np.uint64))
+        self.block_table = RawDeviceBuffer(table.nbytes)
+        self.block_table.upload(table)
+        self.offsets = RawDeviceBuffer(4 * batch)
+        self.offsets.upload((self.lengths - 1).astype(np.int32))
+        shape = (batch, heads, 1, dim)
+        self.q, self.k, self.v, self.out = (DeviceTensor(shape, self.dtype) for _ in range(4))
+        for i, t in enumerate((self.q, self.k, self.v)):
+            rt.check(rt.lib.mt_fill_random(t.ptr, t.size, seed + 1 + i, code))
+
+    def kwargs(self):
+        return dict(b=self.batch, h=self.heads, d=self.dim, page_size=self.page_size,
+                    pages_per_slab=self.pages_per_slab, num_slabs=self.num_slabs, columns=self.columns,
+                    layer=self.layer, layers=self.layers, dtype=self.dtype)
