@@ -108,7 +108,7 @@ def bench_config5(args):
     lengths = config5_lengths(args.seed, 512)
     lines = {}
     fn = paged_ops.paged_library().mt_paged_decode_split
-    fn.argtypes, fn.restype = [P] * 7 + [I] * 12 + [P, Z], I
+    fn.argtypes, fn.restype = paged_ops.SPLIT_ARGTYPES, I
     for page_size in (16, 32):
         case = DeviceRaggedCase(args.seed, batch=512, heads=25, dim=64, page_size=page_size,
                                 lengths=lengths, dtype='bfloat16')
@@ -116,10 +116,13 @@ def bench_config5(args):
         ws_bytes = paged_ops.decode_workspace_bytes(b=512, h=25, page_size=page_size,
                                                     columns=case.columns, split_tokens=args.split)
         ws = RawDeviceBuffer(max(ws_bytes, 4))
+        order = RawDeviceBuffer(4 * 512)
+        order.upload(np.argsort(-case.lengths, kind='stable').astype(np.int32))
         call = (case.out.ptr, case.q.ptr, case.k.ptr, case.v.ptr, case.slab_table.ptr,
                 case.block_table.ptr, case.offsets.ptr, kw['b'], kw['h'], kw['d'], kw['page_size'],
                 kw['pages_per_slab'], kw['num_slabs'], kw['columns'], kw['layer'], kw['layers'],
-                dtype_code(kw['dtype']), args.split, args.unroll, ws.ptr, ws_bytes)
+                dtype_code(kw['dtype']), args.split, args.unroll, args.waves,
+                None if args.natural_order else order.ptr, ws.ptr, ws_bytes)
         per = time_launches(fn, [call], min(args.steps, 50), min(args.warmup, 5))
         s = 2
         L = case.lengths
@@ -129,7 +132,7 @@ def bench_config5(args):
                                 achieved_gbs=nbytes / per / 1e9, frac=nbytes / per / 1e9 / PEAK_HBM_GBS,
                                 algorithmic_bytes=nbytes, columns=case.columns,
                                 rows_over_1024=int((L > 1024).sum()), max_context=int(L.max()))
-        del case, ws
+        del case, ws, order
     main16 = lines[16]
     return {
         'metric': METRIC, 'value': main16['tokens_per_sec'], 'unit': 'tokens/s', 'n_gpus': 1,
@@ -182,6 +185,8 @@ def main():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--split', type=int, default=0, help='split length in tokens (0 = automatic)')
     ap.add_argument('--unroll', type=int, default=0)
+    ap.add_argument('--waves', type=int, default=0, help='waves per decode workgroup (4 or 8; 0 = default)')
+    ap.add_argument('--natural-order', action='store_true', help='schedule rows in batch order')
     ap.add_argument('--cpu-seconds', type=float, default=10.0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--calibrate-copy', type=int, default=0, metavar='MB',
@@ -221,12 +226,16 @@ def main():
     ws = RawDeviceBuffer(max(ws_bytes, 4))
     ws.fill_words(0)
     fn = paged_ops.paged_library().mt_paged_decode_split
-    fn.argtypes, fn.restype = [P] * 7 + [I] * 12 + [P, Z], I
+    fn.argtypes, fn.restype = paged_ops.SPLIT_ARGTYPES, I
     from minitorch_amd.dtypes import dtype_code
+    # Rows scheduled longest first; the scheduler knows the lengths on the host.
+    order = RawDeviceBuffer(4 * case.batch)
+    order.upload(np.argsort(-case.lengths, kind='stable').astype(np.int32))
+    order_ptr = None if args.natural_order else order.ptr
     calls = [(d.out.ptr, d.q.ptr, d.k.ptr, d.v.ptr, d.slab_table.ptr, d.block_table.ptr, d.offsets.ptr,
               kw['b'], kw['h'], kw['d'], kw['page_size'], kw['pages_per_slab'], kw['num_slabs'],
               kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype']), args.split,
-              args.unroll, ws.ptr, ws_bytes) for d in devs]
+              args.unroll, args.waves, order_ptr, ws.ptr, ws_bytes) for d in devs]
 
     def step(i):
         status = fn(*calls[i % len(calls)])

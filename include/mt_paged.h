@@ -54,17 +54,21 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
 int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, int split_tokens,
                                     size_t* bytes);
 
-/* mt_paged_decode_batch with a caller-owned workspace and an explicit split
- * length (a multiple of 64, at most 2048; 0 = automatic) and stream unroll
- * (1, 2 or 4; 0 = default). The workspace holds per-split partials; launches
- * that share one workspace must not overlap.
+/* mt_paged_decode_batch with a caller-owned workspace and tuning knobs:
+ * split_tokens (a multiple of 64, at most 2048; 0 = automatic), unroll (1, 2
+ * or 4 row-blocks per register stage; 0 = default), waves per workgroup (4 or
+ * 8; 0 = default), and row_order (device int32 [b], a permutation of 0..b-1,
+ * or NULL): the order in which rows are scheduled, e.g. longest first so that
+ * long rows do not finish last; outputs are unaffected. The workspace holds
+ * per-split partials; launches that share one workspace must not overlap.
  * No reference counterpart (split-context variant of
  * src/paged_attention_kernel.cu:121-137). */
 int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v,
                           const uint64_t* slabs, const int* table, const int* offsets, int b,
                           int h, int d, int page_size, int pages_per_slab, int num_slabs,
                           int columns, int layer, int layers, int dtype, int split_tokens,
-                          int unroll, void* workspace, size_t workspace_bytes);
+                          int unroll, int waves, const int* row_order, void* workspace,
+                          size_t workspace_bytes);
 
 #ifdef __cplusplus
 }

@@ -55,6 +55,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 #define MT_STAGES 2
 #endif
 constexpr int kStages = MT_STAGES;  // register stages of the K/V stream
+constexpr int kDefaultUnroll = 2;    // row-blocks per register stage
+constexpr int kDefaultWaves = 4;     // waves per decode workgroup
+#ifndef MT_DECODE_GROUP
+#define MT_DECODE_GROUP 4
+#endif
+constexpr int kDecodeGroup = MT_DECODE_GROUP;  // lanes per token in the decode kernel
 
 struct Geometry {
   int heads, dim, page_size, log2_page, pps, num_slabs, columns, layer;
@@ -81,11 +87,25 @@ __device__ __forceinline__ const T* page_base(const uint64_t* slabs, const int* 
   return reinterpret_cast<const T*>(address) + i;
 }
 
+// Page base from an already loaded physical page ID (the table read is
+// issued separately so that it overlaps other loads).
+template <class T>
+__device__ __forceinline__ const T* resolve_page(const uint64_t* slabs, int physical,
+                                                 const Geometry& g, int head) {
+  if (physical < 0 || int64_t(physical) >= int64_t(g.num_slabs) * g.pps) return nullptr;
+  const uint64_t address = slabs[physical / g.pps];
+  if (!address) return nullptr;
+  const int slot = physical % g.pps;
+  const int64_t i = ((int64_t(g.layer) * 2 * g.pps + slot) * g.heads + head) *
+                    int64_t(g.page_size) * g.dim;
+  return reinterpret_cast<const T*>(address) + i;
+}
+
 // Online-softmax state of one token group, in base-2 units (scores are
 // pre-multiplied by log2(e)). A missing page contributes a NaN score, which
 // fmaxf drops from the running max and which then poisons the denominator,
 // matching the reference's NaN propagation (src/paged_attention_kernel.cu:53,66-69,84).
-template <int N>
+template <int N, int G = kGroup>
 struct Softmax {
   float m, l, acc[N];
   __device__ __forceinline__ void init() {
@@ -102,6 +122,30 @@ struct Softmax {
     for (int i = 0; i < N; ++i) acc[i] = fmaf(p, v[i], acc[i] * alpha);
     m = mn;
   }
+  // Add U tokens with one rescale: the running max moves once per call.
+  template <int U, class VF>
+  __device__ __forceinline__ void add_many(const float* s, const bool* valid, VF&& v_of) {
+    float mx = m;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (valid[u]) mx = fmaxf(mx, s[u]);
+    const float alpha = (m == -INFINITY) ? 0.f : fast_exp2(m - mx);
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < N; ++i) acc[i] *= alpha;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (valid[u]) {
+        const float p = fast_exp2(s[u] - mx);
+        l += p;
+        float v[N];
+        v_of(u, v);
+#pragma unroll
+        for (int i = 0; i < N; ++i) acc[i] = fmaf(p, v[i], acc[i]);
+      }
+    }
+    m = mx;
+  }
   __device__ __forceinline__ void merge(float mo, float lo, const float* ao) {
     const float mn = fmaxf(m, mo);
     const float sa = (m == -INFINITY) ? 0.f : fast_exp2(m - mn);
@@ -111,11 +155,11 @@ struct Softmax {
     for (int i = 0; i < N; ++i) acc[i] = acc[i] * sa + ao[i] * sb;
     m = mn;
   }
-  // Merge the states of the 16 token groups of a wave (lanes with equal
-  // lane % 4): afterwards lanes 0..3 hold the wave's state for their chunk.
+  // Merge the states of the token groups of a wave (lanes with equal
+  // lane % G): afterwards lanes 0..G-1 hold the wave's state for their chunk.
   __device__ __forceinline__ void wave_merge() {
 #pragma unroll
-    for (int off = kGroup; off < kWave; off <<= 1) {
+    for (int off = G; off < kWave; off <<= 1) {
       float ao[N];
       const float mo = __shfl_xor(m, off);
       const float lo = __shfl_xor(l, off);
@@ -130,10 +174,14 @@ __device__ __forceinline__ float finalize(float acc, float l) {
   return l > 0.f ? acc / l : (isnan(l) ? NAN : 0.f);
 }
 
-// Sum of a value over the 4 lanes of a token group (DPP quad permutes).
+// Sum of a value over the G lanes of a token group with DPP: quad permutes
+// for 4 lanes, then the half-row mirror (lane i <-> 7 - i) for 8 lanes.
+template <int G = kGroup>
 __device__ __forceinline__ float group_sum(float x) {
   x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));
   x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));
+  if constexpr (G == 8)
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, true));
   return x;
 }
 
@@ -189,10 +237,10 @@ struct Chunk {
 // K conversion is needed and the query takes DL/2 registers; the 1/sqrt(D)
 // and log2(e) factors are applied to the summed score. fp32 and the masked
 // path keep a pre-scaled fp32 query.
-template <int DT, int D, bool VEC>
+template <int DT, int D, bool VEC, int G = kGroup>
 struct Query {
   using T = typename Elem<DT>::T;
-  static constexpr int DL = D / kGroup;
+  static constexpr int DL = D / G;
   static constexpr bool PACKED = VEC && DT != kF32;
   uint32_t qp[PACKED ? DL / 2 : 1];
   float qf[PACKED ? 1 : DL];
@@ -234,7 +282,7 @@ struct Query {
     return s;
   }
   __device__ __forceinline__ float score(const Chunk<DT, DL, VEC>& k) const {
-    return group_sum(partial(k)) * post_scale;
+    return group_sum<G>(partial(k)) * post_scale;
   }
 };
 
@@ -273,15 +321,10 @@ __device__ __forceinline__ void stream_rows(Softmax<D / kGroup>& st, const Query
     }
   };
   auto consume = [&](const C* kc, const C* vc, const bool* valid) {
+    float s[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float s = q.score(kc[u]);
-      if (valid[u]) {
-        float vf[DL];
-        vc[u].to_float(vf);
-        st.add(s, vf);
-      }
-    }
+    for (int u = 0; u < U; ++u) s[u] = q.score(kc[u]);
+    st.template add_many<U>(s, valid, [&](int u, float* vf) { vc[u].to_float(vf); });
   };
   if constexpr (STAGES == 1) {
     for (int rb0 = rb_first; rb0 < nrb; rb0 += rb_step * U) {
@@ -323,26 +366,107 @@ struct DecodeArgs {
   int64_t items;
   Geometry g;
   float* partials;
+  const int* order;  // row visiting order, or nullptr for 0..B-1
 };
 
-// Fused KV append + decode attention over (request, head, split) items.
-template <int DT, int D, bool VEC, int U, int STAGES>
-__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
+// Stream one wave's share of a split: row-blocks j = wave + waves * i
+// (16 tokens each) of tokens [t0, t0 + ntok). Lane s of the wave holds in
+// `base` the page base (K plane) of page slot s, resolved in the prologue:
+// slot i for page sizes >= 16 (one page per row-block), slots 2i and 2i + 1
+// for page size 8. Page bases are broadcast with readlane (scalar registers)
+// or, for page size 8, a lane shuffle; no LDS and no barrier are involved.
+template <int DT, int D, bool VEC, int U, int STAGES, int G>
+__device__ __forceinline__ void stream_wave(Softmax<D / G, G>& st, const Query<DT, D, VEC, G>& q,
+                                            uint64_t base, int ntok, int wave, int waves,
+                                            const Geometry& g, int dim) {
   using T = typename Elem<DT>::T;
-  constexpr int DL = D / kGroup;
+  constexpr int DL = D / G;
+  constexpr int RB = kWave / G;  // tokens per wave step
+  using C = Chunk<DT, DL, VEC>;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int tok = lane / G;
+  const int col0 = (lane % G) * DL;
+  const int pmask = g.page_size - 1;
+  const bool two_pages = g.page_size < RB;
+  const int nrb = (ntok + RB - 1) / RB;
+  const int mine = nrb > wave ? (nrb - wave + waves - 1) / waves : 0;
+  const uint32_t base_lo = uint32_t(base), base_hi = uint32_t(base >> 32);
+  auto issue = [&](int i0, C* kc, C* vc, bool* valid) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u;
+      const int rel = (wave + waves * i) * RB + tok;
+      valid[u] = i < mine && rel < ntok;
+      uint64_t pb;
+      if (two_pages) {
+        const int slot = 2 * i + (tok >> 3);
+        pb = (uint64_t(uint32_t(__shfl(int(base_hi), slot))) << 32) | uint32_t(__shfl(int(base_lo), slot));
+      } else {
+        const int slot = i < kWave ? i : kWave - 1;
+        pb = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(base_hi), slot))) << 32) |
+             uint32_t(__builtin_amdgcn_readlane(int(base_lo), slot));
+      }
+      const T* page = reinterpret_cast<const T*>(pb);
+      if (valid[u] && page) {
+        const T* kp = page + (rel & pmask) * dim + col0;
+        kc[u].load(kp, col0, dim);
+        vc[u].load(kp + g.kind_stride, col0, dim);
+      } else {
+        kc[u].nan_fill();
+        vc[u].nan_fill();
+      }
+    }
+  };
+  auto consume = [&](const C* kc, const C* vc, const bool* valid) {
+    float s[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) s[u] = q.score(kc[u]);
+    st.template add_many<U>(s, valid, [&](int u, float* vf) { vc[u].to_float(vf); });
+  };
+  if constexpr (STAGES == 1) {
+    for (int i0 = 0; i0 < mine; i0 += U) {
+      C kc[U], vc[U];
+      bool valid[U];
+      issue(i0, kc, vc, valid);
+      consume(kc, vc, valid);
+    }
+  } else {
+    C kc[U], vc[U];
+    bool valid[U];
+    if (mine > 0) issue(0, kc, vc, valid);
+    for (int i0 = 0; i0 < mine; i0 += U) {
+      C nk[U], nv[U];
+      bool nvalid[U];
+      if (i0 + U < mine) issue(i0 + U, nk, nv, nvalid);
+      consume(kc, vc, valid);
+#pragma unroll
+      for (int u = 0; u < U; ++u) { kc[u] = nk[u]; vc[u] = nv[u]; valid[u] = nvalid[u]; }
+    }
+  }
+}
+
+// Fused KV append + decode attention over (request, head, split) items.
+// Rows are visited in a.order (when given) so that long rows start first.
+template <int DT, int D, bool VEC, int U, int STAGES, int WAVES, int G>
+__global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
+  using T = typename Elem<DT>::T;
+  constexpr int DL = D / G;
+  constexpr int RB = kWave / G;
   constexpr int PSTRIDE = D + 2;
-  __shared__ const T* s_page[kMaxSplitPages];
-  __shared__ float s_m[kWaves], s_l[kWaves];
-  __shared__ float s_acc[kWaves][D];
+  constexpr int NT = WAVES * kWave;
+  __shared__ float s_m[WAVES], s_l[WAVES];
+  __shared__ float s_acc[WAVES][D];
 
   const Geometry& g = a.g;
   const int dim = VEC ? D : g.dim;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & (kWave - 1);
-  const int col0 = (lane & 3) * DL;
+  const int col0 = (lane % G) * DL;
   const int64_t bh_count = int64_t(a.batch) * g.heads;
   const int64_t cap = int64_t(g.columns) * g.page_size;
+  const int sub_shift = g.page_size < RB ? 1 : 0;
+  const int rb_per_wave = a.split_tokens / RB / WAVES;
   const T* qp = static_cast<const T*>(a.q);
   const T* kin = static_cast<const T*>(a.k);
   const T* vin = static_cast<const T*>(a.v);
@@ -350,55 +474,72 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 
   for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
     const int split = int(item / bh_count);
-    const int64_t bh = item - int64_t(split) * bh_count;
-    const int b = int(bh / g.heads);
-    const int head = int(bh - int64_t(b) * g.heads);
+    const int64_t bhi = item - int64_t(split) * bh_count;
+    const int r = int(bhi / g.heads);
+    const int head = int(bhi - int64_t(r) * g.heads);
+    const int b = a.order ? a.order[r] : r;
+    const int64_t bh = int64_t(b) * g.heads + head;
+
+    // Loads that do not depend on the context length are issued first: the
+    // offset, the query, the new token's K/V (wave 0) and the table entry of
+    // each of this wave's page slots.
     const int offset = a.offsets[b];
+    Query<DT, D, VEC, G> qv;
+    qv.load(qp + bh * dim, col0, dim, a.qscale);
+    Chunk<DT, DL, VEC> kn, vn;
+    if (wave == 0) {
+      kn.load(kin + bh * dim + col0, col0, dim);
+      vn.load(vin + bh * dim + col0, col0, dim);
+    }
+    const int* table_row = a.table + int64_t(b) * g.columns;
+    const int t0i = split * a.split_tokens;
+    const int slot_i = lane >> sub_shift;
+    const int slot_tok = (wave + WAVES * slot_i) * RB + ((lane & sub_shift) << 3);
+    const int64_t slot_logical = (int64_t(t0i) + slot_tok) >> g.log2_page;
+    int physical = -1;
+    if (slot_i < rb_per_wave && slot_logical < g.columns) physical = table_row[slot_logical];
+
     const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
     T* orow = out + bh * dim;
     if (L > cap) {
       // A token beyond the table's columns reads as a missing page: NaN row.
       if (split == 0)
-        for (int t = tid; t < dim; t += kThreads) orow[t] = from_f32<DT>(NAN);
+        for (int t = tid; t < dim; t += NT) orow[t] = from_f32<DT>(NAN);
       continue;
     }
     const int nsplit = L == 0 ? 1 : int((L + a.split_tokens - 1) / a.split_tokens);
     if (split >= nsplit) continue;
-    const int64_t t0 = int64_t(split) * a.split_tokens;
+    const int64_t t0 = t0i;
     const int64_t t1 = L < t0 + a.split_tokens ? L : t0 + a.split_tokens;
     const bool owns_new = L > 0 && split == nsplit - 1;
     const int ntok_paged = int((owns_new ? t1 - 1 : t1) - t0);  // tokens read from pages
+    const T* my_page = (slot_i < rb_per_wave && t0 + slot_tok < t1)
+                           ? resolve_page<T>(a.slabs, physical, g, head) : nullptr;
+    // The new token's page (wave 0, scalar loads; needed only after the stream).
+    const T* new_page = nullptr;
+    if (owns_new && wave == 0) {
+      const int64_t logical = (L - 1) >> g.log2_page;
+      new_page = logical < g.columns ? resolve_page<T>(a.slabs, table_row[logical], g, head) : nullptr;
+    }
 
-    const int* table_row = a.table + int64_t(b) * g.columns;
-    const int npg = int((t1 - t0 + g.page_size - 1) >> g.log2_page);
-    for (int j = tid; j < npg; j += kThreads)
-      s_page[j] = page_base<T>(a.slabs, table_row, (t0 >> g.log2_page) + j, g, head);
-
-    Query<DT, D, VEC> qv;
-    qv.load(qp + bh * dim, col0, dim, a.qscale);
-    Softmax<DL> st;
+    Softmax<DL, G> st;
     st.init();
-    __syncthreads();
-
-    stream_rows<DT, D, VEC, U, STAGES>(st, qv, s_page, ntok_paged, wave, kWaves, g, dim);
+    stream_wave<DT, D, VEC, U, STAGES, G>(st, qv, reinterpret_cast<uint64_t>(my_page), ntok_paged,
+                                           wave, WAVES, g, dim);
 
     if (owns_new && wave == 0) {
       // The new token: read from the K/V inputs, scored by group 0 of wave 0,
       // and written into its page when the page exists (reference append,
       // src/paged_attention_kernel.cu:23-33). A missing page reads as NaN.
       const int64_t pos = L - 1;
-      const T* base = s_page[int((pos - t0) >> g.log2_page)];
-      Chunk<DT, DL, VEC> kc, vc;
-      kc.load(kin + bh * dim + col0, col0, dim);
-      vc.load(vin + bh * dim + col0, col0, dim);
-      if (lane < kGroup && base) {
-        T* kp = const_cast<T*>(base) + (pos & (g.page_size - 1)) * dim + col0;
+      if (lane < G && new_page) {
+        T* kp = const_cast<T*>(new_page) + (pos & (g.page_size - 1)) * dim + col0;
         T* vp = kp + g.kind_stride;
         if constexpr (VEC) {
 #pragma unroll
           for (int i = 0; i < Chunk<DT, DL, VEC>::NV; ++i) {
-            global_view(reinterpret_cast<u32x4*>(kp))[i] = kc.raw[i];
-            global_view(reinterpret_cast<u32x4*>(vp))[i] = vc.raw[i];
+            global_view(reinterpret_cast<u32x4*>(kp))[i] = kn.raw[i];
+            global_view(reinterpret_cast<u32x4*>(vp))[i] = vn.raw[i];
           }
         } else {
           for (int i = 0; i < DL && col0 + i < dim; ++i) {
@@ -407,17 +548,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
           }
         }
       }
-      if (!base) { kc.nan_fill(); vc.nan_fill(); }
-      const float sc = qv.score(kc);
-      if (lane < kGroup) {
+      if (!new_page) { kn.nan_fill(); vn.nan_fill(); }
+      const float sc = qv.score(kn);
+      if (lane < G) {
         float vf[DL];
-        vc.to_float(vf);
+        vn.to_float(vf);
         st.add(sc, vf);
       }
     }
 
     st.wave_merge();
-    if (lane < kGroup) {
+    if (lane < G) {
 #pragma unroll
       for (int i = 0; i < DL; ++i) s_acc[wave][col0 + i] = st.acc[i];
       if (lane == 0) { s_m[wave] = st.m; s_l[wave] = st.l; }
@@ -426,11 +567,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w]);
+    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, s_m[w]);
     float lsum = 0.f, asum = 0.f;
     const int t = tid;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < WAVES; ++w) {
       const float sc = (s_m[w] == -INFINITY) ? 0.f : fast_exp2(s_m[w] - M);
       lsum += s_l[w] * sc;
       if (t < dim) asum += s_acc[w][t] * sc;
@@ -636,38 +777,48 @@ size_t workspace_bytes_for(int64_t bh, int nsplit_max) {
   return size_t(bh) * nsplit_max * (128 + 2) * sizeof(float);
 }
 
-template <int DT, int D, bool VEC>
-hipError_t launch_decode_t(const DecodeArgs& a, int64_t blocks, int unroll) {
+template <int DT, int D, bool VEC, int WAVES, int G>
+hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
   // Row bytes per lane bound the useful unroll: register stages beyond it spill.
   constexpr int kMaxUnroll = !VEC ? 1 : (D * elem_bytes<DT>() >= 256 ? 2 : 4);
+  constexpr int NT = WAVES * kWave;
   if (unroll > kMaxUnroll) unroll = kMaxUnroll;
   if constexpr (kMaxUnroll >= 4) {
-    if (unroll >= 4) decode_kernel<DT, D, VEC, 4, kStages><<<grid_for(blocks), kThreads>>>(a);
+    if (unroll >= 4) decode_kernel<DT, D, VEC, 4, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
   }
   if constexpr (kMaxUnroll >= 2) {
-    if (unroll == 2) decode_kernel<DT, D, VEC, 2, kStages><<<grid_for(blocks), kThreads>>>(a);
+    if (unroll == 2) decode_kernel<DT, D, VEC, 2, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
   }
-  if (unroll <= 1) decode_kernel<DT, D, VEC, 1, kStages><<<grid_for(blocks), kThreads>>>(a);
+  if (unroll <= 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.nsplit_max == 1) return e;
   merge_kernel<DT, (D > 64 ? 128 : 64)><<<grid_for(int64_t(a.batch) * a.g.heads), 128>>>(a);
   return hipGetLastError();
 }
 
+template <int DT, int D, bool VEC>
+hipError_t launch_decode_t(const DecodeArgs& a, int64_t blocks, int unroll, int waves) {
+  if (waves == 8) return launch_decode_w<DT, D, VEC, 8, kDecodeGroup>(a, blocks, unroll);
+  return launch_decode_w<DT, D, VEC, 4, kDecodeGroup>(a, blocks, unroll);
+}
+
 template <int DT>
-hipError_t launch_decode_dt(const DecodeArgs& a, int64_t blocks, bool vec, int d, int unroll) {
-  if (vec && d == 64) return launch_decode_t<DT, 64, true>(a, blocks, unroll);
-  if (vec && d == 128) return launch_decode_t<DT, 128, true>(a, blocks, unroll);
-  return launch_decode_t<DT, 128, false>(a, blocks, 1);
+hipError_t launch_decode_dt(const DecodeArgs& a, int64_t blocks, bool vec, int d, int unroll, int waves) {
+  if (vec && d == 64) return launch_decode_t<DT, 64, true>(a, blocks, unroll, waves);
+  if (vec && d == 128) return launch_decode_t<DT, 128, true>(a, blocks, unroll, waves);
+  return launch_decode_t<DT, 128, false>(a, blocks, 1, waves);
 }
 
 int decode_common(void* out, const void* q, const void* k, const void* v, const uint64_t* slabs,
                   const int* table, const int* offsets, int b, int h, int d, int page_size,
                   int pps, int num_slabs, int columns, int layer, int layers, int dtype,
-                  int split_tokens, int unroll, void* workspace, size_t workspace_bytes) {
+                  int split_tokens, int unroll, int waves, const int* row_order, void* workspace,
+                  size_t workspace_bytes) {
   const int64_t cap = int64_t(columns) * page_size;
   const int S = choose_split(cap, split_tokens);
   if (S < 64 || S % 64 != 0 || S > kMaxSplitTokens) return hipErrorInvalidValue;
+  if (waves != 4 && waves != 8) return hipErrorInvalidValue;
+  if (S % ((kWave / kDecodeGroup) * waves) != 0) waves = 4;
   const int64_t nsplit_max = (cap + S - 1) / S;
   const int64_t bh = int64_t(b) * h;
   if (nsplit_max > INT_MAX) return hipErrorInvalidValue;
@@ -680,10 +831,11 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   a.items = bh * nsplit_max;
   a.g = make_geometry(h, d, page_size, pps, num_slabs, columns, layer);
   a.partials = static_cast<float*>(workspace);
+  a.order = row_order;
   const bool vec = (d == 64 || d == 128) && aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v);
-  if (dtype == kF32) return launch_decode_dt<kF32>(a, a.items, vec, d, unroll);
-  if (dtype == kF16) return launch_decode_dt<kF16>(a, a.items, vec, d, unroll);
-  if (dtype == kBF16) return launch_decode_dt<kBF16>(a, a.items, vec, d, unroll);
+  if (dtype == kF32) return launch_decode_dt<kF32>(a, a.items, vec, d, unroll, waves);
+  if (dtype == kF16) return launch_decode_dt<kF16>(a, a.items, vec, d, unroll, waves);
+  if (dtype == kBF16) return launch_decode_dt<kBF16>(a, a.items, vec, d, unroll, waves);
   return hipErrorInvalidValue;
 }
 
@@ -791,7 +943,8 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
     if (e != hipSuccess) return e;
   }
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
-                       num_slabs, columns, layer, layers, dtype, S, 2, ws, ws_bytes);
+                       num_slabs, columns, layer, layers, dtype, S, kDefaultUnroll, kDefaultWaves,
+                       nullptr, ws, ws_bytes);
 }
 
 int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, int split_tokens,
@@ -811,15 +964,18 @@ int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v
                           const uint64_t* slabs, const int* table, const int* offsets, int b,
                           int h, int d, int page_size, int pages_per_slab, int num_slabs,
                           int columns, int layer, int layers, int dtype, int split_tokens,
-                          int unroll, void* workspace, size_t workspace_bytes) {
+                          int unroll, int waves, const int* row_order, void* workspace,
+                          size_t workspace_bytes) {
   if (!out || !q || !k || !v || !slabs || !table || !offsets ||
       !paged_shape(b, h, 1, 1, d, page_size, pages_per_slab, num_slabs, columns, layer, layers, 0) ||
-      int64_t(columns) * page_size > INT32_MAX || split_tokens < 0 || unroll < 0)
+      int64_t(columns) * page_size > INT32_MAX || split_tokens < 0 || unroll < 0 ||
+      (waves != 0 && waves != 4 && waves != 8))
     return hipErrorInvalidValue;
   if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, split_tokens,
-                       unroll == 0 ? 2 : unroll, workspace, workspace_bytes);
+                       unroll == 0 ? kDefaultUnroll : unroll, waves == 0 ? kDefaultWaves : waves,
+                       row_order, workspace, workspace_bytes);
 }
 
 }  // extern "C"

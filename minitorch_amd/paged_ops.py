@@ -51,15 +51,21 @@ def decode_workspace_bytes(*, b, h, page_size, columns, split_tokens=0):
     return out.value
 
 
+SPLIT_ARGTYPES = [P] * 7 + [I] * 13 + [P, P, Z]
+
+
 def paged_decode_split(out, q, k, v, slab_table, block_table, offsets, *, b, h, d, page_size,
                        pages_per_slab, num_slabs, columns, layer, layers, dtype,
-                       split_tokens=0, unroll=0, workspace=None, workspace_bytes=0):
+                       split_tokens=0, unroll=0, waves=0, row_order=None, workspace=None,
+                       workspace_bytes=0):
     """``mt_paged_decode_split``: the decode of ``mt_paged_decode_batch`` with a
-    caller-owned workspace and an explicit split length (0 = automatic)."""
-    call(paged_library(), 'mt_paged_decode_split', [P] * 7 + [I] * 12 + [P, Z],
+    caller-owned workspace, an explicit split length (0 = automatic), stream
+    unroll and waves per workgroup (0 = defaults) and an optional device row
+    order (longest rows first)."""
+    call(paged_library(), 'mt_paged_decode_split', SPLIT_ARGTYPES,
          out, q, k, v, slab_table, block_table, offsets, b, h, d, page_size, pages_per_slab,
-         num_slabs, columns, layer, layers, dtype_code(dtype), split_tokens, unroll,
-         workspace, workspace_bytes)
+         num_slabs, columns, layer, layers, dtype_code(dtype), split_tokens, unroll, waves,
+         row_order, workspace, workspace_bytes)
 
 
 def embedding_gather(dst, weights, ids, tokens, vocab, dim):

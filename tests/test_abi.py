@@ -100,9 +100,11 @@ def test_split_entry_validation_and_workspace_size():
     assert ws(64, 12, 16, 64, 4096, ct.byref(out)) == 1                    # beyond 2048
     assert ws(64, 12, 12, 64, 0, ct.byref(out)) == 1                       # page size
     split = lib.mt_paged_decode_split
-    split.argtypes, split.restype = [P] * 7 + [I] * 12 + [P, Z], I
+    split.argtypes, split.restype = [P] * 7 + [I] * 13 + [P, P, Z], I
     # a splitting launch without a workspace is rejected
-    assert split(8, 8, 8, 8, 8, 8, 8, 4, 12, 64, 16, 4, 16, 128, 0, 1, 0, 0, 0, None, 0) == 1
+    assert split(8, 8, 8, 8, 8, 8, 8, 4, 12, 64, 16, 4, 16, 128, 0, 1, 0, 0, 0, 0, None, None, 0) == 1
+    # waves must be 4 or 8
+    assert split(8, 8, 8, 8, 8, 8, 8, 4, 12, 64, 16, 4, 16, 64, 0, 1, 0, 0, 0, 6, None, None, 0) == 1
 
 
 def test_inference_entries_reject_invalid_shapes():

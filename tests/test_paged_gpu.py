@@ -126,11 +126,25 @@ def test_null_slab_reads_nan():
 
 @pytest.mark.parametrize('split_tokens', [64, 128, 256, 1024])
 @pytest.mark.parametrize('unroll', [1, 2, 4])
-def test_split_entry_equals_oracle(split_tokens, unroll):
+@pytest.mark.parametrize('waves', [4, 8])
+def test_split_entry_equals_oracle(split_tokens, unroll, waves):
     case = make_decode_case(7, batch=6, heads=3, dim=64, page_size=16,
                             lengths=[1, 64, 65, 500, 1024, 777], pool_pages=256, pages_per_slab=8,
                             dtype='float16')
-    check_case(case, entry='split', split_tokens=split_tokens, unroll=unroll)
+    check_case(case, entry='split', split_tokens=split_tokens, unroll=unroll, waves=waves)
+
+
+@pytest.mark.parametrize('page_size', [8, 16, 32])
+@pytest.mark.parametrize('waves', [4, 8])
+def test_row_order_does_not_change_results(page_size, waves):
+    lengths = [300, 5, 1024, 77, 16, 640, 1]
+    case = make_decode_case(12, batch=7, heads=2, dim=64, page_size=page_size, lengths=lengths,
+                            pool_pages=1024, pages_per_slab=16, dtype='bfloat16')
+    order = RawDeviceBuffer(4 * 7)
+    order.upload(np.argsort(-np.array(lengths), kind='stable').astype(np.int32))
+    dev, ordered = check_case(case, entry='split', waves=waves, row_order=order.ptr)
+    plain = run_decode(DevicePagedCase(case), entry='split', waves=waves)
+    assert np.array_equal(ordered.view(np.uint16), plain.view(np.uint16))
 
 
 def test_repeat_calls_are_deterministic():
