@@ -1,7 +1,8 @@
 """Benchmark of the paged decode hot path on one MI355X.
 
 One step = one fused KV-append + paged decode-attention launch
-(``mt_paged_decode_batch``) over one batch of BASELINE config 2: B = 64
+(``mt_paged_decode_split``: the decode of ``mt_paged_decode_batch`` with the
+rows visited longest first) over one batch of config 2: B = 64
 requests, contexts L ~ U{128..1024}, 12 heads, head_dim 64, page 16, fp16 K/V
 with fp32 accumulation, an 8192-page pool shuffled from the seed. Inputs are
 resident in HBM before the timed region. To measure cold-cache HBM bandwidth,
@@ -105,6 +106,7 @@ def bench_config5(args):
     from minitorch_amd.workloads import DeviceRaggedCase, config5_lengths
     from minitorch_amd.runtime import RawDeviceBuffer
     from minitorch_amd.dtypes import dtype_code
+    rt = runtime()
     lengths = config5_lengths(args.seed, 512)
     lines = {}
     fn = paged_ops.paged_library().mt_paged_decode_split
@@ -113,16 +115,18 @@ def bench_config5(args):
         case = DeviceRaggedCase(args.seed, batch=512, heads=25, dim=64, page_size=page_size,
                                 lengths=lengths, dtype='bfloat16')
         kw = case.kwargs()
+        split = paged_ops.split_tokens_for(page_size=page_size, columns=case.columns, requested=args.split)
         ws_bytes = paged_ops.decode_workspace_bytes(b=512, h=25, page_size=page_size,
-                                                    columns=case.columns, split_tokens=args.split)
+                                                    columns=case.columns, split_tokens=split)
         ws = RawDeviceBuffer(max(ws_bytes, 4))
-        order = RawDeviceBuffer(4 * 512)
-        order.upload(np.argsort(-case.lengths, kind='stable').astype(np.int32))
+        work, items, merges = paged_ops.decode_work_list(case.lengths, 25, split, rt.compute_units())
+        order = RawDeviceBuffer(4 * len(work))
+        order.upload(work)
+        work_args = (None, 0, 0) if args.natural_order else (order.ptr, items, merges)
         call = (case.out.ptr, case.q.ptr, case.k.ptr, case.v.ptr, case.slab_table.ptr,
                 case.block_table.ptr, case.offsets.ptr, kw['b'], kw['h'], kw['d'], kw['page_size'],
                 kw['pages_per_slab'], kw['num_slabs'], kw['columns'], kw['layer'], kw['layers'],
-                dtype_code(kw['dtype']), args.split, args.unroll, args.waves,
-                None if args.natural_order else order.ptr, ws.ptr, ws_bytes)
+                dtype_code(kw['dtype']), split, args.unroll, args.waves, *work_args, ws.ptr, ws_bytes)
         per = time_launches(fn, [call], min(args.steps, 50), min(args.warmup, 5))
         s = 2
         L = case.lengths
@@ -141,7 +145,7 @@ def bench_config5(args):
         'data': 'synthetic (hash-filled K/V)',
         'config': {'workload': 'config 5: ragged op-level paged decode, B=512, H=25, D=64, bf16, '
                                'L~lognormal(ln 256, 1.2) clipped [1, 8192], split reduction for L>1024',
-                   'sum_context_tokens': int(lengths.sum()), 'split_tokens': args.split or 'auto'},
+                   'sum_context_tokens': int(lengths.sum()), 'split_tokens': split},
         'roofline': {'bound': 'hbm', 'achieved': main16['achieved_gbs'], 'peak': PEAK_HBM_GBS,
                      'unit': 'GB/s', 'frac': main16['frac'], 'traffic': None,
                      'algorithmic_bytes_per_launch': main16['algorithmic_bytes']},
@@ -186,7 +190,8 @@ def main():
     ap.add_argument('--split', type=int, default=0, help='split length in tokens (0 = automatic)')
     ap.add_argument('--unroll', type=int, default=0)
     ap.add_argument('--waves', type=int, default=0, help='waves per decode workgroup (4 or 8; 0 = default)')
-    ap.add_argument('--natural-order', action='store_true', help='schedule rows in batch order')
+    ap.add_argument('--natural-order', action='store_true',
+                    help='no work list: schedule every (split, row) in batch order')
     ap.add_argument('--cpu-seconds', type=float, default=10.0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--calibrate-copy', type=int, default=0, metavar='MB',
@@ -220,22 +225,25 @@ def main():
     case = config2_case(args.seed)
     devs = [DevicePagedCase(case) for _ in range(args.pools)]
     kw = devs[0].kwargs()
+    split = paged_ops.split_tokens_for(page_size=case.page_size, columns=case.columns, requested=args.split)
     ws_bytes = paged_ops.decode_workspace_bytes(b=case.batch, h=case.heads, page_size=case.page_size,
-                                                columns=case.columns, split_tokens=args.split)
+                                                columns=case.columns, split_tokens=split)
     from minitorch_amd.runtime import RawDeviceBuffer
     ws = RawDeviceBuffer(max(ws_bytes, 4))
     ws.fill_words(0)
     fn = paged_ops.paged_library().mt_paged_decode_split
     fn.argtypes, fn.restype = paged_ops.SPLIT_ARGTYPES, I
     from minitorch_amd.dtypes import dtype_code
-    # Rows scheduled longest first; the scheduler knows the lengths on the host.
-    order = RawDeviceBuffer(4 * case.batch)
-    order.upload(np.argsort(-case.lengths, kind='stable').astype(np.int32))
-    order_ptr = None if args.natural_order else order.ptr
+    # Work list: rows longest first, balanced over the compute units; the
+    # scheduler knows the lengths on the host.
+    work, items, merges = paged_ops.decode_work_list(case.lengths, case.heads, split, rt.compute_units())
+    order = RawDeviceBuffer(4 * len(work))
+    order.upload(work)
+    work_args = (None, 0, 0) if args.natural_order else (order.ptr, items, merges)
     calls = [(d.out.ptr, d.q.ptr, d.k.ptr, d.v.ptr, d.slab_table.ptr, d.block_table.ptr, d.offsets.ptr,
               kw['b'], kw['h'], kw['d'], kw['page_size'], kw['pages_per_slab'], kw['num_slabs'],
-              kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype']), args.split,
-              args.unroll, args.waves, order_ptr, ws.ptr, ws_bytes) for d in devs]
+              kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype']), split,
+              args.unroll, args.waves, *work_args, ws.ptr, ws_bytes) for d in devs]
 
     def step(i):
         status = fn(*calls[i % len(calls)])
@@ -278,7 +286,7 @@ def main():
             'global_batch': case.batch,
             'sum_context_tokens': int(case.lengths.sum()),
             'pools_rotated': args.pools,
-            'split_tokens': args.split or 'auto',
+            'split_tokens': split,
             'parallelism': 'single GPU',
         },
         'roofline': {

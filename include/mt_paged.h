@@ -54,21 +54,31 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
 int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, int split_tokens,
                                     size_t* bytes);
 
+/* The split length mt_paged_decode_split uses for `requested` (0 = the
+ * automatic choice: 1024 tokens, longer when a table of `columns` pages would
+ * need more than 8 splits). No reference counterpart. */
+int mt_paged_decode_split_tokens(int page_size, int columns, int requested, int* split_tokens);
+
 /* mt_paged_decode_batch with a caller-owned workspace and tuning knobs:
  * split_tokens (a multiple of 64, at most 2048; 0 = automatic), unroll (1, 2
  * or 4 row-blocks per register stage; 0 = default), waves per workgroup (4 or
- * 8; 0 = default), and row_order (device int32 [b], a permutation of 0..b-1,
- * or NULL): the order in which rows are scheduled, e.g. longest first so that
- * long rows do not finish last; outputs are unaffected. The workspace holds
- * per-split partials; launches that share one workspace must not overlap.
+ * 8; 0 = default), and an optional work list built by the caller from the
+ * context lengths it knows on the host (device int32): work_items pairs
+ * (row, split), in the order they should be scheduled (e.g. longest first),
+ * followed by merge_rows row indices, the rows with more than one split. A
+ * work list requires an explicit split_tokens and must hold every (row,
+ * split) of the batch; rows it omits are not written. With work == NULL every
+ * (split, row) is scheduled in batch order and every row is merged as needed.
+ * The workspace holds per-split partials; launches that share one workspace
+ * must not overlap.
  * No reference counterpart (split-context variant of
  * src/paged_attention_kernel.cu:121-137). */
 int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v,
                           const uint64_t* slabs, const int* table, const int* offsets, int b,
                           int h, int d, int page_size, int pages_per_slab, int num_slabs,
                           int columns, int layer, int layers, int dtype, int split_tokens,
-                          int unroll, int waves, const int* row_order, void* workspace,
-                          size_t workspace_bytes);
+                          int unroll, int waves, const int* work, int work_items,
+                          int merge_rows, void* workspace, size_t workspace_bytes);
 
 #ifdef __cplusplus
 }

@@ -32,6 +32,9 @@ int mt_event_destroy(void* e);
 int mt_event_synchronize(void* e);
 /* Number of visible devices. No reference counterpart. */
 int mt_device_count(int* n);
+/* Compute units of the current device (256 on MI355X); sizes the row
+ * visiting order of the decode. No reference counterpart. */
+int mt_compute_units(int* n);
 /* Pinned host memory (hipHostMalloc) for asynchronous uploads.
  * No reference counterpart. */
 int mt_host_alloc(void** p, size_t bytes);

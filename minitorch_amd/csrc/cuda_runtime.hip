@@ -74,6 +74,13 @@ int mt_event_elapsed(float* ms, hipEvent_t a, hipEvent_t b) {
 int mt_event_destroy(hipEvent_t e) { return hipEventDestroy(e); }
 int mt_event_synchronize(hipEvent_t e) { return hipEventSynchronize(e); }
 int mt_device_count(int* n) { return hipGetDeviceCount(n); }
+// Compute units of the current device.
+int mt_compute_units(int* n) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  return hipDeviceGetAttribute(n, hipDeviceAttributeMultiprocessorCount, dev);
+}
 // Pinned host memory for asynchronous uploads (allocated, never registered).
 int mt_host_alloc(void** p, size_t bytes) { return hipHostMalloc(p, bytes, hipHostMallocDefault); }
 int mt_host_free(void* p) { return hipHostFree(p); }

@@ -52,15 +52,19 @@ constexpr int kDefaultSplitTokens = 1024;
 constexpr int kMaxSplitsPerRow = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 #ifndef MT_STAGES
-#define MT_STAGES 2
+#define MT_STAGES 1
 #endif
 constexpr int kStages = MT_STAGES;  // register stages of the K/V stream
-constexpr int kDefaultUnroll = 2;    // row-blocks per register stage
+constexpr int kDefaultUnroll = 4;    // row-blocks per register stage (capped per shape)
 constexpr int kDefaultWaves = 4;     // waves per decode workgroup
 #ifndef MT_DECODE_GROUP
 #define MT_DECODE_GROUP 4
 #endif
 constexpr int kDecodeGroup = MT_DECODE_GROUP;  // lanes per token in the decode kernel
+// Pools of at most this many slabs have their slab table staged in LDS by the
+// decode kernel, so that page resolution after the block-table read is an LDS
+// read instead of a second dependent global load.
+constexpr int kLdsSlabs = 512;
 
 struct Geometry {
   int heads, dim, page_size, log2_page, pps, num_slabs, columns, layer;
@@ -99,6 +103,22 @@ __device__ __forceinline__ const T* resolve_page(const uint64_t* slabs, int phys
   const int64_t i = ((int64_t(g.layer) * 2 * g.pps + slot) * g.heads + head) *
                     int64_t(g.page_size) * g.dim;
   return reinterpret_cast<const T*>(address) + i;
+}
+
+// Page base from a physical page ID and its slab's base address (already
+// looked up); nullptr for a null slab.
+template <class T>
+__device__ __forceinline__ const T* page_in_slab(uint64_t address, int physical, const Geometry& g,
+                                                 int head) {
+  if (!address) return nullptr;
+  const int slot = physical % g.pps;
+  const int64_t i = ((int64_t(g.layer) * 2 * g.pps + slot) * g.heads + head) *
+                    int64_t(g.page_size) * g.dim;
+  return reinterpret_cast<const T*>(address) + i;
+}
+
+__device__ __forceinline__ bool physical_in_pool(int physical, const Geometry& g) {
+  return physical >= 0 && int64_t(physical) < int64_t(g.num_slabs) * g.pps;
 }
 
 // Online-softmax state of one token group, in base-2 units (scores are
@@ -155,6 +175,25 @@ struct Softmax {
     for (int i = 0; i < N; ++i) acc[i] = acc[i] * sa + ao[i] * sb;
     m = mn;
   }
+  // Merge with the state held `rot` lanes further along the same 16-lane row
+  // (DPP row rotate; no LDS traffic).
+  template <int CTRL>
+  __device__ __forceinline__ void merge_dpp() {
+    float ao[N];
+    const float mo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), CTRL, 0xF, 0xF, false));
+    const float lo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(l), CTRL, 0xF, 0xF, false));
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      ao[i] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc[i]), CTRL, 0xF, 0xF, false));
+    merge(mo, lo, ao);
+  }
+  // Merge the token groups of each 16-lane row: afterwards lanes with
+  // lane % 16 < G hold their row's state for chunk lane % G.
+  __device__ __forceinline__ void row_merge() {
+    static_assert(G == 4 || G == 8, "row_merge expects 4 or 8 lanes per token");
+    if constexpr (G == 4) merge_dpp<0x124>();  // row_ror:4
+    merge_dpp<0x128>();                        // row_ror:8
+  }
   // Merge the states of the token groups of a wave (lanes with equal
   // lane % G): afterwards lanes 0..G-1 hold the wave's state for their chunk.
   __device__ __forceinline__ void wave_merge() {
@@ -208,6 +247,16 @@ struct Chunk {
       const auto* g = global_view(p);
 #pragma unroll
       for (int i = 0; i < DL; ++i) val[i] = (col0 + i < dim) ? to_f32<DT>(g[i]) : 0.f;
+    }
+  }
+  // Same chunk from an LDS copy of the row (p points at column col0).
+  __device__ __forceinline__ void load_lds(const T* p, int col0, int dim) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) raw[i] = reinterpret_cast<const u32x4*>(p)[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < DL; ++i) val[i] = (col0 + i < dim) ? to_f32<DT>(p[i]) : 0.f;
     }
   }
   __device__ __forceinline__ void nan_fill() {
@@ -366,7 +415,12 @@ struct DecodeArgs {
   int64_t items;
   Geometry g;
   float* partials;
-  const int* order;  // row visiting order, or nullptr for 0..B-1
+  // Optional work list: work_items (row, split) pairs in visiting order,
+  // then merge_rows row indices whose splits need the reduction. Without it
+  // every (split, row, head) is an item and every row is a merge candidate.
+  const int* work;
+  int work_items;
+  int merge_rows;
 };
 
 // Stream one wave's share of a split: row-blocks j = wave + waves * i
@@ -446,7 +500,8 @@ __device__ __forceinline__ void stream_wave(Softmax<D / G, G>& st, const Query<D
 }
 
 // Fused KV append + decode attention over (request, head, split) items.
-// Rows are visited in a.order (when given) so that long rows start first.
+// Items come from the work list when one is given (visiting order chosen by
+// the caller, e.g. longest first), else from the full (split, row, head) grid.
 template <int DT, int D, bool VEC, int U, int STAGES, int WAVES, int G>
 __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
   using T = typename Elem<DT>::T;
@@ -454,16 +509,37 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
   constexpr int RB = kWave / G;
   constexpr int PSTRIDE = D + 2;
   constexpr int NT = WAVES * kWave;
-  __shared__ float s_m[WAVES], s_l[WAVES];
-  __shared__ float s_acc[WAVES][D];
+  constexpr int NS = WAVES * 4;  // partial states per item: one per 16-lane row
+  constexpr int SLABS_PER_THREAD = (kLdsSlabs + NT - 1) / NT;
+  __shared__ float s_m[NS], s_l[NS];
+  __shared__ float s_acc[NS][D];
+  __shared__ uint64_t s_slabs[kLdsSlabs];
+  __shared__ __align__(16) T s_new[2][D];  // the new token's K and V rows
 
   const Geometry& g = a.g;
   const int dim = VEC ? D : g.dim;
   const int tid = threadIdx.x;
+  const int64_t bh_count = int64_t(a.batch) * g.heads;
+  // The slab table of a small pool is staged in LDS. A workgroup whose first
+  // item is certain to have work (every work-list item; split 0 of the full
+  // grid) reads it before anything else, so that it arrives while the
+  // item's own loads are in flight; others read it once an item has work.
+  const bool lds_slabs = g.num_slabs <= kLdsSlabs;
+  bool slabs_staged = !lds_slabs;
+  bool slabs_loaded = false;
+  uint64_t slab_reg[SLABS_PER_THREAD];
+  auto load_slabs = [&]() {
+#pragma unroll
+    for (int j = 0; j < SLABS_PER_THREAD; ++j) {
+      const int i = tid + j * NT;
+      slab_reg[j] = i < g.num_slabs ? a.slabs[i] : 0;
+    }
+    slabs_loaded = true;
+  };
+  if (lds_slabs && (a.work || blockIdx.x < bh_count)) load_slabs();
   const int wave = tid >> 6;
   const int lane = tid & (kWave - 1);
   const int col0 = (lane % G) * DL;
-  const int64_t bh_count = int64_t(a.batch) * g.heads;
   const int64_t cap = int64_t(g.columns) * g.page_size;
   const int sub_shift = g.page_size < RB ? 1 : 0;
   const int rb_per_wave = a.split_tokens / RB / WAVES;
@@ -473,11 +549,19 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
   T* out = static_cast<T*>(a.out);
 
   for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
-    const int split = int(item / bh_count);
-    const int64_t bhi = item - int64_t(split) * bh_count;
-    const int r = int(bhi / g.heads);
-    const int head = int(bhi - int64_t(r) * g.heads);
-    const int b = a.order ? a.order[r] : r;
+    int split, b, head;
+    if (a.work) {
+      const int64_t w = item / g.heads;
+      head = int(item - w * g.heads);
+      b = a.work[2 * w];
+      split = a.work[2 * w + 1];
+      if (b < 0 || b >= a.batch || split < 0 || split >= a.nsplit_max) continue;
+    } else {
+      split = int(item / bh_count);
+      const int64_t bhi = item - int64_t(split) * bh_count;
+      b = int(bhi / g.heads);
+      head = int(bhi - int64_t(b) * g.heads);
+    }
     const int64_t bh = int64_t(b) * g.heads + head;
 
     // Loads that do not depend on the context length are issued first: the
@@ -486,11 +570,8 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
     const int offset = a.offsets[b];
     Query<DT, D, VEC, G> qv;
     qv.load(qp + bh * dim, col0, dim, a.qscale);
-    Chunk<DT, DL, VEC> kn, vn;
-    if (wave == 0) {
-      kn.load(kin + bh * dim + col0, col0, dim);
-      vn.load(vin + bh * dim + col0, col0, dim);
-    }
+    T new_k{}, new_v{};
+    if (tid < dim) { new_k = kin[bh * dim + tid]; new_v = vin[bh * dim + tid]; }
     const int* table_row = a.table + int64_t(b) * g.columns;
     const int t0i = split * a.split_tokens;
     const int slot_i = lane >> sub_shift;
@@ -513,13 +594,32 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
     const int64_t t1 = L < t0 + a.split_tokens ? L : t0 + a.split_tokens;
     const bool owns_new = L > 0 && split == nsplit - 1;
     const int ntok_paged = int((owns_new ? t1 - 1 : t1) - t0);  // tokens read from pages
-    const T* my_page = (slot_i < rb_per_wave && t0 + slot_tok < t1)
-                           ? resolve_page<T>(a.slabs, physical, g, head) : nullptr;
+    // Staged in LDS once the loads above are in flight: the slab table (first
+    // item only) and the new token's K/V row, which is needed only after the
+    // stream and so holds no registers during it.
+    if (!slabs_staged) {
+      if (!slabs_loaded) load_slabs();
+#pragma unroll
+      for (int j = 0; j < SLABS_PER_THREAD; ++j)
+        if (tid + j * NT < kLdsSlabs) s_slabs[tid + j * NT] = slab_reg[j];
+    }
+    if (tid < dim) { s_new[0][tid] = new_k; s_new[1][tid] = new_v; }
+    __syncthreads();
+    slabs_staged = true;
+    auto slab_of = [&](int physical) -> uint64_t {
+      return lds_slabs ? s_slabs[physical / g.pps] : a.slabs[physical / g.pps];
+    };
+    auto resolve = [&](int physical) -> const T* {
+      return physical_in_pool(physical, g) ? page_in_slab<T>(slab_of(physical), physical, g, head)
+                                           : nullptr;
+    };
+
+    const T* my_page = (slot_i < rb_per_wave && t0 + slot_tok < t1) ? resolve(physical) : nullptr;
     // The new token's page (wave 0, scalar loads; needed only after the stream).
     const T* new_page = nullptr;
     if (owns_new && wave == 0) {
       const int64_t logical = (L - 1) >> g.log2_page;
-      new_page = logical < g.columns ? resolve_page<T>(a.slabs, table_row[logical], g, head) : nullptr;
+      new_page = logical < g.columns ? resolve(table_row[logical]) : nullptr;
     }
 
     Softmax<DL, G> st;
@@ -532,6 +632,9 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
       // and written into its page when the page exists (reference append,
       // src/paged_attention_kernel.cu:23-33). A missing page reads as NaN.
       const int64_t pos = L - 1;
+      Chunk<DT, DL, VEC> kn, vn;
+      kn.load_lds(&s_new[0][col0], col0, dim);
+      vn.load_lds(&s_new[1][col0], col0, dim);
       if (lane < G && new_page) {
         T* kp = const_cast<T*>(new_page) + (pos & (g.page_size - 1)) * dim + col0;
         T* vp = kp + g.kind_stride;
@@ -557,32 +660,37 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
       }
     }
 
-    st.wave_merge();
-    if (lane < G) {
+    // Row merges by DPP, then the WAVES * 4 row states meet in LDS.
+    st.row_merge();
+    const int row = lane >> 4;
+    if ((lane & 15) < G) {
+      const int si = wave * 4 + row;
 #pragma unroll
-      for (int i = 0; i < DL; ++i) s_acc[wave][col0 + i] = st.acc[i];
-      if (lane == 0) { s_m[wave] = st.m; s_l[wave] = st.l; }
+      for (int i = 0; i < DL; ++i) s_acc[si][col0 + i] = st.acc[i];
+      if ((lane & 15) == 0) { s_m[si] = st.m; s_l[si] = st.l; }
     }
     __syncthreads();
 
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, s_m[w]);
-    float lsum = 0.f, asum = 0.f;
     const int t = tid;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
-      const float sc = (s_m[w] == -INFINITY) ? 0.f : fast_exp2(s_m[w] - M);
-      lsum += s_l[w] * sc;
-      if (t < dim) asum += s_acc[w][t] * sc;
-    }
-
-    if (nsplit == 1) {
-      if (t < dim) orow[t] = from_f32<DT>(finalize(asum, lsum));
-    } else {
-      float* part = a.partials + (bh * a.nsplit_max + split) * PSTRIDE;
-      if (t < dim) part[2 + t] = asum;
-      if (t == 0) { part[0] = M; part[1] = lsum; }
+    if (t < dim) {
+      float M = -INFINITY;
+#pragma unroll 4
+      for (int w = 0; w < NS; ++w) M = fmaxf(M, s_m[w]);
+      float lsum = 0.f, asum = 0.f;
+#pragma unroll 4
+      for (int w = 0; w < NS; ++w) {
+        const float mw = s_m[w];
+        const float sc = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
+        lsum = fmaf(s_l[w], sc, lsum);
+        asum = fmaf(s_acc[w][t], sc, asum);
+      }
+      if (nsplit == 1) {
+        orow[t] = from_f32<DT>(finalize(asum, lsum));
+      } else {
+        float* part = a.partials + (bh * a.nsplit_max + split) * PSTRIDE;
+        part[2 + t] = asum;
+        if (t == 0) { part[0] = M; part[1] = lsum; }
+      }
     }
     __syncthreads();  // LDS is reused by the next item
   }
@@ -599,11 +707,16 @@ __global__ __launch_bounds__(128) void merge_kernel(DecodeArgs a) {
   constexpr int PSTRIDE = D + 2;
   const Geometry& g = a.g;
   const int dim = g.dim;
-  const int64_t bh_count = int64_t(a.batch) * g.heads;
+  const int64_t rows = a.work ? a.merge_rows : a.batch;
+  const int64_t count = rows * g.heads;
   const int64_t cap = int64_t(g.columns) * g.page_size;
   T* out = static_cast<T*>(a.out);
-  for (int64_t bh = blockIdx.x; bh < bh_count; bh += gridDim.x) {
-    const int b = int(bh / g.heads);
+  for (int64_t i = blockIdx.x; i < count; i += gridDim.x) {
+    const int64_t m = i / g.heads;
+    const int head = int(i - m * g.heads);
+    const int b = a.work ? a.work[2 * int64_t(a.work_items) + m] : int(m);
+    if (b < 0 || b >= a.batch) continue;
+    const int64_t bh = int64_t(b) * g.heads + head;
     const int offset = a.offsets[b];
     const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
     if (L > cap) continue;
@@ -791,8 +904,9 @@ hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
   }
   if (unroll <= 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.nsplit_max == 1) return e;
-  merge_kernel<DT, (D > 64 ? 128 : 64)><<<grid_for(int64_t(a.batch) * a.g.heads), 128>>>(a);
+  const int64_t merge_rows = a.work ? a.merge_rows : a.batch;
+  if (e != hipSuccess || a.nsplit_max == 1 || merge_rows == 0) return e;
+  merge_kernel<DT, (D > 64 ? 128 : 64)><<<grid_for(merge_rows * a.g.heads), 128>>>(a);
   return hipGetLastError();
 }
 
@@ -812,9 +926,11 @@ hipError_t launch_decode_dt(const DecodeArgs& a, int64_t blocks, bool vec, int d
 int decode_common(void* out, const void* q, const void* k, const void* v, const uint64_t* slabs,
                   const int* table, const int* offsets, int b, int h, int d, int page_size,
                   int pps, int num_slabs, int columns, int layer, int layers, int dtype,
-                  int split_tokens, int unroll, int waves, const int* row_order, void* workspace,
-                  size_t workspace_bytes) {
+                  int split_tokens, int unroll, int waves, const int* work, int work_items,
+                  int merge_rows, void* workspace, size_t workspace_bytes) {
   const int64_t cap = int64_t(columns) * page_size;
+  // A work list is built for one split length, so it must be given.
+  if (work && split_tokens <= 0) return hipErrorInvalidValue;
   const int S = choose_split(cap, split_tokens);
   if (S < 64 || S % 64 != 0 || S > kMaxSplitTokens) return hipErrorInvalidValue;
   if (waves != 4 && waves != 8) return hipErrorInvalidValue;
@@ -822,16 +938,22 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   const int64_t nsplit_max = (cap + S - 1) / S;
   const int64_t bh = int64_t(b) * h;
   if (nsplit_max > INT_MAX) return hipErrorInvalidValue;
+  if (work && (work_items < 0 || merge_rows < 0 || merge_rows > b ||
+               work_items > int64_t(b) * nsplit_max))
+    return hipErrorInvalidValue;
+  if (work && work_items == 0) return hipSuccess;
   if (nsplit_max > 1 && (!workspace || workspace_bytes < workspace_bytes_for(bh, int(nsplit_max))))
     return hipErrorInvalidValue;
   DecodeArgs a;
   a.out = out; a.q = q; a.k = k; a.v = v; a.slabs = slabs; a.table = table; a.offsets = offsets;
   a.batch = b; a.split_tokens = S; a.nsplit_max = int(nsplit_max);
   a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
-  a.items = bh * nsplit_max;
+  a.items = work ? int64_t(work_items) * h : bh * nsplit_max;
   a.g = make_geometry(h, d, page_size, pps, num_slabs, columns, layer);
   a.partials = static_cast<float*>(workspace);
-  a.order = row_order;
+  a.work = work;
+  a.work_items = work ? work_items : 0;
+  a.merge_rows = work ? merge_rows : 0;
   const bool vec = (d == 64 || d == 128) && aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v);
   if (dtype == kF32) return launch_decode_dt<kF32>(a, a.items, vec, d, unroll, waves);
   if (dtype == kF16) return launch_decode_dt<kF16>(a, a.items, vec, d, unroll, waves);
@@ -944,7 +1066,7 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
   }
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, S, kDefaultUnroll, kDefaultWaves,
-                       nullptr, ws, ws_bytes);
+                       nullptr, 0, 0, ws, ws_bytes);
 }
 
 int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, int split_tokens,
@@ -960,12 +1082,22 @@ int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, in
   return hipSuccess;
 }
 
+int mt_paged_decode_split_tokens(int page_size, int columns, int requested, int* split_tokens) {
+  if (!split_tokens || columns < 1 || requested < 0 ||
+      !(page_size == 8 || page_size == 16 || page_size == 32))
+    return hipErrorInvalidValue;
+  const int S = choose_split(int64_t(columns) * page_size, requested);
+  if (S < 64 || S % 64 != 0 || S > kMaxSplitTokens) return hipErrorInvalidValue;
+  *split_tokens = S;
+  return hipSuccess;
+}
+
 int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v,
                           const uint64_t* slabs, const int* table, const int* offsets, int b,
                           int h, int d, int page_size, int pages_per_slab, int num_slabs,
                           int columns, int layer, int layers, int dtype, int split_tokens,
-                          int unroll, int waves, const int* row_order, void* workspace,
-                          size_t workspace_bytes) {
+                          int unroll, int waves, const int* work, int work_items,
+                          int merge_rows, void* workspace, size_t workspace_bytes) {
   if (!out || !q || !k || !v || !slabs || !table || !offsets ||
       !paged_shape(b, h, 1, 1, d, page_size, pages_per_slab, num_slabs, columns, layer, layers, 0) ||
       int64_t(columns) * page_size > INT32_MAX || split_tokens < 0 || unroll < 0 ||
@@ -975,7 +1107,7 @@ int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, split_tokens,
                        unroll == 0 ? kDefaultUnroll : unroll, waves == 0 ? kDefaultWaves : waves,
-                       row_order, workspace, workspace_bytes);
+                       work, work_items, merge_rows, workspace, workspace_bytes);
 }
 
 }  // extern "C"

@@ -12,7 +12,7 @@ the fused append + attention kernel per layer on that metadata.
 import numpy as np
 
 from .paged_kv_cache import PagedKVCache, _DeviceView
-from .runtime import RawDeviceBuffer, PinnedHostBuffer, DeviceTensor, P, I
+from .runtime import RawDeviceBuffer, PinnedHostBuffer, DeviceTensor, runtime, P, I
 from . import paged_ops
 
 
@@ -20,20 +20,29 @@ class _DecodeWorkspace:
     """Per-pool device buffers for decode metadata, grown on demand."""
 
     def __init__(self):
-        self.rows = self.cols = 0
+        self.rows = self.cols = self.work = 0
         self.buffer = None
         self.staging = None
+        self.partials = None
+        self.partial_bytes = 0
 
-    def ensure(self, rows, cols):
-        if rows <= self.rows and cols <= self.cols and self.buffer is not None:
+    def ensure(self, rows, cols, work):
+        if rows <= self.rows and cols <= self.cols and work <= self.work and self.buffer is not None:
             return
-        self.rows, self.cols = max(rows, self.rows), max(cols, self.cols)
+        self.rows, self.cols, self.work = max(rows, self.rows), max(cols, self.cols), max(work, self.work)
         r, c = self.rows, self.cols
-        # slots | offsets | positions | cu_seqlens | new_page | table
-        self.sizes = [4 * r, 4 * r, 4 * r, 4 * (r + 1), 4 * r, 4 * r * c]
+        # slots | work list | offsets | positions | cu_seqlens | new_page | table
+        self.sizes = [4 * r, 4 * self.work, 4 * r, 4 * r, 4 * (r + 1), 4 * r, 4 * r * c]
         self.offsets = np.cumsum([0] + [(s + 255) // 256 * 256 for s in self.sizes]).tolist()
         self.buffer = RawDeviceBuffer(int(self.offsets[-1]))
-        self.staging = PinnedHostBuffer(4 * r)
+        # slots and the work list go up in one copy
+        self.staging = PinnedHostBuffer(int(self.offsets[2]))
+
+    def ensure_partials(self, nbytes):
+        if nbytes > self.partial_bytes:
+            self.partials = RawDeviceBuffer(nbytes)
+            self.partial_bytes = nbytes
+        return self.partials.ptr if nbytes else None
 
     def ptr(self, index):
         return self.buffer.ptr + int(self.offsets[index])
@@ -64,37 +73,47 @@ class PagedDecodeBatch:
                 raise ValueError('Decode caches must share a live pool, have batch=1 and remaining capacity')
         self.offsets = np.array([c.length for c in self.caches], np.int32)
         self.columns = max((c.length + 1 + self.pool.page_size - 1) // self.pool.page_size for c in self.caches)
-        self.table = self.device_offsets = self.position_ids = self.cu_seqlens = None
+        self.table = self.device_offsets = self.position_ids = self.cu_seqlens = self.work = None
         self._prepared, self._written_layers = [], set()
         self._committed = False
         self._device_prepared = False
         self.last_attention_path = 'paged_batch_decode'
 
-    def _workspace(self):
+    def _workspace(self, work_len):
         ws = getattr(self.pool, '_decode_workspace', None)
         if ws is None:
             ws = self.pool._decode_workspace = _DecodeWorkspace()
-        ws.ensure(self.batch_size, self.columns)
+        ws.ensure(self.batch_size, self.columns, work_len)
         return ws
 
     def prepare(self):
         if self._prepared or self._committed:
             raise ValueError('Decode batch already executed')
         pool, b = self.pool, self.batch_size
-        ws = self._workspace()
+        # Work list: every (row, split) longest first, balanced over the
+        # compute units; the kernel writes each row to its own output row.
+        self.split_tokens = paged_ops.split_tokens_for(page_size=pool.page_size, columns=self.columns)
+        work, self.work_items, self.merge_rows = paged_ops.decode_work_list(
+            self.offsets + 1, max(h for h, _ in self.layout), self.split_tokens, runtime().compute_units())
+        ws = self._workspace(len(work))
         slots = np.array([c.slot for c in self.caches], np.int32)
         needs = (self.offsets % pool.page_size) == 0
         avail = pool.max_pages - pool._leased_count
-        ws.staging.upload_async(ws.ptr(0), slots)
+        upload = np.zeros(int(ws.offsets[2]) // 4, np.int32)
+        upload[:b] = slots
+        w0 = int(ws.offsets[1]) // 4
+        upload[w0:w0 + len(work)] = work
+        ws.staging.upload_async(ws.ptr(0), upload[:w0 + len(work)])
         pool._call('mt_sched_decode_prepare', [P, I, I, I, I, P, P, P, P, P],
-                   ws.ptr(0), b, self.columns, pool.page_size, avail, ws.ptr(5), ws.ptr(1),
-                   ws.ptr(2), ws.ptr(3), ws.ptr(4))
+                   ws.ptr(0), b, self.columns, pool.page_size, avail, ws.ptr(6), ws.ptr(2),
+                   ws.ptr(3), ws.ptr(4), ws.ptr(5))
         self._device_prepared = True
         self._ws = ws
-        self.table = _DeviceView(ws.buffer, int(ws.offsets[5]), 4 * b * self.columns)
-        self.device_offsets = _DeviceView(ws.buffer, int(ws.offsets[1]), 4 * b)
-        self.cu_seqlens = _DeviceView(ws.buffer, int(ws.offsets[3]), 4 * (b + 1))
-        self.position_ids = DeviceTensor((b, 1), 'float32', buffer=ws.buffer, byte_offset=int(ws.offsets[2]))
+        self.table = _DeviceView(ws.buffer, int(ws.offsets[6]), 4 * b * self.columns)
+        self.device_offsets = _DeviceView(ws.buffer, int(ws.offsets[2]), 4 * b)
+        self.cu_seqlens = _DeviceView(ws.buffer, int(ws.offsets[4]), 4 * (b + 1))
+        self.work = _DeviceView(ws.buffer, int(ws.offsets[1]), 4 * len(work))
+        self.position_ids = DeviceTensor((b, 1), 'float32', buffer=ws.buffer, byte_offset=int(ws.offsets[3]))
         # Host half, row by row like the reference (paged_decode.py:307-309):
         # the row whose page would exceed the budget raises MemoryError.
         pops = 0
@@ -117,11 +136,17 @@ class PagedDecodeBatch:
             raise ValueError('Invalid batched decode Q/K/V')
         out = DeviceTensor(q.shape, self.dtype)
         pool = self.pool
-        paged_ops.paged_decode_batch(out.ptr, q.ptr, k.ptr, v.ptr, pool.slab_table.ptr, self.table.ptr,
+        partial_bytes = paged_ops.decode_workspace_bytes(b=self.batch_size, h=h, page_size=pool.page_size,
+                                                         columns=self.columns, split_tokens=self.split_tokens)
+        partials = self._ws.ensure_partials(partial_bytes)
+        paged_ops.paged_decode_split(out.ptr, q.ptr, k.ptr, v.ptr, pool.slab_table.ptr, self.table.ptr,
                                      self.device_offsets.ptr, b=self.batch_size, h=h, d=d,
                                      page_size=pool.page_size, pages_per_slab=pool.pages_per_slab,
                                      num_slabs=pool.num_slabs, columns=self.columns, layer=layer,
-                                     layers=len(self.layout), dtype=self.dtype)
+                                     layers=len(self.layout), dtype=self.dtype,
+                                     split_tokens=self.split_tokens, work=self.work.ptr,
+                                     work_items=self.work_items, merge_rows=self.merge_rows,
+                                     workspace=partials, workspace_bytes=partial_bytes)
         self._written_layers.add(layer)
         for cache in self.caches:
             cache._written_layers.add(layer)
@@ -145,7 +170,7 @@ class PagedDecodeBatch:
         if not self._committed:
             if self._device_prepared:
                 self.pool._call('mt_sched_decode_abort', [P, I, P], self._ws.ptr(0), self.batch_size,
-                                self._ws.ptr(4))
+                                self._ws.ptr(5))
             for cache in self._prepared:
                 cache.abort_append(device=False)
         self.position_ids = None

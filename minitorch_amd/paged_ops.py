@@ -7,6 +7,7 @@ goes to ``cuda_kernels/paged_attention_kernel.so`` or
 ``cuda_kernels/inference_kernels.so``.
 """
 import ctypes as ct
+import numpy as np
 from .runtime import library, call, P, I, Z, DeviceTensor, runtime
 from .dtypes import dtype_code
 
@@ -51,21 +52,56 @@ def decode_workspace_bytes(*, b, h, page_size, columns, split_tokens=0):
     return out.value
 
 
-SPLIT_ARGTYPES = [P] * 7 + [I] * 13 + [P, P, Z]
+def split_tokens_for(*, page_size, columns, requested=0):
+    """Split length the decode uses for a table of ``columns`` pages."""
+    out = ct.c_int()
+    call(paged_library(), 'mt_paged_decode_split_tokens', [I, I, I, ct.POINTER(ct.c_int)],
+         page_size, columns, requested, ct.byref(out))
+    return out.value
+
+
+SPLIT_ARGTYPES = [P] * 7 + [I] * 13 + [P, I, I, P, Z]
 
 
 def paged_decode_split(out, q, k, v, slab_table, block_table, offsets, *, b, h, d, page_size,
                        pages_per_slab, num_slabs, columns, layer, layers, dtype,
-                       split_tokens=0, unroll=0, waves=0, row_order=None, workspace=None,
-                       workspace_bytes=0):
+                       split_tokens=0, unroll=0, waves=0, work=None, work_items=0, merge_rows=0,
+                       workspace=None, workspace_bytes=0):
     """``mt_paged_decode_split``: the decode of ``mt_paged_decode_batch`` with a
     caller-owned workspace, an explicit split length (0 = automatic), stream
-    unroll and waves per workgroup (0 = defaults) and an optional device row
-    order (longest rows first)."""
+    unroll and waves per workgroup (0 = defaults) and an optional device work
+    list from :func:`decode_work_list`."""
     call(paged_library(), 'mt_paged_decode_split', SPLIT_ARGTYPES,
          out, q, k, v, slab_table, block_table, offsets, b, h, d, page_size, pages_per_slab,
          num_slabs, columns, layer, layers, dtype_code(dtype), split_tokens, unroll, waves,
-         row_order, workspace, workspace_bytes)
+         work, work_items, merge_rows, workspace, workspace_bytes)
+
+
+def decode_work_list(lengths, heads, split_tokens, compute_units):
+    """Work list for ``mt_paged_decode_split``: returns (int32 array,
+    work_items, merge_rows).
+
+    Every (row, split) of contexts ``lengths`` (keys attended, new token
+    included) is one entry of ``heads`` workgroups. Entries are ordered by
+    their token count, longest first (LPT), and every other dispatch pass of
+    ``compute_units`` workgroups is reversed, so a compute unit that received
+    one of the longest entries in one pass receives one of the shorter
+    entries of the next ("snake" order). The rows with more than one split
+    follow the pairs.
+    """
+    L = np.asarray(lengths, np.int64)
+    nsplit = np.maximum(1, -(-L // split_tokens))
+    rows = np.repeat(np.arange(len(L)), nsplit)
+    first = np.repeat(np.cumsum(nsplit) - nsplit, nsplit)
+    splits = np.arange(len(rows)) - first
+    tokens = np.clip(L[rows] - splits * split_tokens, 0, split_tokens)
+    lpt = np.lexsort((rows, -tokens))
+    per = max(1, compute_units // max(1, heads))
+    passes = [lpt[i:i + per] for i in range(0, len(lpt), per)]
+    order = np.concatenate([p if k % 2 == 0 else p[::-1] for k, p in enumerate(passes)])
+    merge = np.flatnonzero(nsplit > 1)
+    work = np.concatenate([np.stack([rows[order], splits[order]], 1).ravel(), merge])
+    return work.astype(np.int32), len(order), len(merge)
 
 
 def embedding_gather(dst, weights, ids, tokens, vocab, dim):

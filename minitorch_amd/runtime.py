@@ -44,7 +44,7 @@ class HipRuntime:
             'mt_event_create': [ct.POINTER(P)], 'mt_event_record': [P],
             'mt_event_elapsed': [ct.POINTER(F), P, P], 'mt_event_destroy': [P],
             'mt_event_synchronize': [P],
-            'mt_device_count': [ct.POINTER(I)],
+            'mt_device_count': [ct.POINTER(I)], 'mt_compute_units': [ct.POINTER(I)],
             'mt_host_alloc': [ct.POINTER(P), Z], 'mt_host_free': [P],
             'mt_fill_random': [P, ct.c_longlong, ct.c_ulonglong, I],
         }
@@ -60,6 +60,13 @@ class HipRuntime:
 
     def synchronize(self):
         self.check(self.lib.mt_sync())
+
+    def compute_units(self):
+        if getattr(self, '_compute_units', None) is None:
+            n = I()
+            self.check(self.lib.mt_compute_units(ct.byref(n)))
+            self._compute_units = n.value
+        return self._compute_units
 
     def malloc(self, nbytes):
         pointer = P()

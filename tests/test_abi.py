@@ -99,12 +99,28 @@ def test_split_entry_validation_and_workspace_size():
     assert ws(64, 12, 16, 64, 100, ct.byref(out)) == 1                     # not a multiple of 64
     assert ws(64, 12, 16, 64, 4096, ct.byref(out)) == 1                    # beyond 2048
     assert ws(64, 12, 12, 64, 0, ct.byref(out)) == 1                       # page size
+    st = lib.mt_paged_decode_split_tokens
+    st.argtypes, st.restype = [I, I, I, ct.POINTER(ct.c_int)], I
+    s = ct.c_int()
+    assert st(16, 64, 0, ct.byref(s)) == 0 and s.value == 1024
+    assert st(16, 1024, 0, ct.byref(s)) == 0 and s.value == 2048        # 16384 tokens: 8 splits of 2048
+    assert st(16, 100, 0, ct.byref(s)) == 0 and s.value == 1024
+    assert st(8, 64, 256, ct.byref(s)) == 0 and s.value == 256
+    assert st(16, 64, 96, ct.byref(s)) == 1                             # not a multiple of 64
     split = lib.mt_paged_decode_split
-    split.argtypes, split.restype = [P] * 7 + [I] * 13 + [P, P, Z], I
+    split.argtypes, split.restype = [P] * 7 + [I] * 13 + [P, I, I, P, Z], I
+    common = (8, 8, 8, 8, 8, 8, 8, 4, 12, 64, 16, 4, 16)
     # a splitting launch without a workspace is rejected
-    assert split(8, 8, 8, 8, 8, 8, 8, 4, 12, 64, 16, 4, 16, 128, 0, 1, 0, 0, 0, 0, None, None, 0) == 1
+    assert split(*common, 128, 0, 1, 0, 0, 0, 0, None, 0, 0, None, 0) == 1
     # waves must be 4 or 8
-    assert split(8, 8, 8, 8, 8, 8, 8, 4, 12, 64, 16, 4, 16, 64, 0, 1, 0, 0, 0, 6, None, None, 0) == 1
+    assert split(*common, 64, 0, 1, 0, 0, 0, 6, None, 0, 0, None, 0) == 1
+    # a work list needs an explicit split length and counts within the batch
+    assert split(*common, 64, 0, 1, 0, 0, 0, 0, 8, 4, 0, None, 0) == 1
+    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 8, 5, 0, None, 0) == 1   # 5 > 4 rows x 1 split
+    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 8, 4, 5, None, 0) == 1   # 5 merge rows > 4
+    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 8, -1, 0, None, 0) == 1
+    # an empty work list launches nothing
+    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 8, 0, 0, None, 0) == 0
 
 
 def test_inference_entries_reject_invalid_shapes():

@@ -98,6 +98,16 @@ def test_multi_layer_slab_addressing():
     check_case(case)
 
 
+@pytest.mark.parametrize('pool_pages', [512, 513, 700])
+def test_slab_table_sizes(pool_pages):
+    # one page per slab: up to 512 slabs the decode stages the slab table in
+    # LDS, above it reads the table from global memory; both must agree.
+    case = make_decode_case(13, batch=5, heads=3, dim=64, page_size=16, lengths=[1, 17, 200, 513, 90],
+                            pool_pages=pool_pages, pages_per_slab=1, dtype='float16')
+    assert case.table.max() >= min(pool_pages, 512) - 64  # pages spread over the whole pool
+    check_case(case)
+
+
 def test_missing_pages_give_nan_rows():
     case = make_decode_case(5, batch=4, heads=2, dim=64, page_size=16, lengths=[40, 40, 300, 20],
                             pool_pages=64, pages_per_slab=4, dtype='float32')
@@ -134,17 +144,56 @@ def test_split_entry_equals_oracle(split_tokens, unroll, waves):
     check_case(case, entry='split', split_tokens=split_tokens, unroll=unroll, waves=waves)
 
 
+def run_work_list(dev, lengths, split_tokens, waves=0, compute_units=8, reverse=False):
+    c = dev.case
+    work, items, merges = paged_ops.decode_work_list(lengths, c.heads, split_tokens, compute_units)
+    if reverse:
+        pairs = work[:2 * items].reshape(-1, 2)[::-1]
+        work = np.concatenate([pairs.ravel(), work[2 * items:]]).astype(np.int32)
+    buf = RawDeviceBuffer(4 * max(1, len(work)))
+    buf.upload(work)
+    ws_bytes = paged_ops.decode_workspace_bytes(b=c.batch, h=c.heads, page_size=c.page_size,
+                                                columns=c.columns, split_tokens=split_tokens)
+    ws = RawDeviceBuffer(max(4, ws_bytes))
+    paged_ops.paged_decode_split(dev.out.ptr, dev.q.ptr, dev.k.ptr, dev.v.ptr, dev.slab_table.ptr,
+                                 dev.block_table.ptr, dev.offsets.ptr, **dev.kwargs(),
+                                 split_tokens=split_tokens, waves=waves, work=buf.ptr, work_items=items,
+                                 merge_rows=merges, workspace=ws.ptr if ws_bytes else None,
+                                 workspace_bytes=ws_bytes)
+    runtime().synchronize()
+    return dev.out.to_numpy()
+
+
 @pytest.mark.parametrize('page_size', [8, 16, 32])
 @pytest.mark.parametrize('waves', [4, 8])
-def test_row_order_does_not_change_results(page_size, waves):
-    lengths = [300, 5, 1024, 77, 16, 640, 1]
-    case = make_decode_case(12, batch=7, heads=2, dim=64, page_size=page_size, lengths=lengths,
+def test_work_list_equals_oracle_and_grid(page_size, waves):
+    # rows of 0..3 splits visited longest first: same bits as the full grid
+    lengths = [300, 5, 1024, 77, 16, 640, 1, 2100]
+    case = make_decode_case(12, batch=8, heads=2, dim=64, page_size=page_size, lengths=lengths,
                             pool_pages=1024, pages_per_slab=16, dtype='bfloat16')
-    order = RawDeviceBuffer(4 * 7)
-    order.upload(np.argsort(-np.array(lengths), kind='stable').astype(np.int32))
-    dev, ordered = check_case(case, entry='split', waves=waves, row_order=order.ptr)
-    plain = run_decode(DevicePagedCase(case), entry='split', waves=waves)
-    assert np.array_equal(ordered.view(np.uint16), plain.view(np.uint16))
+    dev = DevicePagedCase(case)
+    listed = run_work_list(dev, lengths, 1024, waves)
+    ref, image = oracle_decode(case)
+    assert_attention_close(listed, ref, 'bfloat16')
+    assert np.array_equal(dev.pool_image().view(np.uint8), image.view(np.uint8)), 'append differs'
+    plain = run_decode(DevicePagedCase(case), entry='split', waves=waves, split_tokens=1024)
+    assert np.array_equal(listed.view(np.uint16), plain.view(np.uint16))
+    again = run_work_list(DevicePagedCase(case), lengths, 1024, waves, reverse=True)
+    assert np.array_equal(listed.view(np.uint16), again.view(np.uint16))
+
+
+def test_work_list_ragged_splits_fp16():
+    # many split rows and a 256-token split: every (row, split) pair listed
+    rng = np.random.default_rng(21)
+    lengths = rng.integers(1, 1500, size=24)
+    lengths[[3, 9]] = [1, 256]
+    case = make_decode_case(14, batch=24, heads=4, dim=64, page_size=16, lengths=lengths,
+                            pool_pages=4096, pages_per_slab=32, dtype='float16')
+    dev = DevicePagedCase(case)
+    out = run_work_list(dev, lengths, 256)
+    ref, image = oracle_decode(case)
+    assert_attention_close(out, ref, 'float16')
+    assert np.array_equal(dev.pool_image().view(np.uint8), image.view(np.uint8)), 'append differs'
 
 
 def test_repeat_calls_are_deterministic():
