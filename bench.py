@@ -126,7 +126,7 @@ def bench_config5(args):
         call = (case.out.ptr, case.q.ptr, case.k.ptr, case.v.ptr, case.slab_table.ptr,
                 case.block_table.ptr, case.offsets.ptr, kw['b'], kw['h'], kw['d'], kw['page_size'],
                 kw['pages_per_slab'], kw['num_slabs'], kw['columns'], kw['layer'], kw['layers'],
-                dtype_code(kw['dtype']), split, args.unroll, args.waves, *work_args, ws.ptr, ws_bytes)
+                dtype_code(kw["dtype"]), split, args.unroll, args.waves, 0, *work_args, ws.ptr, ws_bytes)
         per = time_launches(fn, [call], min(args.steps, 50), min(args.warmup, 5))
         s = 2
         L = case.lengths
@@ -243,7 +243,7 @@ def main():
     calls = [(d.out.ptr, d.q.ptr, d.k.ptr, d.v.ptr, d.slab_table.ptr, d.block_table.ptr, d.offsets.ptr,
               kw['b'], kw['h'], kw['d'], kw['page_size'], kw['pages_per_slab'], kw['num_slabs'],
               kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype']), split,
-              args.unroll, args.waves, *work_args, ws.ptr, ws_bytes) for d in devs]
+              args.unroll, args.waves, 0, *work_args, ws.ptr, ws_bytes) for d in devs]
 
     def step(i):
         status = fn(*calls[i % len(calls)])

@@ -6,9 +6,33 @@
 #ifndef MT_MODEL_H
 #define MT_MODEL_H
 
+#include <stddef.h>
+#include <stdint.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* Weights of one GPT-2 layer for mt_decoder_layers: fp32 LayerNorm
+ * parameters; projection weights row-major [in, out] and biases [out] in the
+ * compute type; w_qkv is the fused [d, 3d] query/key/value projection. */
+typedef struct mt_decoder_layer {
+  const float* ln1_gamma; const float* ln1_beta;
+  const void* w_qkv; const void* b_qkv;
+  const void* w_o; const void* b_o;
+  const float* ln2_gamma; const float* ln2_beta;
+  const void* w_fc; const void* b_fc;
+  const void* w_proj; const void* b_proj;
+} mt_decoder_layer;
+
+/* Paged-cache metadata of one decode batch, as mt_paged_decode_split takes it
+ * (include/mt_paged.h); the layer index is supplied per layer. */
+typedef struct mt_decode_attention {
+  const uint64_t* slabs; const int* table; const int* offsets;
+  int page_size, pages_per_slab, num_slabs, columns, layers, split_tokens;
+  const int* work; int work_items, merge_rows;
+  void* partials; size_t partial_bytes;
+} mt_decode_attention;
 
 /* hipBLASLt handle with a 64 MiB workspace and per-shape plans.
  * Replace reference mt_blas_create / mt_blas_destroy (src/cuda_runtime.cu:22-23). */
@@ -56,9 +80,44 @@ int mt_add_f32(float* out, const float* a, const float* b, long long n);
 /* Element type conversion (reference Tensor.to, mixed_precision.cu casts). */
 int mt_cast(void* out, const void* in, long long n, int in_dtype, int out_dtype);
 
-/* split = 1: out [b, h, n, d] <- in [b, n, h*d]; split = 0: the inverse
+/* split = 1: out [b, h, n, d] <- in [b, n, *] whose rows are in_stride
+ * elements apart (0 = h*d; e.g. 3*h*d for one column block of a fused QKV
+ * output); split = 0: the inverse, contiguous, in_stride 0
  * (reference view/permute/contiguous, minitorch/modules_transformer.py:96-104,179-181). */
-int mt_heads(void* out, const void* in, int b, int n, int h, int d, int split, int dtype);
+int mt_heads(void* out, const void* in, int b, int n, int h, int d, int split, int in_stride,
+             int dtype);
+
+/* out[m, n] = epilogue(a[m, k] @ b[k, n] + bias[n]) in dtype, fp32
+ * accumulation; epilogue 0 = none, 1 = tanh GELU, computed by hipBLASLt's
+ * fused GELU epilogue when fused_gelu != 0, else by the mt_gelu kernel after
+ * the GEMM. No reference counterpart (Linear + GELU of
+ * minitorch/modules_transformer.py:278-282 in one call). */
+int mt_gemm_epilogue(void* handle, void* out, const void* a, const void* b, const void* bias, int m,
+                     int n, int k, int dtype, int epilogue, int fused_gelu);
+
+/* x[r, :] += y[r, :] (fp32 x, y in dtype), then out[r, :] = LayerNorm(x[r, :])
+ * in dtype, as mt_layernorm_typed. Replaces the reference's residual add
+ * followed by the next LayerNorm (minitorch/modules_transformer.py:272-282). */
+int mt_residual_layernorm(void* out, float* x, const void* y, const float* gamma, const float* beta,
+                          int rows, int width, float eps, int dtype);
+
+/* Scratch bytes mt_decoder_layers needs for `rows` tokens of width d. */
+size_t mt_decoder_scratch_bytes(int rows, int d, int dtype);
+
+/* The layer loop of one batched decode step, all launches issued from here on
+ * the null stream: for each layer, LayerNorm (fused with the previous
+ * residual add), fused QKV GEMM, paged decode attention
+ * (mt_paged_decode_split reading q/k/v as column blocks of the QKV output),
+ * out-projection, residual add + LayerNorm, fc GEMM + GELU, proj GEMM; after
+ * the last layer the residual add is fused with the final LayerNorm
+ * (final_gamma/final_beta). x [rows, d] fp32 is the residual stream, updated
+ * in place; h [rows, d] in dtype receives the final LayerNorm output (the
+ * tied head's input). Replaces the reference's per-op layer loop of
+ * DecoderLM.decode_batch (minitorch/modules_transformer.py:373-390,258-284). */
+int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
+                      const float* final_gamma, const float* final_beta, int rows, int d, int heads,
+                      float eps, int dtype, int fused_gelu, void* scratch, size_t scratch_bytes,
+                      const mt_decode_attention* att);
 
 #ifdef __cplusplus
 }

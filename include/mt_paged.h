@@ -61,8 +61,12 @@ int mt_paged_decode_split_tokens(int page_size, int columns, int requested, int*
 
 /* mt_paged_decode_batch with a caller-owned workspace and tuning knobs:
  * split_tokens (a multiple of 64, at most 2048; 0 = automatic), unroll (1, 2
- * or 4 row-blocks per register stage; 0 = default), waves per workgroup (4 or
- * 8; 0 = default), and an optional work list built by the caller from the
+ * or 4 row-blocks per register stage, capped by the row size; 0 = automatic:
+ * 4 when the whole grid is resident at its occupancy, else 2), waves per workgroup (4 or
+ * 8; 0 = default), qkv_stride (elements between consecutive rows of q, k and
+ * v, so that they can be column blocks of one fused [b, 3*h*d] projection
+ * output; 0 = h*d, contiguous; out is always contiguous), and an optional
+ * work list built by the caller from the
  * context lengths it knows on the host (device int32): work_items pairs
  * (row, split), in the order they should be scheduled (e.g. longest first),
  * followed by merge_rows row indices, the rows with more than one split. A
@@ -77,8 +81,9 @@ int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v
                           const uint64_t* slabs, const int* table, const int* offsets, int b,
                           int h, int d, int page_size, int pages_per_slab, int num_slabs,
                           int columns, int layer, int layers, int dtype, int split_tokens,
-                          int unroll, int waves, const int* work, int work_items,
-                          int merge_rows, void* workspace, size_t workspace_bytes);
+                          int unroll, int waves, int qkv_stride, const int* work,
+                          int work_items, int merge_rows, void* workspace,
+                          size_t workspace_bytes);
 
 #ifdef __cplusplus
 }

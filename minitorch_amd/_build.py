@@ -16,14 +16,17 @@ SRC = ROOT / 'csrc'
 OUT = ROOT / 'cuda_kernels'
 ARCH = 'gfx950'
 
-# name -> extra link arguments
+# name -> extra link arguments. model_kernels links the paged decode library
+# (its decoder loop launches mt_paged_decode_split), found next to it at run
+# time through an $ORIGIN rpath; that library is therefore built first.
 LIBRARIES = {
     'paged_attention_kernel': [],
     'inference_kernels': [],
     'cuda_runtime': [],
     'sched_kernels': [],
-    'model_kernels': ['-lhipblaslt'],
+    'model_kernels': ['-lhipblaslt', f'-L{OUT}', '-l:paged_attention_kernel.so', '-Wl,-rpath,$ORIGIN'],
 }
+FIRST = ('paged_attention_kernel',)
 
 HIPCC_FLAGS = [
     '-O3', '-std=c++17', '-fPIC', '-shared', f'--offload-arch={ARCH}',
@@ -62,8 +65,9 @@ def build_one(name):
 def build(names=None, jobs=4):
     OUT.mkdir(exist_ok=True)
     names = list(LIBRARIES) if names is None else list(names)
+    results = [build_one(n) for n in FIRST if n in names]
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        results = list(pool.map(build_one, names))
+        results += list(pool.map(build_one, [n for n in names if n not in FIRST]))
     return {name: path for name, path in results if path is not None}
 
 

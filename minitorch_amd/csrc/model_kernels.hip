@@ -9,6 +9,8 @@
 // resident in the compute type (no per-call casts), the projection bias is a
 // hipBLASLt epilogue, and each elementwise step is one kernel.
 #include "mt_device.h"
+#include "../../include/mt_paged.h"
+#include "../../include/mt_model.h"
 #include <hipblaslt/hipblaslt.h>
 #include <climits>
 #include <cmath>
@@ -32,37 +34,89 @@ struct Plan {
 };
 
 // A hipBLASLt handle, a 64 MiB workspace and the plans (descriptors plus the
-// heuristic's first algorithm) per GEMM shape, created on first use.
+// chosen algorithm) per GEMM shape, created on first use.
 struct Blas {
   hipblasLtHandle_t handle = nullptr;
   void* workspace = nullptr;
   size_t workspace_bytes = size_t(64) << 20;
   std::mutex mutex;
-  std::map<std::tuple<int, int, int, int, int, int, int>, Plan> plans;
+  std::map<std::tuple<int, int, int, int, int, int, int, int>, Plan> plans;
 };
 
 int blas_status(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS ? 0 : 1000 + int(s); }
 
-// Row-major C[m, n] = A[m, k] @ op(B) (+ bias[n]) where op(B) = B [k, n] or,
-// with transb, B^T for B [n, k]. Column-major view: C^T = op(B)^T A^T, i.e. a
-// column-major GEMM with rows n, columns m; the bias is per row of C^T.
+enum Epilogue : int { kEpiNone = 0, kEpiGelu = 1 };
+
+// Candidates the heuristic returns per shape; the fastest on the first call's
+// own operands is kept (one timed pass each, on the null stream).
+constexpr int kCandidates = 8;
+
+int pick_fastest(Blas* blas, Plan& p, const hipblasLtMatmulHeuristicResult_t* heur, int count,
+                 void* out, const void* a, const void* b) {
+  if (count == 1) { p.algo = heur[0].algo; return 0; }
+  const float alpha = 1.f, beta = 0.f;
+  hipEvent_t start, stop;
+  if (hipEventCreate(&start) != hipSuccess) return hipErrorOutOfMemory;
+  if (hipEventCreate(&stop) != hipSuccess) { hipEventDestroy(start); return hipErrorOutOfMemory; }
+  float best = INFINITY;
+  int chosen = -1;
+  for (int i = 0; i < count; ++i) {
+    auto run = [&]() {
+      return hipblasLtMatmul(blas->handle, p.desc, &alpha, b, p.la, a, p.lb, &beta, out, p.lc, out,
+                             p.lc, &heur[i].algo, blas->workspace, blas->workspace_bytes, nullptr);
+    };
+    if (run() != HIPBLAS_STATUS_SUCCESS) continue;  // warm-up; unusable candidates drop out
+    hipEventRecord(start, nullptr);
+    bool ok = true;
+    for (int r = 0; r < 3 && ok; ++r) ok = run() == HIPBLAS_STATUS_SUCCESS;
+    hipEventRecord(stop, nullptr);
+    float ms = 0.f;
+    if (!ok || hipEventSynchronize(stop) != hipSuccess || hipEventElapsedTime(&ms, start, stop) != hipSuccess)
+      continue;
+    if (ms < best) { best = ms; chosen = i; }
+  }
+  hipEventDestroy(start);
+  hipEventDestroy(stop);
+  p.algo = heur[chosen >= 0 ? chosen : 0].algo;
+  return 0;
+}
+
+// Row-major C[m, n] = A[m, k] @ op(B) (+ bias[n]) (then GELU) where op(B) =
+// B [k, n] or, with transb, B^T for B [n, k]. Column-major view: C^T =
+// op(B)^T A^T, i.e. a column-major GEMM with rows n, columns m; the bias is
+// per row of C^T.
 int gemm(Blas* blas, void* out, const void* a, const void* b, const void* bias, int m, int n,
-         int k, int transb, int dtype, int out_dtype) {
+         int k, int transb, int dtype, int out_dtype, int epilogue = kEpiNone) {
   std::lock_guard<std::mutex> lock(blas->mutex);
-  auto key = std::make_tuple(m, n, k, transb, dtype, out_dtype, bias ? 1 : 0);
+  auto key = std::make_tuple(m, n, k, transb, dtype, out_dtype, bias ? 1 : 0, epilogue);
   Plan& p = blas->plans[key];
   if (!p.ok) {
+    // On any failure below the partial plan is released so a later call can retry.
+    struct Guard {
+      Blas* blas; Plan* p; decltype(key) k; bool keep = false;
+      ~Guard() {
+        if (keep) return;
+        if (p->la) hipblasLtMatrixLayoutDestroy(p->la);
+        if (p->lb) hipblasLtMatrixLayoutDestroy(p->lb);
+        if (p->lc) hipblasLtMatrixLayoutDestroy(p->lc);
+        if (p->desc) hipblasLtMatmulDescDestroy(p->desc);
+        blas->plans.erase(k);
+      }
+    } guard{blas, &p, key};
     hipblasStatus_t s;
     const hipDataType in = hip_type(dtype), outt = hip_type(out_dtype);
     if ((s = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F))) return blas_status(s);
     hipblasOperation_t opa = transb ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = HIPBLAS_OP_N;
     hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa));
     hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb));
+    hipblasLtEpilogue_t epi = epilogue == kEpiGelu
+                                  ? (bias ? HIPBLASLT_EPILOGUE_GELU_BIAS : HIPBLASLT_EPILOGUE_GELU)
+                                  : (bias ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT);
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi));
     if (bias) {
-      hipblasLtEpilogue_t epi = HIPBLASLT_EPILOGUE_BIAS;
       hipDataType bt = outt;
-      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi));
       hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt));
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
     }
     // A' = B (col-major [n, k], or [k, n] transposed), B' = A (col-major [k, m]).
     if ((s = transb ? hipblasLtMatrixLayoutCreate(&p.la, in, k, n, k)
@@ -74,15 +128,17 @@ int gemm(Blas* blas, void* out, const void* a, const void* b, const void* bias, 
     if ((s = hipblasLtMatmulPreferenceCreate(&pref))) return blas_status(s);
     uint64_t ws = blas->workspace_bytes;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
-    hipblasLtMatmulHeuristicResult_t heur;
+    hipblasLtMatmulHeuristicResult_t heur[kCandidates];
     int returned = 0;
-    s = hipblasLtMatmulAlgoGetHeuristic(blas->handle, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, &heur,
-                                        &returned);
+    s = hipblasLtMatmulAlgoGetHeuristic(blas->handle, p.desc, p.la, p.lb, p.lc, p.lc, pref, kCandidates,
+                                        heur, &returned);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (s) return blas_status(s);
     if (returned < 1) return blas_status(HIPBLAS_STATUS_NOT_SUPPORTED);
-    p.algo = heur.algo;
+    const int e = pick_fastest(blas, p, heur, returned, out, a, b);
+    if (e) return e;
     p.ok = true;
+    guard.keep = true;
   }
   if (bias)
     hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
@@ -130,6 +186,43 @@ __global__ __launch_bounds__(256) void layernorm_kernel(void* out, const float* 
     o[i] = from_f32<DT>(gamma[i] * ((row[i] - mean) * inv) + beta[i]);
 }
 
+// Residual add fused with the next LayerNorm: x[r, :] += y[r, :] (y in DT,
+// the fp32 residual stream updated in place), then out = LayerNorm(x[r, :])
+// exactly as layernorm_kernel computes it.
+template <int DT>
+__global__ __launch_bounds__(256) void residual_layernorm_kernel(void* out, float* x, const void* y,
+                                                                 const float* gamma, const float* beta,
+                                                                 int width, float eps) {
+  using T = typename Elem<DT>::T;
+  __shared__ float s_sum[8], s_sq[8];
+  float* row = x + int64_t(blockIdx.x) * width;
+  const T* yr = static_cast<const T*>(y) + int64_t(blockIdx.x) * width;
+  float sum = 0.f, sq = 0.f;
+  for (int i = threadIdx.x; i < width; i += blockDim.x) {
+    const float v = row[i] + to_f32<DT>(yr[i]);
+    row[i] = v;
+    sum += v;
+    sq += v * v;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    sum += __shfl_xor(sum, off);
+    sq += __shfl_xor(sq, off);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { s_sum[wave] = sum; s_sq[wave] = sq; }
+  __syncthreads();
+  float tsum = 0.f, tsq = 0.f;
+  for (int w = 0; w < int(blockDim.x >> 6); ++w) { tsum += s_sum[w]; tsq += s_sq[w]; }
+  const float mean = tsum / width;
+  const float var = fmaxf(tsq / width - mean * mean, 0.f) + eps;
+  const float inv = 1.f / sqrtf(var);
+  T* o = static_cast<T*>(out) + int64_t(blockIdx.x) * width;
+  // each thread reads back only the elements it wrote above
+  for (int i = threadIdx.x; i < width; i += blockDim.x)
+    o[i] = from_f32<DT>(gamma[i] * ((row[i] - mean) * inv) + beta[i]);
+}
+
 // tanh-form GELU in place (reference minitorch/nn.py:222-226):
 // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), computed in fp32.
 template <int DT>
@@ -165,9 +258,11 @@ __global__ __launch_bounds__(256) void cast_kernel(void* out, const void* in, in
     dst[i] = from_f32<DO>(to_f32<DI>(src[i]));
 }
 
-// [b, n, h*d] <-> [b, h, n, d] (split = 1: to heads; 0: back).
+// [b, n, h*d] <-> [b, h, n, d] (split = 1: to heads, the [b, n, *] rows
+// `stride` elements apart; 0: back, contiguous).
 template <class T>
-__global__ __launch_bounds__(256) void heads_kernel(T* out, const T* in, int b, int n, int h, int d, int split) {
+__global__ __launch_bounds__(256) void heads_kernel(T* out, const T* in, int b, int n, int h, int d, int split,
+                                                    int64_t stride) {
   const int64_t total = int64_t(b) * n * h * d;
   for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
     // i indexes the [b, h, n, d] tensor
@@ -177,13 +272,47 @@ __global__ __launch_bounds__(256) void heads_kernel(T* out, const T* in, int b, 
     const int64_t r2 = r / n;
     const int hh = int(r2 % h);
     const int bb = int(r2 / h);
-    const int64_t j = ((int64_t(bb) * n + t) * h + hh) * d + col;  // [b, n, h, d]
-    if (split) out[i] = in[j];
-    else out[j] = in[i];
+    if (split) out[i] = in[(int64_t(bb) * n + t) * stride + int64_t(hh) * d + col];
+    else out[((int64_t(bb) * n + t) * h + hh) * d + col] = in[i];
   }
 }
 
 bool dtype_ok(int d) { return d >= 0 && d <= 2; }
+
+hipError_t layernorm(void* out, const float* x, const float* gamma, const float* beta, int rows,
+                     int width, float eps, int dtype) {
+  if (dtype == kF32) layernorm_kernel<kF32><<<rows, 256>>>(out, x, gamma, beta, width, eps);
+  else if (dtype == kF16) layernorm_kernel<kF16><<<rows, 256>>>(out, x, gamma, beta, width, eps);
+  else layernorm_kernel<kBF16><<<rows, 256>>>(out, x, gamma, beta, width, eps);
+  return hipGetLastError();
+}
+
+hipError_t residual_layernorm(void* out, float* x, const void* y, const float* gamma,
+                              const float* beta, int rows, int width, float eps, int dtype) {
+  if (dtype == kF32)
+    residual_layernorm_kernel<kF32><<<rows, 256>>>(out, x, y, gamma, beta, width, eps);
+  else if (dtype == kF16)
+    residual_layernorm_kernel<kF16><<<rows, 256>>>(out, x, y, gamma, beta, width, eps);
+  else
+    residual_layernorm_kernel<kBF16><<<rows, 256>>>(out, x, y, gamma, beta, width, eps);
+  return hipGetLastError();
+}
+
+hipError_t gelu(void* x, int64_t n, int dtype) {
+  if (dtype == kF32) gelu_kernel<kF32><<<blocks_for(n), 256>>>(x, n);
+  else if (dtype == kF16) gelu_kernel<kF16><<<blocks_for(n), 256>>>(x, n);
+  else gelu_kernel<kBF16><<<blocks_for(n), 256>>>(x, n);
+  return hipGetLastError();
+}
+
+// GEMM + bias + tanh GELU: hipBLASLt's GELU epilogue when `fused`, else the
+// bias GEMM followed by gelu_kernel.
+int gemm_gelu(Blas* blas, void* out, const void* a, const void* b, const void* bias, int m, int n,
+              int k, int dtype, bool fused) {
+  if (fused) return gemm(blas, out, a, b, bias, m, n, k, 0, dtype, dtype, kEpiGelu);
+  int e = gemm(blas, out, a, b, bias, m, n, k, 0, dtype, dtype);
+  return e ? e : gelu(out, int64_t(m) * n, dtype);
+}
 
 }  // namespace
 
@@ -294,15 +423,86 @@ int mt_cast(void* out, const void* in, long long n, int in_dtype, int out_dtype)
   return hipGetLastError();
 }
 
-// split = 1: out [b, h, n, d] <- in [b, n, h*d]; split = 0: the inverse.
-int mt_heads(void* out, const void* in, int b, int n, int h, int d, int split, int dtype) {
-  if (!out || !in || b < 1 || n < 1 || h < 1 || d < 1 || !dtype_ok(dtype)) return hipErrorInvalidValue;
+// split = 1: out [b, h, n, d] <- in [b, n, *] (rows in_stride elements
+// apart, 0 = h*d); split = 0: the inverse (contiguous).
+int mt_heads(void* out, const void* in, int b, int n, int h, int d, int split, int in_stride, int dtype) {
+  if (!out || !in || b < 1 || n < 1 || h < 1 || d < 1 || !dtype_ok(dtype) || in_stride < 0 ||
+      (in_stride != 0 && int64_t(in_stride) < int64_t(h) * d) || (split == 0 && in_stride != 0))
+    return hipErrorInvalidValue;
   const int64_t total = int64_t(b) * n * h * d;
+  const int64_t stride = in_stride ? in_stride : int64_t(h) * d;
   if (dtype == kF32)
-    heads_kernel<float><<<blocks_for(total), 256>>>(static_cast<float*>(out), static_cast<const float*>(in), b, n, h, d, split);
+    heads_kernel<float><<<blocks_for(total), 256>>>(static_cast<float*>(out), static_cast<const float*>(in), b, n, h, d, split, stride);
   else
-    heads_kernel<uint16_t><<<blocks_for(total), 256>>>(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(in), b, n, h, d, split);
+    heads_kernel<uint16_t><<<blocks_for(total), 256>>>(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(in), b, n, h, d, split, stride);
   return hipGetLastError();
+}
+
+// out[m, n] = epilogue(a[m, k] @ b[k, n] + bias[n]); epilogue 0 = none,
+// 1 = tanh GELU (hipBLASLt's fused GELU when fused_gelu, else a separate
+// pass of the kernel behind mt_gelu).
+int mt_gemm_epilogue(void* handle, void* out, const void* a, const void* b, const void* bias, int m,
+                     int n, int k, int dtype, int epilogue, int fused_gelu) {
+  if (!dtype_ok(dtype) || !handle || !out || !a || !b || m < 1 || n < 1 || k < 1 ||
+      (epilogue != 0 && epilogue != 1))
+    return hipErrorInvalidValue;
+  Blas* blas = static_cast<Blas*>(handle);
+  if (epilogue == 0) return gemm(blas, out, a, b, bias, m, n, k, 0, dtype, dtype);
+  return gemm_gelu(blas, out, a, b, bias, m, n, k, dtype, fused_gelu != 0);
+}
+
+// x[r, :] += y[r, :]; out[r, :] = LayerNorm(x[r, :]) in dtype.
+int mt_residual_layernorm(void* out, float* x, const void* y, const float* gamma, const float* beta,
+                          int rows, int width, float eps, int dtype) {
+  if (!out || !x || !y || !gamma || !beta || rows < 1 || width < 1 || !dtype_ok(dtype))
+    return hipErrorInvalidValue;
+  return residual_layernorm(out, x, y, gamma, beta, rows, width, eps, dtype);
+}
+
+size_t mt_decoder_scratch_bytes(int rows, int d, int dtype) {
+  if (rows < 1 || d < 1 || !dtype_ok(dtype)) return 0;
+  const size_t e = dtype == kF32 ? 4 : 2;
+  // qkv [rows, 3d] | attention [rows, d] | projection [rows, d] | mlp [rows, 4d], each 256-aligned
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+  return al(size_t(rows) * 3 * d * e) + 2 * al(size_t(rows) * d * e) + al(size_t(rows) * 4 * d * e);
+}
+
+int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
+                      const float* final_gamma, const float* final_beta, int rows, int d, int heads,
+                      float eps, int dtype, int fused_gelu, void* scratch, size_t scratch_bytes,
+                      const mt_decode_attention* att) {
+  if (!handle || !layers || n_layer < 1 || !x || !h || !final_gamma || !final_beta || rows < 1 ||
+      d < 1 || heads < 1 || d % heads || !dtype_ok(dtype) || !scratch || !att ||
+      scratch_bytes < mt_decoder_scratch_bytes(rows, d, dtype) || int64_t(rows) * 4 * d > INT32_MAX)
+    return hipErrorInvalidValue;
+  Blas* blas = static_cast<Blas*>(handle);
+  const size_t e = dtype == kF32 ? 4 : 2;
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+  char* base = static_cast<char*>(scratch);
+  char* qkv = base;
+  char* attn = qkv + al(size_t(rows) * 3 * d * e);
+  char* proj = attn + al(size_t(rows) * d * e);
+  char* mlp = proj + al(size_t(rows) * d * e);
+  const int hd = d / heads;
+  int st = layernorm(h, x, layers[0].ln1_gamma, layers[0].ln1_beta, rows, d, eps, dtype);
+  for (int i = 0; i < n_layer && !st; ++i) {
+    const mt_decoder_layer& L = layers[i];
+    if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 0, dtype, dtype))) break;
+    if ((st = mt_paged_decode_split(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, att->slabs,
+                                    att->table, att->offsets, rows, heads, hd, att->page_size,
+                                    att->pages_per_slab, att->num_slabs, att->columns, i, att->layers,
+                                    dtype, att->split_tokens, 0, 0, 3 * d, att->work, att->work_items,
+                                    att->merge_rows, att->partials, att->partial_bytes)))
+      break;
+    if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 0, dtype, dtype))) break;
+    if ((st = residual_layernorm(h, x, proj, L.ln2_gamma, L.ln2_beta, rows, d, eps, dtype))) break;
+    if ((st = gemm_gelu(blas, mlp, h, L.w_fc, L.b_fc, rows, 4 * d, d, dtype, fused_gelu != 0))) break;
+    if ((st = gemm(blas, proj, mlp, L.w_proj, L.b_proj, rows, d, 4 * d, 0, dtype, dtype))) break;
+    const bool last = i + 1 == n_layer;
+    st = residual_layernorm(h, x, proj, last ? final_gamma : layers[i + 1].ln1_gamma,
+                            last ? final_beta : layers[i + 1].ln1_beta, rows, d, eps, dtype);
+  }
+  return st;
 }
 
 }  // extern "C"

@@ -55,7 +55,6 @@ constexpr float kLog2e = 1.4426950408889634f;
 #define MT_STAGES 1
 #endif
 constexpr int kStages = MT_STAGES;  // register stages of the K/V stream
-constexpr int kDefaultUnroll = 4;    // row-blocks per register stage (capped per shape)
 constexpr int kDefaultWaves = 4;     // waves per decode workgroup
 #ifndef MT_DECODE_GROUP
 #define MT_DECODE_GROUP 4
@@ -421,6 +420,7 @@ struct DecodeArgs {
   const int* work;
   int work_items;
   int merge_rows;
+  int64_t qkv_stride;  // elements between the rows of q, k and v (h * d when contiguous)
 };
 
 // Stream one wave's share of a split: row-blocks j = wave + waves * i
@@ -569,9 +569,10 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
     // each of this wave's page slots.
     const int offset = a.offsets[b];
     Query<DT, D, VEC, G> qv;
-    qv.load(qp + bh * dim, col0, dim, a.qscale);
+    const int64_t qrow = int64_t(b) * a.qkv_stride + int64_t(head) * dim;  // q, k, v row
+    qv.load(qp + qrow, col0, dim, a.qscale);
     T new_k{}, new_v{};
-    if (tid < dim) { new_k = kin[bh * dim + tid]; new_v = vin[bh * dim + tid]; }
+    if (tid < dim) { new_k = kin[qrow + tid]; new_v = vin[qrow + tid]; }
     const int* table_row = a.table + int64_t(b) * g.columns;
     const int t0i = split * a.split_tokens;
     const int slot_i = lane >> sub_shift;
@@ -646,8 +647,8 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
           }
         } else {
           for (int i = 0; i < DL && col0 + i < dim; ++i) {
-            kp[i] = kin[bh * dim + col0 + i];
-            vp[i] = vin[bh * dim + col0 + i];
+            kp[i] = kin[qrow + col0 + i];
+            vp[i] = vin[qrow + col0 + i];
           }
         }
       }
@@ -717,21 +718,47 @@ __global__ __launch_bounds__(128) void merge_kernel(DecodeArgs a) {
     const int b = a.work ? a.work[2 * int64_t(a.work_items) + m] : int(m);
     if (b < 0 || b >= a.batch) continue;
     const int64_t bh = int64_t(b) * g.heads + head;
+    const float* base = a.partials + bh * a.nsplit_max * PSTRIDE;
+    const int t = threadIdx.x;
+    // Partials of up to kChunk splits are loaded per pass; the first pass is
+    // issued together with the context-length read that says how many exist.
+    constexpr int kChunk = 8;
+    float pm[kChunk], pl[kChunk], pa[kChunk];
+    auto load_chunk = [&](int s0) {
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) {
+        const int sj = s0 + j < a.nsplit_max ? s0 + j : a.nsplit_max - 1;
+        pm[j] = base[sj * PSTRIDE];
+        pl[j] = base[sj * PSTRIDE + 1];
+        pa[j] = t < dim ? base[sj * PSTRIDE + 2 + t] : 0.f;
+      }
+    };
+    load_chunk(0);
     const int offset = a.offsets[b];
     const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
     if (L > cap) continue;
     const int nsplit = L == 0 ? 1 : int((L + a.split_tokens - 1) / a.split_tokens);
     if (nsplit == 1) continue;
-    const float* base = a.partials + bh * a.nsplit_max * PSTRIDE;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, base[s * PSTRIDE]);
-    float lsum = 0.f, asum = 0.f;
-    const int t = threadIdx.x;
-    for (int s = 0; s < nsplit; ++s) {
-      const float ms = base[s * PSTRIDE];
-      const float sc = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
-      lsum += base[s * PSTRIDE + 1] * sc;
-      if (t < dim) asum += base[s * PSTRIDE + 2 + t] * sc;
+    // Online log-sum-exp merge over the chunks.
+    float M = -INFINITY, lsum = 0.f, asum = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += kChunk) {
+      if (s0 > 0) load_chunk(s0);
+      float cm = M;
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j)
+        if (s0 + j < nsplit) cm = fmaxf(cm, pm[j]);
+      const float rescale = (M == -INFINITY) ? 0.f : fast_exp2(M - cm);
+      lsum *= rescale;
+      asum *= rescale;
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) {
+        if (s0 + j < nsplit) {
+          const float sc = (pm[j] == -INFINITY) ? 0.f : fast_exp2(pm[j] - cm);
+          lsum = fmaf(pl[j], sc, lsum);
+          asum = fmaf(pa[j], sc, asum);
+        }
+      }
+      M = cm;
     }
     if (t < dim) out[bh * dim + t] = from_f32<DT>(finalize(asum, lsum));
   }
@@ -890,19 +917,49 @@ size_t workspace_bytes_for(int64_t bh, int nsplit_max) {
   return size_t(bh) * nsplit_max * (128 + 2) * sizeof(float);
 }
 
+// Compute units of the current device (cached per device).
+int device_compute_units() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <int DT, int D, bool VEC, int WAVES, int G>
 hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
   // Row bytes per lane bound the useful unroll: register stages beyond it spill.
   constexpr int kMaxUnroll = !VEC ? 1 : (D * elem_bytes<DT>() >= 256 ? 2 : 4);
   constexpr int NT = WAVES * kWave;
+  if (unroll == 0) {
+    // Automatic: the deepest unroll when the whole grid is resident at its
+    // occupancy (more loads in flight per wave), else unroll 2, whose lower
+    // register count keeps more workgroups per compute unit.
+    unroll = 2;
+    if constexpr (kMaxUnroll >= 4) {
+      static int per_cu = -1;
+      if (per_cu < 0) {
+        int n = 0;
+        per_cu = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                     &n, decode_kernel<DT, D, VEC, 4, kStages, WAVES, G>, NT, 0) == hipSuccess ? n : 0;
+      }
+      if (blocks <= int64_t(per_cu) * device_compute_units()) unroll = 4;
+    }
+  }
+  // Requests between the supported values round down (3 -> 2, 5+ -> 4).
+  unroll = unroll >= 4 ? 4 : unroll >= 2 ? 2 : 1;
   if (unroll > kMaxUnroll) unroll = kMaxUnroll;
   if constexpr (kMaxUnroll >= 4) {
-    if (unroll >= 4) decode_kernel<DT, D, VEC, 4, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
+    if (unroll == 4) decode_kernel<DT, D, VEC, 4, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
   }
   if constexpr (kMaxUnroll >= 2) {
     if (unroll == 2) decode_kernel<DT, D, VEC, 2, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
   }
-  if (unroll <= 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
+  if (unroll == 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
   hipError_t e = hipGetLastError();
   const int64_t merge_rows = a.work ? a.merge_rows : a.batch;
   if (e != hipSuccess || a.nsplit_max == 1 || merge_rows == 0) return e;
@@ -926,8 +983,8 @@ hipError_t launch_decode_dt(const DecodeArgs& a, int64_t blocks, bool vec, int d
 int decode_common(void* out, const void* q, const void* k, const void* v, const uint64_t* slabs,
                   const int* table, const int* offsets, int b, int h, int d, int page_size,
                   int pps, int num_slabs, int columns, int layer, int layers, int dtype,
-                  int split_tokens, int unroll, int waves, const int* work, int work_items,
-                  int merge_rows, void* workspace, size_t workspace_bytes) {
+                  int split_tokens, int unroll, int waves, int qkv_stride, const int* work,
+                  int work_items, int merge_rows, void* workspace, size_t workspace_bytes) {
   const int64_t cap = int64_t(columns) * page_size;
   // A work list is built for one split length, so it must be given.
   if (work && split_tokens <= 0) return hipErrorInvalidValue;
@@ -951,10 +1008,12 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   a.items = work ? int64_t(work_items) * h : bh * nsplit_max;
   a.g = make_geometry(h, d, page_size, pps, num_slabs, columns, layer);
   a.partials = static_cast<float*>(workspace);
+  a.qkv_stride = qkv_stride ? qkv_stride : int64_t(h) * d;
   a.work = work;
   a.work_items = work ? work_items : 0;
   a.merge_rows = work ? merge_rows : 0;
-  const bool vec = (d == 64 || d == 128) && aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v);
+  const bool vec = (d == 64 || d == 128) && aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v) &&
+                   (a.qkv_stride * (dtype == kF32 ? 4 : 2)) % 16 == 0;
   if (dtype == kF32) return launch_decode_dt<kF32>(a, a.items, vec, d, unroll, waves);
   if (dtype == kF16) return launch_decode_dt<kF16>(a, a.items, vec, d, unroll, waves);
   if (dtype == kBF16) return launch_decode_dt<kBF16>(a, a.items, vec, d, unroll, waves);
@@ -1065,7 +1124,7 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
     if (e != hipSuccess) return e;
   }
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
-                       num_slabs, columns, layer, layers, dtype, S, kDefaultUnroll, kDefaultWaves,
+                       num_slabs, columns, layer, layers, dtype, S, 0, kDefaultWaves, 0,
                        nullptr, 0, 0, ws, ws_bytes);
 }
 
@@ -1096,17 +1155,19 @@ int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v
                           const uint64_t* slabs, const int* table, const int* offsets, int b,
                           int h, int d, int page_size, int pages_per_slab, int num_slabs,
                           int columns, int layer, int layers, int dtype, int split_tokens,
-                          int unroll, int waves, const int* work, int work_items,
-                          int merge_rows, void* workspace, size_t workspace_bytes) {
+                          int unroll, int waves, int qkv_stride, const int* work,
+                          int work_items, int merge_rows, void* workspace,
+                          size_t workspace_bytes) {
   if (!out || !q || !k || !v || !slabs || !table || !offsets ||
       !paged_shape(b, h, 1, 1, d, page_size, pages_per_slab, num_slabs, columns, layer, layers, 0) ||
       int64_t(columns) * page_size > INT32_MAX || split_tokens < 0 || unroll < 0 ||
-      (waves != 0 && waves != 4 && waves != 8))
+      (waves != 0 && waves != 4 && waves != 8) ||
+      (qkv_stride != 0 && int64_t(qkv_stride) < int64_t(h) * d) || qkv_stride < 0)
     return hipErrorInvalidValue;
   if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, split_tokens,
-                       unroll == 0 ? kDefaultUnroll : unroll, waves == 0 ? kDefaultWaves : waves,
+                       unroll, waves == 0 ? kDefaultWaves : waves, qkv_stride,
                        work, work_items, merge_rows, workspace, workspace_bytes);
 }
 

@@ -11,9 +11,12 @@ LayerNorm gains, as HF GPT-2 initializes them) or a host state dict.
 
 MI355X-first choices: projection weights are kept resident on the device in
 the compute type (the reference re-casts fp32 masters on every matmul,
-minitorch/tensor.py:226-231); every projection is one hipBLASLt call with the
-bias as its epilogue; the decode step's Q/K/V are [B, H, 1, D] views of the
-projection outputs (no permute copies).
+minitorch/tensor.py:226-231); Q, K and V come from one fused [d, 3d]
+projection (GPT-2's c_attn) whose output the paged decode reads as three
+column blocks (no split copies); every projection is one hipBLASLt call with
+the bias (and for the MLP's fc, the GELU) as its epilogue; the batched decode
+step runs its whole layer loop in one native call (mt_decoder_layers), with
+the residual adds fused into the following LayerNorms.
 """
 import ctypes as ct
 import numpy as np
@@ -43,6 +46,11 @@ class _Layer:
         self.attention = _Attention(n_head, head_dim)
 
 
+# Whether the fc projection's tanh GELU runs as hipBLASLt's GELU epilogue
+# (else as a separate pass of mt_gelu after the GEMM).
+FUSED_GELU = True
+
+
 class _Blas:
     def __init__(self):
         self.handle = P()
@@ -51,6 +59,25 @@ class _Blas:
     def gemm(self, out, a, b, bias, m, n, k, transb, dtype):
         call(model_library(), 'mt_gemm_ex', [P] * 5 + [I] * 6, self.handle, out, a, b, bias, m, n, k,
              transb, dtype_code(dtype), dtype_code(dtype))
+
+    def gemm_gelu(self, out, a, b, bias, m, n, k, dtype):
+        call(model_library(), 'mt_gemm_epilogue', [P] * 5 + [I] * 6, self.handle, out, a, b, bias, m, n, k,
+             dtype_code(dtype), 1, 1 if FUSED_GELU else 0)
+
+
+class DecoderLayerStruct(ct.Structure):
+    """``mt_decoder_layer`` (include/mt_model.h)."""
+    _fields_ = [(name, P) for name in ('ln1_gamma', 'ln1_beta', 'w_qkv', 'b_qkv', 'w_o', 'b_o',
+                                       'ln2_gamma', 'ln2_beta', 'w_fc', 'b_fc', 'w_proj', 'b_proj')]
+
+
+class DecodeAttentionStruct(ct.Structure):
+    """``mt_decode_attention`` (include/mt_model.h)."""
+    _fields_ = [('slabs', P), ('table', P), ('offsets', P),
+                ('page_size', I), ('pages_per_slab', I), ('num_slabs', I), ('columns', I),
+                ('layers', I), ('split_tokens', I),
+                ('work', P), ('work_items', I), ('merge_rows', I),
+                ('partials', P), ('partial_bytes', ct.c_size_t)]
 
 
 def init_gpt2_state(*, n_vocab, n_embd, n_layer, n_positions, seed=0, std=0.02):
@@ -98,18 +125,19 @@ class _DeviceWeights:
         self.layers = []
         for i in range(n_layer):
             p = f'transformer.h.{i}.'
-            w = state[p + 'attn.c_attn.weight']
-            b = state[p + 'attn.c_attn.bias']
             layer = dict(
                 ln_1=(put(p + 'ln_1.weight', 'float32'), put(p + 'ln_1.bias', 'float32')),
                 ln_2=(put(p + 'ln_2.weight', 'float32'), put(p + 'ln_2.bias', 'float32')),
-                q=(put(None, array=w[:, :d]), put(None, array=b[:d])),
-                k=(put(None, array=w[:, d:2 * d]), put(None, array=b[d:2 * d])),
-                v=(put(None, array=w[:, 2 * d:]), put(None, array=b[2 * d:])),
+                qkv=(put(p + 'attn.c_attn.weight'), put(p + 'attn.c_attn.bias')),   # [d, 3d], [3d]
                 o=(put(p + 'attn.c_proj.weight'), put(p + 'attn.c_proj.bias')),
                 fc=(put(p + 'mlp.c_fc.weight'), put(p + 'mlp.c_fc.bias')),
                 proj=(put(p + 'mlp.c_proj.weight'), put(p + 'mlp.c_proj.bias')))
             self.layers.append(layer)
+        self.layer_array = (DecoderLayerStruct * n_layer)(*[
+            DecoderLayerStruct(L['ln_1'][0].ptr, L['ln_1'][1].ptr, L['qkv'][0].ptr, L['qkv'][1].ptr,
+                               L['o'][0].ptr, L['o'][1].ptr, L['ln_2'][0].ptr, L['ln_2'][1].ptr,
+                               L['fc'][0].ptr, L['fc'][1].ptr, L['proj'][0].ptr, L['proj'][1].ptr)
+            for L in self.layers])
 
 
 class DecoderLM:
@@ -194,18 +222,24 @@ class DecoderLM:
     def _residual(self, x, y):
         call(model_library(), 'mt_residual_add', [P, P, LL, I], x.ptr, y.ptr, x.size, dtype_code(y.dtype))
 
-    def _heads(self, t, b, n, split):
+    def _heads(self, t, b, n, split, column=0):
+        """split: [b, n, *] (columns [column*d_model, (column+1)*d_model) of each
+        row of t) -> [b, h, n, hd]; else [b, h, n, hd] -> [b, n, h*hd]."""
         h, d = self.n_head, self.head_dim
         out = DeviceTensor((b, h, n, d) if split else (b, n, h * d), t.dtype)
-        call(model_library(), 'mt_heads', [P, P, I, I, I, I, I, I], out.ptr, t.ptr, b, n, h, d,
-             1 if split else 0, dtype_code(t.dtype))
+        item = 4 if t.dtype == 'float32' else 2
+        src = t.ptr + column * h * d * item
+        stride = t.shape[-1] if split else 0
+        call(model_library(), 'mt_heads', [P, P, I, I, I, I, I, I, I], out.ptr, src, b, n, h, d,
+             1 if split else 0, stride, dtype_code(t.dtype))
         return out
 
     def _mlp_residual(self, x, layer, dtype):
         d = self.n_embd
         h = self._layernorm(x, layer['ln_2'], dtype)
-        f = self._linear(h, layer['fc'], 4 * d, dtype)
-        call(model_library(), 'mt_gelu', [P, LL, I], f.ptr, f.size, dtype_code(dtype))
+        rows = h.shape[0]
+        f = DeviceTensor((rows, 4 * d), dtype)
+        self.blas().gemm_gelu(f.ptr, h.ptr, layer['fc'][0].ptr, layer['fc'][1].ptr, rows, 4 * d, d, dtype)
         y = self._linear(f, layer['proj'], d, dtype)
         self._residual(x, y)
 
@@ -248,8 +282,8 @@ class DecoderLM:
             d = self.n_embd
             for i, layer in enumerate(w.layers):
                 hdn = self._layernorm(x, layer['ln_1'], dtype)
-                q, k, v = (self._heads(self._linear(hdn, layer[name], d, dtype), b, n, True)
-                           for name in ('q', 'k', 'v'))
+                qkv = self._linear(hdn, layer['qkv'], 3 * d, dtype)
+                q, k, v = (self._heads(qkv, b, n, True, column) for column in range(3))
                 att = cache.prefill_attention(i, q, k, v) if prefill else cache.decode_attention(i, q, k, v)
                 merged = self._heads(att, b, n, False).view(b * n, d)
                 self._residual(x, self._linear(merged, layer['o'], d, dtype))
@@ -270,18 +304,28 @@ class DecoderLM:
             batch.prepare()
             dtype = batch.dtype
             w = self._weights(dtype)
-            b, d, h, hd = batch.batch_size, self.n_embd, self.n_head, self.head_dim
+            b, d = batch.batch_size, self.n_embd
             x = self._embed(w, idx, batch.position_ids)
-            for i, layer in enumerate(w.layers):
-                hdn = self._layernorm(x, layer['ln_1'], dtype)
-                q, k, v = (self._linear(hdn, layer[name], d, dtype).view(b, h, 1, hd)
-                           for name in ('q', 'k', 'v'))
-                att = batch.decode_attention(i, q, k, v).view(b, d)
-                self._residual(x, self._linear(att, layer['o'], d, dtype))
-                self._mlp_residual(x, layer, dtype)
-            logits = self._head(w, x, dtype)
+            h = DeviceTensor((b, d), dtype)
+            lib = model_library()
+            scratch_bytes = _scratch_bytes(lib, b, d, dtype)
+            scratch = DeviceTensor(((scratch_bytes + 3) // 4,), 'float32')
+            att = batch.attention_metadata()
+            call(lib, 'mt_decoder_layers', [P, P, I, P, P, P, P, I, I, I, F, I, I, P, ct.c_size_t, P],
+                 self.blas().handle, w.layer_array, self.n_layer, x.ptr, h.ptr, w.ln_f[0].ptr,
+                 w.ln_f[1].ptr, b, d, self.n_head, self.ln_eps, dtype_code(dtype), 1 if FUSED_GELU else 0,
+                 scratch.ptr, scratch_bytes, ct.byref(att))
+            batch.mark_layers_written()
+            logits = DeviceTensor((b, 1, self.n_vocab), dtype)
+            self.blas().gemm(logits.ptr, h.ptr, w.head.ptr, None, b, self.n_vocab, d, 1, dtype)
             batch.commit()
             return logits
+
+
+def _scratch_bytes(lib, rows, d, dtype):
+    f = lib.mt_decoder_scratch_bytes
+    f.argtypes, f.restype = [I, I, I], ct.c_size_t
+    return int(f(rows, d, dtype_code(dtype)))
 
 
 def distilgpt2(seed=0):

@@ -153,6 +153,31 @@ class PagedDecodeBatch:
             cache.last_attention_path = self.last_attention_path
         return out
 
+    def attention_metadata(self):
+        """The batch's paged metadata for every layer at once (``mt_decode_attention``
+        of include/mt_model.h), for the native decoder loop; the split partials
+        are sized for the widest layer."""
+        from .model import DecodeAttentionStruct
+        if self.table is None or self._written_layers:
+            raise ValueError('Invalid decode batch layer/transaction')
+        pool = self.pool
+        heads = max(h for h, _ in self.layout)
+        partial_bytes = paged_ops.decode_workspace_bytes(b=self.batch_size, h=heads, page_size=pool.page_size,
+                                                         columns=self.columns, split_tokens=self.split_tokens)
+        partials = self._ws.ensure_partials(partial_bytes)
+        return DecodeAttentionStruct(pool.slab_table.ptr, self.table.ptr, self.device_offsets.ptr,
+                                     pool.page_size, pool.pages_per_slab, pool.num_slabs, self.columns,
+                                     len(self.layout), self.split_tokens, self.work.ptr, self.work_items,
+                                     self.merge_rows, partials, partial_bytes)
+
+    def mark_layers_written(self):
+        """Record that every layer's K/V was appended (by the native decoder loop)."""
+        for layer in range(len(self.layout)):
+            self._written_layers.add(layer)
+            for cache in self.caches:
+                cache._written_layers.add(layer)
+                cache.last_attention_path = self.last_attention_path
+
     def commit(self):
         if len(self._written_layers) != len(self.layout):
             raise ValueError('Cannot commit incomplete decode batch')

@@ -60,21 +60,22 @@ def split_tokens_for(*, page_size, columns, requested=0):
     return out.value
 
 
-SPLIT_ARGTYPES = [P] * 7 + [I] * 13 + [P, I, I, P, Z]
+SPLIT_ARGTYPES = [P] * 7 + [I] * 14 + [P, I, I, P, Z]
 
 
 def paged_decode_split(out, q, k, v, slab_table, block_table, offsets, *, b, h, d, page_size,
                        pages_per_slab, num_slabs, columns, layer, layers, dtype,
-                       split_tokens=0, unroll=0, waves=0, work=None, work_items=0, merge_rows=0,
-                       workspace=None, workspace_bytes=0):
+                       split_tokens=0, unroll=0, waves=0, qkv_stride=0, work=None, work_items=0,
+                       merge_rows=0, workspace=None, workspace_bytes=0):
     """``mt_paged_decode_split``: the decode of ``mt_paged_decode_batch`` with a
     caller-owned workspace, an explicit split length (0 = automatic), stream
-    unroll and waves per workgroup (0 = defaults) and an optional device work
-    list from :func:`decode_work_list`."""
+    unroll and waves per workgroup (0 = defaults), the row stride of q/k/v
+    (0 = contiguous) and an optional device work list from
+    :func:`decode_work_list`."""
     call(paged_library(), 'mt_paged_decode_split', SPLIT_ARGTYPES,
          out, q, k, v, slab_table, block_table, offsets, b, h, d, page_size, pages_per_slab,
          num_slabs, columns, layer, layers, dtype_code(dtype), split_tokens, unroll, waves,
-         work, work_items, merge_rows, workspace, workspace_bytes)
+         qkv_stride, work, work_items, merge_rows, workspace, workspace_bytes)
 
 
 def decode_work_list(lengths, heads, split_tokens, compute_units):

@@ -108,19 +108,21 @@ def test_split_entry_validation_and_workspace_size():
     assert st(8, 64, 256, ct.byref(s)) == 0 and s.value == 256
     assert st(16, 64, 96, ct.byref(s)) == 1                             # not a multiple of 64
     split = lib.mt_paged_decode_split
-    split.argtypes, split.restype = [P] * 7 + [I] * 13 + [P, I, I, P, Z], I
+    split.argtypes, split.restype = [P] * 7 + [I] * 14 + [P, I, I, P, Z], I
     common = (8, 8, 8, 8, 8, 8, 8, 4, 12, 64, 16, 4, 16)
     # a splitting launch without a workspace is rejected
-    assert split(*common, 128, 0, 1, 0, 0, 0, 0, None, 0, 0, None, 0) == 1
+    assert split(*common, 128, 0, 1, 0, 0, 0, 0, 0, None, 0, 0, None, 0) == 1
     # waves must be 4 or 8
-    assert split(*common, 64, 0, 1, 0, 0, 0, 6, None, 0, 0, None, 0) == 1
+    assert split(*common, 64, 0, 1, 0, 0, 0, 6, 0, None, 0, 0, None, 0) == 1
     # a work list needs an explicit split length and counts within the batch
-    assert split(*common, 64, 0, 1, 0, 0, 0, 0, 8, 4, 0, None, 0) == 1
-    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 8, 5, 0, None, 0) == 1   # 5 > 4 rows x 1 split
-    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 8, 4, 5, None, 0) == 1   # 5 merge rows > 4
-    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 8, -1, 0, None, 0) == 1
+    assert split(*common, 64, 0, 1, 0, 0, 0, 0, 0, 8, 4, 0, None, 0) == 1
+    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 0, 8, 5, 0, None, 0) == 1   # 5 > 4 rows x 1 split
+    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 0, 8, 4, 5, None, 0) == 1   # 5 merge rows > 4
+    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 0, 8, -1, 0, None, 0) == 1
+    # q/k/v row stride below h*d is rejected
+    assert split(*common, 64, 0, 1, 0, 0, 0, 0, 700, None, 0, 0, None, 0) == 1
     # an empty work list launches nothing
-    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 8, 0, 0, None, 0) == 0
+    assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 0, 8, 0, 0, None, 0) == 0
 
 
 def test_inference_entries_reject_invalid_shapes():

@@ -196,6 +196,35 @@ def test_work_list_ragged_splits_fp16():
     assert np.array_equal(dev.pool_image().view(np.uint8), image.view(np.uint8)), 'append differs'
 
 
+@pytest.mark.parametrize('dtype', ['float32', 'bfloat16'])
+def test_qkv_row_stride_reads_fused_projection_blocks(dtype):
+    # q, k, v as the three column blocks of one [B, 3*H*D] buffer: same bits
+    # as contiguous inputs
+    lengths = [3, 70, 512, 1025, 40]
+    case = make_decode_case(15, batch=5, heads=4, dim=64, page_size=16, lengths=lengths,
+                            pool_pages=256, pages_per_slab=8, dtype=dtype)
+    plain = run_decode(DevicePagedCase(case), entry='split', split_tokens=512)
+    dev = DevicePagedCase(case)
+    hd = case.heads * case.dim
+    fused = np.concatenate([a.reshape(case.batch, hd) for a in (case.q, case.k, case.v)], axis=1)
+    qkv = DeviceTensor((case.batch, 3 * hd), dtype)
+    runtime().h2d(qkv.ptr, np.ascontiguousarray(fused))
+    item = 4 if dtype == 'float32' else 2
+    ws_bytes = paged_ops.decode_workspace_bytes(b=case.batch, h=case.heads, page_size=16,
+                                                columns=case.columns, split_tokens=512)
+    ws = RawDeviceBuffer(ws_bytes)
+    paged_ops.paged_decode_split(dev.out.ptr, qkv.ptr, qkv.ptr + hd * item, qkv.ptr + 2 * hd * item,
+                                 dev.slab_table.ptr, dev.block_table.ptr, dev.offsets.ptr, **dev.kwargs(),
+                                 split_tokens=512, qkv_stride=3 * hd, workspace=ws.ptr,
+                                 workspace_bytes=ws_bytes)
+    runtime().synchronize()
+    strided = dev.out.to_numpy()
+    view = np.uint32 if dtype == 'float32' else np.uint16
+    assert np.array_equal(strided.view(view), plain.view(view))
+    ref, image = oracle_decode(case)
+    assert np.array_equal(dev.pool_image().view(np.uint8), image.view(np.uint8)), 'append differs'
+
+
 def test_repeat_calls_are_deterministic():
     case = config2_case(1, batch=16)
     dev = DevicePagedCase(case)
