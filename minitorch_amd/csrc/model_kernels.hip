@@ -49,7 +49,10 @@ enum Epilogue : int { kEpiNone = 0, kEpiGelu = 1 };
 
 // Candidates the heuristic returns per shape; the fastest on the first call's
 // own operands is kept (one timed pass each, on the null stream).
-constexpr int kCandidates = 8;
+#ifndef MT_GEMM_CANDIDATES
+#define MT_GEMM_CANDIDATES 8
+#endif
+constexpr int kCandidates = MT_GEMM_CANDIDATES;
 
 int pick_fastest(Blas* blas, Plan& p, const hipblasLtMatmulHeuristicResult_t* heur, int count,
                  void* out, const void* a, const void* b) {
