@@ -511,8 +511,13 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
   constexpr int NT = WAVES * kWave;
   constexpr int NS = WAVES * 4;  // partial states per item: one per 16-lane row
   constexpr int SLABS_PER_THREAD = (kLdsSlabs + NT - 1) / NT;
+  constexpr int GROUPS = NT / D;    // thread groups of the first merge level
+  constexpr int PER = NS / GROUPS;  // row states each group merges
+  static_assert(NT % D == 0 && NS % GROUPS == 0, "merge partition");
   __shared__ float s_m[NS], s_l[NS];
   __shared__ float s_acc[NS][D];
+  __shared__ float s2_m[GROUPS], s2_l[GROUPS];
+  __shared__ float s2_acc[GROUPS][D];
   __shared__ uint64_t s_slabs[kLdsSlabs];
   __shared__ __align__(16) T s_new[2][D];  // the new token's K and V rows
 
@@ -672,18 +677,39 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
     }
     __syncthreads();
 
+    // Two-level merge with every thread busy: group q of D threads merges
+    // row states [q*PER, (q+1)*PER) per dim, then D threads merge the groups.
+    {
+      const int d = tid % D, q = tid / D;
+      float M = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) M = fmaxf(M, s_m[q * PER + j]);
+      float lq = 0.f, aq = 0.f;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int w = q * PER + j;
+        const float mw = s_m[w];
+        const float sc = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
+        lq = fmaf(s_l[w], sc, lq);
+        aq = fmaf(s_acc[w][d], sc, aq);
+      }
+      s2_acc[q][d] = aq;
+      if (d == 0) { s2_m[q] = M; s2_l[q] = lq; }
+    }
+    __syncthreads();
+
     const int t = tid;
     if (t < dim) {
       float M = -INFINITY;
-#pragma unroll 4
-      for (int w = 0; w < NS; ++w) M = fmaxf(M, s_m[w]);
+#pragma unroll
+      for (int q = 0; q < GROUPS; ++q) M = fmaxf(M, s2_m[q]);
       float lsum = 0.f, asum = 0.f;
-#pragma unroll 4
-      for (int w = 0; w < NS; ++w) {
-        const float mw = s_m[w];
-        const float sc = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
-        lsum = fmaf(s_l[w], sc, lsum);
-        asum = fmaf(s_acc[w][t], sc, asum);
+#pragma unroll
+      for (int q = 0; q < GROUPS; ++q) {
+        const float mq = s2_m[q];
+        const float sc = (mq == -INFINITY) ? 0.f : fast_exp2(mq - M);
+        lsum = fmaf(s2_l[q], sc, lsum);
+        asum = fmaf(s2_acc[q][t], sc, asum);
       }
       if (nsplit == 1) {
         orow[t] = from_f32<DT>(finalize(asum, lsum));
