@@ -111,12 +111,16 @@ size_t mt_decoder_scratch_bytes(int rows, int d, int dtype);
  * out-projection, residual add + LayerNorm, fc GEMM + GELU, proj GEMM; after
  * the last layer the residual add is fused with the final LayerNorm
  * (final_gamma/final_beta). x [rows, d] fp32 is the residual stream, updated
- * in place; h [rows, d] in dtype receives the final LayerNorm output (the
- * tied head's input). Replaces the reference's per-op layer loop of
- * DecoderLM.decode_batch (minitorch/modules_transformer.py:373-390,258-284). */
+ * in place; h [rows, d] in dtype receives the final LayerNorm output and,
+ * when logits is not null, logits [rows, vocab] = h @ head_weight^T (the tied
+ * head, head_weight [vocab, d]). The projections of this loop choose their
+ * hipBLASLt algorithm by timing (cold caches) on the third call of a shape.
+ * Replaces the reference's per-op layer loop of DecoderLM.decode_batch
+ * (minitorch/modules_transformer.py:373-390,258-284). */
 int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
-                      const float* final_gamma, const float* final_beta, int rows, int d, int heads,
-                      float eps, int dtype, int fused_gelu, void* scratch, size_t scratch_bytes,
+                      const float* final_gamma, const float* final_beta, const void* head_weight,
+                      void* logits, int vocab, int rows, int d, int heads, float eps, int dtype,
+                      int fused_gelu, void* scratch, size_t scratch_bytes,
                       const mt_decode_attention* att);
 
 #ifdef __cplusplus

@@ -83,12 +83,27 @@ __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, 
   const int tail = head + nvec * E;
   if (tid < head) consider(c, to_f32<DT>(p[tid]), tid);
   const auto* vp = global_view(reinterpret_cast<const u32x4*>(p + head));
-  for (int j = tid; j < nvec; j += kArgmaxThreads) {
-    float f[E];
-    const u32x4 x = vp[j];
-    unpack16<DT>(x, f);
+  // kBatch vectors per thread are loaded before any is compared, so one row
+  // is read in a few round trips instead of one per 8 KiB. The candidate
+  // order is total (value, then lower index), so visiting order is free.
+  constexpr int kBatch = 8;
+  for (int j0 = tid; j0 < nvec; j0 += kArgmaxThreads * kBatch) {
+    u32x4 x[kBatch];
 #pragma unroll
-    for (int e = 0; e < E; ++e) consider(c, f[e], head + j * E + e);
+    for (int u = 0; u < kBatch; ++u) {
+      const int j = j0 + u * kArgmaxThreads;
+      if (j < nvec) x[u] = vp[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int j = j0 + u * kArgmaxThreads;
+      if (j < nvec) {
+        float f[E];
+        unpack16<DT>(x[u], f);
+#pragma unroll
+        for (int e = 0; e < E; ++e) consider(c, f[e], head + j * E + e);
+      }
+    }
   }
   for (int j = tail + tid; j < width; j += kArgmaxThreads) consider(c, to_f32<DT>(p[j]), j);
 #pragma unroll

@@ -963,9 +963,9 @@ hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
   constexpr int NT = WAVES * kWave;
   if (unroll == 0) {
     // Automatic: the deepest unroll when the whole grid is resident at its
-    // occupancy (more loads in flight per wave), else unroll 2, whose lower
-    // register count keeps more workgroups per compute unit.
-    unroll = 2;
+    // occupancy (more loads in flight per wave), else unroll 1, whose lower
+    // register count keeps the most workgroups per compute unit.
+    unroll = 1;
     if constexpr (kMaxUnroll >= 4) {
       static int per_cu = -1;
       if (per_cu < 0) {

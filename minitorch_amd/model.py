@@ -311,13 +311,12 @@ class DecoderLM:
             scratch_bytes = _scratch_bytes(lib, b, d, dtype)
             scratch = DeviceTensor(((scratch_bytes + 3) // 4,), 'float32')
             att = batch.attention_metadata()
-            call(lib, 'mt_decoder_layers', [P, P, I, P, P, P, P, I, I, I, F, I, I, P, ct.c_size_t, P],
-                 self.blas().handle, w.layer_array, self.n_layer, x.ptr, h.ptr, w.ln_f[0].ptr,
-                 w.ln_f[1].ptr, b, d, self.n_head, self.ln_eps, dtype_code(dtype), 1 if FUSED_GELU else 0,
-                 scratch.ptr, scratch_bytes, ct.byref(att))
-            batch.mark_layers_written()
             logits = DeviceTensor((b, 1, self.n_vocab), dtype)
-            self.blas().gemm(logits.ptr, h.ptr, w.head.ptr, None, b, self.n_vocab, d, 1, dtype)
+            call(lib, 'mt_decoder_layers', [P, P, I, P, P, P, P, P, P, I, I, I, I, F, I, I, P, ct.c_size_t, P],
+                 self.blas().handle, w.layer_array, self.n_layer, x.ptr, h.ptr, w.ln_f[0].ptr,
+                 w.ln_f[1].ptr, w.head.ptr, logits.ptr, self.n_vocab, b, d, self.n_head, self.ln_eps,
+                 dtype_code(dtype), 1 if FUSED_GELU else 0, scratch.ptr, scratch_bytes, ct.byref(att))
+            batch.mark_layers_written()
             batch.commit()
             return logits
 
