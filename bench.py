@@ -83,6 +83,42 @@ def cpu_baseline(case, seconds):
                        f'on fp16 pages, OpenMP over (request, head)')
 
 
+def pattern_ceiling(case, devs, steps, warmup):
+    """Bandwidth of the decode step's K/V access pattern alone: every (row,
+    head, page) K and V page-head chunk (P*D*s bytes, randomly placed by the
+    shuffled table) read by mt_chunk_read, a kernel with no address
+    arithmetic, math or merge, at the decode's grid and at a large grid."""
+    from minitorch_amd.runtime import RawDeviceBuffer
+    rt = runtime()
+    s = 2 if case.dtype != 'float32' else 4
+    H, Pg, D, pps = case.heads, case.page_size, case.dim, case.pages_per_slab
+    chunk = Pg * D * s
+    plane = pps * H * Pg * D * s
+    lists = []
+    for d in devs:
+        addrs = []
+        for b in range(case.batch):
+            pages = case.table[b, :(int(case.lengths[b]) + Pg - 1) // Pg]
+            for h in range(H):
+                for p in pages:
+                    base = d.pool.ptr + (int(p) // pps) * case.slab_bytes + ((int(p) % pps) * H + h) * chunk
+                    addrs += [base, base + plane]
+        buf = RawDeviceBuffer(8 * len(addrs))
+        buf.upload(np.array(addrs, np.uint64))
+        lists.append((buf, len(addrs)))
+    sink = RawDeviceBuffer(4)
+    f = rt.lib.mt_chunk_read
+    f.argtypes, f.restype = [P, I, I, I, P], I
+    out = {}
+    for blocks in (case.batch * case.heads, 6144):
+        calls = [(buf.ptr, n, chunk, blocks, sink.ptr) for buf, n in lists]
+        per = time_launches(f, calls, steps, warmup)
+        nbytes = lists[0][1] * chunk
+        out[f'grid_{blocks}'] = dict(us_per_launch=per * 1e6, bytes=nbytes, achieved_gbs=nbytes / per / 1e9,
+                                     frac=nbytes / per / 1e9 / PEAK_HBM_GBS)
+    return out
+
+
 def time_launches(fn, calls, steps, warmup):
     """Mean seconds per launch from HIP events around ``steps`` launches."""
     rt = runtime()
@@ -196,6 +232,9 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--calibrate-copy', type=int, default=0, metavar='MB',
                     help='only run device-to-device copies of MB MiB (counter calibration) and exit')
+    ap.add_argument('--no-ceiling', action='store_true',
+                    help='config 2: skip timing the plain kernel that reads exactly the K/V pages of the '
+                         'step (2 KiB page-head chunks, no math), reported as pattern_ceiling')
     ap.add_argument('--config', type=int, default=2, choices=(2, 3, 4, 5),
                     help='2: op-level decode (default, the headline line); 5: ragged op-level '
                          'decode, bf16, H=25, P=16 and 32; 3 / 4: end-to-end decode')
@@ -301,6 +340,8 @@ def main():
             'kernel': 'decode_kernel<kF16,64,true,U> (mt_paged_decode_split)',
         },
     }
+    if not args.no_ceiling:
+        result['pattern_ceiling'] = pattern_ceiling(case, devs, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         result['cpu_baseline'] = cpu_baseline(case, args.cpu_seconds)
     print(json.dumps(result), flush=True)

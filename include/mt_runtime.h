@@ -35,6 +35,13 @@ int mt_device_count(int* n);
 /* Compute units of the current device (256 on MI355X); sizes the row
  * visiting order of the decode. No reference counterpart. */
 int mt_compute_units(int* n);
+/* Measuring kernel: reads `count` chunks of chunk_bytes (multiple of 1 KiB,
+ * addresses listed in the device array `chunks`, 16-byte aligned) with
+ * `blocks` workgroups of 4 waves, each wave taking every (waves)-th chunk.
+ * Used by bench.py --ceiling to time a decode step's exact K/V access pattern
+ * without the decode's work. No reference counterpart. */
+int mt_chunk_read(const unsigned long long* chunks, int count, int chunk_bytes, int blocks,
+                  unsigned* sink);
 /* Pinned host memory (hipHostMalloc) for asynchronous uploads.
  * No reference counterpart. */
 int mt_host_alloc(void** p, size_t bytes);

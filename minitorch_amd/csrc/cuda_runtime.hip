@@ -102,6 +102,37 @@ int mt_fill_words(void* p, size_t words, unsigned int value) {
 
 // n elements of dtype (0 fp32, 1 fp16, 2 bf16) set to a deterministic
 // hash of (seed, index), uniform in [-2, 2): synthetic K/V for large pools.
+// Reads `count` chunks of `chunk_bytes` (a multiple of 1 KiB) whose addresses
+// are listed in `chunks`, each wave taking chunks wave, wave + waves, ...,
+// and XORs what it read into sink[0] only if the XOR equals a sentinel (so the
+// loads cannot be dropped and nothing is written in practice). A measuring
+// kernel: the bandwidth of exactly the K/V access pattern of a decode step,
+// with no address arithmetic, math or merging.
+__global__ __launch_bounds__(256) void chunk_read_kernel(const unsigned long long* chunks, int count,
+                                                          int vec_per_chunk, unsigned* sink) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63;
+  const int wave = (blockIdx.x * int(blockDim.x) + int(threadIdx.x)) >> 6;
+  const int waves = int(gridDim.x * blockDim.x) >> 6;
+  unsigned acc = 0;
+  for (int c = wave; c < count; c += waves) {
+    const auto* p = reinterpret_cast<const __attribute__((address_space(1))) u32x4*>(chunks[c]);
+    for (int v = lane; v < vec_per_chunk; v += 64) {
+      const u32x4 x = p[v];
+      acc ^= x.x ^ x.y ^ x.z ^ x.w;
+    }
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+int mt_chunk_read(const unsigned long long* chunks, int count, int chunk_bytes, int blocks,
+                  unsigned* sink) {
+  if (!chunks || !sink || count < 1 || chunk_bytes < 1024 || chunk_bytes % 1024 || blocks < 1)
+    return hipErrorInvalidValue;
+  chunk_read_kernel<<<blocks, 256>>>(chunks, count, chunk_bytes / 16, sink);
+  return hipGetLastError();
+}
+
 int mt_fill_random(void* p, long long n, unsigned long long seed, int dtype) {
   if ((!p && n) || n < 0 || dtype < 0 || dtype > 2) return hipErrorInvalidValue;
   if (n) fill_random_kernel<<<blocks_for(n), 256>>>(p, n, seed, dtype);
