@@ -863,6 +863,231 @@ struct AppendArgs {
   Geometry g;
 };
 
+
+// ---------------------------------------------------------------------------
+// Causal paged prefill attention on the matrix cores (fp16/bf16, head_dim 64
+// or 128), same semantics as query_kernel: query qi attends keys
+// kj < nk with kj <= offset + qi, and a query whose keys touch a missing page
+// reads NaN. One workgroup of 4 waves per (request, head, 64-query tile),
+// each wave owning 16 queries; keys stream in blocks of 64 staged in LDS from
+// the pages (K row-major, V transposed). Per block a wave computes
+// S^T = K Q^T with v_mfma_f32_16x16x32 (keys x queries, so each lane holds 16
+// scores of one query), updates that query's online softmax in registers and
+// accumulates O^T += V^T P^T, feeding the scores' own register layout as the
+// B operand (the MFMA sums over its k index in any order, so A's key order is
+// chosen to match). The MFMA takes P in the input type, so P is split into a
+// high and a low part of that type (two MFMAs): the weights keep about 16
+// (bf16) or 22 (fp16) significant bits instead of 8 or 11, which holds the
+// output to the fp32 path's accuracy when |V| is large.
+constexpr int kPfQueries = 64;     // queries per workgroup
+constexpr int kPfKeys = 64;        // keys per staged block
+constexpr int kPfWindowPages = 512;  // page bases resolved into LDS at a time
+#ifndef MT_PREFILL_MIN_QUERIES
+#define MT_PREFILL_MIN_QUERIES 16
+#endif
+constexpr int kPfMinQueries = MT_PREFILL_MIN_QUERIES;  // fewer queries use query_kernel
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+struct Mfma;
+template <>
+struct Mfma<kF16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ floatx4 run(const v8& a, const v8& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<kBF16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ floatx4 run(const v8& a, const v8& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <int DT, int D>
+__global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
+  using T = typename Elem<DT>::T;
+  using V8 = typename Mfma<DT>::v8;
+  constexpr int KS = kPfKeys;
+  constexpr int KP = D + 8;     // LDS row of K, padded (elements)
+  constexpr int VP = KS + 8;    // LDS row of V^T, padded
+  constexpr int DT16 = D / 16;  // 16-dim tiles of the output
+  constexpr int DS = D / 32;    // 32-dim steps of q.k
+  constexpr int CPR = D / 8;    // 16-byte chunks per key row
+  constexpr bool SPLIT_P = true;
+  __shared__ const T* s_page[kPfWindowPages];
+  __shared__ __align__(16) T s_k[KS][KP];
+  __shared__ __align__(16) T s_vt[D][VP];
+
+  const Geometry& g = a.g;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & (kWave - 1);
+  const int grp = lane >> 4;  // 0..3
+  const int col = lane & 15;  // this lane's query within its wave's 16
+  const int tiles = (a.nq + kPfQueries - 1) / kPfQueries;
+  const int64_t bh_count = a.items / tiles;
+  const T* qp = static_cast<const T*>(a.q);
+  T* out = static_cast<T*>(a.out);
+  const int win_keys = kPfWindowPages << g.log2_page;
+
+  for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
+    // Longest (last) query tiles first.
+    const int tile = tiles - 1 - int(item / bh_count);
+    const int64_t bh = item - int64_t(tiles - 1 - tile) * bh_count;
+    const int b = int(bh / g.heads), head = int(bh - int64_t(b) * g.heads);
+    const int* table_row = a.table + int64_t(b) * g.columns;
+
+    // B operand of S^T = K Q^T: dims [32*ds + 8*grp, +8) of query q0 + col.
+    const int q0 = tile * kPfQueries + wave * 16;
+    const int qi = q0 + col;
+    const bool q_ok = qi < a.nq;
+    V8 qv[DS];
+    {
+      const T* row = qp + (bh * a.nq + (q_ok ? qi : 0)) * D;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+        qv[ds] = __builtin_bit_cast(V8, *global_view(reinterpret_cast<const u32x4*>(row + 32 * ds + 8 * grp)));
+    }
+    const int qpos = a.offset + qi;
+    const bool wave_live = q0 < a.nq;
+    const int wave_last = a.offset + (q0 + 15 < a.nq ? q0 + 15 : a.nq - 1);
+    const int tile_q = (tile + 1) * kPfQueries - 1 < a.nq ? (tile + 1) * kPfQueries - 1 : a.nq - 1;
+    const int kend = a.offset + tile_q + 1 < a.nk ? a.offset + tile_q + 1 : a.nk;
+
+    float m = -INFINITY, l = 0.f;
+    floatx4 o[DT16];
+#pragma unroll
+    for (int dt = 0; dt < DT16; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    for (int w0 = 0; w0 < kend; w0 += win_keys) {
+      const int w1 = w0 + win_keys < kend ? w0 + win_keys : kend;
+      const int npg = (w1 - w0 + g.page_size - 1) >> g.log2_page;
+      __syncthreads();
+      for (int j = tid; j < npg; j += kThreads)
+        s_page[j] = page_base<T>(a.slabs, table_row, (w0 >> g.log2_page) + j, g, head);
+      for (int k0 = w0; k0 < w1; k0 += KS) {
+        __syncthreads();
+        // Stage K (row-major) and V (transposed) of keys [k0, k0 + 64); keys
+        // past the tile's last attended key are zero, a missing page is NaN
+        // in K (so its score is NaN) and zero in V (so a query that does not
+        // attend it is unaffected).
+        for (int c = tid; c < KS * CPR; c += kThreads) {
+          const int kr = c / CPR, part = c - kr * CPR;
+          const int key = k0 + kr;
+          u32x4 kx = u32x4{0u, 0u, 0u, 0u}, vx = u32x4{0u, 0u, 0u, 0u};
+          if (key < w1) {
+            const T* page = s_page[(key - w0) >> g.log2_page];
+            if (page) {
+              const T* kp = page + (key & (g.page_size - 1)) * D + part * 8;
+              kx = *global_view(reinterpret_cast<const u32x4*>(kp));
+              vx = *global_view(reinterpret_cast<const u32x4*>(kp + g.kind_stride));
+            } else {
+              kx = u32x4{~0u, ~0u, ~0u, ~0u};
+            }
+          }
+          *reinterpret_cast<u32x4*>(&s_k[kr][part * 8]) = kx;
+          const uint32_t vw[4] = {vx.x, vx.y, vx.z, vx.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            s_vt[part * 8 + 2 * j][kr] = static_cast<T>(vw[j] & 0xffffu);
+            s_vt[part * 8 + 2 * j + 1][kr] = static_cast<T>(vw[j] >> 16);
+          }
+        }
+        __syncthreads();
+        if (!wave_live || k0 > wave_last) continue;
+
+        // Scores: lane holds keys k0 + 16*kt + 4*grp + i of query qi.
+        floatx4 sc[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          sc[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ds = 0; ds < DS; ++ds) {
+            const V8 kk = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(&s_k[16 * kt + col][32 * ds + 8 * grp]));
+            sc[kt] = Mfma<DT>::run(kk, qv[ds], sc[kt]);
+          }
+        }
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = k0 + 16 * kt + 4 * grp + i;
+            float v = sc[kt][i] * a.qscale;
+            if (key > qpos || key >= kend) v = -INFINITY;
+            sc[kt][i] = v;
+            bmax = fmaxf(bmax, v);
+          }
+        }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        const float mn = fmaxf(m, bmax);
+        const float alpha = (m == -INFINITY) ? 0.f : fast_exp2(m - mn);
+        // B operand of the PV step: k slot j of 32-key step ks holds key
+        // 32*ks + 4*grp + j (j < 4) or 32*ks + 16 + 4*grp + (j - 4).
+        uint32_t phi[2][4], plo[2][4];
+        float psum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+          for (int i = 0; i < 4; i += 2) {
+            const float p0 = sc[kt][i] == -INFINITY ? 0.f : fast_exp2(sc[kt][i] - mn);
+            const float p1 = sc[kt][i + 1] == -INFINITY ? 0.f : fast_exp2(sc[kt][i + 1] - mn);
+            psum += p0 + p1;
+            const T h0 = from_f32<DT>(p0), h1 = from_f32<DT>(p1);
+            const int ks = kt >> 1, w = (kt & 1) * 2 + (i >> 1);
+            phi[ks][w] = uint32_t(h0) | (uint32_t(h1) << 16);
+            if constexpr (SPLIT_P) {
+              const T l0 = from_f32<DT>(p0 - to_f32<DT>(h0)), l1 = from_f32<DT>(p1 - to_f32<DT>(h1));
+              plo[ks][w] = uint32_t(l0) | (uint32_t(l1) << 16);
+            }
+          }
+        }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l = l * alpha + psum;
+        m = mn;
+        V8 pv[2], pl[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          pv[ks] = __builtin_bit_cast(V8, u32x4{phi[ks][0], phi[ks][1], phi[ks][2], phi[ks][3]});
+          if constexpr (SPLIT_P) pl[ks] = __builtin_bit_cast(V8, u32x4{plo[ks][0], plo[ks][1], plo[ks][2], plo[ks][3]});
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT16; ++dt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[dt][i] *= alpha;
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            // A = V^T rows dt*16 + col, keys in pv's k-slot order.
+            const T* vrow = &s_vt[dt * 16 + col][32 * ks + 4 * grp];
+            const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+            const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16);
+            const V8 va = __builtin_bit_cast(V8, u32x4{lo.x, lo.y, hi.x, hi.y});
+            o[dt] = Mfma<DT>::run(va, pv[ks], o[dt]);
+            if constexpr (SPLIT_P) o[dt] = Mfma<DT>::run(va, pl[ks], o[dt]);
+          }
+        }
+      }
+    }
+
+    // O^T lane layout: dims dt*16 + 4*grp + i of query qi.
+    if (q_ok) {
+      T* orow = out + (bh * a.nq + qi) * D;
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) {
+        const T r0 = from_f32<DT>(finalize(o[dt][0], l)), r1 = from_f32<DT>(finalize(o[dt][1], l));
+        const T r2 = from_f32<DT>(finalize(o[dt][2], l)), r3 = from_f32<DT>(finalize(o[dt][3], l));
+        *reinterpret_cast<uint2*>(orow + dt * 16 + 4 * grp) =
+            uint2{uint32_t(r0) | (uint32_t(r1) << 16), uint32_t(r2) | (uint32_t(r3) << 16)};
+      }
+    }
+  }
+}
+
 // Multi-token append at a common offset (reference paged_append with
 // offsets == nullptr, src/paged_attention_kernel.cu:23-33): K/V[b,h,pos,:]
 // goes to token offset + pos of request b; rows whose page is missing are
@@ -1118,6 +1343,18 @@ int mt_paged_attention(void* out, const void* q, const uint64_t* slabs, const in
   a.items = int64_t(b) * h * ((nq + kWaves - 1) / kWaves);
   a.g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
   const bool vec = (d == 64 || d == 128) && aligned16(out) && aligned16(q);
+  if (vec && dtype != kF32 && nq >= kPfMinQueries) {
+    a.items = int64_t(b) * h * ((nq + kPfQueries - 1) / kPfQueries);
+    const int blocks = grid_for(a.items);
+    if (dtype == kF16) {
+      if (d == 64) prefill_kernel<kF16, 64><<<blocks, kThreads>>>(a);
+      else prefill_kernel<kF16, 128><<<blocks, kThreads>>>(a);
+    } else {
+      if (d == 64) prefill_kernel<kBF16, 64><<<blocks, kThreads>>>(a);
+      else prefill_kernel<kBF16, 128><<<blocks, kThreads>>>(a);
+    }
+    return hipGetLastError();
+  }
   const int blocks = grid_for(a.items);
 #define MT_QUERY(DT)                                                                   \
   if (vec && d == 64) query_kernel<DT, 64, true, 2><<<blocks, kThreads>>>(a);          \

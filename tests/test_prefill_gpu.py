@@ -1,0 +1,134 @@
+"""GPU parity of causal paged prefill attention (``mt_paged_attention``)
+against the float64 oracle.
+
+For fp16/bf16 with head_dim 64 or 128 and at least 16 queries the library
+runs the matrix-core prefill kernel; the other shapes run the per-query
+kernel. Both follow reference paged_forward with offsets == nullptr
+(src/paged_attention_kernel.cu:35-85): nk = offset + nq, query qi attends
+keys kj <= offset + qi, and a missing page gives NaN for every query that
+attends it. Page sizes are 8, 16 and 32 (the entry point rejects others). Tolerances are in tests/tolerances.py.
+"""
+import numpy as np
+import pytest
+
+from minitorch_amd import paged_ops
+from minitorch_amd.runtime import DeviceTensor, RawDeviceBuffer, runtime
+from minitorch_amd.workloads import make_decode_case, DevicePagedCase
+from oracle import paged_oracle as po
+from tolerances import assert_attention_close
+
+pytestmark = pytest.mark.gpu
+CODES = {'float32': po.F32, 'float16': po.F16, 'bfloat16': po.BF16}
+
+
+def prefill_case(seed, *, batch, heads, dim, page_size, nk, dtype, layers=1, layer=0,
+                 pages_per_slab=4, spare_pages=0):
+    pages = -(-nk // page_size) * batch + spare_pages
+    pool = -(-pages // pages_per_slab) * pages_per_slab
+    return make_decode_case(seed, batch=batch, heads=heads, dim=dim, page_size=page_size,
+                            lengths=[nk] * batch, pool_pages=pool, pages_per_slab=pages_per_slab,
+                            dtype=dtype, layers=layers, layer=layer)
+
+
+def run_prefill(case, nq, nk, offset, seed=0, dev=None, present=None):
+    rng = np.random.default_rng(seed)
+    dt = case.dtype
+    q = po.encode(rng.standard_normal((case.batch, case.heads, nq, case.dim), dtype=np.float32),
+                  CODES[dt])
+    dev = dev or DevicePagedCase(case)
+    qd = DeviceTensor(q.shape, dt)
+    runtime().h2d(qd.ptr, q)
+    out = DeviceTensor(q.shape, dt)
+    paged_ops.paged_attention(out.ptr, qd.ptr, dev.slab_table.ptr, dev.block_table.ptr,
+                              b=case.batch, h=case.heads, nq=nq, nk=nk, d=case.dim,
+                              page_size=case.page_size, pages_per_slab=case.pages_per_slab,
+                              num_slabs=case.num_slabs, columns=case.columns, layer=case.layer,
+                              layers=case.layers, offset=offset, dtype=dt)
+    runtime().synchronize()
+    ref = po.image_paged_attention(case.image, CODES[dt], case.table, case.columns, q, case.layer,
+                                   offset, nk, present=present)
+    got = out.to_numpy()
+    assert_attention_close(got, ref, dt, context=f'{dt} nq={nq} nk={nk} off={offset}')
+    return got, ref
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+@pytest.mark.parametrize('dim', [64, 128])
+@pytest.mark.parametrize('nq,offset', [(16, 0), (64, 0), (100, 0), (200, 37), (130, 300)])
+def test_prefill_shapes(dtype, dim, nq, offset):
+    case = prefill_case(20 + nq + offset, batch=2, heads=3, dim=dim, page_size=16,
+                        nk=offset + nq, dtype=dtype)
+    run_prefill(case, nq, offset + nq, offset, seed=nq)
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+@pytest.mark.parametrize('page_size', [8, 32])
+def test_prefill_page_sizes(dtype, page_size):
+    nq, offset = 90, 45
+    case = prefill_case(30 + page_size, batch=2, heads=2, dim=64, page_size=page_size,
+                        nk=offset + nq, dtype=dtype, pages_per_slab=8)
+    run_prefill(case, nq, offset + nq, offset, seed=page_size)
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+def test_prefill_window_crossing(dtype):
+    # page_size 8 and more than 512 pages: the page bases are resolved in
+    # windows of 512 pages (4096 keys).
+    nq, offset = 96, 4100
+    case = prefill_case(42, batch=1, heads=2, dim=64, page_size=8, nk=offset + nq, dtype=dtype,
+                        pages_per_slab=16)
+    run_prefill(case, nq, offset + nq, offset, seed=4)
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+def test_prefill_multi_layer(dtype):
+    case = prefill_case(43, batch=2, heads=2, dim=128, page_size=16, nk=150, dtype=dtype,
+                        layers=3, layer=1, pages_per_slab=5)
+    run_prefill(case, 150, 150, 0, seed=5)
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+def test_prefill_missing_pages(dtype):
+    # A hole at page 2 (keys 32..47) of request 0 and an out-of-pool page at
+    # page 6 (keys 96..111) of request 1: queries attending them are NaN,
+    # earlier queries are not.
+    nq, offset = 120, 0
+    case = prefill_case(44, batch=2, heads=2, dim=64, page_size=16, nk=nq, dtype=dtype)
+    case.table[0, 2] = -1
+    case.table[1, 6] = 10 ** 6
+    got, ref = run_prefill(case, nq, nq, offset, seed=6)
+    assert np.isnan(ref[0, :, 32:]).all() and not np.isnan(ref[0, :, :32]).any()
+    assert np.isnan(ref[1, :, 96:]).all() and not np.isnan(ref[1, :, :96]).any()
+
+
+def test_prefill_null_slab():
+    case = prefill_case(45, batch=2, heads=2, dim=64, page_size=16, nk=100, dtype='float16')
+    dev = DevicePagedCase(case)
+    phys = int(case.table[1, 3])
+    slabs = np.array([dev.pool.ptr + s * case.slab_bytes for s in range(case.num_slabs)], np.uint64)
+    slabs[phys // case.pages_per_slab] = 0
+    dev.slab_table.upload(slabs)
+    present = np.ones(case.num_slabs, bool)
+    present[phys // case.pages_per_slab] = False
+    got, ref = run_prefill(case, 100, 100, 0, seed=7, dev=dev, present=present)
+    assert np.isnan(ref).any() and not np.isnan(ref).all()
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+def test_prefill_large_scores(dtype):
+    # Scaled inputs push the scores far apart, so the running max moves and
+    # most weights underflow; the rescaling has to stay exact.
+    nq = 70
+    case = prefill_case(46, batch=1, heads=2, dim=64, page_size=16, nk=nq, dtype=dtype)
+    f = po.decode(case.image, CODES[dtype]) * 6.0
+    case.image[...] = po.encode(f.astype(np.float32), CODES[dtype])
+    run_prefill(case, nq, nq, 0, seed=8)
+
+
+def test_prefill_matches_per_query_kernel_below_threshold():
+    # 15 queries run the per-query kernel, 16 the matrix-core kernel; both
+    # against the oracle on the same pages.
+    case = prefill_case(47, batch=2, heads=2, dim=64, page_size=16, nk=60, dtype='float16')
+    dev = DevicePagedCase(case)
+    run_prefill(case, 15, 59, 44, seed=9, dev=dev)
+    run_prefill(case, 16, 60, 44, seed=9, dev=dev)
