@@ -906,6 +906,48 @@ struct Mfma<kBF16> {
   }
 };
 
+// x of lane l ^ 16 and of lane l ^ 32, combined with x by the caller: the
+// permlane swaps exchange rows of 16 (32) lanes between two registers, so
+// after swapping two copies of x, lane l holds x[l] in one and x[l ^ 16]
+// (x[l ^ 32]) in the other.
+__device__ __forceinline__ float lane_swap16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return (threadIdx.x & 16) ? a : b;
+}
+__device__ __forceinline__ float lane_swap32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return (threadIdx.x & 32) ? a : b;
+}
+
+// Two probabilities rounded to the input type, packed as the MFMA operand;
+// r0/r1 receive the rounded values as floats (for the low part of the split).
+// fp16 rounds toward zero (one packed conversion; the low part carries the
+// remainder), bf16 to nearest even.
+template <int DT>
+struct PackP;
+template <>
+struct PackP<kF16> {
+  static __device__ __forceinline__ uint32_t pack(float p0, float p1, float& r0, float& r1) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(p0, p1);
+    r0 = float(h[0]);
+    r1 = float(h[1]);
+    return __builtin_bit_cast(uint32_t, h);
+  }
+};
+template <>
+struct PackP<kBF16> {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ uint32_t pack(float p0, float p1, float& r0, float& r1) {
+    const bf2 h = {static_cast<__bf16>(p0), static_cast<__bf16>(p1)};
+    const uint32_t u = __builtin_bit_cast(uint32_t, h);
+    r0 = __uint_as_float(u << 16);
+    r1 = __uint_as_float(u & 0xffff0000u);
+    return u;
+  }
+};
+
 template <int DT, int D>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
   using T = typename Elem<DT>::T;
@@ -916,7 +958,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
   constexpr int DT16 = D / 16;  // 16-dim tiles of the output
   constexpr int DS = D / 32;    // 32-dim steps of q.k
   constexpr int CPR = D / 8;    // 16-byte chunks per key row
-  constexpr bool SPLIT_P = true;
+  constexpr int NC = KS * CPR / kThreads;  // chunks per thread and plane
+  static_assert(NC * kThreads == KS * CPR, "block staging must divide over the workgroup");
   __shared__ const T* s_page[kPfWindowPages];
   __shared__ __align__(16) T s_k[KS][KP];
   __shared__ __align__(16) T s_vt[D][VP];
@@ -962,41 +1005,60 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
 #pragma unroll
     for (int dt = 0; dt < DT16; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+    // Staging of a 64-key block: K row-major, V transposed. Keys past the
+    // window are zero; a missing page is NaN in K (so its score is NaN) and
+    // zero in V (so a query that does not attend it is unaffected). The loads
+    // are issued unconditionally (from this lane's query row when the key has
+    // no page) and the substitution happens at the LDS store, so that no
+    // branch waits for them before the block in between is computed.
+    u32x4 kx[NC], vx[NC];
+    int kstate[NC];  // 0 = loaded, 1 = missing page, 2 = past the window
+    const T* dummy = qp + (bh * a.nq + (q_ok ? qi : 0)) * D;
+    auto stage_load = [&](int k0, int w0, int w1) {
+#pragma unroll
+      for (int n = 0; n < NC; ++n) {
+        const int c = tid + n * kThreads;
+        const int kr = c / CPR, part = c - kr * CPR;
+        const int key = k0 + kr;
+        const T* page = key < w1 ? s_page[(key - w0) >> g.log2_page] : nullptr;
+        kstate[n] = key >= w1 ? 2 : (page ? 0 : 1);
+        const T* kp = page ? page + (key & (g.page_size - 1)) * D + part * 8 : dummy;
+        const int64_t vstep = page ? g.kind_stride : 0;
+        kx[n] = *global_view(reinterpret_cast<const u32x4*>(kp));
+        vx[n] = *global_view(reinterpret_cast<const u32x4*>(kp + vstep));
+      }
+    };
+    auto stage_store = [&]() {
+#pragma unroll
+      for (int n = 0; n < NC; ++n) {
+        const int c = tid + n * kThreads;
+        const int kr = c / CPR, part = c - kr * CPR;
+        const uint32_t kfill = kstate[n] == 1 ? ~0u : 0u;
+        const bool ok = kstate[n] == 0;
+        const u32x4 kk = ok ? kx[n] : u32x4{kfill, kfill, kfill, kfill};
+        *reinterpret_cast<u32x4*>(&s_k[kr][part * 8]) = kk;
+        const uint32_t vw[4] = {ok ? vx[n].x : 0u, ok ? vx[n].y : 0u, ok ? vx[n].z : 0u, ok ? vx[n].w : 0u};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s_vt[part * 8 + 2 * j][kr] = static_cast<T>(vw[j] & 0xffffu);
+          s_vt[part * 8 + 2 * j + 1][kr] = static_cast<T>(vw[j] >> 16);
+        }
+      }
+    };
     for (int w0 = 0; w0 < kend; w0 += win_keys) {
       const int w1 = w0 + win_keys < kend ? w0 + win_keys : kend;
       const int npg = (w1 - w0 + g.page_size - 1) >> g.log2_page;
       __syncthreads();
       for (int j = tid; j < npg; j += kThreads)
         s_page[j] = page_base<T>(a.slabs, table_row, (w0 >> g.log2_page) + j, g, head);
+      __syncthreads();
+      stage_load(w0, w0, w1);
       for (int k0 = w0; k0 < w1; k0 += KS) {
+        if (k0 > w0) __syncthreads();  // every wave is done with the previous block
+        stage_store();
         __syncthreads();
-        // Stage K (row-major) and V (transposed) of keys [k0, k0 + 64); keys
-        // past the tile's last attended key are zero, a missing page is NaN
-        // in K (so its score is NaN) and zero in V (so a query that does not
-        // attend it is unaffected).
-        for (int c = tid; c < KS * CPR; c += kThreads) {
-          const int kr = c / CPR, part = c - kr * CPR;
-          const int key = k0 + kr;
-          u32x4 kx = u32x4{0u, 0u, 0u, 0u}, vx = u32x4{0u, 0u, 0u, 0u};
-          if (key < w1) {
-            const T* page = s_page[(key - w0) >> g.log2_page];
-            if (page) {
-              const T* kp = page + (key & (g.page_size - 1)) * D + part * 8;
-              kx = *global_view(reinterpret_cast<const u32x4*>(kp));
-              vx = *global_view(reinterpret_cast<const u32x4*>(kp + g.kind_stride));
-            } else {
-              kx = u32x4{~0u, ~0u, ~0u, ~0u};
-            }
-          }
-          *reinterpret_cast<u32x4*>(&s_k[kr][part * 8]) = kx;
-          const uint32_t vw[4] = {vx.x, vx.y, vx.z, vx.w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            s_vt[part * 8 + 2 * j][kr] = static_cast<T>(vw[j] & 0xffffu);
-            s_vt[part * 8 + 2 * j + 1][kr] = static_cast<T>(vw[j] >> 16);
-          }
-        }
-        __syncthreads();
+        // The next block's loads are in flight while this one is computed.
+        if (k0 + KS < w1) stage_load(k0 + KS, w0, w1);
         if (!wave_live || k0 > wave_last) continue;
 
         // Scores: lane holds keys k0 + 16*kt + 4*grp + i of query qi.
@@ -1010,51 +1072,54 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
             sc[kt] = Mfma<DT>::run(kk, qv[ds], sc[kt]);
           }
         }
-        float bmax = -INFINITY;
+        // Causal / length mask, only for blocks that reach past the wave's
+        // first query or past kend (a wave-uniform test).
+        if (k0 + KS - 1 > a.offset + q0 || k0 + KS > kend) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
+          for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = k0 + 16 * kt + 4 * grp + i;
-            float v = sc[kt][i] * a.qscale;
-            if (key > qpos || key >= kend) v = -INFINITY;
-            sc[kt][i] = v;
-            bmax = fmaxf(bmax, v);
+            for (int i = 0; i < 4; ++i) {
+              const int key = k0 + 16 * kt + 4 * grp + i;
+              if (key > qpos || key >= kend) sc[kt][i] = -INFINITY;
+            }
           }
         }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-        const float mn = fmaxf(m, bmax);
+        // Block max of the raw scores (qscale > 0 commutes with the max; NaN
+        // scores are dropped by fmaxf), shared by the four lanes of a query.
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          bmax = fmaxf(fmaxf(bmax, fmaxf(sc[kt][0], sc[kt][1])), fmaxf(sc[kt][2], sc[kt][3]));
+        bmax = fmaxf(bmax, lane_swap16(bmax));
+        bmax = fmaxf(bmax, lane_swap32(bmax));
+        const float mn = fmaxf(m, bmax * a.qscale);
         const float alpha = (m == -INFINITY) ? 0.f : fast_exp2(m - mn);
+        const float mref = (mn == -INFINITY) ? 0.f : mn;  // masked scores give exp2(-inf) = 0
         // B operand of the PV step: k slot j of 32-key step ks holds key
-        // 32*ks + 4*grp + j (j < 4) or 32*ks + 16 + 4*grp + (j - 4).
+        // 32*ks + 4*grp + j (j < 4) or 32*ks + 16 + 4*grp + (j - 4). The
+        // denominator stays per lane (this lane's 16 keys) until the end.
         uint32_t phi[2][4], plo[2][4];
         float psum = 0.f;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
           for (int i = 0; i < 4; i += 2) {
-            const float p0 = sc[kt][i] == -INFINITY ? 0.f : fast_exp2(sc[kt][i] - mn);
-            const float p1 = sc[kt][i + 1] == -INFINITY ? 0.f : fast_exp2(sc[kt][i + 1] - mn);
+            const float p0 = fast_exp2(fmaf(sc[kt][i], a.qscale, -mref));
+            const float p1 = fast_exp2(fmaf(sc[kt][i + 1], a.qscale, -mref));
             psum += p0 + p1;
-            const T h0 = from_f32<DT>(p0), h1 = from_f32<DT>(p1);
             const int ks = kt >> 1, w = (kt & 1) * 2 + (i >> 1);
-            phi[ks][w] = uint32_t(h0) | (uint32_t(h1) << 16);
-            if constexpr (SPLIT_P) {
-              const T l0 = from_f32<DT>(p0 - to_f32<DT>(h0)), l1 = from_f32<DT>(p1 - to_f32<DT>(h1));
-              plo[ks][w] = uint32_t(l0) | (uint32_t(l1) << 16);
-            }
+            float r0, r1;
+            phi[ks][w] = PackP<DT>::pack(p0, p1, r0, r1);
+            plo[ks][w] = PackP<DT>::pack(p0 - r0, p1 - r1, r0, r1);
           }
         }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
         l = l * alpha + psum;
         m = mn;
         V8 pv[2], pl[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           pv[ks] = __builtin_bit_cast(V8, u32x4{phi[ks][0], phi[ks][1], phi[ks][2], phi[ks][3]});
-          if constexpr (SPLIT_P) pl[ks] = __builtin_bit_cast(V8, u32x4{plo[ks][0], plo[ks][1], plo[ks][2], plo[ks][3]});
+          pl[ks] = __builtin_bit_cast(V8, u32x4{plo[ks][0], plo[ks][1], plo[ks][2], plo[ks][3]});
         }
 #pragma unroll
         for (int dt = 0; dt < DT16; ++dt) {
@@ -1068,12 +1133,15 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
             const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16);
             const V8 va = __builtin_bit_cast(V8, u32x4{lo.x, lo.y, hi.x, hi.y});
             o[dt] = Mfma<DT>::run(va, pv[ks], o[dt]);
-            if constexpr (SPLIT_P) o[dt] = Mfma<DT>::run(va, pl[ks], o[dt]);
+            o[dt] = Mfma<DT>::run(va, pl[ks], o[dt]);
           }
         }
       }
     }
 
+    // The query's denominator is the sum over its four lanes.
+    l += lane_swap16(l);
+    l += lane_swap32(l);
     // O^T lane layout: dims dt*16 + 4*grp + i of query qi.
     if (q_ok) {
       T* orow = out + (bh * a.nq + qi) * D;
