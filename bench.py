@@ -32,6 +32,7 @@ from minitorch_amd import paged_ops  # noqa: E402
 from minitorch_amd.workloads import config2_case, DevicePagedCase  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0
+PEAK_MFMA_TFLOPS = 2500.0  # dense fp16/bf16 matrix cores
 METRIC = 'decode tokens/s (1 GPU) + paged-attn achieved HBM GB/s as % of MI355X peak'
 
 
@@ -189,6 +190,70 @@ def bench_config5(args):
     }
 
 
+def prefill_flops(n, heads, dim):
+    """Causal attention flops of one n-token prompt: q.k and p.v over the
+    n(n+1)/2 attended (query, key) pairs, 2 flops per multiply-add."""
+    return 2.0 * heads * dim * n * (n + 1)
+
+
+def bench_prefill_shape(heads, dtype, lengths, steps, warmup, seed):
+    """Mean time of mt_paged_attention over prompts of the given lengths (one
+    request per call, nq = nk = n, offset 0), the pages of all prompts in one
+    shuffled pool."""
+    from minitorch_amd.workloads import make_decode_case
+    from minitorch_amd.runtime import DeviceTensor
+    from minitorch_amd.dtypes import dtype_code
+    dim, page = 64, 16
+    lengths = np.asarray(lengths, np.int64)
+    pages = int(((lengths + page - 1) // page).sum())
+    case = make_decode_case(seed, batch=len(lengths), heads=heads, dim=dim, page_size=page,
+                            lengths=lengths, pool_pages=-(-pages // 16) * 16, pages_per_slab=16,
+                            dtype=dtype)
+    dev = DevicePagedCase(case)
+    nmax = int(lengths.max())
+    q = DeviceTensor((1, heads, nmax, dim), dtype)
+    rt = runtime()
+    from minitorch_amd.workloads import _normal
+    rt.h2d(q.ptr, _normal(np.random.default_rng([seed, 6]), (1, heads, nmax, dim), dtype))
+    out = DeviceTensor((1, heads, nmax, dim), dtype)
+    fn = paged_ops.paged_library().mt_paged_attention
+    fn.argtypes, fn.restype = [P] * 4 + [I] * 13, I
+    calls = [(out.ptr, q.ptr, dev.slab_table.ptr, dev.block_table.ptr + 4 * i * case.columns, 1, heads,
+              int(n), int(n), dim, page, case.pages_per_slab, case.num_slabs, case.columns, 0, 1, 0,
+              dtype_code(dtype)) for i, n in enumerate(lengths)]
+    per_round = time_launches(fn, calls, steps * len(calls), warmup * len(calls)) * len(calls)
+    flops = sum(prefill_flops(int(n), heads, dim) for n in lengths)
+    return dict(prompts=len(lengths), mean_prompt=float(lengths.mean()), max_prompt=nmax,
+                us_per_prefill=per_round / len(calls) * 1e6, tflops=flops / per_round / 1e12,
+                frac=flops / per_round / 1e12 / PEAK_MFMA_TFLOPS)
+
+
+def bench_prefill(args):
+    """Causal paged prefill attention (the matrix-core kernel behind
+    mt_paged_attention) on the prompt shapes of configs 3 and 4: config 3's
+    first 64 prompts (U{32..512}, 12 heads, fp16) and 64 config-4 contexts
+    (lognormal median 256, clipped [16, 1024], 16 heads, bf16), one request per
+    call as the batcher admits them, plus single 512- and 1024-token prompts."""
+    from minitorch_amd.e2e import config3_trace, config4_lengths
+    steps, warmup = max(1, args.steps // 20), max(1, args.warmup // 10)
+    c3 = [len(p) for _, _, p, _ in config3_trace(args.seed)[:64]]
+    c4 = config4_lengths(np.random.default_rng([args.seed, 4]), 64)
+    r3 = bench_prefill_shape(12, 'float16', c3, steps, warmup, args.seed)
+    r4 = bench_prefill_shape(16, 'bfloat16', c4, steps, warmup, args.seed)
+    r512 = bench_prefill_shape(12, 'float16', [512], steps * 20, warmup * 10, args.seed)
+    r1024 = bench_prefill_shape(16, 'bfloat16', [1024], steps * 20, warmup * 10, args.seed)
+    return {'metric': 'causal paged prefill attention TFLOP/s (1 GPU)', 'value': r3['tflops'],
+            'unit': 'TFLOP/s', 'n_gpus': 1, 'steps': steps, 'warmup': warmup,
+            'ms_per_step': r3['us_per_prefill'] * r3['prompts'] / 1e3, 'higher_is_better': True,
+            'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
+            'config': {'workload': 'config-3 prompt shapes: 64 prompts U{32..512}, 12 heads, D 64, page 16, '
+                                   'fp16, one request per mt_paged_attention call (a step = the 64 calls)'},
+            'roofline': {'bound': 'mfma', 'achieved': r3['tflops'], 'peak': PEAK_MFMA_TFLOPS,
+                         'unit': 'TFLOP/s', 'frac': r3['frac'], 'traffic': None},
+            'config3_prompts_fp16': r3, 'config4_contexts_bf16': r4, 'prompt512_h12_fp16': r512,
+            'prompt1024_h16_bf16': r1024}
+
+
 def bench_e2e(args):
     from minitorch_amd import model as model_mod, e2e
     if args.config == 3:
@@ -238,6 +303,8 @@ def main():
     ap.add_argument('--config', type=int, default=2, choices=(2, 3, 4, 5),
                     help='2: op-level decode (default, the headline line); 5: ragged op-level '
                          'decode, bf16, H=25, P=16 and 32; 3 / 4: end-to-end decode')
+    ap.add_argument('--prefill', action='store_true',
+                    help='op-level causal paged prefill attention on the prompt shapes of configs 3 and 4')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: this build has no multi-GPU path '
@@ -257,6 +324,9 @@ def main():
         return
     if args.config == 5:
         print(json.dumps(bench_config5(args)), flush=True)
+        return
+    if args.prefill:
+        print(json.dumps(bench_prefill(args)), flush=True)
         return
     if args.config in (3, 4):
         print(json.dumps(bench_e2e(args)), flush=True)
