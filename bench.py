@@ -262,6 +262,9 @@ def bench_e2e(args):
         warm = e2e.config3_trace(args.seed + 1, requests=8, rate=1000.0)
         e2e.run_config3(model, warm, precision='fp16')
         r = e2e.run_config3(model, trace, precision='fp16')
+        # the same trace through the sync-free loop (device-side token feedback)
+        e2e.run_config3(model, warm, precision='fp16', token_feedback=True)
+        r['sync_free'] = e2e.run_config3(model, trace, precision='fp16', token_feedback=True)
         value, workload = r['busy_decode_tokens_per_sec'], (
             'config 3: continuous batching, random-init DistilGPT-2 (6 layers, d 768, 12 heads, vocab '
             '50257), fp16, 256 Poisson requests at 32 req/s, prompts U[32,512], outputs geometric mean '
@@ -270,6 +273,8 @@ def bench_e2e(args):
     else:
         model = model_mod.gpt2_medium(seed=args.seed)
         r = e2e.run_config4(model, seed=args.seed, steps=min(args.steps, 40), warmup=min(args.warmup, 5))
+        r['sync_free'] = e2e.run_config4(model, seed=args.seed, steps=min(args.steps, 40),
+                                         warmup=min(args.warmup, 5), token_feedback=True)
         value, workload = r['decode_tokens_per_sec'], (
             'config 4: steady state of 128 requests, random-init GPT-2-medium (24 layers, d 1024, 16 '
             'heads), bf16, contexts lognormal(median 256, sigma 1.2) clipped [16,1024], page 16, 5% '

@@ -20,6 +20,21 @@ int mt_embedding_gather(float* dst, const float* weights, const float* ids, int 
  * (src/inference_kernels.cu:73-79). */
 int mt_row_argmax(float* dst, const void* src, int rows, int width, int dtype);
 
+/* Token feedback of a sync-free decode loop: every cache slot of a page pool
+ * keeps its request's last token on the device (slot_tokens, fp32 ids,
+ * num_slots entries), so the next step reads it there instead of from the
+ * host. mt_row_argmax_feedback is mt_row_argmax that also writes
+ * slot_tokens[slots[r]] = dst[r] (slots outside [0, num_slots) are skipped;
+ * slot_tokens == NULL writes dst only). mt_gather_slot_tokens sets
+ * ids[r] = slot_tokens[slots[r]] (NaN for a slot outside the table).
+ * No reference counterpart: they replace the per-step host round trip of the
+ * token ids (reference minitorch/continuous_batching.py:143,146,
+ * minitorch/kv_cache.py:39-53). */
+int mt_row_argmax_feedback(float* dst, float* slot_tokens, const int* slots, int num_slots,
+                           const void* src, int rows, int width, int dtype);
+int mt_gather_slot_tokens(float* ids, const float* slot_tokens, const int* slots, int num_slots,
+                          int rows);
+
 /* dst[b, 0, :] = src[b, n - 1, :] for src [b, n, w]. Replaces reference
  * mt_last_row (src/inference_kernels.cu:66-72). */
 int mt_last_row(void* dst, const void* src, int b, int n, int w, int dtype);

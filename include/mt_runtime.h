@@ -30,6 +30,10 @@ int mt_event_elapsed(float* ms, void* a, void* b);
 int mt_event_destroy(void* e);
 /* Wait for an event. No reference counterpart. */
 int mt_event_synchronize(void* e);
+/* 0 when the work before the event's record has completed, 600
+ * (hipErrorNotReady) while it is pending. No reference counterpart (the
+ * sync-free decode loop polls token readbacks with it). */
+int mt_event_query(void* e);
 /* Number of visible devices. No reference counterpart. */
 int mt_device_count(int* n);
 /* Compute units of the current device (256 on MI355X); sizes the row

@@ -8,6 +8,15 @@ admissions, at most ``max_prefills_per_step`` prefills per step within
 EOS or length, cancel of queued or active requests, and the same per-step
 statistics. Page IDs, tables and offsets of every decode step are built on
 the device (``PagedDecodeBatch``); the host reads back only the new tokens.
+
+With ``token_feedback=True`` the decode loop is sync-free: each step's
+greedy tokens stay on the device as the next step's input (the pool's
+per-slot last tokens), requests without an EOS token finish by count, and
+the token values reach the host through asynchronous copies that ``step``
+delivers one step later (a step returns the events of the tokens that
+arrived during it). Scheduling decisions, pages and tokens are the same as in
+the synchronous mode; a step whose batch has a request with an EOS token
+waits for its tokens, since finishing then depends on their values.
 """
 from collections import deque
 from contextlib import nullcontext
@@ -17,7 +26,7 @@ import time
 import numpy as np
 
 from .amp import autocast
-from .kv_cache import greedy_token
+from .kv_cache import greedy_token, TokenReadback
 from .paged_kv_cache import KVPagePool
 from .runtime import DeviceTensor
 
@@ -38,6 +47,7 @@ class GenerationRequest:
     output_ids: list = field(default_factory=list)
     token_times: list = field(default_factory=list)
     cache: object = field(default=None, repr=False)
+    generated: int = 0  # tokens produced on the device, delivered or not
 
     @property
     def done(self):
@@ -54,7 +64,7 @@ class ContinuousBatcher:
 
     def __init__(self, model, *, max_batch_size=4, page_size=16, kv_budget_bytes=256 * 1024 ** 2,
                  pages_per_slab=4, precision='fp32', max_prefills_per_step=1,
-                 prefill_token_budget=512, clock=time.perf_counter):
+                 prefill_token_budget=512, clock=time.perf_counter, token_feedback=False):
         for value in (max_batch_size, max_prefills_per_step, prefill_token_budget):
             if type(value) is not int or value < 1:
                 raise ValueError('Positive integer batch size and prefill limits required')
@@ -76,6 +86,9 @@ class ContinuousBatcher:
         self.iteration = 0
         self.last_step = None
         self.closed = False
+        self.token_feedback = bool(token_feedback)
+        self._readback = TokenReadback(max_prefills_per_step + 4) if self.token_feedback else None
+        self._inflight = deque()  # (readback ticket, requests) in issue order
 
     def _precision_context(self):
         if self.precision == 'fp32':
@@ -84,7 +97,7 @@ class ContinuousBatcher:
 
     @property
     def has_work(self):
-        return bool(self.active or self.pending)
+        return bool(self.active or self.pending or self._inflight)
 
     def submit(self, request_id, prompt_ids, *, max_new_tokens=32, eos_token_id=None):
         if self.closed:
@@ -130,23 +143,70 @@ class ContinuousBatcher:
         return True
 
     def _emit(self, request, token_id, arrival):
+        request.generated += 1
+        return self._deliver(request, token_id, arrival, finish=True)
+
+    def _deliver(self, request, token_id, arrival, finish):
         request.output_ids.append(int(token_id))
         request.token_times.append(arrival)
         reason = ('eos' if token_id == request.eos_token_id else
                   'length' if len(request.output_ids) >= request.max_new_tokens else None)
-        if reason is not None:
+        if reason is not None and finish and not request.done:
             self._finish(request, 'completed', reason)
         return dict(request_id=request.request_id, token_id=int(token_id),
                     output_index=len(request.output_ids) - 1, arrival_time=arrival, finish_reason=reason)
+
+    # ------------------------------------------------ sync-free decoding ---
+    def _issue(self, requests, ids):
+        """Queue the read-back of the device tokens ``ids`` of ``requests`` and
+        finish, by count, the requests that reached their length. Requests
+        with an EOS token finish when their tokens are delivered."""
+        self._inflight.append((self._readback.push(ids), list(requests)))
+        for request in requests:
+            request.generated += 1
+            if request.eos_token_id is None and request.generated >= request.max_new_tokens:
+                self._finish(request, 'completed', 'length')
+
+    def _drain(self, keep=0, block=True):
+        """Deliver arrived tokens in issue order, leaving ``keep`` read-backs
+        in flight; without ``block`` only those already complete."""
+        events = []
+        while len(self._inflight) > keep:
+            ticket, requests = self._inflight[0]
+            if not block and not self._readback.ready(ticket):
+                break
+            tokens = self._readback.read(ticket)
+            self._inflight.popleft()
+            arrival = self.clock()
+            for request, token in zip(requests, tokens):
+                finish = request.eos_token_id is not None
+                events.append(self._deliver(request, int(token), arrival, finish))
+        return events
 
     def step(self):
         if self.closed:
             raise ValueError('Batcher is closed')
         start = self.clock()
         events, decode_ids, prefill_ids = [], list(self.active), []
+        if self.token_feedback:
+            events.extend(self._drain(block=False))
+            first_ticket = self._readback.issued
         prefill_tokens = 0
         with self._precision_context():
-            if decode_ids:
+            if decode_ids and self.token_feedback:
+                batch = [self.active[rid] for rid in decode_ids]
+                try:
+                    ids = self.model.decode_greedy([r.cache for r in batch])
+                    self.peak_used_pages = max(self.peak_used_pages, self.pool.used_pages)
+                    self._issue(batch, ids)
+                    if any(r.eos_token_id is not None for r in batch):
+                        events.extend(self._drain())
+                except Exception:
+                    for request in batch:
+                        if not request.done:
+                            self._finish(request, 'failed', 'decode_error')
+                    raise
+            elif decode_ids:
                 batch = [self.active[rid] for rid in decode_ids]
                 try:
                     ids = DeviceTensor.from_numpy(np.array([[r.output_ids[-1]] for r in batch], np.float32))
@@ -177,13 +237,22 @@ class ContinuousBatcher:
                     ids = DeviceTensor.from_numpy(np.array([request.prompt_ids], np.float32))
                     logits, _ = self.model.prefill(ids, request.cache)
                     self.peak_used_pages = max(self.peak_used_pages, self.pool.used_pages)
-                    token = greedy_token(logits).to_numpy()[0, 0]
-                    events.append(self._emit(request, token, self.clock()))
+                    if self.token_feedback:
+                        self._issue([request], greedy_token(logits, feedback=request.cache))
+                        if request.eos_token_id is not None:
+                            events.extend(self._drain())
+                    else:
+                        token = greedy_token(logits).to_numpy()[0, 0]
+                        events.append(self._emit(request, token, self.clock()))
                 except Exception:
                     self._finish(request, 'failed', 'prefill_error')
                     raise
                 prefill_ids.append(request.request_id)
                 prefill_tokens += len(request.prompt_ids)
+        if self.token_feedback:
+            # Only the read-backs issued in this step stay in flight: the
+            # previous step's tokens are delivered while this step runs.
+            events.extend(self._drain(keep=sum(1 for t, _ in self._inflight if t >= first_ticket)))
         capacity_bytes = sum(r.cache.nbytes for r in self.active.values())
         live_bytes = sum(r.cache.length * self.pool.page_bytes // self.pool.page_size for r in self.active.values())
         self.last_step = dict(iteration=self.iteration, decode_request_ids=decode_ids,
@@ -194,6 +263,7 @@ class ContinuousBatcher:
                               kv_capacity_bytes=capacity_bytes,
                               kv_slot_utilization=live_bytes / capacity_bytes if capacity_bytes else None,
                               peak_used_pages=self.peak_used_pages, step_seconds=self.clock() - start,
+                              token_feedback=self.token_feedback, tokens_in_flight=len(self._inflight),
                               **self.pool.memory_stats())
         self.iteration += 1
         return events
@@ -201,6 +271,8 @@ class ContinuousBatcher:
     def close(self):
         if self.closed:
             return
+        if self._inflight:
+            self._drain()
         for request in tuple(self.requests.values()):
             if not request.done:
                 self.cancel(request.request_id)

@@ -73,6 +73,7 @@ int mt_event_elapsed(float* ms, hipEvent_t a, hipEvent_t b) {
 }
 int mt_event_destroy(hipEvent_t e) { return hipEventDestroy(e); }
 int mt_event_synchronize(hipEvent_t e) { return hipEventSynchronize(e); }
+int mt_event_query(hipEvent_t e) { return hipEventQuery(e); }
 int mt_device_count(int* n) { return hipGetDeviceCount(n); }
 // Compute units of the current device.
 int mt_compute_units(int* n) {

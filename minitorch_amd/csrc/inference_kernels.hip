@@ -66,7 +66,8 @@ constexpr int kArgmaxThreads = 512;
 // with 16-byte loads; the unaligned head and tail element by element.
 template <int DT>
 __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, const void* src,
-                                                                    int width) {
+                                                                    int width, float* slot_tokens,
+                                                                    const int* slots, int num_slots) {
   using T = typename Elem<DT>::T;
   constexpr int E = per16<DT>();
   __shared__ float s_v[kArgmaxThreads / 64];
@@ -121,7 +122,24 @@ __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, 
       if (better(o, best)) best = o;
     }
     dst[row] = float(best.i);
+    // Token feedback: the row's cache slot keeps the chosen token for the
+    // next decode step (a slot outside the table is skipped).
+    if (slot_tokens) {
+      const int s = slots[row];
+      if (s >= 0 && s < num_slots) slot_tokens[s] = float(best.i);
+    }
   }
+}
+
+// ids[r] = slot_tokens[slots[r]]; a slot outside the table gives a NaN id,
+// which the embedding gather turns into a NaN row.
+__global__ __launch_bounds__(256) void gather_slot_tokens_kernel(float* ids, const float* slot_tokens,
+                                                                 const int* slots, int rows,
+                                                                 int num_slots) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const int s = slots[r];
+  ids[r] = (s >= 0 && s < num_slots) ? slot_tokens[s] : NAN;
 }
 
 // dst[b, :] = src[b, n-1, :] (reference src/inference_kernels.cu:28-30).
@@ -161,14 +179,29 @@ int mt_embedding_gather(float* dst, const float* weights, const float* ids, int 
   return hipGetLastError();
 }
 
-int mt_row_argmax(float* dst, const void* src, int rows, int width, int dtype) {
+int mt_row_argmax_feedback(float* dst, float* slot_tokens, const int* slots, int num_slots,
+                           const void* src, int rows, int width, int dtype) {
   if (rows < 1 || width < 1 || width > 16777216 || int64_t(rows) * width > INT32_MAX)
     return hipErrorInvalidValue;
-  if (!dst || !src) return hipErrorInvalidValue;
-  if (dtype == kF32) row_argmax_kernel<kF32><<<rows, kArgmaxThreads>>>(dst, src, width);
-  else if (dtype == kF16) row_argmax_kernel<kF16><<<rows, kArgmaxThreads>>>(dst, src, width);
-  else if (dtype == kBF16) row_argmax_kernel<kBF16><<<rows, kArgmaxThreads>>>(dst, src, width);
+  if (!dst || !src || (slot_tokens && (!slots || num_slots < 1))) return hipErrorInvalidValue;
+#define MT_ARGMAX(DT) \
+  row_argmax_kernel<DT><<<rows, kArgmaxThreads>>>(dst, src, width, slot_tokens, slots, num_slots)
+  if (dtype == kF32) MT_ARGMAX(kF32);
+  else if (dtype == kF16) MT_ARGMAX(kF16);
+  else if (dtype == kBF16) MT_ARGMAX(kBF16);
   else return hipErrorInvalidValue;
+#undef MT_ARGMAX
+  return hipGetLastError();
+}
+
+int mt_row_argmax(float* dst, const void* src, int rows, int width, int dtype) {
+  return mt_row_argmax_feedback(dst, nullptr, nullptr, 0, src, rows, width, dtype);
+}
+
+int mt_gather_slot_tokens(float* ids, const float* slot_tokens, const int* slots, int num_slots,
+                          int rows) {
+  if (!ids || !slot_tokens || !slots || rows < 1 || num_slots < 1) return hipErrorInvalidValue;
+  gather_slot_tokens_kernel<<<(rows + 255) / 256, 256>>>(ids, slot_tokens, slots, rows, num_slots);
   return hipGetLastError();
 }
 

@@ -46,13 +46,20 @@ def _progress(message):
 
 def run_config3(model, trace, *, precision='fp16', max_batch_size=256, page_size=16, kv_pages=16384,
                 max_prefills_per_step=1, prefill_token_budget=512, clock=time.perf_counter,
-                report_every=200):
+                report_every=200, token_feedback=False):
+    """Replay a config-3 trace through the batcher. ``busy_step_tokens_per_sec``
+    is decode tokens over the wall time of the steps (decode, prefill and
+    scheduling, idle gaps between arrivals excluded), comparable between the
+    synchronous and the sync-free (``token_feedback``) loop;
+    ``busy_decode_tokens_per_sec`` (synchronous loop only) counts just the
+    decode part of each step up to its tokens on the host."""
     itemsize = 4 if precision == 'fp32' else 2
     page_bytes = 2 * model.n_layer * model.n_embd * page_size * itemsize
     batcher = ContinuousBatcher(model, max_batch_size=max_batch_size, page_size=page_size,
                                 kv_budget_bytes=kv_pages * page_bytes, precision=precision,
                                 max_prefills_per_step=max_prefills_per_step,
-                                prefill_token_budget=prefill_token_budget, clock=clock)
+                                prefill_token_budget=prefill_token_budget, clock=clock,
+                                token_feedback=token_feedback)
     pending = list(trace)
     steps = []
     start = clock()
@@ -73,11 +80,15 @@ def run_config3(model, trace, *, precision='fp16', max_batch_size=256, page_size
     generated = sum(len(r.output_ids) for r in batcher.requests.values())
     decode_tokens = sum(s['decode_batch_size'] for s in steps)
     decode_seconds = sum(s['decode_seconds'] for s in steps if s['decode_batch_size'])
+    step_seconds = sum(s['step_seconds'] for s in steps)
     ttft = [r.ttft_seconds for r in batcher.requests.values() if r.ttft_seconds is not None]
     result = dict(
+        token_feedback=token_feedback,
         generated_tokens=generated, elapsed_seconds=elapsed,
         output_tokens_per_sec=generated / elapsed,
-        busy_decode_tokens_per_sec=decode_tokens / decode_seconds if decode_seconds else None,
+        busy_decode_tokens_per_sec=(decode_tokens / decode_seconds if decode_seconds and not token_feedback
+                                    else None),
+        busy_step_tokens_per_sec=decode_tokens / step_seconds, step_seconds=step_seconds,
         decode_tokens=decode_tokens, decode_seconds=decode_seconds, steps=len(steps),
         max_decode_batch_size=max(s['decode_batch_size'] for s in steps),
         mean_decode_batch_size=float(np.mean([s['decode_batch_size'] for s in steps if s['decode_batch_size']])),
@@ -95,8 +106,15 @@ def config4_lengths(rng, n):
 
 
 def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_rate=0.05,
-                precision='bf16', page_size=16, kv_pages=None):
-    """Steady-state decode throughput; returns a dict of measurements."""
+                precision='bf16', page_size=16, kv_pages=None, token_feedback=False):
+    """Steady-state decode throughput; returns a dict of measurements.
+
+    ``decode_tokens_per_sec`` (synchronous loop only) times each step's decode
+    up to its tokens on the host. ``loop_tokens_per_sec`` times the whole
+    timed loop (decode steps plus the replacement prefills, synchronized only
+    at its start and end), which is comparable between the synchronous loop
+    and the sync-free one (``token_feedback``: tokens stay on the device as
+    the next step's input and are never read)."""
     dtype = {'fp16': 'float16', 'bf16': 'bfloat16', 'fp32': 'float32'}[precision]
     rng = np.random.default_rng([seed, 4])
     rt = runtime()
@@ -113,6 +131,9 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
             prompt = rng.integers(0, model.n_vocab, length)
             cache = model.create_kv_cache(1, model.n_positions, page_size=page_size, page_pool=pool)
             logits, _ = model.prefill(DeviceTensor.from_numpy(prompt[None].astype(np.float32)), cache)
+            if token_feedback:
+                greedy_token(logits, feedback=cache)
+                return cache, None
             return cache, int(greedy_token(logits).to_numpy()[0, 0])
 
         for _ in range(concurrent):
@@ -120,33 +141,48 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
             caches.append(c)
             last.append(t)
         decode_seconds, tokens, replaced, context = 0.0, 0, 0, []
+        loop0 = None
         for step in range(warmup + steps):
-            ids = DeviceTensor.from_numpy(np.array(last, np.float32)[:, None])
             context.append(sum(c.length + 1 for c in caches))
-            rt.synchronize()
-            t0 = time.perf_counter()
-            logits = model.decode_batch(ids, caches)
-            nxt = greedy_token(logits).to_numpy()[:, 0]
-            t1 = time.perf_counter()
-            if step >= warmup:
-                decode_seconds += t1 - t0
-                tokens += len(caches)
-            last = [int(t) for t in nxt]
-            if step % 10 == 0:
-                _progress(f'config 4: step {step}, decode {(t1 - t0) * 1e3:.2f} ms')
+            if step == warmup:
+                rt.synchronize()
+                loop0 = time.perf_counter()
+            if token_feedback:
+                model.decode_greedy(caches)
+                if step >= warmup:
+                    tokens += len(caches)
+            else:
+                ids = DeviceTensor.from_numpy(np.array(last, np.float32)[:, None])
+                rt.synchronize()
+                t0 = time.perf_counter()
+                logits = model.decode_batch(ids, caches)
+                nxt = greedy_token(logits).to_numpy()[:, 0]
+                t1 = time.perf_counter()
+                if step >= warmup:
+                    decode_seconds += t1 - t0
+                    tokens += len(caches)
+                last = [int(t) for t in nxt]
+                if step % 10 == 0:
+                    _progress(f'config 4: step {step}, decode {(t1 - t0) * 1e3:.2f} ms')
             for i in range(len(caches)):
                 if rng.random() < replace_rate or caches[i].length + 1 >= caches[i].capacity:
                     caches[i].close()
                     caches[i], last[i] = admit()
                     replaced += 1
+        rt.synchronize()
+        loop_seconds = time.perf_counter() - loop0
         stats = pool.memory_stats()
         for c in caches:
             c.close()
         pool.close()
-    return dict(decode_tokens_per_sec=tokens / decode_seconds, decode_seconds=decode_seconds,
-                steps=steps, concurrent=concurrent, mean_context_tokens=float(np.mean(context) / concurrent),
+    return dict(token_feedback=token_feedback,
+                decode_tokens_per_sec=tokens / decode_seconds if decode_seconds else None,
+                decode_seconds=decode_seconds, loop_tokens_per_sec=tokens / loop_seconds,
+                loop_seconds=loop_seconds, steps=steps, concurrent=concurrent,
+                mean_context_tokens=float(np.mean(context) / concurrent),
                 replaced_requests=replaced, page_reuses=stats['kv_pool_page_reuses'],
-                ms_per_step=decode_seconds / steps * 1e3)
+                ms_per_step=decode_seconds / steps * 1e3 if decode_seconds else None,
+                loop_ms_per_step=loop_seconds / steps * 1e3)
 
 
 class _null:

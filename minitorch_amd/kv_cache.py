@@ -9,8 +9,9 @@ validation of model, precision and weight version; kv_cache.py:56-160).
 checks have nothing to check.
 """
 import weakref
+import numpy as np
 from .amp import autocast_dtype
-from .runtime import DeviceTensor
+from .runtime import DeviceTensor, PinnedHostBuffer, CudaEvent, runtime
 from . import paged_ops
 
 
@@ -27,18 +28,81 @@ def last_position(x):
     return out
 
 
-def greedy_token(logits):
+def greedy_token(logits, feedback=None):
     """GPU argmax over [B, 1, V] logits, returning fp32 token IDs [B, 1]; ties
     and NaNs choose the first index, like numpy.argmax (reference
-    minitorch/kv_cache.py:39-53)."""
+    minitorch/kv_cache.py:39-53). With ``feedback`` (a paged cache of B rows)
+    the tokens are also stored as its slots' last tokens in the pool, where
+    the next decode step reads them without a host round trip."""
     if not isinstance(logits, DeviceTensor) or logits.dims != 3 or logits.shape[1] != 1:
         raise ValueError('greedy_token requires no_grad and device logits [B,1,V]')
     b, _, v = logits.shape
     if b < 1 or not 1 <= v <= 2 ** 24:
         raise ValueError('Vocabulary must fit exact FP32 token IDs')
     out = DeviceTensor((b, 1), 'float32')
-    paged_ops.row_argmax(out.ptr, logits.ptr, b, v, logits.dtype)
+    if feedback is None:
+        paged_ops.row_argmax(out.ptr, logits.ptr, b, v, logits.dtype)
+    else:
+        pool = feedback.pool
+        if feedback.batch_size != b or pool.closed:
+            raise ValueError('Feedback cache must be live and have one row per logits row')
+        paged_ops.row_argmax_feedback(out.ptr, pool.slot_tokens.ptr, feedback.slots_ptr, pool.max_slots,
+                                      logits.ptr, b, v, logits.dtype)
     return out
+
+
+class TokenReadback:
+    """Token IDs copied to pinned host memory without waiting for the device:
+    ``push`` enqueues the copy of a [B, 1] fp32 id tensor behind the work
+    that produces it and returns a ticket; ``ready`` polls it and ``read``
+    waits for it and returns the ids as int64. Tickets are served in order.
+    Used by the sync-free decode loop, where the host schedules the next step
+    before the tokens of the last one have arrived."""
+
+    def __init__(self, depth=8):
+        self.depth = depth
+        self._buffers = [None] * depth
+        self._events = [None] * depth
+        self._rows = [0] * depth
+        self._issued = 0
+        self._read = 0
+
+    def push(self, ids):
+        if self._issued - self._read >= self.depth:
+            raise RuntimeError('Too many unread token readbacks')
+        k = self._issued % self.depth
+        nbytes = 4 * ids.size
+        if self._buffers[k] is None or self._buffers[k].nbytes < nbytes:
+            self._buffers[k] = PinnedHostBuffer(max(nbytes, 4096))
+        rt = runtime()
+        rt.check(rt.lib.mt_copy_async(self._buffers[k].pointer.value, ids.ptr, nbytes, 2))
+        if self._events[k] is None:
+            self._events[k] = CudaEvent()
+        self._events[k].record()
+        self._rows[k] = ids.size
+        self._issued += 1
+        return self._issued - 1
+
+    @property
+    def pending(self):
+        return self._issued - self._read
+
+    @property
+    def issued(self):
+        """Ticket of the next push."""
+        return self._issued
+
+    def ready(self, ticket):
+        return self._events[ticket % self.depth].query()
+
+    def read(self, ticket):
+        if ticket != self._read:
+            raise ValueError('Token readbacks are read in order')
+        k = ticket % self.depth
+        self._events[k].synchronize()
+        raw = self._buffers[k].array[:4 * self._rows[k]].view(np.float32)
+        self._read += 1
+        return raw.astype(np.int64)
 
 
 class CacheBase:

@@ -299,12 +299,30 @@ class DecoderLM:
     def decode_batch(self, idx, caches):
         """One token per independent paged request in one model batch; rows
         may have different context lengths (reference modules_transformer.py:373-390)."""
+        return self._decode_batch(idx, caches, greedy=False)
+
+    def decode_greedy(self, caches, idx=None):
+        """``decode_batch`` with greedy selection on the device, for the
+        sync-free decode loop: the input token of each row is ``idx`` or, when
+        None, the last token its cache slot holds in the pool (written by the
+        previous step's selection); the chosen tokens are written back there
+        and returned as fp32 IDs [B, 1] on the device. Nothing waits for the
+        device. No reference counterpart (the reference reads every step's
+        tokens on the host, minitorch/continuous_batching.py:143,146)."""
+        return self._decode_batch(idx, caches, greedy=True)
+
+    def _decode_batch(self, idx, caches, greedy):
         from .paged_decode import PagedDecodeBatch
         with PagedDecodeBatch(self, idx, caches) as batch:
             batch.prepare()
             dtype = batch.dtype
             w = self._weights(dtype)
             b, d = batch.batch_size, self.n_embd
+            pool = batch.pool
+            if idx is None:
+                idx = DeviceTensor((b, 1), 'float32')
+                paged_ops.gather_slot_tokens(idx.ptr, pool.slot_tokens.ptr, batch.device_slots.ptr,
+                                             pool.max_slots, b)
             x = self._embed(w, idx, batch.position_ids)
             h = DeviceTensor((b, d), dtype)
             lib = model_library()
@@ -317,8 +335,12 @@ class DecoderLM:
                  w.ln_f[1].ptr, w.head.ptr, logits.ptr, self.n_vocab, b, d, self.n_head, self.ln_eps,
                  dtype_code(dtype), 1 if FUSED_GELU else 0, scratch.ptr, scratch_bytes, ct.byref(att))
             batch.mark_layers_written()
+            if greedy:
+                ids = DeviceTensor((b, 1), 'float32')
+                paged_ops.row_argmax_feedback(ids.ptr, pool.slot_tokens.ptr, batch.device_slots.ptr,
+                                              pool.max_slots, logits.ptr, b, self.n_vocab, dtype)
             batch.commit()
-            return logits
+            return ids if greedy else logits
 
 
 def _scratch_bytes(lib, rows, d, dtype):

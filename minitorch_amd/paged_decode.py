@@ -22,7 +22,7 @@ class _DecodeWorkspace:
     def __init__(self):
         self.rows = self.cols = self.work = 0
         self.buffer = None
-        self.staging = None
+        self.stagings = None
         self.partials = None
         self.partial_bytes = 0
 
@@ -35,8 +35,16 @@ class _DecodeWorkspace:
         self.sizes = [4 * r, 4 * self.work, 4 * r, 4 * r, 4 * (r + 1), 4 * r, 4 * r * c]
         self.offsets = np.cumsum([0] + [(s + 255) // 256 * 256 for s in self.sizes]).tolist()
         self.buffer = RawDeviceBuffer(int(self.offsets[-1]))
-        # slots and the work list go up in one copy
-        self.staging = PinnedHostBuffer(int(self.offsets[2]))
+        # slots and the work list go up in one copy, from two staging buffers
+        # used in turn, so that a step can be prepared while the previous
+        # step's upload is still queued
+        self.stagings = [PinnedHostBuffer(int(self.offsets[2])) for _ in range(2)]
+        self.turn = 0
+
+    @property
+    def staging(self):
+        self.turn ^= 1
+        return self.stagings[self.turn]
 
     def ensure_partials(self, nbytes):
         if nbytes > self.partial_bytes:
@@ -64,7 +72,10 @@ class PagedDecodeBatch:
         self.pool = self.caches[0].pool
         self.dtype, self.layout = self.pool.dtype, self.pool.layout
         self.batch_size = len(self.caches)
-        if not isinstance(idx, DeviceTensor) or idx.shape != (self.batch_size, 1) or idx.dtype != 'float32':
+        # idx None: the token IDs are the caches' last tokens kept on the
+        # device (token feedback of the sync-free decode loop).
+        if idx is not None and (not isinstance(idx, DeviceTensor) or idx.shape != (self.batch_size, 1)
+                                or idx.dtype != 'float32'):
             raise ValueError('Expected FP32 token IDs [request_count,1] on model backend')
         for cache in self.caches:
             cache._validate_model(model)
@@ -110,6 +121,7 @@ class PagedDecodeBatch:
         self._device_prepared = True
         self._ws = ws
         self.table = _DeviceView(ws.buffer, int(ws.offsets[6]), 4 * b * self.columns)
+        self.device_slots = _DeviceView(ws.buffer, int(ws.offsets[0]), 4 * b)
         self.device_offsets = _DeviceView(ws.buffer, int(ws.offsets[2]), 4 * b)
         self.cu_seqlens = _DeviceView(ws.buffer, int(ws.offsets[4]), 4 * (b + 1))
         self.work = _DeviceView(ws.buffer, int(ws.offsets[1]), 4 * len(work))

@@ -108,6 +108,7 @@ class KVPagePool:
         self._leased_count = 0
         self.page_acquires = self.page_releases = self.page_reuses = 0
         self._slot_used = bytearray(self.max_slots)
+        self._slot_tokens = None
         self._owner_ids = {}
         self._next_owner = self.max_slots
         self.closed = False
@@ -190,6 +191,17 @@ class KVPagePool:
     def _free_slots(self, first, n):
         self._slot_used[first:first + n] = b'\x00' * n
 
+    @property
+    def slot_tokens(self):
+        """Device fp32 array [max_slots]: the last token of each cache slot's
+        request, written by the greedy selection of a prefill or decode step
+        and read by the next decode step (device-side token feedback). Starts
+        as NaN (an unset token embeds as a NaN row)."""
+        if self._slot_tokens is None:
+            self._slot_tokens = RawDeviceBuffer(4 * self.max_slots)
+            self._slot_tokens.fill_words(0x7FC00000)
+        return self._slot_tokens
+
     def _owner_id(self, owner):
         key = id(owner)
         if key not in self._owner_ids:
@@ -243,8 +255,9 @@ class KVPagePool:
             raise ValueError('Cannot close page pool while caches own pages')
         self._slabs.clear()
         self._free_issued.clear()
-        for buffer in (self.kv, self.state, self.slot_ids, self._scratch):
-            buffer.close()
+        for buffer in (self.kv, self.state, self.slot_ids, self._scratch, self._slot_tokens):
+            if buffer is not None:
+                buffer.close()
         self.closed = True
 
 

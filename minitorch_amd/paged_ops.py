@@ -117,6 +117,21 @@ def row_argmax(dst, src, rows, width, dtype):
          dtype_code(dtype))
 
 
+def row_argmax_feedback(dst, slot_tokens, slots, num_slots, src, rows, width, dtype):
+    """``mt_row_argmax_feedback``: ``row_argmax`` that also stores each row's
+    token in ``slot_tokens[slots[r]]`` (the device-side token feedback of the
+    sync-free decode loop)."""
+    call(inference_library(), 'mt_row_argmax_feedback', [P, P, P, I, P, I, I, I], dst, slot_tokens,
+         slots, num_slots, src, rows, width, dtype_code(dtype))
+
+
+def gather_slot_tokens(ids, slot_tokens, slots, num_slots, rows):
+    """``mt_gather_slot_tokens``: ``ids[r] = slot_tokens[slots[r]]`` (NaN for a
+    slot outside the table)."""
+    call(inference_library(), 'mt_gather_slot_tokens', [P, P, P, I, I], ids, slot_tokens, slots,
+         num_slots, rows)
+
+
 def last_row(dst, src, b, n, w, dtype):
     """``mt_last_row`` (reference src/inference_kernels.cu:66-72)."""
     call(inference_library(), 'mt_last_row', [P, P, I, I, I, I], dst, src, b, n, w,

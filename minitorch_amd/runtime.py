@@ -43,7 +43,7 @@ class HipRuntime:
             'mt_fill': [P, I, F], 'mt_fill_words': [P, Z, ct.c_uint],
             'mt_event_create': [ct.POINTER(P)], 'mt_event_record': [P],
             'mt_event_elapsed': [ct.POINTER(F), P, P], 'mt_event_destroy': [P],
-            'mt_event_synchronize': [P],
+            'mt_event_synchronize': [P], 'mt_event_query': [P],
             'mt_device_count': [ct.POINTER(I)], 'mt_compute_units': [ct.POINTER(I)],
             'mt_host_alloc': [ct.POINTER(P), Z], 'mt_host_free': [P],
             'mt_fill_random': [P, ct.c_longlong, ct.c_ulonglong, I],
@@ -53,6 +53,7 @@ class HipRuntime:
             f.argtypes, f.restype = args, I
         self.lib.mt_error.argtypes = [I]
         self.lib.mt_error.restype = ct.c_char_p
+        self._staging = None
 
     def check(self, status):
         if status:
@@ -86,7 +87,17 @@ class HipRuntime:
             self.stats['frees'] += 1
 
     def h2d(self, dst, array):
+        """Copy a host array to device memory. Arrays up to STAGED_UPLOAD_BYTES
+        are copied into pinned staging memory and uploaded asynchronously on
+        the null stream (stream-ordered before any later launch or read-back),
+        so a small upload does not wait for the work already queued; larger
+        ones use a blocking copy."""
         a = np.ascontiguousarray(array)
+        if a.nbytes <= STAGED_UPLOAD_BYTES:
+            if self._staging is None:
+                self._staging = _StagingRing()
+            self._staging.upload(dst, a)
+            return
         self.check(self.lib.mt_copy(dst, a.ctypes.data, a.nbytes, 1))
         self.stats['h2d_bytes'] += a.nbytes
 
@@ -241,6 +252,24 @@ def allocator():
     return _allocator
 
 
+STAGED_UPLOAD_BYTES = 1 << 16
+HIP_ERROR_NOT_READY = 600
+
+
+class _StagingRing:
+    """Pinned staging buffers used round-robin by small uploads; a buffer is
+    reused only after the upload that last read it has run."""
+
+    def __init__(self, count=16):
+        self.buffers = [PinnedHostBuffer(STAGED_UPLOAD_BYTES) for _ in range(count)]
+        self.next = 0
+
+    def upload(self, dst, array):
+        buffer = self.buffers[self.next]
+        self.next = (self.next + 1) % len(self.buffers)
+        buffer.upload_async(dst, array)
+
+
 class PinnedHostBuffer:
     """Pinned host staging memory for asynchronous host-to-device uploads."""
 
@@ -369,6 +398,14 @@ class CudaEvent:
 
     def synchronize(self):
         self.runtime.check(self.runtime.lib.mt_event_synchronize(self.handle))
+
+    def query(self):
+        """True once the work before the last record has completed."""
+        status = self.runtime.lib.mt_event_query(self.handle)
+        if status == HIP_ERROR_NOT_READY:
+            return False
+        self.runtime.check(status)
+        return True
 
     def seconds_since(self, start):
         ms = F()

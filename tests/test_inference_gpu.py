@@ -66,3 +66,38 @@ def test_last_position(dtype):
     got = last_position(t).raw_numpy()
     ref = po.last_row(t.raw_numpy())
     assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize('dtype', ['float32', 'float16', 'bfloat16'])
+def test_row_argmax_feedback_scatters_to_slots_and_gather_reads_them(dtype):
+    # Token feedback of the sync-free decode loop: the argmax of row r is also
+    # stored in slot_tokens[slots[r]] (slots outside the table are skipped),
+    # and the gather reads slot_tokens[slots[r]] back (NaN outside the table).
+    from minitorch_amd import paged_ops
+    from minitorch_amd.runtime import RawDeviceBuffer
+    code = {'float32': 0, 'float16': 1, 'bfloat16': 2}[dtype]
+    rng = np.random.default_rng(21)
+    rows, width, num_slots = 6, 50257, 40
+    x = rng.standard_normal((rows, 1, width)).astype(np.float32)
+    stored = po.encode(x, code)
+    t = DeviceTensor(x.shape, dtype)
+    runtime().h2d(t.ptr, stored)
+    slots = np.array([3, 17, -1, 39, 40, 5], np.int32)
+    slot_dev = RawDeviceBuffer(4 * rows)
+    slot_dev.upload(slots)
+    table = RawDeviceBuffer(4 * num_slots)
+    table.upload(np.full(num_slots, 7.0, np.float32))
+    ids = DeviceTensor((rows, 1), 'float32')
+    paged_ops.row_argmax_feedback(ids.ptr, table.ptr, slot_dev.ptr, num_slots, t.ptr, rows, width, dtype)
+    got = ids.to_numpy()[:, 0]
+    ref = po.row_argmax(po.decode(stored, code))[:, 0]
+    assert got.tolist() == ref.tolist()
+    expect = np.full(num_slots, 7.0, np.float32)
+    for r, s in enumerate(slots):
+        if 0 <= s < num_slots:
+            expect[s] = ref[r]
+    assert np.array_equal(table.download(np.float32), expect)
+    back = DeviceTensor((rows, 1), 'float32')
+    paged_ops.gather_slot_tokens(back.ptr, table.ptr, slot_dev.ptr, num_slots, rows)
+    want = np.array([expect[s] if 0 <= s < num_slots else np.nan for s in slots], np.float32)
+    assert np.array_equal(back.to_numpy()[:, 0], want, equal_nan=True)

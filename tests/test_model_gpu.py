@@ -79,19 +79,24 @@ def test_decode_batch_equals_independent_decode_fp32():
     assert pool.memory_stats()['kv_pool_used_pages'] == 0
 
 
-def run_trace(model, trace, precision='fp32', max_batch_size=4, budget_pages=None, page_size=16):
-    """Replay (arrival_step, id, prompt, new_tokens) on a step-indexed clock."""
+def run_trace(model, trace, precision='fp32', max_batch_size=4, budget_pages=None, page_size=16,
+              token_feedback=False, eos=None):
+    """Replay (arrival_step, id, prompt, new_tokens) on a step-indexed clock;
+    ``eos`` maps request IDs to EOS token IDs. Returns the batcher, the
+    per-step statistics and the events each step returned."""
     page_bytes = 2 * model.n_layer * model.n_embd * page_size * (4 if precision == 'fp32' else 2)
     budget = (budget_pages or 4096) * page_bytes
     batcher = ContinuousBatcher(model, max_batch_size=max_batch_size, page_size=page_size,
-                                kv_budget_bytes=budget, precision=precision)
-    steps, pending = [], sorted(trace)
+                                kv_budget_bytes=budget, precision=precision, token_feedback=token_feedback)
+    steps, pending, events = [], sorted(trace), []
     while pending or batcher.has_work:
         while pending and pending[0][0] <= batcher.iteration:
             _, rid, prompt, new = pending.pop(0)
-            batcher.submit(rid, np.array(prompt), max_new_tokens=new)
-        batcher.step()
+            batcher.submit(rid, np.array(prompt), max_new_tokens=new, eos_token_id=(eos or {}).get(rid))
+        events.append(batcher.step())
         steps.append(dict(batcher.last_step))
+    if token_feedback:
+        return batcher, steps, events
     return batcher, steps
 
 
@@ -162,3 +167,94 @@ def test_distilgpt2_shape_fp32_tokens_match_oracle():
     got = generate(model, prompt, 4)
     ref, margins = go.greedy(model.state, prompt, 4, n_head=12, n_layer=6)
     assert got == ref, margins
+
+
+SCHEDULE_KEYS = ('decode_request_ids', 'prefill_request_ids', 'active_request_ids', 'logical_reserved_pages',
+                 'peak_used_pages', 'kv_pool_used_pages', 'kv_pool_free_pages', 'kv_pool_page_acquires',
+                 'kv_pool_page_releases', 'kv_pool_page_reuses')
+
+
+def assert_same_run(sync, sync_steps, fb, fb_steps, fb_events, trace):
+    """The sync-free loop makes the synchronous loop's decisions, pages and
+    tokens; it only delivers tokens later (trailing steps just deliver)."""
+    for rid in (t[1] for t in trace):
+        a, b = sync.requests[rid], fb.requests[rid]
+        assert (b.output_ids, b.state, b.finish_reason) == (a.output_ids, a.state, a.finish_reason), rid
+    assert len(fb_steps) >= len(sync_steps)
+    for i, (s, f) in enumerate(zip(sync_steps, fb_steps)):
+        for key in SCHEDULE_KEYS:
+            assert s[key] == f[key], (i, key, s[key], f[key])
+    for f in fb_steps[len(sync_steps):]:
+        assert f['decode_batch_size'] == 0 and not f['prefill_request_ids']
+    assert fb_steps[-1]['tokens_in_flight'] == 0
+    delivered = {}
+    for step_events in fb_events:
+        for e in step_events:
+            delivered.setdefault(e['request_id'], []).append(e['token_id'])
+    assert delivered == {rid: fb.requests[rid].output_ids for rid in delivered}
+    assert sum(map(len, delivered.values())) == sum(len(fb.requests[t[1]].output_ids) for t in trace)
+
+
+@pytest.mark.parametrize('precision', ['fp32', 'bf16'])
+def test_sync_free_loop_matches_synchronous_loop(precision):
+    model = tiny(seed=14)
+    rng = np.random.default_rng(14)
+    trace = make_trace(model, rng, 12)
+    sync, sync_steps = run_trace(model, trace, precision=precision, max_batch_size=3, budget_pages=30)
+    fb, fb_steps, fb_events = run_trace(model, trace, precision=precision, max_batch_size=3, budget_pages=30,
+                                        token_feedback=True)
+    assert_same_run(sync, sync_steps, fb, fb_steps, fb_events, trace)
+    if precision == 'fp32':
+        for _, rid, prompt, new in trace:
+            assert fb.requests[rid].output_ids == generate(model, prompt, new), rid
+    assert fb_steps[-1]['kv_pool_used_pages'] == 0 and fb.reserved_pages == 0
+    sync.close()
+    fb.close()
+
+
+def test_sync_free_loop_with_eos_waits_for_tokens():
+    # Requests with an EOS token finish on its value, so their steps read the
+    # tokens back before scheduling on; the EOS IDs are taken from the
+    # synchronous run's tokens so that some requests stop early.
+    model = tiny(seed=15)
+    rng = np.random.default_rng(15)
+    trace = make_trace(model, rng, 10)
+    plain, _ = run_trace(model, trace, max_batch_size=3, budget_pages=30)
+    eos = {rid: plain.requests[rid].output_ids[len(plain.requests[rid].output_ids) // 2]
+           for _, rid, _, new in trace[::2] if new > 2}
+    plain.close()
+    sync, sync_steps = run_trace(model, trace, max_batch_size=3, budget_pages=30, eos=eos)
+    assert any(sync.requests[rid].finish_reason == 'eos' for rid in eos)
+    fb, fb_steps, fb_events = run_trace(model, trace, max_batch_size=3, budget_pages=30, token_feedback=True,
+                                        eos=eos)
+    assert_same_run(sync, sync_steps, fb, fb_steps, fb_events, trace)
+    sync.close()
+    fb.close()
+
+
+def test_decode_greedy_reads_and_writes_slot_tokens():
+    # decode_greedy with idx None takes each row's last token from the pool's
+    # slot table (set by the prefill's greedy selection) and equals the host
+    # round-trip path.
+    model = tiny(seed=16)
+    rng = np.random.default_rng(16)
+    prompts = [rng.integers(0, model.n_vocab, n).tolist() for n in (4, 19, 33)]
+    expect = [generate(model, p, 5) for p in prompts]
+    from minitorch_amd.paged_kv_cache import KVPagePool
+    pool = KVPagePool(model, page_size=16, max_bytes=64 * 1024 ** 2)
+    caches, first = [], []
+    for p in prompts:
+        c = model.create_kv_cache(1, len(p) + 4, page_size=16, page_pool=pool)
+        logits, _ = model.prefill(DeviceTensor.from_numpy(np.array([p], np.float32)), c)
+        first.append(int(greedy_token(logits, feedback=c).to_numpy()[0, 0]))
+        caches.append(c)
+    tokens = [[t] for t in first]
+    for _ in range(4):
+        ids = model.decode_greedy(caches).to_numpy()[:, 0]
+        for t, n in zip(tokens, ids):
+            t.append(int(n))
+    assert tokens == expect
+    slot_tokens = pool.slot_tokens.download(np.float32)
+    assert [int(slot_tokens[c.slot]) for c in caches] == [t[-1] for t in tokens]
+    for c in caches:
+        c.close()
