@@ -34,6 +34,14 @@ typedef struct mt_decode_attention {
   void* partials; size_t partial_bytes;
 } mt_decode_attention;
 
+/* Paged-cache metadata of one prefill (n new tokens per request at a common
+ * offset), as mt_paged_prefill takes it (include/mt_paged.h); the layer index
+ * is supplied per layer. */
+typedef struct mt_prefill_attention {
+  const uint64_t* slabs; const int* table;
+  int page_size, pages_per_slab, num_slabs, columns, layers, offset;
+} mt_prefill_attention;
+
 /* hipBLASLt handle with a 64 MiB workspace and per-shape plans.
  * Replace reference mt_blas_create / mt_blas_destroy (src/cuda_runtime.cu:22-23). */
 int mt_blas_create(void** handle);
@@ -122,6 +130,23 @@ int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
                       void* logits, int vocab, int rows, int d, int heads, float eps, int dtype,
                       int fused_gelu, void* scratch, size_t scratch_bytes,
                       const mt_decode_attention* att);
+
+/* The layer loop of a prefill of n tokens for each of batch requests, all
+ * launches issued from here on the null stream: as mt_decoder_layers, with
+ * rows = batch * n token rows (x [rows, d] fp32, updated in place; h [rows, d]
+ * in dtype) and, per layer, mt_paged_prefill appending K/V at att->offset and
+ * computing causal attention, with q/k/v read as column blocks of the fused
+ * QKV output and the output written with heads merged. When logits is not
+ * null, logits [batch, vocab] = final-LayerNorm(x)[last position of each
+ * request] @ head_weight^T. The projections keep hipBLASLt's first heuristic
+ * choice (prompt lengths vary). Scratch as mt_decoder_scratch_bytes(rows).
+ * Replaces the reference's per-op layer loop of DecoderLM.prefill
+ * (minitorch/modules_transformer.py:355-365,258-284). */
+int mt_prefill_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
+                      const float* final_gamma, const float* final_beta, const void* head_weight,
+                      void* logits, int vocab, int batch, int n, int d, int heads, float eps,
+                      int dtype, int fused_gelu, void* scratch, size_t scratch_bytes,
+                      const mt_prefill_attention* att);
 
 #ifdef __cplusplus
 }

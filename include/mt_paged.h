@@ -85,6 +85,21 @@ int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v
                           int work_items, int merge_rows, void* workspace,
                           size_t workspace_bytes);
 
+/* Prefill of n tokens per request at a common offset, in one call: appends
+ * k/v (as mt_paged_append) and computes causal attention of the n queries
+ * over keys [0, offset + n) (as mt_paged_attention), with token-major rows:
+ * q, k and v are [b, n, qkv_stride] with head j at columns [j*d, (j+1)*d)
+ * (qkv_stride = 3*h*d when they are column blocks of one fused projection;
+ * 0 = h*d) and out is [b, n, out_stride] with heads merged the same way
+ * (0 = h*d). The matrix-core kernel serves fp16/bf16 with d 64 or 128 and
+ * n >= 16. No reference counterpart as one entry (reference
+ * paged_kv_cache.py:205-221 calls mt_paged_append and mt_paged_attention on
+ * head-split copies). */
+int mt_paged_prefill(void* out, const void* q, const void* k, const void* v, const uint64_t* slabs,
+                     const int* table, int b, int h, int n, int d, int page_size,
+                     int pages_per_slab, int num_slabs, int columns, int layer, int layers,
+                     int offset, int dtype, int qkv_stride, int out_stride);
+
 #ifdef __cplusplus
 }
 #endif

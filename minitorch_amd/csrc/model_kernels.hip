@@ -55,7 +55,7 @@ struct Blas {
   bool tune = true;       // MT_GEMM_TUNE=0 keeps the heuristic's first choice everywhere
   size_t workspace_bytes = size_t(64) << 20;
   std::mutex mutex;
-  std::map<std::tuple<int, int, int, int, int, int, int, int>, Plan> plans;
+  std::map<std::tuple<int, int, int, int, int, int, int, int, int>, Plan> plans;
 };
 
 int blas_status(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS ? 0 : 1000 + int(s); }
@@ -116,9 +116,11 @@ int pick_fastest(Blas* blas, Plan& p, const hipblasLtMatmulHeuristicResult_t* he
 // op(B)^T A^T, i.e. a column-major GEMM with rows n, columns m; the bias is
 // per row of C^T.
 int gemm(Blas* blas, void* out, const void* a, const void* b, const void* bias, int m, int n,
-         int k, int transb, int dtype, int out_dtype, int epilogue = kEpiNone, bool tunable = false) {
+         int k, int transb, int dtype, int out_dtype, int epilogue = kEpiNone, bool tunable = false,
+         int lda = 0) {
+  if (lda == 0) lda = k;  // elements between consecutive rows of a
   std::lock_guard<std::mutex> lock(blas->mutex);
-  auto key = std::make_tuple(m, n, k, transb, dtype, out_dtype, bias ? 1 : 0, epilogue);
+  auto key = std::make_tuple(m, n, k, transb, dtype, out_dtype, bias ? 1 : 0, epilogue, lda);
   Plan& p = blas->plans[key];
   if (!p.ok) {
     // On any failure below the partial plan is released so a later call can retry.
@@ -152,7 +154,7 @@ int gemm(Blas* blas, void* out, const void* a, const void* b, const void* bias, 
     if ((s = transb ? hipblasLtMatrixLayoutCreate(&p.la, in, k, n, k)
                     : hipblasLtMatrixLayoutCreate(&p.la, in, n, k, n)))
       return blas_status(s);
-    if ((s = hipblasLtMatrixLayoutCreate(&p.lb, in, k, m, k))) return blas_status(s);
+    if ((s = hipblasLtMatrixLayoutCreate(&p.lb, in, k, m, lda))) return blas_status(s);
     if ((s = hipblasLtMatrixLayoutCreate(&p.lc, outt, n, m, n))) return blas_status(s);
     hipblasLtMatmulPreference_t pref;
     if ((s = hipblasLtMatmulPreferenceCreate(&pref))) return blas_status(s);
@@ -545,6 +547,52 @@ int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
   // Tied head: logits [rows, vocab] = h @ head_weight^T (head_weight [vocab, d]).
   if (!st && logits)
     st = gemm(blas, logits, h, head_weight, nullptr, rows, vocab, d, 1, dtype, dtype, kEpiNone, true);
+  return st;
+}
+
+int mt_prefill_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
+                      const float* final_gamma, const float* final_beta, const void* head_weight,
+                      void* logits, int vocab, int batch, int n, int d, int heads, float eps,
+                      int dtype, int fused_gelu, void* scratch, size_t scratch_bytes,
+                      const mt_prefill_attention* att) {
+  const int64_t rows64 = int64_t(batch) * n;
+  if (!handle || !layers || n_layer < 1 || !x || !h || !final_gamma || !final_beta ||
+      (logits && (!head_weight || vocab < 1)) || batch < 1 || n < 1 || rows64 > INT32_MAX ||
+      d < 1 || heads < 1 || d % heads || !dtype_ok(dtype) || !scratch || !att ||
+      scratch_bytes < mt_decoder_scratch_bytes(int(rows64), d, dtype) || rows64 * 4 * d > INT32_MAX)
+    return hipErrorInvalidValue;
+  const int rows = int(rows64);
+  Blas* blas = static_cast<Blas*>(handle);
+  const size_t e = dtype == kF32 ? 4 : 2;
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+  char* base = static_cast<char*>(scratch);
+  char* qkv = base;
+  char* attn = qkv + al(size_t(rows) * 3 * d * e);
+  char* proj = attn + al(size_t(rows) * d * e);
+  char* mlp = proj + al(size_t(rows) * d * e);
+  const int hd = d / heads;
+  int st = layernorm(h, x, layers[0].ln1_gamma, layers[0].ln1_beta, rows, d, eps, dtype);
+  for (int i = 0; i < n_layer && !st; ++i) {
+    const mt_decoder_layer& L = layers[i];
+    if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 0, dtype, dtype))) break;
+    if ((st = mt_paged_prefill(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, att->slabs,
+                               att->table, batch, heads, n, hd, att->page_size, att->pages_per_slab,
+                               att->num_slabs, att->columns, i, att->layers, att->offset, dtype, 3 * d,
+                               d)))
+      break;
+    if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 0, dtype, dtype))) break;
+    if ((st = residual_layernorm(h, x, proj, L.ln2_gamma, L.ln2_beta, rows, d, eps, dtype))) break;
+    if ((st = gemm_gelu(blas, mlp, h, L.w_fc, L.b_fc, rows, 4 * d, d, dtype, fused_gelu != 0, false))) break;
+    if ((st = gemm(blas, proj, mlp, L.w_proj, L.b_proj, rows, d, 4 * d, 0, dtype, dtype))) break;
+    const bool last = i + 1 == n_layer;
+    st = residual_layernorm(h, x, proj, last ? final_gamma : layers[i + 1].ln1_gamma,
+                            last ? final_beta : layers[i + 1].ln1_beta, rows, d, eps, dtype);
+  }
+  // Tied head over the last position of each request: rows n - 1, 2n - 1, ...
+  // of h, read with a row stride of n * d.
+  if (!st && logits)
+    st = gemm(blas, logits, static_cast<char*>(h) + size_t(n - 1) * d * e, head_weight, nullptr, batch,
+              vocab, d, 1, dtype, dtype, kEpiNone, false, n * d);
   return st;
 }
 

@@ -799,6 +799,9 @@ struct QueryArgs {
   float qscale;
   int64_t items;
   Geometry g;
+  // Element strides of q and out per request, head and query: [b, h, nq, d]
+  // by default, [b, nq, row] for head-interleaved token rows.
+  int64_t q_b, q_h, q_r, o_b, o_h, o_r;
 };
 
 // Causal paged attention for nq >= 1 queries per (request, head)
@@ -830,7 +833,7 @@ __global__ __launch_bounds__(kThreads) void query_kernel(QueryArgs a) {
     const int64_t kmax = int64_t(a.offset) + qlast + 1 < a.nk ? int64_t(a.offset) + qlast + 1 : a.nk;
     const int* table_row = a.table + int64_t(b) * g.columns;
     Query<DT, D, VEC> qv;
-    qv.load(qp + (bh * a.nq + (has_q ? qi : 0)) * dim, col0, dim, a.qscale);
+    qv.load(qp + b * a.q_b + head * a.q_h + (has_q ? qi : 0) * a.q_r, col0, dim, a.qscale);
     Softmax<DL> st;
     st.init();
     for (int64_t c0 = 0; c0 < kmax; c0 += kMaxSplitTokens) {
@@ -845,7 +848,7 @@ __global__ __launch_bounds__(kThreads) void query_kernel(QueryArgs a) {
     }
     st.wave_merge();
     if (has_q && lane < kGroup) {
-      T* orow = out + (bh * a.nq + qi) * dim;
+      T* orow = out + b * a.o_b + head * a.o_h + qi * a.o_r;
       for (int i = 0; i < DL; ++i)
         if (col0 + i < dim) orow[col0 + i] = from_f32<DT>(finalize(st.acc[i], st.l));
     }
@@ -861,6 +864,7 @@ struct AppendArgs {
   int batch, n, offset;
   int64_t vectors;  // number of per-thread units
   Geometry g;
+  int64_t src_b, src_h, src_r;  // element strides of k/v per request, head and token
 };
 
 
@@ -989,7 +993,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
     const bool q_ok = qi < a.nq;
     V8 qv[DS];
     {
-      const T* row = qp + (bh * a.nq + (q_ok ? qi : 0)) * D;
+      const T* row = qp + b * a.q_b + head * a.q_h + (q_ok ? qi : 0) * a.q_r;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds)
         qv[ds] = __builtin_bit_cast(V8, *global_view(reinterpret_cast<const u32x4*>(row + 32 * ds + 8 * grp)));
@@ -1013,7 +1017,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
     // branch waits for them before the block in between is computed.
     u32x4 kx[NC], vx[NC];
     int kstate[NC];  // 0 = loaded, 1 = missing page, 2 = past the window
-    const T* dummy = qp + (bh * a.nq + (q_ok ? qi : 0)) * D;
+    const T* dummy = qp + b * a.q_b + head * a.q_h + (q_ok ? qi : 0) * a.q_r;
     auto stage_load = [&](int k0, int w0, int w1) {
 #pragma unroll
       for (int n = 0; n < NC; ++n) {
@@ -1144,7 +1148,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
     l += lane_swap32(l);
     // O^T lane layout: dims dt*16 + 4*grp + i of query qi.
     if (q_ok) {
-      T* orow = out + (bh * a.nq + qi) * D;
+      T* orow = out + b * a.o_b + head * a.o_h + qi * a.o_r;
 #pragma unroll
       for (int dt = 0; dt < DT16; ++dt) {
         const T r0 = from_f32<DT>(finalize(o[dt][0], l)), r1 = from_f32<DT>(finalize(o[dt][1], l));
@@ -1179,7 +1183,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     if (!base) continue;
     T* kp = const_cast<T*>(base) + (pos & (g.page_size - 1)) * dim + col;
     T* vp = kp + g.kind_stride;
-    const int64_t src = row * dim + col;
+    const int64_t src = b * a.src_b + head * a.src_h + pos_in * a.src_r + col;
     if constexpr (VEC) {
       *global_view(reinterpret_cast<u32x4*>(kp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k) + src));
       *global_view(reinterpret_cast<u32x4*>(vp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v) + src));
@@ -1366,6 +1370,63 @@ int library_workspace(size_t bytes, void** out) {
   return hipSuccess;
 }
 
+// Launch of the append kernel for any source strides; the 16-byte path needs
+// 16-byte aligned rows.
+hipError_t launch_append(AppendArgs& a, int dtype) {
+  const int d = a.g.dim;
+  const int esize = dtype == kF32 ? 4 : 2;
+  const int E = 16 / esize;
+  const bool vec = d % E == 0 && aligned16(a.k) && aligned16(a.v) &&
+                   (a.src_b * esize) % 16 == 0 && (a.src_h * esize) % 16 == 0 &&
+                   (a.src_r * esize) % 16 == 0;
+  a.vectors = int64_t(a.batch) * a.g.heads * a.n * (vec ? d / E : d);
+  const int blocks = int((a.vectors + 255) / 256 < 65536 * 16 ? (a.vectors + 255) / 256 : 65536 * 16);
+#define MT_APPEND(DT)                                                        \
+  if (vec) append_kernel<DT, true><<<blocks, 256>>>(a);                      \
+  else append_kernel<DT, false><<<blocks, 256>>>(a);
+  if (dtype == kF32) { MT_APPEND(kF32) }
+  else if (dtype == kF16) { MT_APPEND(kF16) }
+  else { MT_APPEND(kBF16) }
+#undef MT_APPEND
+  return hipGetLastError();
+}
+
+// Causal attention launch for any q/out strides: the matrix-core prefill
+// kernel for fp16/bf16, head_dim 64/128, 16-byte aligned rows and at least
+// kPfMinQueries queries; the per-query kernel otherwise.
+hipError_t launch_query(QueryArgs& a, int dtype) {
+  const int d = a.g.dim;
+  const int esize = dtype == kF32 ? 4 : 2;
+  auto rows16 = [&](int64_t x) { return (x * esize) % 16 == 0; };
+  const bool vec = (d == 64 || d == 128) && aligned16(a.out) && aligned16(a.q) && rows16(a.q_b) &&
+                   rows16(a.q_h) && rows16(a.q_r) && rows16(a.o_b) && rows16(a.o_h) && rows16(a.o_r);
+  a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
+  const int h = a.g.heads;
+  if (vec && dtype != kF32 && a.nq >= kPfMinQueries) {
+    a.items = int64_t(a.batch) * h * ((a.nq + kPfQueries - 1) / kPfQueries);
+    const int blocks = grid_for(a.items);
+    if (dtype == kF16) {
+      if (d == 64) prefill_kernel<kF16, 64><<<blocks, kThreads>>>(a);
+      else prefill_kernel<kF16, 128><<<blocks, kThreads>>>(a);
+    } else {
+      if (d == 64) prefill_kernel<kBF16, 64><<<blocks, kThreads>>>(a);
+      else prefill_kernel<kBF16, 128><<<blocks, kThreads>>>(a);
+    }
+    return hipGetLastError();
+  }
+  a.items = int64_t(a.batch) * h * ((a.nq + kWaves - 1) / kWaves);
+  const int blocks = grid_for(a.items);
+#define MT_QUERY(DT)                                                                   \
+  if (vec && d == 64) query_kernel<DT, 64, true, 2><<<blocks, kThreads>>>(a);          \
+  else if (vec && d == 128) query_kernel<DT, 128, true, 2><<<blocks, kThreads>>>(a);   \
+  else query_kernel<DT, 128, false, 1><<<blocks, kThreads>>>(a);
+  if (dtype == kF32) { MT_QUERY(kF32) }
+  else if (dtype == kF16) { MT_QUERY(kF16) }
+  else { MT_QUERY(kBF16) }
+#undef MT_QUERY
+  return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" {
@@ -1382,18 +1443,8 @@ int mt_paged_append(const void* k, const void* v, const uint64_t* slabs, const i
   AppendArgs a;
   a.k = k; a.v = v; a.slabs = slabs; a.table = table; a.batch = b; a.n = n; a.offset = offset;
   a.g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
-  const int E = dtype == kF32 ? 4 : 8;
-  const bool vec = d % E == 0 && aligned16(k) && aligned16(v);
-  a.vectors = int64_t(b) * h * n * (vec ? d / E : d);
-  const int blocks = int((a.vectors + 255) / 256 < 65536 * 16 ? (a.vectors + 255) / 256 : 65536 * 16);
-#define MT_APPEND(DT)                                                        \
-  if (vec) append_kernel<DT, true><<<blocks, 256>>>(a);                      \
-  else append_kernel<DT, false><<<blocks, 256>>>(a);
-  if (dtype == kF32) { MT_APPEND(kF32) }
-  else if (dtype == kF16) { MT_APPEND(kF16) }
-  else { MT_APPEND(kBF16) }
-#undef MT_APPEND
-  return hipGetLastError();
+  a.src_b = int64_t(h) * n * d; a.src_h = int64_t(n) * d; a.src_r = d;
+  return launch_append(a, dtype);
 }
 
 int mt_paged_attention(void* out, const void* q, const uint64_t* slabs, const int* table, int b,
@@ -1407,32 +1458,40 @@ int mt_paged_attention(void* out, const void* q, const uint64_t* slabs, const in
   QueryArgs a;
   a.out = out; a.q = q; a.slabs = slabs; a.table = table;
   a.batch = b; a.nq = nq; a.nk = nk; a.offset = offset;
-  a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
-  a.items = int64_t(b) * h * ((nq + kWaves - 1) / kWaves);
   a.g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
-  const bool vec = (d == 64 || d == 128) && aligned16(out) && aligned16(q);
-  if (vec && dtype != kF32 && nq >= kPfMinQueries) {
-    a.items = int64_t(b) * h * ((nq + kPfQueries - 1) / kPfQueries);
-    const int blocks = grid_for(a.items);
-    if (dtype == kF16) {
-      if (d == 64) prefill_kernel<kF16, 64><<<blocks, kThreads>>>(a);
-      else prefill_kernel<kF16, 128><<<blocks, kThreads>>>(a);
-    } else {
-      if (d == 64) prefill_kernel<kBF16, 64><<<blocks, kThreads>>>(a);
-      else prefill_kernel<kBF16, 128><<<blocks, kThreads>>>(a);
-    }
-    return hipGetLastError();
-  }
-  const int blocks = grid_for(a.items);
-#define MT_QUERY(DT)                                                                   \
-  if (vec && d == 64) query_kernel<DT, 64, true, 2><<<blocks, kThreads>>>(a);          \
-  else if (vec && d == 128) query_kernel<DT, 128, true, 2><<<blocks, kThreads>>>(a);   \
-  else query_kernel<DT, 128, false, 1><<<blocks, kThreads>>>(a);
-  if (dtype == kF32) { MT_QUERY(kF32) }
-  else if (dtype == kF16) { MT_QUERY(kF16) }
-  else { MT_QUERY(kBF16) }
-#undef MT_QUERY
-  return hipGetLastError();
+  a.q_b = a.o_b = int64_t(h) * nq * d;
+  a.q_h = a.o_h = int64_t(nq) * d;
+  a.q_r = a.o_r = d;
+  return launch_query(a, dtype);
+}
+
+int mt_paged_prefill(void* out, const void* q, const void* k, const void* v, const uint64_t* slabs,
+                     const int* table, int b, int h, int n, int d, int page_size,
+                     int pages_per_slab, int num_slabs, int columns, int layer, int layers,
+                     int offset, int dtype, int qkv_stride, int out_stride) {
+  if (!out || !q || !k || !v || !slabs || !table) return hipErrorInvalidValue;
+  const int64_t hd = int64_t(h) * d;
+  if (qkv_stride == 0) qkv_stride = int(hd);
+  if (out_stride == 0) out_stride = int(hd);
+  if (int64_t(offset) + n > INT32_MAX || qkv_stride < hd || out_stride < hd ||
+      int64_t(b) * n * qkv_stride > INT32_MAX || int64_t(b) * n * out_stride > INT32_MAX ||
+      !paged_shape(b, h, n, offset + n, d, page_size, pages_per_slab, num_slabs, columns, layer,
+                   layers, offset))
+    return hipErrorInvalidValue;
+  if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
+  AppendArgs ap;
+  ap.k = k; ap.v = v; ap.slabs = slabs; ap.table = table; ap.batch = b; ap.n = n; ap.offset = offset;
+  ap.g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
+  ap.src_b = int64_t(n) * qkv_stride; ap.src_h = d; ap.src_r = qkv_stride;
+  hipError_t e = launch_append(ap, dtype);
+  if (e != hipSuccess) return e;
+  QueryArgs a;
+  a.out = out; a.q = q; a.slabs = slabs; a.table = table;
+  a.batch = b; a.nq = n; a.nk = offset + n; a.offset = offset;
+  a.g = ap.g;
+  a.q_b = int64_t(n) * qkv_stride; a.q_h = d; a.q_r = qkv_stride;
+  a.o_b = int64_t(n) * out_stride; a.o_h = d; a.o_r = out_stride;
+  return launch_query(a, dtype);
 }
 
 int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v,

@@ -71,6 +71,12 @@ class DecoderLayerStruct(ct.Structure):
                                        'ln2_gamma', 'ln2_beta', 'w_fc', 'b_fc', 'w_proj', 'b_proj')]
 
 
+class PrefillAttentionStruct(ct.Structure):
+    """``mt_prefill_attention`` (include/mt_model.h)."""
+    _fields_ = [('slabs', P), ('table', P), ('page_size', I), ('pages_per_slab', I), ('num_slabs', I),
+                ('columns', I), ('layers', I), ('offset', I)]
+
+
 class DecodeAttentionStruct(ct.Structure):
     """``mt_decode_attention`` (include/mt_model.h)."""
     _fields_ = [('slabs', P), ('table', P), ('offsets', P),
@@ -280,6 +286,10 @@ class DecoderLM:
                 np.tile(np.arange(offset, offset + n, dtype=np.float32), (b, 1)), 'float32')
             x = self._embed(w, idx, positions)                      # [b*n, d] fp32
             d = self.n_embd
+            if getattr(cache, 'pool', None) is not None:
+                logits = self._paged_layers(w, x, cache, b, n, offset, dtype, prefill)
+                cache.commit_append()
+                return logits
             for i, layer in enumerate(w.layers):
                 hdn = self._layernorm(x, layer['ln_1'], dtype)
                 qkv = self._linear(hdn, layer['qkv'], 3 * d, dtype)
@@ -295,6 +305,28 @@ class DecoderLM:
         except Exception:
             cache.abort_append()
             raise
+
+    def _paged_layers(self, w, x, cache, b, n, offset, dtype, prefill):
+        """The whole layer loop and the last position's logits in one native
+        call (``mt_prefill_layers``), for a paged cache: every layer appends
+        its K/V at ``offset`` and runs causal paged attention."""
+        pool = cache.pool
+        h = DeviceTensor((b * n, self.n_embd), dtype)
+        lib = model_library()
+        scratch_bytes = _scratch_bytes(lib, b * n, self.n_embd, dtype)
+        scratch = DeviceTensor(((scratch_bytes + 3) // 4,), 'float32')
+        att = PrefillAttentionStruct(pool.slab_table.ptr, cache.block_table.ptr, cache.page_size,
+                                     pool.pages_per_slab, pool.num_slabs, pool.max_cols, len(cache.layout),
+                                     offset)
+        logits = DeviceTensor((b, 1, self.n_vocab), dtype)
+        call(lib, 'mt_prefill_layers', [P, P, I, P, P, P, P, P, P, I, I, I, I, I, F, I, I, P, ct.c_size_t, P],
+             self.blas().handle, w.layer_array, self.n_layer, x.ptr, h.ptr, w.ln_f[0].ptr, w.ln_f[1].ptr,
+             w.head.ptr, logits.ptr, self.n_vocab, b, n, self.n_embd, self.n_head, self.ln_eps,
+             dtype_code(dtype), 1 if FUSED_GELU else 0, scratch.ptr, scratch_bytes, ct.byref(att))
+        cache._written_layers.update(range(len(cache.layout)))
+        cache.last_attention_path = ('paged_reference_prefill' if prefill and cache.paged_prefill_impl == 'paged_reference'
+                                     else 'paged_prefill' if prefill else 'paged_decode')
+        return logits
 
     def decode_batch(self, idx, caches):
         """One token per independent paged request in one model batch; rows

@@ -36,6 +36,15 @@ def paged_attention(out, q, slab_table, block_table, *, b, h, nq, nk, d, page_si
          num_slabs, columns, layer, layers, offset, dtype_code(dtype))
 
 
+def paged_prefill(out, q, k, v, slab_table, block_table, *, b, h, n, d, page_size, pages_per_slab,
+                  num_slabs, columns, layer, layers, offset, dtype, qkv_stride=0, out_stride=0):
+    """``mt_paged_prefill``: append + causal attention of n tokens per request
+    over token-major rows (q/k/v [b, n, qkv_stride], out [b, n, out_stride])."""
+    call(paged_library(), 'mt_paged_prefill', [P] * 6 + [I] * 14,
+         out, q, k, v, slab_table, block_table, b, h, n, d, page_size, pages_per_slab, num_slabs,
+         columns, layer, layers, offset, dtype_code(dtype), qkv_stride, out_stride)
+
+
 def paged_decode_batch(out, q, k, v, slab_table, block_table, offsets, *, b, h, d, page_size,
                        pages_per_slab, num_slabs, columns, layer, layers, dtype):
     """``mt_paged_decode_batch`` (reference src/paged_attention_kernel.cu:121-137)."""

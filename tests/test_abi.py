@@ -148,3 +148,17 @@ def test_error_strings():
     lib.mt_error.argtypes, lib.mt_error.restype = [I], ct.c_char_p
     assert lib.mt_error(0)
     assert lib.mt_error(1)
+
+
+def test_paged_prefill_rejects_invalid_arguments():
+    lib = library('paged_attention_kernel')
+    f = lib.mt_paged_prefill
+    f.argtypes, f.restype = [P] * 6 + [I] * 14, I
+    ptrs = (8, 8, 8, 8, 8, 8)
+    #       b  h  n  d   P   pps slabs cols layer layers offset dtype qkv_stride out_stride
+    assert f(*ptrs, 2, 3, 5, 64, 16, 4, 4, 8, 0, 1, 0, 1, 100, 0) == 1      # qkv_stride < h*d
+    assert f(*ptrs, 2, 3, 5, 64, 16, 4, 4, 8, 0, 1, 0, 1, 0, 100) == 1      # out_stride < h*d
+    assert f(*ptrs, 2, 3, 5, 64, 12, 4, 4, 8, 0, 1, 0, 1, 0, 0) == 1        # page size
+    assert f(*ptrs, 2, 3, 5, 64, 16, 4, 4, 8, 0, 1, 0, 3, 0, 0) == 1        # dtype
+    assert f(*ptrs, 2, 3, 5, 64, 16, 4, 4, 8, 1, 1, 0, 1, 0, 0) == 1        # layer >= layers
+    assert f(None, *ptrs[1:], 2, 3, 5, 64, 16, 4, 4, 8, 0, 1, 0, 1, 0, 0) == 1

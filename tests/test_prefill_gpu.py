@@ -132,3 +132,46 @@ def test_prefill_matches_per_query_kernel_below_threshold():
     dev = DevicePagedCase(case)
     run_prefill(case, 15, 59, 44, seed=9, dev=dev)
     run_prefill(case, 16, 60, 44, seed=9, dev=dev)
+
+
+@pytest.mark.parametrize('dtype', ['float32', 'float16', 'bfloat16'])
+@pytest.mark.parametrize('n', [5, 70])
+def test_paged_prefill_token_major_equals_append_then_attention(dtype, n):
+    # mt_paged_prefill reads q/k/v as column blocks of a fused [b, n, 3*h*d]
+    # projection and writes [b, n, h*d]; it must equal mt_paged_append +
+    # mt_paged_attention on head-split copies bit for bit (same kernels), and
+    # the oracle within tolerance.
+    b, h, d, offset = 2, 3, 64, 21
+    case = prefill_case(50 + n, batch=b, heads=h, dim=d, page_size=16, nk=offset + n, dtype=dtype)
+    rng = np.random.default_rng(n)
+    qkv = po.encode(rng.standard_normal((b, n, 3 * h * d), dtype=np.float32), CODES[dtype])
+    heads = lambda blk: np.ascontiguousarray(qkv[:, :, blk * h * d:(blk + 1) * h * d]
+                                             .reshape(b, n, h, d).transpose(0, 2, 1, 3))
+    q, k, v = heads(0), heads(1), heads(2)
+    common = dict(page_size=16, pages_per_slab=case.pages_per_slab, num_slabs=case.num_slabs,
+                  columns=case.columns, layer=0, layers=1, dtype=dtype)
+    one, two = DevicePagedCase(case), DevicePagedCase(case)
+    fused = DeviceTensor(qkv.shape, dtype)
+    runtime().h2d(fused.ptr, qkv)
+    item = 4 if dtype == 'float32' else 2
+    out1 = DeviceTensor((b, n, h * d), dtype)
+    paged_ops.paged_prefill(out1.ptr, fused.ptr, fused.ptr + h * d * item, fused.ptr + 2 * h * d * item,
+                            one.slab_table.ptr, one.block_table.ptr, b=b, h=h, n=n, d=d, offset=offset,
+                            qkv_stride=3 * h * d, out_stride=h * d, **common)
+    qd, kd, vd = (DeviceTensor(x.shape, dtype) for x in (q, k, v))
+    for t, x in ((qd, q), (kd, k), (vd, v)):
+        runtime().h2d(t.ptr, x)
+    out2 = DeviceTensor(q.shape, dtype)
+    paged_ops.paged_append(kd.ptr, vd.ptr, two.slab_table.ptr, two.block_table.ptr, b=b, h=h, n=n, d=d,
+                           offset=offset, **common)
+    paged_ops.paged_attention(out2.ptr, qd.ptr, two.slab_table.ptr, two.block_table.ptr, b=b, h=h, nq=n,
+                              nk=offset + n, d=d, offset=offset, **common)
+    runtime().synchronize()
+    assert np.array_equal(one.pool_image().view(np.uint8), two.pool_image().view(np.uint8))
+    got1 = out1.raw_numpy().reshape(b, n, h, d).transpose(0, 2, 1, 3)
+    got2 = out2.raw_numpy()
+    assert np.array_equal(got1.view(np.uint8), got2.view(np.uint8))
+    image = case.image.copy()
+    po.image_append(image, case.table, case.columns, k, v, 0, offset=offset)
+    ref = po.image_paged_attention(image, CODES[dtype], case.table, case.columns, q, 0, offset, offset + n)
+    assert_attention_close(out2.to_numpy(), ref, dtype)
