@@ -260,25 +260,30 @@ def bench_e2e(args):
         model = model_mod.distilgpt2(seed=args.seed)
         trace = e2e.config3_trace(args.seed)
         warm = e2e.config3_trace(args.seed + 1, requests=8, rate=1000.0)
-        e2e.run_config3(model, warm, precision='fp16')
-        r = e2e.run_config3(model, trace, precision='fp16')
-        # the same trace through the sync-free loop (device-side token feedback)
-        e2e.run_config3(model, warm, precision='fp16', token_feedback=True)
-        r['sync_free'] = e2e.run_config3(model, trace, precision='fp16', token_feedback=True)
-        value, workload = r['busy_decode_tokens_per_sec'], (
+        r = {}
+        if args.loop in ('both', 'sync'):
+            e2e.run_config3(model, warm, precision='fp16')
+            r = e2e.run_config3(model, trace, precision='fp16')
+        if args.loop in ('both', 'sync-free'):
+            # the same trace through the sync-free loop (device-side token feedback)
+            e2e.run_config3(model, warm, precision='fp16', token_feedback=True)
+            r['sync_free'] = e2e.run_config3(model, trace, precision='fp16', token_feedback=True)
+        value, workload = r.get('busy_decode_tokens_per_sec'), (
             'config 3: continuous batching, random-init DistilGPT-2 (6 layers, d 768, 12 heads, vocab '
             '50257), fp16, 256 Poisson requests at 32 req/s, prompts U[32,512], outputs geometric mean '
             '128, greedy, EOS off, 16384 pages of 16 tokens, FIFO, max_batch_size 256')
         dtype = 'f16'
     else:
         model = model_mod.gpt2_medium(seed=args.seed)
-        r = e2e.run_config4(model, seed=args.seed, steps=min(args.steps, 40), warmup=min(args.warmup, 5))
-        r['sync_free'] = e2e.run_config4(model, seed=args.seed, steps=min(args.steps, 40),
-                                         warmup=min(args.warmup, 5), token_feedback=True)
-        value, workload = r['decode_tokens_per_sec'], (
+        kw = dict(seed=args.seed, steps=min(args.steps, 40), warmup=min(args.warmup, 5),
+                  replace_rate=args.replace_rate)
+        r = e2e.run_config4(model, **kw) if args.loop in ('both', 'sync') else {}
+        if args.loop in ('both', 'sync-free'):
+            r['sync_free'] = e2e.run_config4(model, **kw, token_feedback=True)
+        value, workload = r.get('decode_tokens_per_sec'), (
             'config 4: steady state of 128 requests, random-init GPT-2-medium (24 layers, d 1024, 16 '
-            'heads), bf16, contexts lognormal(median 256, sigma 1.2) clipped [16,1024], page 16, 5% '
-            'replaced per step')
+            'heads), bf16, contexts lognormal(median 256, sigma 1.2) clipped [16,1024], page 16, '
+            f'{args.replace_rate:.0%} replaced per step')
         dtype = 'bf16'
     return {'metric': 'decode tokens/s (1 GPU), end to end', 'value': value, 'unit': 'tokens/s',
             'n_gpus': 1, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
@@ -308,6 +313,10 @@ def main():
     ap.add_argument('--config', type=int, default=2, choices=(2, 3, 4, 5),
                     help='2: op-level decode (default, the headline line); 5: ragged op-level '
                          'decode, bf16, H=25, P=16 and 32; 3 / 4: end-to-end decode')
+    ap.add_argument('--loop', choices=('both', 'sync', 'sync-free'), default='both',
+                    help='configs 3/4: the synchronous loop, the sync-free one, or both')
+    ap.add_argument('--replace-rate', type=float, default=0.05,
+                    help='config 4: fraction of requests replaced per step (0 = decode steps only)')
     ap.add_argument('--prefill', action='store_true',
                     help='op-level causal paged prefill attention on the prompt shapes of configs 3 and 4')
     args = ap.parse_args()

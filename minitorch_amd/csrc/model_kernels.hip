@@ -260,6 +260,75 @@ __global__ __launch_bounds__(256) void residual_layernorm_kernel(void* out, floa
     o[i] = from_f32<DT>(gamma[i] * ((row[i] - mean) * inv) + beta[i]);
 }
 
+// The same residual add + LayerNorm with one wave per row, for widths that are
+// a multiple of 256 (at most 256 * NJ): lane l owns columns 4l + 256j of
+// every 256-column block j. All loads of a row (x, y, gamma, beta) are issued
+// at once and the row stays in registers, so the kernel makes one dependent
+// memory round trip and reduces within the wave (no LDS, no barrier).
+// XOR-butterfly sums leave every lane with the row total.
+template <int DT, int NJ>
+__global__ __launch_bounds__(256) void residual_layernorm_wave_kernel(void* out, float* x, const void* y,
+                                                                      const float* gamma,
+                                                                      const float* beta, int rows,
+                                                                      int width, float eps,
+                                                                      int has_residual) {
+  using T = typename Elem<DT>::T;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nj = width >> 8;
+  float* xr = x + int64_t(row) * width;
+  const T* yr = static_cast<const T*>(y) + int64_t(row) * width;
+  float4 v[NJ], g[NJ], b[NJ];
+  float sum = 0.f, sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (j >= nj) break;
+    const int c = 256 * j + 4 * lane;
+    v[j] = *reinterpret_cast<const float4*>(xr + c);
+    g[j] = *reinterpret_cast<const float4*>(gamma + c);
+    b[j] = *reinterpret_cast<const float4*>(beta + c);
+    if (has_residual) {
+      if constexpr (DT == kF32) {
+        const float4 r = *reinterpret_cast<const float4*>(yr + c);
+        v[j].x += r.x; v[j].y += r.y; v[j].z += r.z; v[j].w += r.w;
+      } else {
+        const uint2 r = *reinterpret_cast<const uint2*>(yr + c);
+        v[j].x += to_f32<DT>(T(r.x & 0xffffu)); v[j].y += to_f32<DT>(T(r.x >> 16));
+        v[j].z += to_f32<DT>(T(r.y & 0xffffu)); v[j].w += to_f32<DT>(T(r.y >> 16));
+      }
+      *reinterpret_cast<float4*>(xr + c) = v[j];
+    }
+    sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    sq += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    sum += __shfl_xor(sum, off);
+    sq += __shfl_xor(sq, off);
+  }
+  const float mean = sum / width;
+  const float var = fmaxf(sq / width - mean * mean, 0.f) + eps;
+  const float inv = 1.f / sqrtf(var);
+  T* o = static_cast<T*>(out) + int64_t(row) * width;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (j >= nj) break;
+    const int c = 256 * j + 4 * lane;
+    const float r0 = g[j].x * ((v[j].x - mean) * inv) + b[j].x;
+    const float r1 = g[j].y * ((v[j].y - mean) * inv) + b[j].y;
+    const float r2 = g[j].z * ((v[j].z - mean) * inv) + b[j].z;
+    const float r3 = g[j].w * ((v[j].w - mean) * inv) + b[j].w;
+    if constexpr (DT == kF32) {
+      *reinterpret_cast<float4*>(o + c) = float4{r0, r1, r2, r3};
+    } else {
+      *reinterpret_cast<uint2*>(o + c) =
+          uint2{uint32_t(from_f32<DT>(r0)) | (uint32_t(from_f32<DT>(r1)) << 16),
+                uint32_t(from_f32<DT>(r2)) | (uint32_t(from_f32<DT>(r3)) << 16)};
+    }
+  }
+}
+
 // tanh-form GELU in place (reference minitorch/nn.py:222-226):
 // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), computed in fp32.
 template <int DT>
@@ -316,8 +385,35 @@ __global__ __launch_bounds__(256) void heads_kernel(T* out, const T* in, int b, 
 
 bool dtype_ok(int d) { return d >= 0 && d <= 2; }
 
+// One wave per row when the row fits the wave kernel (width a multiple of 256,
+// at most 2048, 16-byte aligned rows); y == nullptr means no residual.
+bool wave_rows(const void* out, const float* x, const void* y, const float* gamma, const float* beta,
+               int width, int dtype) {
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  const bool y_ok = !y || (dtype == kF32 ? a16(y) : (reinterpret_cast<uintptr_t>(y) & 7u) == 0);
+  return width % 256 == 0 && width <= 2048 && a16(x) && a16(gamma) && a16(beta) && y_ok &&
+         (dtype == kF32 ? a16(out) : (reinterpret_cast<uintptr_t>(out) & 7u) == 0);
+}
+
+template <int DT>
+void launch_wave_rows(void* out, float* x, const void* y, const float* gamma, const float* beta,
+                      int rows, int width, float eps) {
+  const int blocks = (rows + 3) / 4;
+  if (width <= 1024)
+    residual_layernorm_wave_kernel<DT, 4><<<blocks, 256>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr);
+  else
+    residual_layernorm_wave_kernel<DT, 8><<<blocks, 256>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr);
+}
+
 hipError_t layernorm(void* out, const float* x, const float* gamma, const float* beta, int rows,
                      int width, float eps, int dtype) {
+  if (wave_rows(out, x, nullptr, gamma, beta, width, dtype)) {
+    float* xm = const_cast<float*>(x);  // not written without a residual
+    if (dtype == kF32) launch_wave_rows<kF32>(out, xm, nullptr, gamma, beta, rows, width, eps);
+    else if (dtype == kF16) launch_wave_rows<kF16>(out, xm, nullptr, gamma, beta, rows, width, eps);
+    else launch_wave_rows<kBF16>(out, xm, nullptr, gamma, beta, rows, width, eps);
+    return hipGetLastError();
+  }
   if (dtype == kF32) layernorm_kernel<kF32><<<rows, 256>>>(out, x, gamma, beta, width, eps);
   else if (dtype == kF16) layernorm_kernel<kF16><<<rows, 256>>>(out, x, gamma, beta, width, eps);
   else layernorm_kernel<kBF16><<<rows, 256>>>(out, x, gamma, beta, width, eps);
@@ -326,6 +422,12 @@ hipError_t layernorm(void* out, const float* x, const float* gamma, const float*
 
 hipError_t residual_layernorm(void* out, float* x, const void* y, const float* gamma,
                               const float* beta, int rows, int width, float eps, int dtype) {
+  if (wave_rows(out, x, y, gamma, beta, width, dtype)) {
+    if (dtype == kF32) launch_wave_rows<kF32>(out, x, y, gamma, beta, rows, width, eps);
+    else if (dtype == kF16) launch_wave_rows<kF16>(out, x, y, gamma, beta, rows, width, eps);
+    else launch_wave_rows<kBF16>(out, x, y, gamma, beta, rows, width, eps);
+    return hipGetLastError();
+  }
   if (dtype == kF32)
     residual_layernorm_kernel<kF32><<<rows, 256>>>(out, x, y, gamma, beta, width, eps);
   else if (dtype == kF16)

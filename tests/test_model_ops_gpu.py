@@ -52,10 +52,13 @@ def test_gemm_gelu_epilogue(dtype, fused):
     assert np.all(np.abs(got - ref) <= tol), float(np.max(np.abs(got - ref) / np.maximum(tol, 1e-30)))
 
 
-@pytest.mark.parametrize('dtype', ['float32', 'bfloat16'])
-def test_residual_layernorm(dtype):
+@pytest.mark.parametrize('width', [1000, 768, 1024, 2048])
+@pytest.mark.parametrize('dtype', ['float32', 'float16', 'bfloat16'])
+def test_residual_layernorm(dtype, width):
+    # widths that are multiples of 256 (up to 2048) take the one-wave-per-row
+    # kernel, others the workgroup-per-row kernel
     rng = np.random.default_rng(4)
-    rows, width = 9, 1000
+    rows = 9
     x = (rng.standard_normal((rows, width)) * 3 + 1).astype(np.float32)
     y = rng.standard_normal((rows, width)).astype(np.float32)
     g = rng.standard_normal(width).astype(np.float32)
@@ -68,6 +71,32 @@ def test_residual_layernorm(dtype):
          G.ptr, Bt.ptr, rows, width, 1e-5, dtype_code(dtype))
     xs = x.astype(np.float64) + round_to(y, dtype)
     assert np.allclose(to_host(X), xs, rtol=1e-6, atol=1e-6)
+    mean = xs.mean(axis=1, keepdims=True)
+    var = np.maximum((xs ** 2).mean(axis=1, keepdims=True) - mean ** 2, 0) + 1e-5
+    ref = g * ((xs - mean) / np.sqrt(var)) + be
+    got = to_host(out)
+    if dtype == 'float32':
+        assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max()
+    else:
+        unit = 2 ** -7 if dtype == 'bfloat16' else 2 ** -10
+        assert np.all(np.abs(got - ref) <= unit * np.abs(ref) + 1e-3)
+
+
+@pytest.mark.parametrize('width', [1000, 768])
+@pytest.mark.parametrize('dtype', ['float32', 'bfloat16'])
+def test_layernorm_typed(dtype, width):
+    rng = np.random.default_rng(5)
+    rows = 7
+    x = (rng.standard_normal((rows, width)) * 2 - 1).astype(np.float32)
+    g = rng.standard_normal(width).astype(np.float32)
+    be = rng.standard_normal(width).astype(np.float32)
+    X = DeviceTensor.from_numpy(x, 'float32')
+    G, Bt = DeviceTensor.from_numpy(g, 'float32'), DeviceTensor.from_numpy(be, 'float32')
+    out = DeviceTensor((rows, width), dtype)
+    call(model_library(), 'mt_layernorm_typed', [P, P, P, P, I, I, F, I], out.ptr, X.ptr, G.ptr, Bt.ptr,
+         rows, width, 1e-5, dtype_code(dtype))
+    assert np.array_equal(to_host(X), x)  # the input is not written
+    xs = x.astype(np.float64)
     mean = xs.mean(axis=1, keepdims=True)
     var = np.maximum((xs ** 2).mean(axis=1, keepdims=True) - mean ** 2, 0) + 1e-5
     ref = g * ((xs - mean) / np.sqrt(var)) + be
