@@ -14,7 +14,8 @@ greedy tokens stay on the device as the next step's input (the pool's
 per-slot last tokens), requests without an EOS token finish by count, and
 the token values reach the host through asynchronous copies that ``step``
 delivers one step later (a step returns the events of the tokens that
-arrived during it). Scheduling decisions, pages and tokens are the same as in
+arrived during it; a step that admits requests waits for all its tokens, so
+first tokens are not delayed). Scheduling decisions, pages and tokens are the same as in
 the synchronous mode; a step whose batch has a request with an EOS token
 waits for its tokens, since finishing then depends on their values.
 """
@@ -251,8 +252,11 @@ class ContinuousBatcher:
                 prefill_tokens += len(request.prompt_ids)
         if self.token_feedback:
             # Only the read-backs issued in this step stay in flight: the
-            # previous step's tokens are delivered while this step runs.
-            events.extend(self._drain(keep=sum(1 for t, _ in self._inflight if t >= first_ticket)))
+            # previous step's tokens are delivered while this step runs. A
+            # step that admitted requests delivers everything, so that a first
+            # token is not held back a step (time to first token).
+            keep = 0 if prefill_ids else sum(1 for t, _ in self._inflight if t >= first_ticket)
+            events.extend(self._drain(keep=keep))
         capacity_bytes = sum(r.cache.nbytes for r in self.active.values())
         live_bytes = sum(r.cache.length * self.pool.page_bytes // self.pool.page_size for r in self.active.values())
         self.last_step = dict(iteration=self.iteration, decode_request_ids=decode_ids,

@@ -12,6 +12,7 @@
 #include "../../include/mt_paged.h"
 #include "../../include/mt_model.h"
 #include <hipblaslt/hipblaslt.h>
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <climits>
 #include <cstdlib>
 #include <cmath>
@@ -56,7 +57,19 @@ struct Blas {
   size_t workspace_bytes = size_t(64) << 20;
   std::mutex mutex;
   std::map<std::tuple<int, int, int, int, int, int, int, int, int>, Plan> plans;
+  // Algorithm per problem class of the one-off shapes (rows rounded up to a
+  // multiple of kRowBucket, any row stride): the heuristic's first choice for
+  // the class's largest row count.
+  std::map<std::tuple<int, int, int, int, int, int, int, int>, hipblasLtMatmulAlgo_t> class_algos;
 };
+
+// One-off shapes (a prefill's prompt length, its last-position head with a
+// row stride that follows the prompt length) would each cost a heuristic
+// query (~0.1 ms of host time, on the prefill's critical path). Rows above
+// kRowBucket share the algorithm of their class when hipBLASLt accepts it for
+// the exact shape; the class algorithm is a function of the class only, so
+// the choice does not depend on which shapes came first.
+constexpr int kRowBucket = 64;
 
 int blas_status(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS ? 0 : 1000 + int(s); }
 
@@ -115,6 +128,100 @@ int pick_fastest(Blas* blas, Plan& p, const hipblasLtMatmulHeuristicResult_t* he
 // B [k, n] or, with transb, B^T for B [n, k]. Column-major view: C^T =
 // op(B)^T A^T, i.e. a column-major GEMM with rows n, columns m; the bias is
 // per row of C^T.
+void release_plan(Plan& p) {
+  if (p.la) hipblasLtMatrixLayoutDestroy(p.la);
+  if (p.lb) hipblasLtMatrixLayoutDestroy(p.lb);
+  if (p.lc) hipblasLtMatrixLayoutDestroy(p.lc);
+  if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+  p = Plan();
+}
+
+// The heuristic's first choice for a row-major [m, k] x [k, n] problem with
+// the descriptor of `p`, through temporary layouts (lda = k).
+bool class_algorithm(Blas* blas, const Plan& p, int m, int n, int k, hipDataType in, hipDataType outt,
+                     hipblasLtMatmulAlgo_t* algo) {
+  hipblasLtMatrixLayout_t rb = nullptr, rc = nullptr;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  hipblasLtMatmulHeuristicResult_t h[1];
+  int got = 0;
+  uint64_t ws = blas->workspace_bytes;
+  bool ok = !hipblasLtMatrixLayoutCreate(&rb, in, k, m, k) && !hipblasLtMatrixLayoutCreate(&rc, outt, n, m, n) &&
+            !hipblasLtMatmulPreferenceCreate(&pref);
+  if (ok) {
+    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
+    ok = !hipblasLtMatmulAlgoGetHeuristic(blas->handle, p.desc, p.la, rb, rc, rc, pref, 1, h, &got) && got > 0;
+    if (ok) *algo = h[0].algo;
+  }
+  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  if (rb) hipblasLtMatrixLayoutDestroy(rb);
+  if (rc) hipblasLtMatrixLayoutDestroy(rc);
+  return ok;
+}
+
+// Descriptors and algorithm candidates of one exact GEMM shape.
+int make_plan(Blas* blas, Plan& p, int m, int n, int k, int transb, int dtype, int out_dtype,
+              const void* bias, int epilogue, bool tunable, int lda) {
+  hipblasStatus_t s;
+  const hipDataType in = hip_type(dtype), outt = hip_type(out_dtype);
+  if ((s = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F))) return blas_status(s);
+  hipblasOperation_t opa = transb ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = HIPBLAS_OP_N;
+  hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa));
+  hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb));
+  hipblasLtEpilogue_t epi = epilogue == kEpiGelu
+                                ? (bias ? HIPBLASLT_EPILOGUE_GELU_BIAS : HIPBLASLT_EPILOGUE_GELU)
+                                : (bias ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT);
+  hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi));
+  if (bias) {
+    hipDataType bt = outt;
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt));
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
+  }
+  // A' = B (col-major [n, k], or [k, n] transposed), B' = A (col-major [k, m]).
+  if ((s = transb ? hipblasLtMatrixLayoutCreate(&p.la, in, k, n, k)
+                  : hipblasLtMatrixLayoutCreate(&p.la, in, n, k, n)))
+    return blas_status(s);
+  if ((s = hipblasLtMatrixLayoutCreate(&p.lb, in, k, m, lda))) return blas_status(s);
+  if ((s = hipblasLtMatrixLayoutCreate(&p.lc, outt, n, m, n))) return blas_status(s);
+  if (!tunable && (m > kRowBucket || lda != k)) {
+    const int mb = m > kRowBucket ? (m + kRowBucket - 1) / kRowBucket * kRowBucket : m;
+    const auto ckey = std::make_tuple(mb, n, k, transb, dtype, out_dtype, bias ? 1 : 0, epilogue);
+    auto it = blas->class_algos.find(ckey);
+    if (it == blas->class_algos.end()) {
+      hipblasLtMatmulAlgo_t algo;
+      if (class_algorithm(blas, p, mb, n, k, in, outt, &algo))
+        it = blas->class_algos.emplace(ckey, algo).first;
+    }
+    if (it != blas->class_algos.end()) {
+      const float one = 1.f, zero = 0.f;
+      hipblasLtMatmulAlgo_t algo = it->second;
+      size_t need = 0;
+      if (hipblaslt_ext::matmulIsAlgoSupported(blas->handle, p.desc, &one, p.la, p.lb, &zero, p.lc, p.lc,
+                                               algo, need) == HIPBLAS_STATUS_SUCCESS &&
+          need <= blas->workspace_bytes) {
+        p.heur[0].algo = algo;
+        p.candidates = 1;
+        p.algo = algo;
+        p.ok = true;
+        return 0;
+      }
+    }
+  }
+  hipblasLtMatmulPreference_t pref;
+  if ((s = hipblasLtMatmulPreferenceCreate(&pref))) return blas_status(s);
+  uint64_t ws = blas->workspace_bytes;
+  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
+  int returned = 0;
+  s = hipblasLtMatmulAlgoGetHeuristic(blas->handle, p.desc, p.la, p.lb, p.lc, p.lc, pref, kCandidates,
+                                      p.heur, &returned);
+  hipblasLtMatmulPreferenceDestroy(pref);
+  if (s) return blas_status(s);
+  if (returned < 1) return blas_status(HIPBLAS_STATUS_NOT_SUPPORTED);
+  p.candidates = returned;
+  p.algo = p.heur[0].algo;
+  p.ok = true;
+  return 0;
+}
+
 int gemm(Blas* blas, void* out, const void* a, const void* b, const void* bias, int m, int n,
          int k, int transb, int dtype, int out_dtype, int epilogue = kEpiNone, bool tunable = false,
          int lda = 0) {
@@ -123,53 +230,13 @@ int gemm(Blas* blas, void* out, const void* a, const void* b, const void* bias, 
   auto key = std::make_tuple(m, n, k, transb, dtype, out_dtype, bias ? 1 : 0, epilogue, lda);
   Plan& p = blas->plans[key];
   if (!p.ok) {
-    // On any failure below the partial plan is released so a later call can retry.
-    struct Guard {
-      Blas* blas; Plan* p; decltype(key) k; bool keep = false;
-      ~Guard() {
-        if (keep) return;
-        if (p->la) hipblasLtMatrixLayoutDestroy(p->la);
-        if (p->lb) hipblasLtMatrixLayoutDestroy(p->lb);
-        if (p->lc) hipblasLtMatrixLayoutDestroy(p->lc);
-        if (p->desc) hipblasLtMatmulDescDestroy(p->desc);
-        blas->plans.erase(k);
-      }
-    } guard{blas, &p, key};
-    hipblasStatus_t s;
-    const hipDataType in = hip_type(dtype), outt = hip_type(out_dtype);
-    if ((s = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F))) return blas_status(s);
-    hipblasOperation_t opa = transb ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = HIPBLAS_OP_N;
-    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa));
-    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb));
-    hipblasLtEpilogue_t epi = epilogue == kEpiGelu
-                                  ? (bias ? HIPBLASLT_EPILOGUE_GELU_BIAS : HIPBLASLT_EPILOGUE_GELU)
-                                  : (bias ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT);
-    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi));
-    if (bias) {
-      hipDataType bt = outt;
-      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt));
-      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
+    // On failure the partial plan is released so a later call can retry.
+    const int st = make_plan(blas, p, m, n, k, transb, dtype, out_dtype, bias, epilogue, tunable, lda);
+    if (st) {
+      release_plan(p);
+      blas->plans.erase(key);
+      return st;
     }
-    // A' = B (col-major [n, k], or [k, n] transposed), B' = A (col-major [k, m]).
-    if ((s = transb ? hipblasLtMatrixLayoutCreate(&p.la, in, k, n, k)
-                    : hipblasLtMatrixLayoutCreate(&p.la, in, n, k, n)))
-      return blas_status(s);
-    if ((s = hipblasLtMatrixLayoutCreate(&p.lb, in, k, m, lda))) return blas_status(s);
-    if ((s = hipblasLtMatrixLayoutCreate(&p.lc, outt, n, m, n))) return blas_status(s);
-    hipblasLtMatmulPreference_t pref;
-    if ((s = hipblasLtMatmulPreferenceCreate(&pref))) return blas_status(s);
-    uint64_t ws = blas->workspace_bytes;
-    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
-    int returned = 0;
-    s = hipblasLtMatmulAlgoGetHeuristic(blas->handle, p.desc, p.la, p.lb, p.lc, p.lc, pref, kCandidates,
-                                        p.heur, &returned);
-    hipblasLtMatmulPreferenceDestroy(pref);
-    if (s) return blas_status(s);
-    if (returned < 1) return blas_status(HIPBLAS_STATUS_NOT_SUPPORTED);
-    p.candidates = returned;
-    p.algo = p.heur[0].algo;
-    p.ok = true;
-    guard.keep = true;
   }
   if (tunable && ++p.calls == kTuneAfterCalls && p.candidates > 1 && blas->tune) {
     if (bias)
