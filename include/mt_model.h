@@ -13,9 +13,11 @@
 extern "C" {
 #endif
 
-/* Weights of one GPT-2 layer for mt_decoder_layers: fp32 LayerNorm
- * parameters; projection weights row-major [in, out] and biases [out] in the
- * compute type; w_qkv is the fused [d, 3d] query/key/value projection. */
+/* Weights of one GPT-2 layer for mt_decoder_layers / mt_prefill_layers: fp32
+ * LayerNorm parameters; projection weights row-major [out, in] (GPT-2's
+ * [in, out] Conv1D arrays transposed once, so that the GEMMs read them
+ * K-contiguous) and biases [out] in the compute type; w_qkv is the fused
+ * [3d, d] query/key/value projection. */
 typedef struct mt_decoder_layer {
   const float* ln1_gamma; const float* ln1_beta;
   const void* w_qkv; const void* b_qkv;

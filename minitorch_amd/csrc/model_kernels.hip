@@ -514,9 +514,9 @@ hipError_t gelu(void* x, int64_t n, int dtype) {
 // GEMM + bias + tanh GELU: hipBLASLt's GELU epilogue when `fused`, else the
 // bias GEMM followed by gelu_kernel.
 int gemm_gelu(Blas* blas, void* out, const void* a, const void* b, const void* bias, int m, int n,
-              int k, int dtype, bool fused, bool tunable = false) {
-  if (fused) return gemm(blas, out, a, b, bias, m, n, k, 0, dtype, dtype, kEpiGelu, tunable);
-  int e = gemm(blas, out, a, b, bias, m, n, k, 0, dtype, dtype, kEpiNone, tunable);
+              int k, int dtype, bool fused, bool tunable = false, int transb = 0) {
+  if (fused) return gemm(blas, out, a, b, bias, m, n, k, transb, dtype, dtype, kEpiGelu, tunable);
+  int e = gemm(blas, out, a, b, bias, m, n, k, transb, dtype, dtype, kEpiNone, tunable);
   return e ? e : gelu(out, int64_t(m) * n, dtype);
 }
 
@@ -698,17 +698,17 @@ int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
   int st = layernorm(h, x, layers[0].ln1_gamma, layers[0].ln1_beta, rows, d, eps, dtype);
   for (int i = 0; i < n_layer && !st; ++i) {
     const mt_decoder_layer& L = layers[i];
-    if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 0, dtype, dtype, kEpiNone, true))) break;
+    if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 1, dtype, dtype, kEpiNone, true))) break;
     if ((st = mt_paged_decode_split(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, att->slabs,
                                     att->table, att->offsets, rows, heads, hd, att->page_size,
                                     att->pages_per_slab, att->num_slabs, att->columns, i, att->layers,
                                     dtype, att->split_tokens, 0, 0, 3 * d, att->work, att->work_items,
                                     att->merge_rows, att->partials, att->partial_bytes)))
       break;
-    if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 0, dtype, dtype, kEpiNone, true))) break;
+    if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 1, dtype, dtype, kEpiNone, true))) break;
     if ((st = residual_layernorm(h, x, proj, L.ln2_gamma, L.ln2_beta, rows, d, eps, dtype))) break;
-    if ((st = gemm_gelu(blas, mlp, h, L.w_fc, L.b_fc, rows, 4 * d, d, dtype, fused_gelu != 0, true))) break;
-    if ((st = gemm(blas, proj, mlp, L.w_proj, L.b_proj, rows, d, 4 * d, 0, dtype, dtype, kEpiNone, true))) break;
+    if ((st = gemm_gelu(blas, mlp, h, L.w_fc, L.b_fc, rows, 4 * d, d, dtype, fused_gelu != 0, true, 1))) break;
+    if ((st = gemm(blas, proj, mlp, L.w_proj, L.b_proj, rows, d, 4 * d, 1, dtype, dtype, kEpiNone, true))) break;
     const bool last = i + 1 == n_layer;
     st = residual_layernorm(h, x, proj, last ? final_gamma : layers[i + 1].ln1_gamma,
                             last ? final_beta : layers[i + 1].ln1_beta, rows, d, eps, dtype);
@@ -743,16 +743,16 @@ int mt_prefill_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
   int st = layernorm(h, x, layers[0].ln1_gamma, layers[0].ln1_beta, rows, d, eps, dtype);
   for (int i = 0; i < n_layer && !st; ++i) {
     const mt_decoder_layer& L = layers[i];
-    if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 0, dtype, dtype))) break;
+    if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 1, dtype, dtype))) break;
     if ((st = mt_paged_prefill(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, att->slabs,
                                att->table, batch, heads, n, hd, att->page_size, att->pages_per_slab,
                                att->num_slabs, att->columns, i, att->layers, att->offset, dtype, 3 * d,
                                d)))
       break;
-    if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 0, dtype, dtype))) break;
+    if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 1, dtype, dtype))) break;
     if ((st = residual_layernorm(h, x, proj, L.ln2_gamma, L.ln2_beta, rows, d, eps, dtype))) break;
-    if ((st = gemm_gelu(blas, mlp, h, L.w_fc, L.b_fc, rows, 4 * d, d, dtype, fused_gelu != 0, false))) break;
-    if ((st = gemm(blas, proj, mlp, L.w_proj, L.b_proj, rows, d, 4 * d, 0, dtype, dtype))) break;
+    if ((st = gemm_gelu(blas, mlp, h, L.w_fc, L.b_fc, rows, 4 * d, d, dtype, fused_gelu != 0, false, 1))) break;
+    if ((st = gemm(blas, proj, mlp, L.w_proj, L.b_proj, rows, d, 4 * d, 1, dtype, dtype))) break;
     const bool last = i + 1 == n_layer;
     st = residual_layernorm(h, x, proj, last ? final_gamma : layers[i + 1].ln1_gamma,
                             last ? final_beta : layers[i + 1].ln1_beta, rows, d, eps, dtype);
