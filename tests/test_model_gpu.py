@@ -258,3 +258,30 @@ def test_decode_greedy_reads_and_writes_slot_tokens():
     assert [int(slot_tokens[c.slot]) for c in caches] == [t[-1] for t in tokens]
     for c in caches:
         c.close()
+
+
+@pytest.mark.parametrize('precision', ['fp16', 'bf16'])
+def test_low_precision_prefill_and_decode_logits_near_oracle(precision):
+    # The native prefill and decode loops in fp16/bf16 against the fp64 numpy
+    # GPT-2: activations and weights are rounded to the compute type, so the
+    # bound is loose (2 % of the logits' range), but a wrong weight layout,
+    # head split or position would miss it by far.
+    model = tiny(seed=17)
+    rng = np.random.default_rng(17)
+    prompt = rng.integers(0, model.n_vocab, 45).tolist()
+    dtype = 'float16' if precision == 'fp16' else 'bfloat16'
+    with autocast(dtype):
+        cache = model.create_kv_cache(1, 64)
+        logits, _ = model.prefill(DeviceTensor.from_numpy(np.array([prompt], np.float32)), cache)
+        got = [logits.to_numpy()[0, 0].astype(np.float64)]
+        nxt = int(greedy_token(logits).to_numpy()[0, 0])
+        seq = prompt + [nxt]
+        for _ in range(3):
+            logits = model.decode_batch(DeviceTensor.from_numpy(np.array([[seq[-1]]], np.float32)), [cache])
+            got.append(logits.to_numpy()[0, 0].astype(np.float64))
+            seq.append(int(greedy_token(logits).to_numpy()[0, 0]))
+        cache.close()
+    for i, g in enumerate(got):
+        ref = go.forward(model.state, seq[:len(prompt) + i], n_head=model.n_head, n_layer=model.n_layer)[-1]
+        err = np.abs(g - ref).max()
+        assert err <= 0.02 * (ref.max() - ref.min()), (i, err, ref.max() - ref.min())
