@@ -162,3 +162,55 @@ def test_paged_prefill_rejects_invalid_arguments():
     assert f(*ptrs, 2, 3, 5, 64, 16, 4, 4, 8, 0, 1, 0, 3, 0, 0) == 1        # dtype
     assert f(*ptrs, 2, 3, 5, 64, 16, 4, 4, 8, 1, 1, 0, 1, 0, 0) == 1        # layer >= layers
     assert f(None, *ptrs[1:], 2, 3, 5, 64, 16, 4, 4, 8, 0, 1, 0, 1, 0, 0) == 1
+
+
+def test_token_feedback_entries_reject_invalid_arguments():
+    lib = library('inference_kernels')
+    a = lib.mt_row_argmax_feedback
+    a.argtypes, a.restype = [P, P, P, I, P, I, I, I], I
+    assert a(8, 8, None, 4, 8, 1, 10, 0) == 1          # slot table without slots
+    assert a(8, 8, 8, 0, 8, 1, 10, 0) == 1             # empty slot table
+    assert a(8, None, None, 0, 8, 0, 10, 0) == 1       # no rows
+    assert a(8, None, None, 0, 8, 1, 10, 3) == 1       # dtype
+    assert a(None, None, None, 0, 8, 1, 10, 0) == 1
+    g = lib.mt_gather_slot_tokens
+    g.argtypes, g.restype = [P, P, P, I, I], I
+    assert g(8, 8, 8, 4, 0) == 1
+    assert g(8, 8, 8, 0, 1) == 1
+    assert g(None, 8, 8, 4, 1) == 1
+
+
+class _Layer(ct.Structure):
+    _fields_ = [(n, P) for n in ('ln1_gamma', 'ln1_beta', 'w_qkv', 'b_qkv', 'w_o', 'b_o',
+                                 'ln2_gamma', 'ln2_beta', 'w_fc', 'b_fc', 'w_proj', 'b_proj')]
+
+
+class _Prefill(ct.Structure):
+    _fields_ = [('slabs', P), ('table', P), ('page_size', I), ('pages_per_slab', I), ('num_slabs', I),
+                ('columns', I), ('layers', I), ('offset', I)]
+
+
+def test_prefill_layers_rejects_invalid_arguments():
+    lib = library('model_kernels')
+    f = lib.mt_prefill_layers
+    f.argtypes = [P, P, I, P, P, P, P, P, P, I, I, I, I, I, ct.c_float, I, I, P, Z, P]
+    f.restype = I
+    layer = _Layer(*([8] * 12))
+    att = _Prefill(8, 8, 16, 4, 4, 8, 1, 0)
+    need = lib.mt_decoder_scratch_bytes
+    need.argtypes, need.restype = [I, I, I], Z
+    scratch = need(2 * 5, 64, 1)
+    args = dict(handle=8, layers=ct.byref(layer), n_layer=1, x=8, h=8, fg=8, fb=8, head=8, logits=8, vocab=10,
+                batch=2, n=5, d=64, heads=2, eps=1e-5, dtype=1, gelu=1, scratch=8, scratch_bytes=scratch,
+                att=ct.byref(att))
+
+    def call(**over):
+        a = dict(args, **over)
+        return f(*a.values())
+    assert call(handle=None) == 1
+    assert call(heads=3) == 1                     # d % heads
+    assert call(scratch_bytes=scratch - 1) == 1   # scratch too small
+    assert call(batch=0) == 1
+    assert call(dtype=5) == 1
+    assert call(logits=8, head=None) == 1         # logits need the head weight
+    assert call(att=None) == 1
