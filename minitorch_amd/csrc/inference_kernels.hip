@@ -36,28 +36,35 @@ __global__ __launch_bounds__(256) void embedding_gather_kernel(float* dst, const
   }
 }
 
-// Candidate (value, index) for argmax. Order: a NaN beats any number, a larger
-// number beats a smaller one, and on equal keys (both NaN, or equal values)
-// the lower index wins; index INT_MAX marks "no candidate". This is
-// numpy.argmax's first-maximum rule, as in the reference
-// (src/inference_kernels.cu:37-41,47-48).
+// Argmax with numpy.argmax's rule, as in the reference
+// (src/inference_kernels.cu:37-41,47-48): a NaN beats any number, a larger
+// number beats a smaller one, and on equal keys (both NaN, or equal values,
+// -0 == +0) the lower index wins.
+//
+// Each element is mapped to an integer key with the same order: the stored
+// bits' magnitude, negated for negative values (so -0 and +0 both map to 0),
+// and NaN above +inf. A thread visits its elements in increasing index order,
+// so "strictly greater key" keeps the first maximum; the (key, index) pairs of
+// the threads are then merged with the full rule.
+template <int DT>
+__device__ __forceinline__ int order_key(uint32_t bits) {
+  if constexpr (DT == kF32) {
+    const int mag = int(bits & 0x7fffffffu);
+    return mag > 0x7f800000 ? INT_MAX : ((bits >> 31) ? -mag : mag);
+  } else {
+    constexpr int kInf = DT == kF16 ? 0x7c00 : 0x7f80;  // exponent all ones, zero mantissa
+    const int mag = int(bits & 0x7fffu);
+    return mag > kInf ? INT_MAX : ((bits & 0x8000u) ? -mag : mag);
+  }
+}
+
 struct Cand {
-  float v;
-  int i;
+  int k;  // order key
+  int i;  // index, INT_MAX for no candidate
 };
 
 __device__ __forceinline__ bool better(const Cand& b, const Cand& a) {
-  if (b.i == INT_MAX) return false;
-  if (a.i == INT_MAX) return true;
-  const bool na = isnan(a.v), nb = isnan(b.v);
-  if (nb != na) return nb;
-  if (!na && b.v != a.v) return b.v > a.v;
-  return b.i < a.i;
-}
-
-__device__ __forceinline__ void consider(Cand& c, float v, int j) {
-  const Cand n{v, j};
-  if (better(n, c)) c = n;
+  return b.k > a.k || (b.k == a.k && b.i < a.i);
 }
 
 constexpr int kArgmaxThreads = 512;
@@ -70,23 +77,30 @@ __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, 
                                                                     const int* slots, int num_slots) {
   using T = typename Elem<DT>::T;
   constexpr int E = per16<DT>();
-  __shared__ float s_v[kArgmaxThreads / 64];
+  __shared__ int s_k[kArgmaxThreads / 64];
   __shared__ int s_i[kArgmaxThreads / 64];
   const int row = blockIdx.x;
   const T* p = static_cast<const T*>(src) + int64_t(row) * width;
   const int tid = threadIdx.x;
-  Cand c{-INFINITY, INT_MAX};
+  int bk = INT_MIN, bi = INT_MAX;  // below every element's key
+  auto consider = [&](uint32_t bits, int j) {
+    const int k = order_key<DT>(bits);
+    if (k > bk) { bk = k; bi = j; }
+  };
+  auto raw = [&](const T& x) -> uint32_t {
+    if constexpr (DT == kF32) return __float_as_uint(x);
+    else return uint32_t(x);
+  };
   const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
   int head = int(((16 - (addr & 15)) & 15) / sizeof(T));
   if (head > width) head = width;
   if ((addr & (sizeof(T) - 1)) != 0) head = width;  // misaligned element type: scalar path
   const int nvec = (width - head) / E;
   const int tail = head + nvec * E;
-  if (tid < head) consider(c, to_f32<DT>(p[tid]), tid);
+  if (tid < head) consider(raw(p[tid]), tid);
   const auto* vp = global_view(reinterpret_cast<const u32x4*>(p + head));
   // kBatch vectors per thread are loaded before any is compared, so one row
-  // is read in a few round trips instead of one per 8 KiB. The candidate
-  // order is total (value, then lower index), so visiting order is free.
+  // is read in a few round trips instead of one per 8 KiB.
   constexpr int kBatch = 8;
   for (int j0 = tid; j0 < nvec; j0 += kArgmaxThreads * kBatch) {
     u32x4 x[kBatch];
@@ -99,26 +113,35 @@ __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, 
     for (int u = 0; u < kBatch; ++u) {
       const int j = j0 + u * kArgmaxThreads;
       if (j < nvec) {
-        float f[E];
-        unpack16<DT>(x[u], f);
+        const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+        const int base = head + j * E;
+        if constexpr (DT == kF32) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) consider(c, f[e], head + j * E + e);
+          for (int e = 0; e < 4; ++e) consider(w[e], base + e);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            consider(w[e] & 0xffffu, base + 2 * e);
+            consider(w[e] >> 16, base + 2 * e + 1);
+          }
+        }
       }
     }
   }
-  for (int j = tail + tid; j < width; j += kArgmaxThreads) consider(c, to_f32<DT>(p[j]), j);
+  for (int j = tail + tid; j < width; j += kArgmaxThreads) consider(raw(p[j]), j);
+  Cand c{bk, bi};
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
-    Cand o{__shfl_xor(c.v, off), __shfl_xor(c.i, off)};
+    const Cand o{__shfl_xor(c.k, off), __shfl_xor(c.i, off)};
     if (better(o, c)) c = o;
   }
   const int wave = tid >> 6;
-  if ((tid & 63) == 0) { s_v[wave] = c.v; s_i[wave] = c.i; }
+  if ((tid & 63) == 0) { s_k[wave] = c.k; s_i[wave] = c.i; }
   __syncthreads();
   if (tid == 0) {
-    Cand best{s_v[0], s_i[0]};
+    Cand best{s_k[0], s_i[0]};
     for (int w = 1; w < kArgmaxThreads / 64; ++w) {
-      Cand o{s_v[w], s_i[w]};
+      const Cand o{s_k[w], s_i[w]};
       if (better(o, best)) best = o;
     }
     dst[row] = float(best.i);

@@ -39,6 +39,10 @@ def test_row_argmax_first_max_and_nan(dtype, width):
         x[3, 0, :] = -np.inf                     # all -inf: index 0
         x[4, 0, :] = 2.0                         # all equal: index 0
         x[5, 0, -1] = np.inf
+        x[6, 0, :] = -1.0
+        x[6, 0, [3, 7]] = [-0.0, 0.0]            # -0 == +0: the first (index 3) wins
+        x[7, 0, :] = -np.inf
+        x[7, 0, [width - 2, 4]] = [np.nan, -5.0] # a NaN beats every number, even at a later index
     stored = po.encode(x, {'float32': 0, 'float16': 1, 'bfloat16': 2}[dtype])
     t = DeviceTensor(x.shape, dtype)
     runtime().h2d(t.ptr, stored)
