@@ -1,4 +1,5 @@
-// Paged KV append and paged decode attention for gfx950 (CDNA4, wave64).
+// Paged KV append, paged decode attention and causal paged (prefill)
+// attention for gfx950 (CDNA4, wave64).
 //
 // Slab layout (reference src/paged_attention_kernel.cu:2,18-19 and
 // minitorch/paged_kv_cache.py:30): every slab is
@@ -16,8 +17,9 @@
 //     denominator, fp32 accumulator), so the stream needs no cross-lane
 //     reduction except the 4-lane dot-product sum; groups, waves and splits are
 //     merged once at the end with the log-sum-exp rule;
-//   * the page table and slab lookups for a split are resolved once into LDS
-//     before streaming, so the dependent table -> slab -> K/V chain is paid once;
+//   * the slab table of a small pool is staged in LDS and each lane resolves
+//     the page of one of its wave's row-blocks before streaming (broadcast with
+//     readlane), so the dependent table -> slab -> K/V chain is paid once;
 //   * the KV append of the new token is fused: the workgroup that owns the
 //     last split scores the new token from the K/V inputs and writes it into
 //     its page, so append + attention is a single launch;
@@ -27,6 +29,11 @@
 //     release/acquire fences, which write back and invalidate the XCD's L2 per
 //     workgroup; measured on MI355X that made the decode 10x slower than a
 //     separate launch.)
+//
+// Causal attention of several queries per request (a prefill) runs on the
+// matrix cores for fp16/bf16 (prefill_kernel: 64-query tiles, S^T = K Q^T and
+// O^T += V^T P^T with v_mfma_f32_16x16x32); fp32 and the shapes it does not
+// take use the per-query query_kernel.
 #include "mt_device.h"
 #include <climits>
 
