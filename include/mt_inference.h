@@ -35,6 +35,17 @@ int mt_row_argmax_feedback(float* dst, float* slot_tokens, const int* slots, int
 int mt_gather_slot_tokens(float* ids, const float* slot_tokens, const int* slots, int num_slots,
                           int rows);
 
+/* x[t, :] = wte[id_t, :] + wpe[positions[t], :] (fp32) in one launch, with
+ * id_t = ids[t], or slot_tokens[slots[t]] when slot_tokens is not null (token
+ * feedback); an id or position that is non-finite, negative, too large or not
+ * an integer gives a NaN row, as mt_embedding_gather. dim % 4 == 0 and
+ * 16-byte aligned x/wte/wpe. No reference counterpart as one call (reference
+ * minitorch/pretrained_gpt2.py:16-32 gathers both tables with
+ * mt_embedding_gather and adds them, minitorch/modules_transformer.py:384). */
+int mt_embed_tokens(float* x, const float* wte, const float* wpe, const float* ids,
+                    const float* slot_tokens, const int* slots, int num_slots, const float* positions,
+                    int tokens, int vocab, int n_positions, int dim);
+
 /* dst[b, 0, :] = src[b, n - 1, :] for src [b, n, w]. Replaces reference
  * mt_last_row (src/inference_kernels.cu:66-72). */
 int mt_last_row(void* dst, const void* src, int b, int n, int w, int dtype);

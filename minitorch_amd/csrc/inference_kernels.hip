@@ -36,6 +36,44 @@ __global__ __launch_bounds__(256) void embedding_gather_kernel(float* dst, const
   }
 }
 
+// x[t, :] = wte[id_t, :] + wpe[pos_t, :] in one pass: the token and position
+// gathers of the reference (same invalid-id rule: a NaN row) and their sum.
+// id_t is ids[t], or slot_tokens[slots[t]] when slot_tokens is given (the
+// sync-free decode loop's token feedback; a slot outside the table gives a
+// NaN row). One thread moves 4 floats (dim % 4 == 0, 16-byte aligned rows).
+__device__ __forceinline__ bool bad_id(float raw, int limit) {
+  return !isfinite(raw) || raw < 0.f || raw >= float(limit) || raw != floorf(raw);
+}
+
+__global__ __launch_bounds__(256) void embed_tokens_kernel(float* x, const float* wte, const float* wpe,
+                                                           const float* ids, const float* slot_tokens,
+                                                           const int* slots, int num_slots,
+                                                           const float* positions, int tokens,
+                                                           int vocab, int n_positions, int dim) {
+  const int per_row = dim / 4;
+  const int64_t total = int64_t(tokens) * per_row;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t t = i / per_row;
+    const int col = int(i - t * per_row) * 4;
+    float id;
+    if (slot_tokens) {
+      const int s = slots[t];
+      id = (s >= 0 && s < num_slots) ? slot_tokens[s] : NAN;
+    } else {
+      id = ids[t];
+    }
+    const float pos = positions[t];
+    float4 v = make_float4(NAN, NAN, NAN, NAN);
+    if (!bad_id(id, vocab) && !bad_id(pos, n_positions)) {
+      const float4 a = *reinterpret_cast<const float4*>(wte + int64_t(id) * dim + col);
+      const float4 b = *reinterpret_cast<const float4*>(wpe + int64_t(pos) * dim + col);
+      v = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    }
+    *reinterpret_cast<float4*>(x + t * dim + col) = v;
+  }
+}
+
 // Argmax with numpy.argmax's rule, as in the reference
 // (src/inference_kernels.cu:37-41,47-48): a NaN beats any number, a larger
 // number beats a smaller one, and on equal keys (both NaN, or equal values,
@@ -219,6 +257,21 @@ int mt_row_argmax_feedback(float* dst, float* slot_tokens, const int* slots, int
 
 int mt_row_argmax(float* dst, const void* src, int rows, int width, int dtype) {
   return mt_row_argmax_feedback(dst, nullptr, nullptr, 0, src, rows, width, dtype);
+}
+
+int mt_embed_tokens(float* x, const float* wte, const float* wpe, const float* ids,
+                    const float* slot_tokens, const int* slots, int num_slots, const float* positions,
+                    int tokens, int vocab, int n_positions, int dim) {
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (!x || !wte || !wpe || !positions || (slot_tokens ? (!slots || num_slots < 1) : !ids) ||
+      tokens < 1 || vocab < 1 || n_positions < 1 || dim < 4 || dim % 4 || !a16(x) || !a16(wte) ||
+      !a16(wpe) || int64_t(tokens) * dim > INT32_MAX || int64_t(vocab) * dim > INT32_MAX ||
+      int64_t(n_positions) * dim > INT32_MAX)
+    return hipErrorInvalidValue;
+  const int64_t threads = int64_t(tokens) * (dim / 4);
+  embed_tokens_kernel<<<blocks_for(threads), 256>>>(x, wte, wpe, ids, slot_tokens, slots, num_slots,
+                                                    positions, tokens, vocab, n_positions, dim);
+  return hipGetLastError();
 }
 
 int mt_gather_slot_tokens(float* ids, const float* slot_tokens, const int* slots, int num_slots,

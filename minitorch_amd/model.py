@@ -26,7 +26,6 @@ from .dtypes import dtype_code
 from .runtime import DeviceTensor, library, call, runtime, P, I, F
 from . import paged_ops
 
-LL = ct.c_longlong
 
 
 def model_library():
@@ -200,15 +199,23 @@ class DecoderLM:
                             paged_prefill_impl=paged_prefill_impl)
 
     # -------------------------------------------------------------- ops ---
-    def _embed(self, w, ids, positions):
-        rows = ids.size
+    def _embed(self, w, ids, positions, rows=None, feedback=None):
+        """Token + position embeddings [rows, d] fp32 in one launch (reference
+        minitorch/modules_transformer.py:384, pretrained_gpt2.py:16-32); with
+        ``feedback`` = (pool, device slots) the token ids are the slots' last
+        tokens instead of ``ids``."""
+        rows = ids.size if rows is None else rows
         d = self.n_embd
-        tok = DeviceTensor((rows, d), 'float32')
-        pos = DeviceTensor((rows, d), 'float32')
-        paged_ops.embedding_gather(tok.ptr, w.wte.ptr, ids.ptr, rows, self.n_vocab, d)
-        paged_ops.embedding_gather(pos.ptr, w.wpe.ptr, positions.ptr, rows, self.n_positions, d)
-        call(model_library(), 'mt_add_f32', [P, P, P, LL], tok.ptr, tok.ptr, pos.ptr, rows * d)
-        return tok
+        x = DeviceTensor((rows, d), 'float32')
+        if feedback is None:
+            paged_ops.embed_tokens(x.ptr, w.wte.ptr, w.wpe.ptr, ids.ptr, positions.ptr, rows, self.n_vocab,
+                                   self.n_positions, d)
+        else:
+            pool, slots = feedback
+            paged_ops.embed_tokens(x.ptr, w.wte.ptr, w.wpe.ptr, None, positions.ptr, rows, self.n_vocab,
+                                   self.n_positions, d, slot_tokens=pool.slot_tokens.ptr, slots=slots,
+                                   num_slots=pool.max_slots)
+        return x
 
     # ------------------------------------------------- inference entries ---
     def prefill(self, idx, cache=None):
@@ -290,11 +297,8 @@ class DecoderLM:
             w = self._weights(dtype)
             b, d = batch.batch_size, self.n_embd
             pool = batch.pool
-            if idx is None:
-                idx = DeviceTensor((b, 1), 'float32')
-                paged_ops.gather_slot_tokens(idx.ptr, pool.slot_tokens.ptr, batch.device_slots.ptr,
-                                             pool.max_slots, b)
-            x = self._embed(w, idx, batch.position_ids)
+            feedback = (pool, batch.device_slots.ptr) if idx is None else None
+            x = self._embed(w, idx, batch.position_ids, rows=b, feedback=feedback)
             h = DeviceTensor((b, d), dtype)
             lib = model_library()
             scratch_bytes = _scratch_bytes(lib, b, d, dtype)

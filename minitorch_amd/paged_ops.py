@@ -141,6 +141,14 @@ def gather_slot_tokens(ids, slot_tokens, slots, num_slots, rows):
          num_slots, rows)
 
 
+def embed_tokens(x, wte, wpe, ids, positions, tokens, vocab, n_positions, dim, *, slot_tokens=None,
+                 slots=None, num_slots=0):
+    """``mt_embed_tokens``: ``x = wte[id] + wpe[position]`` per token, the ids
+    from ``ids`` or, with ``slot_tokens``, from the pool's per-slot last tokens."""
+    call(inference_library(), 'mt_embed_tokens', [P, P, P, P, P, P, I, P, I, I, I, I], x, wte, wpe, ids,
+         slot_tokens, slots, num_slots, positions, tokens, vocab, n_positions, dim)
+
+
 def last_row(dst, src, b, n, w, dtype):
     """``mt_last_row`` (reference src/inference_kernels.cu:66-72)."""
     call(inference_library(), 'mt_last_row', [P, P, I, I, I, I], dst, src, b, n, w,

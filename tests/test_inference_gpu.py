@@ -105,3 +105,39 @@ def test_row_argmax_feedback_scatters_to_slots_and_gather_reads_them(dtype):
     paged_ops.gather_slot_tokens(back.ptr, table.ptr, slot_dev.ptr, num_slots, rows)
     want = np.array([expect[s] if 0 <= s < num_slots else np.nan for s in slots], np.float32)
     assert np.array_equal(back.to_numpy()[:, 0], want, equal_nan=True)
+
+
+def test_embed_tokens_equals_two_gathers_and_sum():
+    # mt_embed_tokens against the oracle gathers (NaN rows for invalid token
+    # ids or positions) and their sum, bit for bit; ids given directly and
+    # through the slot table of the token feedback.
+    from minitorch_amd import paged_ops
+    from minitorch_amd.runtime import RawDeviceBuffer
+    rng = np.random.default_rng(31)
+    vocab, npos, dim, rows = 50, 20, 64, 9
+    wte = rng.standard_normal((vocab, dim)).astype(np.float32)
+    wpe = rng.standard_normal((npos, dim)).astype(np.float32)
+    ids = np.array([0, 49, 7, -1, 50, 2.5, np.nan, 3, 4], np.float32)
+    pos = np.array([0, 19, 5, 1, 2, 3, 4, 20, -0.0], np.float32)
+    ref = po.embedding_gather(wte, ids) + po.embedding_gather(wpe, pos)
+    W, Pt = DeviceTensor.from_numpy(wte), DeviceTensor.from_numpy(wpe)
+    I, Q = DeviceTensor.from_numpy(ids), DeviceTensor.from_numpy(pos)
+    x = DeviceTensor((rows, dim), 'float32')
+    paged_ops.embed_tokens(x.ptr, W.ptr, Pt.ptr, I.ptr, Q.ptr, rows, vocab, npos, dim)
+    assert np.array_equal(x.to_numpy(), ref, equal_nan=True)
+    # the same ids through slots (one slot outside the table -> NaN row)
+    num_slots = 16
+    slots = np.array([5, 0, 15, 3, 9, 1, 2, 16, 8], np.int32)
+    table = np.full(num_slots, 11.0, np.float32)
+    for r, s in enumerate(slots):
+        if s < num_slots:
+            table[s] = ids[r]
+    T = DeviceTensor.from_numpy(table)
+    S = RawDeviceBuffer(4 * rows)
+    S.upload(slots)
+    x2 = DeviceTensor((rows, dim), 'float32')
+    paged_ops.embed_tokens(x2.ptr, W.ptr, Pt.ptr, None, Q.ptr, rows, vocab, npos, dim, slot_tokens=T.ptr,
+                           slots=S.ptr, num_slots=num_slots)
+    want = ref.copy()
+    want[7] = np.nan
+    assert np.array_equal(x2.to_numpy(), want, equal_nan=True)
