@@ -88,7 +88,9 @@ def pattern_ceiling(case, devs, steps, warmup):
     """Bandwidth of the decode step's K/V access pattern alone: every (row,
     head, page) K and V page-head chunk (P*D*s bytes, randomly placed by the
     shuffled table) read by mt_chunk_read, a kernel with no address
-    arithmetic, math or merge, at the decode's grid and at a large grid."""
+    arithmetic, math or merge, at the decode's grid and at a large grid; and,
+    for reference, the same number of bytes read sequentially (consecutive
+    chunks of rotated buffers) by the same kernel in one launch."""
     from minitorch_amd.runtime import RawDeviceBuffer
     rt = runtime()
     s = 2 if case.dtype != 'float32' else 4
@@ -117,6 +119,18 @@ def pattern_ceiling(case, devs, steps, warmup):
         nbytes = lists[0][1] * chunk
         out[f'grid_{blocks}'] = dict(us_per_launch=per * 1e6, bytes=nbytes, achieved_gbs=nbytes / per / 1e9,
                                      frac=nbytes / per / 1e9 / PEAK_HBM_GBS)
+    n = lists[0][1]
+    seq = []
+    for _ in lists:
+        region = RawDeviceBuffer(n * chunk)
+        addrs = RawDeviceBuffer(8 * n)
+        addrs.upload(region.ptr + np.arange(n, dtype=np.uint64) * np.uint64(chunk))
+        seq.append((region, addrs))
+    calls = [(addrs.ptr, n, chunk, 6144, sink.ptr) for _, addrs in seq]
+    per = time_launches(f, calls, steps, warmup)
+    out['sequential_grid_6144'] = dict(us_per_launch=per * 1e6, bytes=n * chunk,
+                                       achieved_gbs=n * chunk / per / 1e9,
+                                       frac=n * chunk / per / 1e9 / PEAK_HBM_GBS)
     return out
 
 
