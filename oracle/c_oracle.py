@@ -25,6 +25,8 @@ def library():
     P, I = ct.c_void_p, ct.c_int
     lib.oracle_paged_decode_batch.argtypes = [P] * 7 + [I] * 11
     lib.oracle_paged_decode_batch.restype = I
+    lib.oracle_paged_attention.argtypes = [P] * 4 + [I] * 14
+    lib.oracle_paged_attention.restype = I
     lib.oracle_max_threads.argtypes = []
     lib.oracle_max_threads.restype = I
     return lib
@@ -55,3 +57,23 @@ class HostCase:
         if status:
             raise RuntimeError(f'oracle_paged_decode_batch returned {status}')
         return self.out
+
+
+def paged_attention(lib, case, q, nq, nk, offset, image=None, threads=0):
+    """Causal attention of q [B, H, nq, D] (stored values) over the pages of
+    ``case`` (or of ``image``, an image of the same shape) through
+    oracle_paged_attention; returns the output in storage format."""
+    c = case
+    image = np.ascontiguousarray(c.image if image is None else image)
+    base = image.ctypes.data
+    slabs = np.array([base + s * c.slab_bytes for s in range(c.num_slabs)], np.uint64)
+    table = np.ascontiguousarray(c.table, np.int32)
+    q = np.ascontiguousarray(q)
+    out = np.zeros_like(q)
+    status = lib.oracle_paged_attention(out.ctypes.data, q.ctypes.data, slabs.ctypes.data, table.ctypes.data,
+                                        c.batch, c.heads, nq, nk, c.dim, c.page_size, c.pages_per_slab,
+                                        c.num_slabs, c.columns, c.layer, c.layers, offset, CODES[c.dtype],
+                                        threads)
+    if status:
+        raise RuntimeError(f'oracle_paged_attention returned {status}')
+    return out

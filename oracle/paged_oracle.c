@@ -18,6 +18,12 @@
  * OpenMP parallelises over (b, h), the prange-equivalent of FastOps
  * (minitorch/fast_ops.py:33-353). Pinned against the numpy oracle in
  * tests/test_oracle.py.
+ *
+ * oracle_paged_attention() has the argument list of the reference's
+ * mt_paged_attention (src/paged_attention_kernel.cu:108-117, paged_forward
+ * with offsets == nullptr, :35-85): for every (b, h) and query qi of q
+ * [B,H,nq,D], attention over keys [0, min(offset + qi + 1, nk)) of the pages,
+ * in the same fp32 composition as the decode above.
  */
 #include <math.h>
 #include <stdint.h>
@@ -183,6 +189,62 @@ int oracle_paged_decode_batch(void* out, const void* q, const void* k, const voi
         for (int64_t j = 0; j < n; ++j) acc += scores[j] / sum * vals[j * d + c];
         float o = n == 0 ? 0.f : (poisoned ? NAN : acc);
         store(out, bh * d + c, o, dtype);
+      }
+    }
+    free(keys); free(vals); free(scores);
+  }
+  return 0;
+}
+
+int oracle_paged_attention(void* out, const void* q, const uint64_t* slabs, const int* table, int b,
+                           int h, int nq, int nk, int d, int page_size, int pps, int num_slabs,
+                           int columns, int layer, int layers, int offset, int dtype, int threads) {
+  if (!out || !q || !slabs || !table || b < 1 || h < 1 || nq < 1 || nk < 1 || d < 1 || d > 128 ||
+      offset < 0 || layer < 0 || layer >= layers || dtype < 0 || dtype > 2)
+    return 1;
+  if (threads > 0) omp_set_num_threads(threads);
+  const float scale = 1.0f / sqrtf((float)d);
+#pragma omp parallel
+  {
+    float* keys = (float*)malloc(sizeof(float) * (size_t)nk * d);
+    float* vals = (float*)malloc(sizeof(float) * (size_t)nk * d);
+    float* scores = (float*)malloc(sizeof(float) * (size_t)nk);
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t bh = 0; bh < (int64_t)b * h; ++bh) {
+      const int bi = (int)(bh / h), head = (int)(bh % h);
+      for (int64_t j = 0; j < nk; ++j) {
+        const char* kp = page_element(slabs, table, bi, head, j, 0, 0, layer, h, d, page_size, pps, num_slabs, columns, dtype);
+        const char* vp = page_element(slabs, table, bi, head, j, 0, 1, layer, h, d, page_size, pps, num_slabs, columns, dtype);
+        for (int c = 0; c < d; ++c) {
+          keys[j * d + c] = kp ? load(kp, c, dtype) : NAN;
+          vals[j * d + c] = vp ? load(vp, c, dtype) : NAN;
+        }
+      }
+      for (int qi = 0; qi < nq; ++qi) {
+        const int64_t n = (int64_t)offset + qi + 1 < nk ? (int64_t)offset + qi + 1 : nk;
+        const int64_t row = bh * nq + qi;
+        float qv[128];
+        for (int c = 0; c < d; ++c) qv[c] = load(q, row * d + c, dtype);
+        float mx = -INFINITY;
+        int poisoned = 0;
+        for (int64_t j = 0; j < n; ++j) {
+          float s = 0.f;
+          for (int c = 0; c < d; ++c) s += qv[c] * keys[j * d + c];
+          s *= scale;
+          scores[j] = s;
+          if (isnan(s)) poisoned = 1;
+          else if (s > mx) mx = s;
+        }
+        float sum = 0.f;
+        for (int64_t j = 0; j < n; ++j) {
+          scores[j] = expf(scores[j] - mx);
+          sum += scores[j];
+        }
+        for (int c = 0; c < d; ++c) {
+          float acc = 0.f;
+          for (int64_t j = 0; j < n; ++j) acc += scores[j] / sum * vals[j * d + c];
+          store(out, row * d + c, poisoned ? NAN : acc, dtype);
+        }
       }
     }
     free(keys); free(vals); free(scores);

@@ -284,3 +284,21 @@ def test_planted_last_max_tie_rule_is_caught():
     row = np.array([1, 5, 5, 2], np.float32)
     last = len(row) - 1 - int(np.argmax(row[::-1]))
     assert last != _argmax_loop(row) == 1
+
+
+@pytest.mark.parametrize('dtype', ['float32', 'float16', 'bfloat16'])
+def test_c_oracle_causal_attention_agrees_with_numpy_oracle(clib, dtype):
+    # oracle_paged_attention (the C restatement of mt_paged_attention) against
+    # the numpy fp64 oracle: causal masks at an offset, a hole in the pages
+    # (queries that reach it are NaN), two requests, page size 8.
+    nq, offset = 37, 20
+    case = make_decode_case(7, batch=2, heads=3, dim=64, page_size=8, lengths=[offset + nq] * 2,
+                            pool_pages=32, pages_per_slab=4, dtype=dtype)
+    case.table[1, 4] = -1                      # keys 32..39 of request 1 missing
+    q = po.encode(np.random.default_rng(7).standard_normal((2, 3, nq, 64)).astype(np.float32), CODES[dtype])
+    got = po.decode(c_oracle.paged_attention(clib, case, q, nq, offset + nq, offset, threads=4), CODES[dtype])
+    ref = po.image_paged_attention(case.image, CODES[dtype], case.table, case.columns, q, 0, offset, offset + nq)
+    assert np.isnan(ref[1, :, 12:]).all() and not np.isnan(ref[1, :, :12]).any()
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    tol = 1e-5 * np.nanmax(np.abs(ref)) if dtype == 'float32' else 1e-2
+    assert np.nanmax(np.abs(got - ref)) <= tol
