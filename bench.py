@@ -242,6 +242,57 @@ def bench_prefill_shape(heads, dtype, lengths, steps, warmup, seed):
                 frac=flops / per_round / 1e12 / PEAK_MFMA_TFLOPS)
 
 
+def prefill_cpu_baseline(heads, dtype, lengths, seed, seconds):
+    """The C oracle's causal paged attention (oracle_paged_attention) over the
+    same prompts and pages as :func:`bench_prefill_shape`, one prompt per call,
+    the prompts spread over a pool of host threads (one OpenMP thread per
+    call), repeated until ``seconds`` have passed."""
+    from concurrent.futures import ThreadPoolExecutor
+    from minitorch_amd.workloads import make_decode_case, _normal
+    try:
+        from oracle import c_oracle
+        lib = c_oracle.library()
+    except Exception as error:  # the oracle library is optional on the GPU box
+        return dict(value=None, unit='TFLOP/s', cores=None, kind='port', sample=f'unavailable: {error}')
+    dim, page = 64, 16
+    lengths = np.asarray(lengths, np.int64)
+    pages = int(((lengths + page - 1) // page).sum())
+    case = make_decode_case(seed, batch=len(lengths), heads=heads, dim=dim, page_size=page,
+                            lengths=lengths, pool_pages=-(-pages // 16) * 16, pages_per_slab=16,
+                            dtype=dtype)
+    nmax = int(lengths.max())
+    q = np.ascontiguousarray(_normal(np.random.default_rng([seed, 6]), (1, heads, nmax, dim), dtype))
+    image = np.ascontiguousarray(case.image)
+    slabs = np.array([image.ctypes.data + s * case.slab_bytes for s in range(case.num_slabs)], np.uint64)
+    table = np.ascontiguousarray(case.table, np.int32)
+    code = c_oracle.CODES[dtype]
+
+    def one(i):
+        n = int(lengths[i])
+        qi = np.ascontiguousarray(q[:, :, :n])
+        out = np.empty_like(qi)
+        status = lib.oracle_paged_attention(out.ctypes.data, qi.ctypes.data, slabs.ctypes.data,
+                                            table.ctypes.data + 4 * i * case.columns, 1, heads, n, n, dim,
+                                            page, case.pages_per_slab, case.num_slabs, case.columns, 0, 1, 0,
+                                            code, 1)
+        if status:
+            raise RuntimeError(f'oracle_paged_attention returned {status}')
+
+    threads = min(os.cpu_count() or 1, 16)
+    flops = sum(prefill_flops(int(n), heads, dim) for n in lengths)
+    with ThreadPoolExecutor(threads) as pool:
+        rounds, t0 = 0, time.perf_counter()
+        while True:
+            list(pool.map(one, range(len(lengths))))
+            rounds += 1
+            elapsed = time.perf_counter() - t0
+            if elapsed >= seconds:
+                break
+    return dict(value=flops * rounds / elapsed / 1e12, unit='TFLOP/s', cores=threads, kind='port',
+                sample=f'{rounds} passes over the {len(lengths)} prompts in {elapsed:.1f} s, fp32 arithmetic '
+                       f'on {dtype} pages, one prompt per call, {threads} host threads')
+
+
 def bench_prefill(args):
     """Causal paged prefill attention (the matrix-core kernel behind
     mt_paged_attention) on the prompt shapes of configs 3 and 4: config 3's
@@ -265,7 +316,9 @@ def bench_prefill(args):
             'roofline': {'bound': 'mfma', 'achieved': r3['tflops'], 'peak': PEAK_MFMA_TFLOPS,
                          'unit': 'TFLOP/s', 'frac': r3['frac'], 'traffic': None},
             'config3_prompts_fp16': r3, 'config4_contexts_bf16': r4, 'prompt512_h12_fp16': r512,
-            'prompt1024_h16_bf16': r1024}
+            'prompt1024_h16_bf16': r1024,
+            'cpu_baseline': None if args.no_cpu_baseline else prefill_cpu_baseline(
+                12, 'float16', c3, args.seed, args.cpu_seconds)}
 
 
 def bench_e2e(args):
