@@ -63,7 +63,32 @@ def measured_traffic():
     return None
 
 
+def host_cpu_model():
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def timed_steps(run, seconds, min_steps=10):
+    """Per-step wall times of ``run()`` repeated for ``seconds`` (at least
+    ``min_steps`` steps) after one untimed warm-up step."""
+    run()
+    times, t_end = [], time.perf_counter() + seconds
+    while len(times) < min_steps or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return np.asarray(times)
+
+
 def cpu_baseline(case, seconds):
+    """The C oracle's decode step (append + attention, fp32 arithmetic, OpenMP
+    over (request, head)) on the host cores: the median step time on up to 16
+    threads over ``seconds``, and on one thread over half as long."""
     try:
         from oracle import c_oracle
         lib = c_oracle.library()
@@ -71,17 +96,14 @@ def cpu_baseline(case, seconds):
         return dict(value=None, unit='tokens/s', cores=None, kind='port', sample=f'unavailable: {error}')
     host = c_oracle.HostCase(case)
     threads = min(os.cpu_count() or 1, 16)
-    host.run(lib, threads)  # warm
-    steps, t0 = 0, time.perf_counter()
-    while True:
-        host.run(lib, threads)
-        steps += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed >= seconds:
-            break
-    return dict(value=case.batch * steps / elapsed, unit='tokens/s', cores=threads, kind='port',
-                sample=f'{steps} steps of config 2 (B=64, same seed) in {elapsed:.1f} s, fp32 arithmetic '
-                       f'on fp16 pages, OpenMP over (request, head)')
+    many = timed_steps(lambda: host.run(lib, threads), seconds)
+    one = timed_steps(lambda: host.run(lib, 1), seconds / 2)
+    rate = lambda t: case.batch / float(np.median(t))
+    return dict(value=rate(many), unit='tokens/s', cores=threads, kind='port',
+                sample=f'median of {len(many)} steps of config 2 (B=64, same seed, {many.sum():.1f} s), fp32 '
+                       f'arithmetic on fp16 pages, OpenMP over (request, head)',
+                single_core=dict(value=rate(one), cores=1, steps=len(one)),
+                host=dict(nproc=os.cpu_count(), cpu_model=host_cpu_model()))
 
 
 def pattern_ceiling(case, devs, steps, warmup):

@@ -81,6 +81,17 @@ def test_prefill_window_crossing(dtype):
 
 
 @pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+def test_prefill_more_slabs_than_lds_holds(dtype):
+    # one page per slab and 525 pages: the slab table (> 512 entries) is read
+    # from global memory instead of LDS, across two windows of page bases.
+    nq, offset = 96, 4100
+    case = prefill_case(45, batch=1, heads=2, dim=64, page_size=8, nk=offset + nq, dtype=dtype,
+                        pages_per_slab=1)
+    assert case.num_slabs > 512
+    run_prefill(case, nq, offset + nq, offset, seed=7)
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
 def test_prefill_multi_layer(dtype):
     case = prefill_case(43, batch=2, heads=2, dim=128, page_size=16, nk=150, dtype=dtype,
                         layers=3, layer=1, pages_per_slab=5)
