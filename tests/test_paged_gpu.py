@@ -251,6 +251,54 @@ def test_config5_ragged_bf16_sampled_rows():
         check_case(case, rows=rows)
 
 
+@pytest.mark.parametrize('page_size', [16, 32])
+def test_config5_full_size_bench_case(page_size):
+    # The exact case `bench.py --config 5` times: B=512, H=25, bf16, contexts
+    # lognormal(ln 256, 1.2) clipped to [1, 8192], the hash-filled device pool,
+    # the library's split length and the longest-first work list. Every row
+    # is checked against the C oracle and the whole pool image bit for bit.
+    import ctypes as ct
+    from minitorch_amd.workloads import DeviceRaggedCase
+    from minitorch_amd.dtypes import decode_host
+    from oracle import c_oracle
+    lib = c_oracle.library()
+    rt = runtime()
+    lengths = config5_lengths(0, 512)
+    case = DeviceRaggedCase(0, batch=512, heads=25, dim=64, page_size=page_size, lengths=lengths,
+                            dtype='bfloat16')
+    kw = case.kwargs()
+    image = case.pool.download(np.uint16)
+    q, k, v = (t.raw_numpy() for t in (case.q, case.k, case.v))
+    split = paged_ops.split_tokens_for(page_size=page_size, columns=case.columns)
+    ws_bytes = paged_ops.decode_workspace_bytes(b=512, h=25, page_size=page_size, columns=case.columns,
+                                                split_tokens=split)
+    ws = RawDeviceBuffer(max(ws_bytes, 4))
+    work, items, merges = paged_ops.decode_work_list(case.lengths, 25, split, rt.compute_units())
+    assert merges > 0 and case.lengths.max() > 1024  # the split reduction runs
+    order = RawDeviceBuffer(4 * len(work))
+    order.upload(work)
+    paged_ops.paged_decode_split(case.out.ptr, case.q.ptr, case.k.ptr, case.v.ptr, case.slab_table.ptr,
+                                 case.block_table.ptr, case.offsets.ptr, **kw, split_tokens=split,
+                                 work=order.ptr, work_items=items, merge_rows=merges,
+                                 workspace=ws.ptr, workspace_bytes=ws_bytes)
+    runtime().synchronize()
+    got = case.out.to_numpy()
+    after = case.pool.download(np.uint16)
+
+    slabs = np.array([image.ctypes.data + s * case.slab_bytes for s in range(case.num_slabs)], np.uint64)
+    table = np.ascontiguousarray(case.table_host, np.int32)
+    offsets = (case.lengths - 1).astype(np.int32)
+    out = np.zeros_like(q)
+    status = lib.oracle_paged_decode_batch(out.ctypes.data, q.ctypes.data, k.ctypes.data, v.ctypes.data,
+                                           slabs.ctypes.data, table.ctypes.data, offsets.ctypes.data,
+                                           512, 25, 64, page_size, case.pages_per_slab, case.num_slabs,
+                                           case.columns, 0, 1, c_oracle.CODES['bfloat16'], 0)
+    assert status == 0
+    ref = decode_host(out, 'bfloat16').reshape(got.shape)
+    assert_attention_close(got, ref, 'bfloat16', context=f'config 5 P={page_size}')
+    assert np.array_equal(after, image), 'append differs from the oracle'
+
+
 @pytest.mark.parametrize('dtype', ['float32', 'float16', 'bfloat16'])
 def test_multi_token_append_and_causal_attention(dtype):
     # Prefill-style use (reference minitorch/paged_kv_cache.py:205-221):
