@@ -35,6 +35,7 @@
 // O^T += V^T P^T with v_mfma_f32_16x16x32); fp32 and the shapes it does not
 // take use the per-query query_kernel.
 #include "mt_device.h"
+#include "../../include/mt_paged.h"
 #include <climits>
 
 #ifndef MT_NT_LOADS
