@@ -106,6 +106,44 @@ def cpu_baseline(case, seconds):
                 host=dict(nproc=os.cpu_count(), cpu_model=host_cpu_model()))
 
 
+def ragged_cpu_baseline(case, seconds):
+    """The C oracle's decode step (append + attention, fp32 arithmetic) on a
+    device-built ragged case, downloaded to the host: median step time on up
+    to 16 threads over ``seconds`` and on one thread (at least 10 steps each)."""
+    try:
+        from oracle import c_oracle
+        lib = c_oracle.library()
+    except Exception as error:  # the oracle library is optional on the GPU box
+        return dict(value=None, unit='tokens/s', cores=None, kind='port', sample=f'unavailable: {error}')
+    image = case.pool.download(np.uint16 if case.dtype != 'float32' else np.float32)
+    q, k, v = (t.raw_numpy() for t in (case.q, case.k, case.v))
+    slabs = np.array([image.ctypes.data + s * case.slab_bytes for s in range(case.num_slabs)], np.uint64)
+    table = np.ascontiguousarray(case.table_host, np.int32)
+    offsets = (case.lengths - 1).astype(np.int32)
+    out = np.zeros_like(q)
+    code = c_oracle.CODES[case.dtype]
+
+    def run(threads):
+        status = lib.oracle_paged_decode_batch(out.ctypes.data, q.ctypes.data, k.ctypes.data, v.ctypes.data,
+                                               slabs.ctypes.data, table.ctypes.data, offsets.ctypes.data,
+                                               case.batch, case.heads, case.dim, case.page_size,
+                                               case.pages_per_slab, case.num_slabs, case.columns, 0, 1, code,
+                                               threads)
+        if status:
+            raise RuntimeError(f'oracle_paged_decode_batch returned {status}')
+
+    threads = min(os.cpu_count() or 1, 16)
+    many = timed_steps(lambda: run(threads), seconds)
+    one = timed_steps(lambda: run(1), seconds / 2)
+    rate = lambda t: case.batch / float(np.median(t))
+    return dict(value=rate(many), unit='tokens/s', cores=threads, kind='port',
+                sample=f'median of {len(many)} full config-5 steps (B=512, H=25, P={case.page_size}, same '
+                       f'hash-filled pool downloaded from the device, {many.sum():.1f} s), fp32 arithmetic on '
+                       f'{case.dtype} pages, OpenMP over (request, head)',
+                single_core=dict(value=rate(one), cores=1, steps=len(one)),
+                host=dict(nproc=os.cpu_count(), cpu_model=host_cpu_model()))
+
+
 def pattern_ceiling(case, devs, steps, warmup):
     """Bandwidth of the decode step's K/V access pattern alone: every (row,
     head, page) K and V page-head chunk (P*D*s bytes, randomly placed by the
@@ -209,6 +247,8 @@ def bench_config5(args):
                                 achieved_gbs=nbytes / per / 1e9, frac=nbytes / per / 1e9 / PEAK_HBM_GBS,
                                 algorithmic_bytes=nbytes, columns=case.columns,
                                 rows_over_1024=int((L > 1024).sum()), max_context=int(L.max()))
+        if page_size == 16 and not args.no_cpu_baseline:
+            lines['cpu_baseline'] = ragged_cpu_baseline(case, args.cpu_seconds)
         del case, ws, order
     main16 = lines[16]
     return {
@@ -223,6 +263,7 @@ def bench_config5(args):
                      'unit': 'GB/s', 'frac': main16['frac'], 'traffic': None,
                      'algorithmic_bytes_per_launch': main16['algorithmic_bytes']},
         'page_size_16': lines[16], 'page_size_32': lines[32],
+        'cpu_baseline': lines.get('cpu_baseline'),
     }
 
 
@@ -343,6 +384,45 @@ def bench_prefill(args):
                 12, 'float16', c3, args.seed, args.cpu_seconds)}
 
 
+def e2e_cpu_baseline(model, lengths, seconds, seed):
+    """Decode steps of the same architecture on the host: the oracle's
+    KV-cached batched decode (numpy fp32, BLAS threads for the projections)
+    over caches of the given context lengths (capped 16 below the position
+    limit, so that steps can follow) holding zero K/V (a step's cost does not
+    depend on their values), median step time over ``seconds`` (at least 10
+    steps)."""
+    from oracle import gpt2_oracle as go
+    rng = np.random.default_rng([seed, 7])
+    state = go._cast(model.state, np.float32)
+    hd = model.n_embd // model.n_head
+    lengths = [min(int(n), model.n_positions - 16) for n in lengths]
+    room = model.n_positions - max(lengths)
+    caches = [{'length': n, 'k': [np.zeros((model.n_head, n + room, hd), np.float32) for _ in range(model.n_layer)],
+               'v': [np.zeros((model.n_head, n + room, hd), np.float32) for _ in range(model.n_layer)]}
+              for n in lengths]
+    ids = rng.integers(0, model.n_vocab, len(lengths))
+    start = [c['length'] for c in caches]
+
+    def step():
+        nonlocal ids
+        if caches[0]['length'] - start[0] >= room - 1:  # rewind: same work per step
+            for c, n in zip(caches, start):
+                c['length'] = n
+        ids = go.decode_step(state, caches, ids, n_head=model.n_head, n_layer=model.n_layer).argmax(axis=1)
+
+    many = timed_steps(step, seconds)
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((p.get('num_threads', 1) for p in threadpool_info()), default=None)
+    except Exception:
+        threads = None
+    return dict(value=len(lengths) / float(np.median(many)), unit='tokens/s', cores=threads, kind='port',
+                sample=f'median of {len(many)} decode steps ({many.sum():.1f} s) of B={len(lengths)} rows, contexts '
+                       f'{min(lengths)}..{max(lengths)} (mean {np.mean(lengths):.0f}), numpy fp32 KV-cached '
+                       f'decode (oracle/gpt2_oracle.py), zero K/V',
+                host=dict(nproc=os.cpu_count(), cpu_model=host_cpu_model()))
+
+
 def bench_e2e(args):
     from minitorch_amd import model as model_mod, e2e
     if args.config == 3:
@@ -357,6 +437,11 @@ def bench_e2e(args):
             # the same trace through the sync-free loop (device-side token feedback)
             e2e.run_config3(model, warm, precision='fp16', token_feedback=True)
             r['sync_free'] = e2e.run_config3(model, trace, precision='fp16', token_feedback=True)
+        if not args.no_cpu_baseline:
+            # the trace's mean decode batch, mid-generation contexts of its first requests
+            batch = max(1, int(round((r.get('sync_free') or r).get('mean_decode_batch_size', 2))))
+            r['cpu_baseline'] = e2e_cpu_baseline(model, [len(p) + 64 for _, _, p, _ in trace[:batch]],
+                                                 args.cpu_seconds, args.seed)
         value, workload = r.get('busy_decode_tokens_per_sec'), (
             'config 3: continuous batching, random-init DistilGPT-2 (6 layers, d 768, 12 heads, vocab '
             '50257), fp16, 256 Poisson requests at 32 req/s, prompts U[32,512], outputs geometric mean '
@@ -369,6 +454,9 @@ def bench_e2e(args):
         r = e2e.run_config4(model, **kw) if args.loop in ('both', 'sync') else {}
         if args.loop in ('both', 'sync-free'):
             r['sync_free'] = e2e.run_config4(model, **kw, token_feedback=True)
+        if not args.no_cpu_baseline:
+            r['cpu_baseline'] = e2e_cpu_baseline(model, e2e.config4_lengths(np.random.default_rng([args.seed, 4]), 128),
+                                                 args.cpu_seconds, args.seed)
         value, workload = r.get('decode_tokens_per_sec'), (
             'config 4: steady state of 128 requests, random-init GPT-2-medium (24 layers, d 1024, 16 '
             'heads), bf16, contexts lognormal(median 256, sigma 1.2) clipped [16,1024], page 16, '
@@ -377,7 +465,7 @@ def bench_e2e(args):
     return {'metric': 'decode tokens/s (1 GPU), end to end', 'value': value, 'unit': 'tokens/s',
             'n_gpus': 1, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
             'dtype': dtype, 'data': 'synthetic (random-init weights, random token ids)',
-            'config': {'workload': workload}, 'measurements': r}
+            'config': {'workload': workload}, 'cpu_baseline': r.pop('cpu_baseline', None), 'measurements': r}
 
 
 def main():

@@ -65,3 +65,78 @@ def greedy(state, prompt, steps, *, n_head, n_layer, eps=1e-5):
         out.append(token)
         ids.append(token)
     return out, margins
+
+
+def prefill_cache(state, ids, *, n_head, n_layer, capacity=None, eps=1e-5, dtype=np.float32):
+    """K/V cache of a prompt and the logits of its last position, computed as
+    ``forward`` does. The cache is {'length': n, 'k': [...], 'v': [...]} with
+    per-layer K and V arrays [n_head, capacity, hd] (capacity defaults to n)."""
+    g = _cast(state, dtype)
+    ids = np.asarray(ids, np.int64)
+    n = ids.size
+    capacity = n if capacity is None else capacity
+    x = g['transformer.wte.weight'][ids] + g['transformer.wpe.weight'][np.arange(n)]
+    d = x.shape[-1]
+    hd = d // n_head
+    mask = np.triu(np.full((n, n), -np.inf, dtype), 1)
+    cache = {'length': n, 'k': [], 'v': []}
+    for i in range(n_layer):
+        p = f'transformer.h.{i}.'
+        h = layernorm(x, g[p + 'ln_1.weight'], g[p + 'ln_1.bias'], eps)
+        qkv = h @ g[p + 'attn.c_attn.weight'] + g[p + 'attn.c_attn.bias']
+        q, k, v = (qkv[:, j * d:(j + 1) * d].reshape(n, n_head, hd).transpose(1, 0, 2) for j in range(3))
+        for name, t in (('k', k), ('v', v)):
+            buf = np.zeros((n_head, capacity, hd), dtype)
+            buf[:, :n] = t
+            cache[name].append(buf)
+        s = q @ k.transpose(0, 2, 1) / np.sqrt(dtype(hd)) + mask
+        a = np.exp(s - s.max(-1, keepdims=True))
+        a = a / a.sum(-1, keepdims=True)
+        o = (a @ v).transpose(1, 0, 2).reshape(n, d)
+        x = x + o @ g[p + 'attn.c_proj.weight'] + g[p + 'attn.c_proj.bias']
+        h = layernorm(x, g[p + 'ln_2.weight'], g[p + 'ln_2.bias'], eps)
+        x = x + gelu(h @ g[p + 'mlp.c_fc.weight'] + g[p + 'mlp.c_fc.bias']) @ g[p + 'mlp.c_proj.weight'] + g[p + 'mlp.c_proj.bias']
+    x = layernorm(x[-1:], g['transformer.ln_f.weight'], g['transformer.ln_f.bias'], eps)
+    return cache, (x @ g['transformer.wte.weight'].T)[0]
+
+
+def decode_step(state, caches, ids, *, n_head, n_layer, eps=1e-5, dtype=np.float32):
+    """One batched decode step with K/V caches (reference DecoderLM.decode_batch,
+    minitorch/modules_transformer.py:373-390): token ids[b] at position
+    caches[b]['length']; writes each row's K/V into its cache, advances the
+    lengths and returns logits [B, V]. The projections run on the whole batch
+    at once, attention per row over its own cache."""
+    g = _cast(state, dtype)
+    ids = np.asarray(ids, np.int64)
+    pos = np.array([c['length'] for c in caches], np.int64)
+    x = g['transformer.wte.weight'][ids] + g['transformer.wpe.weight'][pos]
+    b, d = x.shape
+    hd = d // n_head
+    scale = 1 / np.sqrt(dtype(hd))
+    for i in range(n_layer):
+        p = f'transformer.h.{i}.'
+        h = layernorm(x, g[p + 'ln_1.weight'], g[p + 'ln_1.bias'], eps)
+        qkv = h @ g[p + 'attn.c_attn.weight'] + g[p + 'attn.c_attn.bias']
+        o = np.empty((b, d), dtype)
+        for r, cache in enumerate(caches):
+            n = cache['length']
+            q, k, v = (qkv[r, j * d:(j + 1) * d].reshape(n_head, hd) for j in range(3))
+            kc, vc = cache['k'][i], cache['v'][i]
+            kc[:, n], vc[:, n] = k, v
+            s = np.einsum('hd,hnd->hn', q, kc[:, :n + 1]) * scale
+            a = np.exp(s - s.max(-1, keepdims=True))
+            a = a / a.sum(-1, keepdims=True)
+            o[r] = np.einsum('hn,hnd->hd', a, vc[:, :n + 1]).reshape(d)
+        x = x + o @ g[p + 'attn.c_proj.weight'] + g[p + 'attn.c_proj.bias']
+        h = layernorm(x, g[p + 'ln_2.weight'], g[p + 'ln_2.bias'], eps)
+        x = x + gelu(h @ g[p + 'mlp.c_fc.weight'] + g[p + 'mlp.c_fc.bias']) @ g[p + 'mlp.c_proj.weight'] + g[p + 'mlp.c_proj.bias']
+    for c in caches:
+        c['length'] += 1
+    x = layernorm(x, g['transformer.ln_f.weight'], g['transformer.ln_f.bias'], eps)
+    return x @ g['transformer.wte.weight'].T
+
+
+def _cast(state, dtype):
+    if all(np.asarray(v).dtype == dtype for v in state.values()):
+        return state
+    return {k: np.asarray(v, dtype) for k, v in state.items()}

@@ -35,3 +35,28 @@ def test_greedy_margins_reported():
     assert len(tokens) == 5 and all(m >= 0 for m in margins)
     logits = go.forward(state, [1, 2, 3] + tokens[:2], n_head=2, n_layer=1)[-1]
     assert tokens[2] == int(np.argmax(logits))
+
+
+@pytest.mark.parametrize('dtype,tol', [(np.float64, 1e-10), (np.float32, 2e-4)])
+def test_cached_decode_step_equals_full_forward(dtype, tol):
+    # The KV-cached batched decode (the CPU baseline of the end-to-end
+    # configs) gives, row by row, the last-position logits of the full
+    # forward over the whole sequence; a wrong position, a stale cache row or
+    # a row mixed into another's attention fails it.
+    state = init_gpt2_state(n_vocab=97, n_embd=32, n_layer=2, n_positions=64, seed=5)
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, 97, n).tolist() for n in (1, 7, 20)]
+    caches, seqs = [], []
+    for p in prompts:
+        cache, last = go.prefill_cache(state, p, n_head=4, n_layer=2, capacity=len(p) + 4, dtype=dtype)
+        full = go.forward(state, p, n_head=4, n_layer=2)[-1]
+        assert np.abs(last - full).max() <= tol * np.abs(full).max()
+        caches.append(cache)
+        seqs.append(list(p) + [int(np.argmax(full))])
+    for _ in range(4):
+        logits = go.decode_step(state, caches, [s[-1] for s in seqs], n_head=4, n_layer=2, dtype=dtype)
+        for r, s in enumerate(seqs):
+            full = go.forward(state, s, n_head=4, n_layer=2)[-1]
+            assert np.abs(logits[r] - full).max() <= tol * np.abs(full).max(), r
+            s.append(int(np.argmax(full)))
+    assert [c['length'] for c in caches] == [len(s) - 1 for s in seqs]
