@@ -450,7 +450,7 @@ def bench_e2e(args):
     else:
         model = model_mod.gpt2_medium(seed=args.seed)
         kw = dict(seed=args.seed, steps=min(args.steps, 40), warmup=min(args.warmup, 5),
-                  replace_rate=args.replace_rate)
+                  replace_rate=args.replace_rate, batch_prefills=not args.prefill_each)
         r = e2e.run_config4(model, **kw) if args.loop in ('both', 'sync') else {}
         if args.loop in ('both', 'sync-free'):
             r['sync_free'] = e2e.run_config4(model, **kw, token_feedback=True)
@@ -492,6 +492,8 @@ def main():
                          'decode, bf16, H=25, P=16 and 32; 3 / 4: end-to-end decode')
     ap.add_argument('--loop', choices=('both', 'sync', 'sync-free'), default='both',
                     help='configs 3/4: the synchronous loop, the sync-free one, or both')
+    ap.add_argument('--prefill-each', action='store_true',
+                    help='config 4: one prefill call per replaced request instead of one batched call per step')
     ap.add_argument('--replace-rate', type=float, default=0.05,
                     help='config 4: fraction of requests replaced per step (0 = decode steps only)')
     ap.add_argument('--prefill', action='store_true',

@@ -150,6 +150,25 @@ int mt_prefill_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
                       int dtype, int fused_gelu, void* scratch, size_t scratch_bytes,
                       const mt_prefill_attention* att);
 
+/* The prefill of `requests` prompts of different lengths in one layer loop:
+ * tokens[r] rows for request r (host array), token-major and concatenated in
+ * request order (x [sum tokens, d] fp32, updated in place; h [sum tokens, d]
+ * in dtype). The projections, LayerNorms and GELU run once over all rows;
+ * per layer, each request's K/V are appended and its causal attention
+ * computed with mt_paged_prefill over its own pages, att[r] (host array of
+ * `requests` structs: the request's table row, offset and pool geometry).
+ * When logits is not null, logits [requests, vocab] = final-LayerNorm(x)[last
+ * row of each request] @ head_weight^T. Scratch as
+ * mt_decoder_scratch_bytes(sum tokens). Results equal one mt_prefill_layers
+ * call per request up to the projections' algorithm choice for the row
+ * count. No reference counterpart (the reference prefills one request per
+ * call, minitorch/continuous_batching.py:164-170). */
+int mt_prefill_layers_ragged(void* handle, const mt_decoder_layer* layers, int n_layer, float* x,
+                             void* h, const float* final_gamma, const float* final_beta,
+                             const void* head_weight, void* logits, int vocab, int requests,
+                             const int* tokens, int d, int heads, float eps, int dtype, int fused_gelu,
+                             void* scratch, size_t scratch_bytes, const mt_prefill_attention* att);
+
 #ifdef __cplusplus
 }
 #endif

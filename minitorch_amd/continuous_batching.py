@@ -222,6 +222,7 @@ class ContinuousBatcher:
                             self._finish(request, 'failed', 'decode_error')
                     raise
             decode_seconds = self.clock() - start
+            admitted = []
             while self.pending and len(self.active) < self.max_batch_size and len(prefill_ids) < self.max_prefills_per_step:
                 request = self.pending[0]
                 if self.reserved_pages + request.reserved_pages > self.pool.max_pages:
@@ -235,21 +236,14 @@ class ContinuousBatcher:
                 try:
                     request.cache = self.model.create_kv_cache(1, request.capacity, cache_impl='paged',
                                                                page_size=self.pool.page_size, page_pool=self.pool)
-                    ids = DeviceTensor.from_numpy(np.array([request.prompt_ids], np.float32))
-                    logits, _ = self.model.prefill(ids, request.cache)
-                    self.peak_used_pages = max(self.peak_used_pages, self.pool.used_pages)
-                    if self.token_feedback:
-                        self._issue([request], greedy_token(logits, feedback=request.cache))
-                        if request.eos_token_id is not None:
-                            events.extend(self._drain())
-                    else:
-                        token = greedy_token(logits).to_numpy()[0, 0]
-                        events.append(self._emit(request, token, self.clock()))
                 except Exception:
                     self._finish(request, 'failed', 'prefill_error')
                     raise
+                admitted.append(request)
                 prefill_ids.append(request.request_id)
                 prefill_tokens += len(request.prompt_ids)
+            if admitted:
+                events.extend(self._prefill(admitted))
         if self.token_feedback:
             # Only the read-backs issued in this step stay in flight: the
             # previous step's tokens are delivered while this step runs. A
@@ -270,6 +264,39 @@ class ContinuousBatcher:
                               token_feedback=self.token_feedback, tokens_in_flight=len(self._inflight),
                               **self.pool.memory_stats())
         self.iteration += 1
+        return events
+
+    def _prefill(self, admitted):
+        """Prefill the requests admitted in this step and emit (or, sync-free,
+        issue) their first tokens. One request goes through ``prefill`` as in
+        the reference; several admitted together go through one
+        ``prefill_batch`` call (pages acquired in admission order, as
+        consecutive prefills would)."""
+        events = []
+        try:
+            if len(admitted) == 1:
+                request = admitted[0]
+                ids = DeviceTensor.from_numpy(np.array([request.prompt_ids], np.float32))
+                logits, _ = self.model.prefill(ids, request.cache)
+                feedback = request.cache
+            else:
+                logits = self.model.prefill_batch([np.array(r.prompt_ids) for r in admitted],
+                                                  [r.cache for r in admitted])
+                feedback = [r.cache for r in admitted]
+            self.peak_used_pages = max(self.peak_used_pages, self.pool.used_pages)
+            if self.token_feedback:
+                self._issue(admitted, greedy_token(logits, feedback=feedback))
+                if any(r.eos_token_id is not None for r in admitted):
+                    events.extend(self._drain())
+            else:
+                tokens = greedy_token(logits).to_numpy()[:, 0]
+                arrival = self.clock()
+                events.extend(self._emit(r, t, arrival) for r, t in zip(admitted, tokens))
+        except Exception:
+            for request in admitted:
+                if not request.done:
+                    self._finish(request, 'failed', 'prefill_error')
+            raise
         return events
 
     def close(self):

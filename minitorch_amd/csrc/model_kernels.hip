@@ -19,6 +19,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <vector>
 
 using namespace mt;
 
@@ -520,6 +521,42 @@ int gemm_gelu(Blas* blas, void* out, const void* a, const void* b, const void* b
   return e ? e : gelu(out, int64_t(m) * n, dtype);
 }
 
+// Row gather with the source rows in the launch arguments: out[i, :] =
+// in[row[i], :] for i < count (at most kGatherRows per launch), width in
+// 16-bit or 32-bit elements moved as 32-bit words.
+constexpr int kGatherRows = 64;
+struct GatherRows {
+  int count;
+  int row[kGatherRows];
+};
+
+__global__ __launch_bounds__(256) void gather_rows_kernel(uint32_t* out, const uint32_t* in, int64_t words,
+                                                          GatherRows g) {
+  const int i = blockIdx.y;
+  if (i >= g.count) return;
+  const uint32_t* src = in + int64_t(g.row[i]) * words;
+  uint32_t* dst = out + int64_t(i) * words;
+  for (int64_t w = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; w < words; w += int64_t(gridDim.x) * blockDim.x)
+    dst[w] = src[w];
+}
+
+// out[i, :] = in[rows[i], :] for `count` rows of `row_bytes` (a multiple of 4).
+hipError_t gather_rows(void* out, const void* in, const int* rows, int count, size_t row_bytes) {
+  if (row_bytes % 4) return hipErrorInvalidValue;
+  const int64_t words = int64_t(row_bytes / 4);
+  for (int c0 = 0; c0 < count; c0 += kGatherRows) {
+    GatherRows g;
+    g.count = count - c0 < kGatherRows ? count - c0 : kGatherRows;
+    for (int i = 0; i < g.count; ++i) g.row[i] = rows[c0 + i];
+    const dim3 grid(unsigned((words + 255) / 256), unsigned(g.count));
+    gather_rows_kernel<<<grid, 256>>>(static_cast<uint32_t*>(out) + int64_t(c0) * words,
+                                      static_cast<const uint32_t*>(in), words, g);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 }  // namespace
 
 extern "C" {
@@ -762,6 +799,67 @@ int mt_prefill_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
   if (!st && logits)
     st = gemm(blas, logits, static_cast<char*>(h) + size_t(n - 1) * d * e, head_weight, nullptr, batch,
               vocab, d, 1, dtype, dtype, kEpiNone, false, n * d);
+  return st;
+}
+
+int mt_prefill_layers_ragged(void* handle, const mt_decoder_layer* layers, int n_layer, float* x,
+                             void* h, const float* final_gamma, const float* final_beta,
+                             const void* head_weight, void* logits, int vocab, int requests,
+                             const int* tokens, int d, int heads, float eps, int dtype, int fused_gelu,
+                             void* scratch, size_t scratch_bytes, const mt_prefill_attention* att) {
+  if (!handle || !layers || n_layer < 1 || !x || !h || !final_gamma || !final_beta ||
+      (logits && (!head_weight || vocab < 1)) || requests < 1 || !tokens || d < 1 || heads < 1 ||
+      d % heads || !dtype_ok(dtype) || !scratch || !att)
+    return hipErrorInvalidValue;
+  int64_t total = 0;
+  for (int r = 0; r < requests; ++r) {
+    if (tokens[r] < 1) return hipErrorInvalidValue;
+    total += tokens[r];
+  }
+  if (total > INT32_MAX || total * 4 * d > INT32_MAX ||
+      scratch_bytes < mt_decoder_scratch_bytes(int(total), d, dtype))
+    return hipErrorInvalidValue;
+  const int rows = int(total);
+  Blas* blas = static_cast<Blas*>(handle);
+  const size_t e = dtype == kF32 ? 4 : 2;
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+  char* qkv = static_cast<char*>(scratch);
+  char* attn = qkv + al(size_t(rows) * 3 * d * e);
+  char* proj = attn + al(size_t(rows) * d * e);
+  char* mlp = proj + al(size_t(rows) * d * e);
+  const int hd = d / heads;
+  int st = layernorm(h, x, layers[0].ln1_gamma, layers[0].ln1_beta, rows, d, eps, dtype);
+  for (int i = 0; i < n_layer && !st; ++i) {
+    const mt_decoder_layer& L = layers[i];
+    if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 1, dtype, dtype))) break;
+    // Attention per request over its own pages: rows [first, first + n).
+    int64_t first = 0;
+    for (int r = 0; r < requests && !st; ++r) {
+      const mt_prefill_attention& A = att[r];
+      st = mt_paged_prefill(attn + size_t(first) * d * e, qkv + size_t(first) * 3 * d * e,
+                            qkv + (size_t(first) * 3 * d + d) * e, qkv + (size_t(first) * 3 * d + 2 * d) * e,
+                            A.slabs, A.table, 1, heads, tokens[r], hd, A.page_size, A.pages_per_slab,
+                            A.num_slabs, A.columns, i, A.layers, A.offset, dtype, 3 * d, d);
+      first += tokens[r];
+    }
+    if (st) break;
+    if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 1, dtype, dtype))) break;
+    if ((st = residual_layernorm(h, x, proj, L.ln2_gamma, L.ln2_beta, rows, d, eps, dtype))) break;
+    if ((st = gemm_gelu(blas, mlp, h, L.w_fc, L.b_fc, rows, 4 * d, d, dtype, fused_gelu != 0, false, 1))) break;
+    if ((st = gemm(blas, proj, mlp, L.w_proj, L.b_proj, rows, d, 4 * d, 1, dtype, dtype))) break;
+    const bool last = i + 1 == n_layer;
+    st = residual_layernorm(h, x, proj, last ? final_gamma : layers[i + 1].ln1_gamma,
+                            last ? final_beta : layers[i + 1].ln1_beta, rows, d, eps, dtype);
+  }
+  // Tied head over each request's last row, gathered into the (now free)
+  // attention scratch.
+  if (!st && logits) {
+    std::vector<int> last(requests);
+    int64_t end = 0;
+    for (int r = 0; r < requests; ++r) last[r] = int((end += tokens[r]) - 1);
+    st = gather_rows(attn, h, last.data(), requests, size_t(d) * e);
+    if (!st) st = gemm(blas, logits, attn, head_weight, nullptr, requests, vocab, d, 1, dtype, dtype);
+  }
   return st;
 }
 

@@ -106,7 +106,7 @@ def config4_lengths(rng, n):
 
 
 def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_rate=0.05,
-                precision='bf16', page_size=16, kv_pages=None, token_feedback=False):
+                precision='bf16', page_size=16, kv_pages=None, token_feedback=False, batch_prefills=True):
     """Steady-state decode throughput; returns a dict of measurements.
 
     ``decode_tokens_per_sec`` (synchronous loop only) times each step's decode
@@ -114,7 +114,10 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
     timed loop (decode steps plus the replacement prefills, synchronized only
     at its start and end), which is comparable between the synchronous loop
     and the sync-free one (``token_feedback``: tokens stay on the device as
-    the next step's input and are never read)."""
+    the next step's input and are never read). With ``batch_prefills`` the
+    requests replaced in a step are prefilled together
+    (``DecoderLM.prefill_batch``), else one ``prefill`` call each; the random
+    draws, and so the replacements and prompts, are the same either way."""
     dtype = {'fp16': 'float16', 'bf16': 'bfloat16', 'fp32': 'float32'}[precision]
     rng = np.random.default_rng([seed, 4])
     rt = runtime()
@@ -125,21 +128,35 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
         pool = KVPagePool(model, page_size=page_size, max_bytes=kv_pages * page_bytes, pages_per_slab=16)
         caches, last = [], []
 
-        def admit():
+        def draw():
             # context length L counts the token being decoded: prompt of L - 1
             length = int(config4_lengths(rng, 1)[0]) - 1
-            prompt = rng.integers(0, model.n_vocab, length)
-            cache = model.create_kv_cache(1, model.n_positions, page_size=page_size, page_pool=pool)
-            logits, _ = model.prefill(DeviceTensor.from_numpy(prompt[None].astype(np.float32)), cache)
-            if token_feedback:
-                greedy_token(logits, feedback=cache)
-                return cache, None
-            return cache, int(greedy_token(logits).to_numpy()[0, 0])
+            return rng.integers(0, model.n_vocab, length)
 
-        for _ in range(concurrent):
-            c, t = admit()
-            caches.append(c)
-            last.append(t)
+        def admit(prompts):
+            """New caches prefilled with ``prompts``, and their first tokens."""
+            new = [model.create_kv_cache(1, model.n_positions, page_size=page_size, page_pool=pool)
+                   for _ in prompts]
+            if batch_prefills:
+                logits = model.prefill_batch(prompts, new)
+            else:
+                logits = [model.prefill(DeviceTensor.from_numpy(p[None].astype(np.float32)), c)[0]
+                          for p, c in zip(prompts, new)]
+            if token_feedback:
+                if batch_prefills:
+                    greedy_token(logits, feedback=new)
+                else:
+                    for c, l in zip(new, logits):
+                        greedy_token(l, feedback=c)
+                return new, [None] * len(new)
+            if batch_prefills:
+                return new, [int(t) for t in greedy_token(logits).to_numpy()[:, 0]]
+            return new, [int(greedy_token(l).to_numpy()[0, 0]) for l in logits]
+
+        for c0 in range(0, concurrent, 32):
+            new, first = admit([draw() for _ in range(min(32, concurrent - c0))])
+            caches += new
+            last += first
         decode_seconds, tokens, replaced, context = 0.0, 0, 0, []
         loop0 = None
         for step in range(warmup + steps):
@@ -164,18 +181,24 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
                 last = [int(t) for t in nxt]
                 if step % 10 == 0:
                     _progress(f'config 4: step {step}, decode {(t1 - t0) * 1e3:.2f} ms')
+            slots, prompts = [], []
             for i in range(len(caches)):
                 if rng.random() < replace_rate or caches[i].length + 1 >= caches[i].capacity:
                     caches[i].close()
-                    caches[i], last[i] = admit()
-                    replaced += 1
+                    slots.append(i)
+                    prompts.append(draw())
+            if slots:
+                new, first = admit(prompts)
+                for i, c, t in zip(slots, new, first):
+                    caches[i], last[i] = c, t
+                replaced += len(slots)
         rt.synchronize()
         loop_seconds = time.perf_counter() - loop0
         stats = pool.memory_stats()
         for c in caches:
             c.close()
         pool.close()
-    return dict(token_feedback=token_feedback,
+    return dict(token_feedback=token_feedback, batch_prefills=batch_prefills,
                 decode_tokens_per_sec=tokens / decode_seconds if decode_seconds else None,
                 decode_seconds=decode_seconds, loop_tokens_per_sec=tokens / loop_seconds,
                 loop_seconds=loop_seconds, steps=steps, concurrent=concurrent,

@@ -31,9 +31,10 @@ def last_position(x):
 def greedy_token(logits, feedback=None):
     """GPU argmax over [B, 1, V] logits, returning fp32 token IDs [B, 1]; ties
     and NaNs choose the first index, like numpy.argmax (reference
-    minitorch/kv_cache.py:39-53). With ``feedback`` (a paged cache of B rows)
-    the tokens are also stored as its slots' last tokens in the pool, where
-    the next decode step reads them without a host round trip."""
+    minitorch/kv_cache.py:39-53). With ``feedback`` (a paged cache of B rows,
+    or a sequence of B paged caches of one row each, on one pool) the tokens
+    are also stored as the slots' last tokens in the pool, where the next
+    decode step reads them without a host round trip."""
     if not isinstance(logits, DeviceTensor) or logits.dims != 3 or logits.shape[1] != 1:
         raise ValueError('greedy_token requires no_grad and device logits [B,1,V]')
     b, _, v = logits.shape
@@ -42,6 +43,14 @@ def greedy_token(logits, feedback=None):
     out = DeviceTensor((b, 1), 'float32')
     if feedback is None:
         paged_ops.row_argmax(out.ptr, logits.ptr, b, v, logits.dtype)
+    elif isinstance(feedback, (list, tuple)):
+        pool = feedback[0].pool if feedback else None
+        if (len(feedback) != b or pool is None or pool.closed or
+                any(c.pool is not pool or c.batch_size != 1 for c in feedback)):
+            raise ValueError('Feedback caches must be live, share a pool and hold one row per logits row')
+        slots = DeviceTensor.from_numpy(np.array([c.slot for c in feedback], np.int32), 'int32')
+        paged_ops.row_argmax_feedback(out.ptr, pool.slot_tokens.ptr, slots.ptr, pool.max_slots,
+                                      logits.ptr, b, v, logits.dtype)
     else:
         pool = feedback.pool
         if feedback.batch_size != b or pool.closed:

@@ -234,6 +234,69 @@ class DecoderLM:
         """One new token per batch row of one cache (reference :367-371)."""
         return self._cached_forward(idx, cache, False)
 
+    def prefill_batch(self, prompts, caches):
+        """Prefill prompts of different lengths, each into its own empty paged
+        cache of batch size 1 (all on one pool), in one native layer loop
+        (``mt_prefill_layers_ragged``): the projections run once over every
+        prompt row, attention per prompt over its own pages. Returns the
+        last-position logits [R, 1, V], row r for prompt r. Pages are acquired
+        cache by cache in the given order, as consecutive ``prefill`` calls
+        would. No reference counterpart (the reference prefills one request per
+        call, minitorch/continuous_batching.py:164-170)."""
+        from .paged_kv_cache import PagedKVCache
+        caches = tuple(caches)
+        prompts = [np.asarray(p) for p in prompts]
+        if not caches or len(prompts) != len(caches) or len({id(c) for c in caches}) != len(caches):
+            raise ValueError('prefill_batch needs one prompt per distinct cache')
+        pool = getattr(caches[0], 'pool', None)
+        for cache, prompt in zip(caches, prompts):
+            if not isinstance(cache, PagedKVCache) or cache.pool is not pool or cache.batch_size != 1:
+                raise ValueError('prefill_batch requires paged caches of batch size 1 on one pool')
+            if prompt.ndim != 1 or prompt.size < 1 or prompt.dtype.kind not in 'iuf':
+                raise ValueError('Each prompt must be a nonempty 1-D array of token IDs')
+            cache._validate_model(self)
+            if cache.length != 0:
+                raise ValueError('prefill requires an empty cache')
+            if prompt.size > cache.capacity:
+                raise ValueError('KV cache capacity exceeded or empty prompt')
+        tokens = [int(p.size) for p in prompts]
+        dtype, d = caches[0].dtype, self.n_embd
+        w = self._weights(dtype)
+        prepared = []
+        try:
+            for cache, n in zip(caches, tokens):
+                cache.prepare_append(n)
+                prepared.append(cache)
+            total = sum(tokens)
+            ids = DeviceTensor.from_numpy(np.concatenate(prompts).astype(np.float32)[None], 'float32')
+            positions = DeviceTensor.from_numpy(
+                np.concatenate([np.arange(n, dtype=np.float32) for n in tokens])[None], 'float32')
+            x = self._embed(w, ids, positions)                      # [total, d] fp32
+            h = DeviceTensor((total, d), dtype)
+            lib = model_library()
+            scratch_bytes = _scratch_bytes(lib, total, d, dtype)
+            scratch = DeviceTensor(((scratch_bytes + 3) // 4,), 'float32')
+            att = (PrefillAttentionStruct * len(caches))(*[
+                PrefillAttentionStruct(pool.slab_table.ptr, c.block_table.ptr, c.page_size, pool.pages_per_slab,
+                                       pool.num_slabs, pool.max_cols, len(c.layout), 0) for c in caches])
+            counts = (I * len(caches))(*tokens)
+            logits = DeviceTensor((len(caches), 1, self.n_vocab), dtype)
+            call(lib, 'mt_prefill_layers_ragged',
+                 [P, P, I, P, P, P, P, P, P, I, I, P, I, I, F, I, I, P, ct.c_size_t, P],
+                 self.blas().handle, w.layer_array, self.n_layer, x.ptr, h.ptr, w.ln_f[0].ptr, w.ln_f[1].ptr,
+                 w.head.ptr, logits.ptr, self.n_vocab, len(caches), counts, d, self.n_head, self.ln_eps,
+                 dtype_code(dtype), 1 if FUSED_GELU else 0, scratch.ptr, scratch_bytes, att)
+            for cache in caches:
+                cache._written_layers.update(range(len(cache.layout)))
+                cache.last_attention_path = 'paged_prefill'
+                cache.commit_append()
+            return logits
+        except Exception:
+            for cache in prepared:
+                if cache._pending_tokens is not None:
+                    cache.abort_append()
+            raise
+
     def _cached_forward(self, idx, cache, prefill):
         cache.validate(self, idx, prefill)
         b, n = idx.shape

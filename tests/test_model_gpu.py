@@ -3,6 +3,8 @@ batched ragged decode vs independent per-request decode, and the
 continuous-batching gates of the reference's benchmark
 (project/benchmark_continuous_batching.py:50-66,115,189-191): every completed
 request's tokens equal independent generation, and the pool is drained."""
+from contextlib import nullcontext
+
 import numpy as np
 import pytest
 
@@ -80,14 +82,15 @@ def test_decode_batch_equals_independent_decode_fp32():
 
 
 def run_trace(model, trace, precision='fp32', max_batch_size=4, budget_pages=None, page_size=16,
-              token_feedback=False, eos=None):
+              token_feedback=False, eos=None, max_prefills_per_step=1):
     """Replay (arrival_step, id, prompt, new_tokens) on a step-indexed clock;
     ``eos`` maps request IDs to EOS token IDs. Returns the batcher, the
     per-step statistics and the events each step returned."""
     page_bytes = 2 * model.n_layer * model.n_embd * page_size * (4 if precision == 'fp32' else 2)
     budget = (budget_pages or 4096) * page_bytes
     batcher = ContinuousBatcher(model, max_batch_size=max_batch_size, page_size=page_size,
-                                kv_budget_bytes=budget, precision=precision, token_feedback=token_feedback)
+                                kv_budget_bytes=budget, precision=precision, token_feedback=token_feedback,
+                                max_prefills_per_step=max_prefills_per_step)
     steps, pending, events = [], sorted(trace), []
     while pending or batcher.has_work:
         while pending and pending[0][0] <= batcher.iteration:
@@ -105,11 +108,16 @@ def make_trace(model, rng, n=10):
              int(rng.integers(1, 12))) for i in range(n)]
 
 
-def test_continuous_batching_gates_fp32():
+@pytest.mark.parametrize('max_prefills', [1, 3])
+def test_continuous_batching_gates_fp32(max_prefills):
+    # with several prefills per step, those admitted together run as one
+    # batched prefill (DecoderLM.prefill_batch)
     model = tiny(seed=11)
     rng = np.random.default_rng(11)
     trace = make_trace(model, rng)
-    batcher, steps = run_trace(model, trace, budget_pages=40)
+    batcher, steps = run_trace(model, trace, budget_pages=40, max_prefills_per_step=max_prefills)
+    if max_prefills > 1:
+        assert max(len(s['prefill_request_ids']) for s in steps) > 1
     for _, rid, prompt, new in trace:
         r = batcher.requests[rid]
         assert r.state == 'completed'
@@ -120,18 +128,20 @@ def test_continuous_batching_gates_fp32():
     batcher.close()
 
 
-def test_continuous_batching_schedule_and_pages_match_oracle():
+@pytest.mark.parametrize('max_prefills', [1, 3])
+def test_continuous_batching_schedule_and_pages_match_oracle(max_prefills):
     """Scheduling decisions, KV statistics and every decode step's block table
-    equal the integer restatement, with the tokens the GPU produced."""
+    equal the integer restatement, with the tokens the GPU produced (with
+    several prefills per step, batched into one prefill call)."""
     model = tiny(seed=12)
     rng = np.random.default_rng(12)
     trace = make_trace(model, rng, 12)
-    batcher, steps = run_trace(model, trace, max_batch_size=3, budget_pages=30)
+    batcher, steps = run_trace(model, trace, max_batch_size=3, budget_pages=30, max_prefills_per_step=max_prefills)
     tokens = {rid: batcher.requests[rid].output_ids for _, rid, _, _ in trace}
     page_bytes = batcher.pool.page_bytes
     oracle_pool = PoolOracle(page_bytes=page_bytes, page_size=16, max_bytes=30 * page_bytes, pages_per_slab=4)
     ob = BatcherOracle(oracle_pool, lambda rid, i: tokens[rid][i], max_batch_size=3,
-                       n_positions=model.n_positions)
+                       max_prefills_per_step=max_prefills, n_positions=model.n_positions)
     pending = sorted(trace)
     ours = iter(steps)
     while pending or ob.has_work:
@@ -195,14 +205,15 @@ def assert_same_run(sync, sync_steps, fb, fb_steps, fb_events, trace):
     assert sum(map(len, delivered.values())) == sum(len(fb.requests[t[1]].output_ids) for t in trace)
 
 
-@pytest.mark.parametrize('precision', ['fp32', 'bf16'])
-def test_sync_free_loop_matches_synchronous_loop(precision):
+@pytest.mark.parametrize('precision,max_prefills', [('fp32', 1), ('bf16', 1), ('fp32', 3)])
+def test_sync_free_loop_matches_synchronous_loop(precision, max_prefills):
     model = tiny(seed=14)
     rng = np.random.default_rng(14)
     trace = make_trace(model, rng, 12)
-    sync, sync_steps = run_trace(model, trace, precision=precision, max_batch_size=3, budget_pages=30)
+    sync, sync_steps = run_trace(model, trace, precision=precision, max_batch_size=3, budget_pages=30,
+                                 max_prefills_per_step=max_prefills)
     fb, fb_steps, fb_events = run_trace(model, trace, precision=precision, max_batch_size=3, budget_pages=30,
-                                        token_feedback=True)
+                                        token_feedback=True, max_prefills_per_step=max_prefills)
     assert_same_run(sync, sync_steps, fb, fb_steps, fb_events, trace)
     if precision == 'fp32':
         for _, rid, prompt, new in trace:
@@ -285,3 +296,90 @@ def test_low_precision_prefill_and_decode_logits_near_oracle(precision):
         ref = go.forward(model.state, seq[:len(prompt) + i], n_head=model.n_head, n_layer=model.n_layer)[-1]
         err = np.abs(g - ref).max()
         assert err <= 0.02 * (ref.max() - ref.min()), (i, err, ref.max() - ref.min())
+
+
+@pytest.mark.parametrize('precision', ['fp32', 'bf16'])
+def test_prefill_batch_equals_one_prefill_per_request(precision):
+    # mt_prefill_layers_ragged: prompts of different lengths in one layer loop
+    # give the logits of one prefill call each (fp32: same tokens, 1e-4 of the
+    # logits' range; bf16: 2 %), and the caches they fill decode alike.
+    from minitorch_amd.paged_kv_cache import KVPagePool
+    model = tiny(seed=29)
+    rng = np.random.default_rng(29)
+    prompts = [rng.integers(0, model.n_vocab, n) for n in (1, 17, 40, 5, 63, 16)]
+    dtype = 'bfloat16' if precision == 'bf16' else None
+    bound = 1e-4 if precision == 'fp32' else 0.02
+
+    def run(batched):
+        pool = KVPagePool(model, page_size=16, max_bytes=64 * 1024 ** 2)
+        caches = [model.create_kv_cache(1, len(p) + 3, page_size=16, page_pool=pool) for p in prompts]
+        if batched:
+            logits = model.prefill_batch(prompts, caches).to_numpy()[:, 0]
+        else:
+            logits = np.stack([model.prefill(DeviceTensor.from_numpy(p[None].astype(np.float32)), c)[0]
+                               .to_numpy()[0, 0] for p, c in zip(prompts, caches)])
+        first = logits.argmax(axis=1)
+        step = model.decode_batch(DeviceTensor.from_numpy(first[:, None].astype(np.float32)), caches)
+        out = (logits.astype(np.float64), step.to_numpy()[:, 0].astype(np.float64), [c.length for c in caches],
+               pool.memory_stats()['kv_pool_used_pages'])
+        for c in caches:
+            c.close()
+        pool.close()
+        return out
+
+    with autocast(dtype) if dtype else nullcontext():
+        one, one_step, one_len, one_pages = run(False)
+        many, many_step, many_len, many_pages = run(True)
+    for a, b in ((one, many), (one_step, many_step)):
+        span = a.max() - a.min()
+        assert np.abs(a - b).max() <= bound * span
+    if precision == 'fp32':
+        assert np.array_equal(one.argmax(axis=1), many.argmax(axis=1))
+        assert np.array_equal(one_step.argmax(axis=1), many_step.argmax(axis=1))
+    assert one_len == many_len == [len(p) + 1 for p in prompts]
+    assert one_pages == many_pages
+
+
+def test_prefill_batch_feedback_tokens_feed_the_next_decode():
+    # greedy_token(logits, feedback=[caches]) stores each prompt's first token
+    # in its cache slot; decode_greedy then reads them on the device and gives
+    # the tokens of the host-fed decode.
+    from minitorch_amd.paged_kv_cache import KVPagePool
+    model = tiny(seed=31)
+    rng = np.random.default_rng(31)
+    prompts = [rng.integers(0, model.n_vocab, n) for n in (9, 30, 2)]
+    pool = KVPagePool(model, page_size=16, max_bytes=64 * 1024 ** 2)
+    a = [model.create_kv_cache(1, 40, page_size=16, page_pool=pool) for _ in prompts]
+    b = [model.create_kv_cache(1, 40, page_size=16, page_pool=pool) for _ in prompts]
+    la = model.prefill_batch(prompts, a)
+    first = greedy_token(la, feedback=a).to_numpy()[:, 0]
+    lb = model.prefill_batch(prompts, b)
+    host = greedy_token(lb).to_numpy()[:, 0]
+    assert np.array_equal(first, host)
+    dev = model.decode_greedy(a).to_numpy()[:, 0]
+    fed = greedy_token(model.decode_batch(DeviceTensor.from_numpy(host[:, None].astype(np.float32)), b)).to_numpy()[:, 0]
+    assert np.array_equal(dev, fed)
+    for c in a + b:
+        c.close()
+    pool.close()
+
+
+def test_prefill_batch_rejects_bad_input():
+    from minitorch_amd.paged_kv_cache import KVPagePool
+    model = tiny(seed=33)
+    pool = KVPagePool(model, page_size=16, max_bytes=64 * 1024 ** 2)
+    c1 = model.create_kv_cache(1, 20, page_size=16, page_pool=pool)
+    c2 = model.create_kv_cache(1, 20, page_size=16, page_pool=pool)
+    with pytest.raises(ValueError):
+        model.prefill_batch([np.arange(3)], [c1, c2])          # count mismatch
+    with pytest.raises(ValueError):
+        model.prefill_batch([np.arange(3), np.arange(4)], [c1, c1])   # same cache twice
+    with pytest.raises(ValueError):
+        model.prefill_batch([np.arange(3), np.arange(30)], [c1, c2])  # beyond capacity
+    model.prefill_batch([np.arange(3), np.arange(4)], [c1, c2])
+    with pytest.raises(ValueError):
+        model.prefill_batch([np.arange(3)], [c1])                  # not empty
+    assert c1.length == 3 and c2.length == 4
+    for c in (c1, c2):
+        c.close()
+    pool.close()
