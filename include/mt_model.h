@@ -155,8 +155,9 @@ int mt_prefill_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
  * request order (x [sum tokens, d] fp32, updated in place; h [sum tokens, d]
  * in dtype). The projections, LayerNorms and GELU run once over all rows;
  * per layer, each request's K/V are appended and its causal attention
- * computed with mt_paged_prefill over its own pages, att[r] (host array of
- * `requests` structs: the request's table row, offset and pool geometry).
+ * computed over its own pages (mt_paged_prefill_ragged), att[r] (host array of
+ * `requests` structs: the request's table row and offset; all must describe
+ * the same pool).
  * When logits is not null, logits [requests, vocab] = final-LayerNorm(x)[last
  * row of each request] @ head_weight^T. Scratch as
  * mt_decoder_scratch_bytes(sum tokens). Results equal one mt_prefill_layers

@@ -100,6 +100,21 @@ int mt_paged_prefill(void* out, const void* q, const void* k, const void* v, con
                      int pages_per_slab, int num_slabs, int columns, int layer, int layers,
                      int offset, int dtype, int qkv_stride, int out_stride);
 
+/* mt_paged_prefill for `requests` prompts of different lengths in one call:
+ * prompt r has tokens[r] token-major rows, concatenated in prompt order in
+ * q/k/v (row stride qkv_stride, 0 = h*d) and out (out_stride, 0 = h*d), key
+ * offset offsets[r] and its own block-table row tables[r] (a device pointer
+ * to `columns` entries); tables, tokens and offsets are host arrays. Each
+ * prompt's K/V are appended and its causal attention computed as
+ * mt_paged_prefill would; with fp16/bf16, d 64/128 and 16-byte rows, up to 16
+ * prompts (256 query tiles) share one append and one matrix-core launch.
+ * No reference counterpart (the reference prefills one request per call). */
+int mt_paged_prefill_ragged(void* out, const void* q, const void* k, const void* v,
+                            const uint64_t* slabs, const int* const* tables, const int* tokens,
+                            const int* offsets, int requests, int h, int d, int page_size,
+                            int pages_per_slab, int num_slabs, int columns, int layer, int layers,
+                            int dtype, int qkv_stride, int out_stride);
+
 #ifdef __cplusplus
 }
 #endif

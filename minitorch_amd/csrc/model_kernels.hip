@@ -819,6 +819,18 @@ int mt_prefill_layers_ragged(void* handle, const mt_decoder_layer* layers, int n
   if (total > INT32_MAX || total * 4 * d > INT32_MAX ||
       scratch_bytes < mt_decoder_scratch_bytes(int(total), d, dtype))
     return hipErrorInvalidValue;
+  // One pool: every request's attention metadata shares the pool geometry.
+  std::vector<const int*> tables(requests);
+  std::vector<int> offsets(requests);
+  for (int r = 0; r < requests; ++r) {
+    const mt_prefill_attention& A = att[r];
+    if (A.slabs != att[0].slabs || A.page_size != att[0].page_size ||
+        A.pages_per_slab != att[0].pages_per_slab || A.num_slabs != att[0].num_slabs ||
+        A.columns != att[0].columns || A.layers != att[0].layers)
+      return hipErrorInvalidValue;
+    tables[r] = A.table;
+    offsets[r] = A.offset;
+  }
   const int rows = int(total);
   Blas* blas = static_cast<Blas*>(handle);
   const size_t e = dtype == kF32 ? 4 : 2;
@@ -832,17 +844,12 @@ int mt_prefill_layers_ragged(void* handle, const mt_decoder_layer* layers, int n
   for (int i = 0; i < n_layer && !st; ++i) {
     const mt_decoder_layer& L = layers[i];
     if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 1, dtype, dtype))) break;
-    // Attention per request over its own pages: rows [first, first + n).
-    int64_t first = 0;
-    for (int r = 0; r < requests && !st; ++r) {
-      const mt_prefill_attention& A = att[r];
-      st = mt_paged_prefill(attn + size_t(first) * d * e, qkv + size_t(first) * 3 * d * e,
-                            qkv + (size_t(first) * 3 * d + d) * e, qkv + (size_t(first) * 3 * d + 2 * d) * e,
-                            A.slabs, A.table, 1, heads, tokens[r], hd, A.page_size, A.pages_per_slab,
-                            A.num_slabs, A.columns, i, A.layers, A.offset, dtype, 3 * d, d);
-      first += tokens[r];
-    }
-    if (st) break;
+    // Every request's append and causal attention over its own pages.
+    if ((st = mt_paged_prefill_ragged(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, att[0].slabs,
+                                      tables.data(), tokens, offsets.data(), requests, heads, hd,
+                                      att[0].page_size, att[0].pages_per_slab, att[0].num_slabs,
+                                      att[0].columns, i, att[0].layers, dtype, 3 * d, d)))
+      break;
     if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 1, dtype, dtype))) break;
     if ((st = residual_layernorm(h, x, proj, L.ln2_gamma, L.ln2_beta, rows, d, eps, dtype))) break;
     if ((st = gemm_gelu(blas, mlp, h, L.w_fc, L.b_fc, rows, 4 * d, d, dtype, fused_gelu != 0, false, 1))) break;

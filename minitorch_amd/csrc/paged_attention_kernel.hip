@@ -36,6 +36,7 @@
 // take use the per-query query_kernel.
 #include "mt_device.h"
 #include "../../include/mt_paged.h"
+#include <algorithm>
 #include <climits>
 
 #ifndef MT_NT_LOADS
@@ -960,8 +961,66 @@ struct PackP<kBF16> {
   }
 };
 
-template <int DT, int D>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
+// What one prefill workgroup works on: query tile `tile` of `head` of a
+// request whose queries start at element q0 of q (o0 of out), nq queries at
+// key offset `offset` over the pages of table_row.
+struct PfItem {
+  int tile, head, nq, offset;
+  int64_t q0, o0;
+  const int* table_row;
+};
+
+// The uniform batch of QueryArgs (b requests of nq queries at one offset):
+// items ordered by tile, last (longest) tiles first.
+struct UniformItems {
+  __device__ __forceinline__ int64_t count(const QueryArgs& a) const { return a.items; }
+  __device__ __forceinline__ PfItem get(int64_t item, const QueryArgs& a) const {
+    const int tiles = (a.nq + kPfQueries - 1) / kPfQueries;
+    const int64_t bh_count = a.items / tiles;
+    PfItem it;
+    it.tile = tiles - 1 - int(item / bh_count);
+    const int64_t bh = item - int64_t(tiles - 1 - it.tile) * bh_count;
+    const int b = int(bh / a.g.heads);
+    it.head = int(bh - int64_t(b) * a.g.heads);
+    it.nq = a.nq;
+    it.offset = a.offset;
+    it.q0 = b * a.q_b + it.head * a.q_h;
+    it.o0 = b * a.o_b + it.head * a.o_h;
+    it.table_row = a.table + int64_t(b) * a.g.columns;
+    return it;
+  }
+};
+
+// Prompts of different lengths in one launch (token-major rows, prompt r at
+// rows [first_row[r], first_row[r] + n[r]) of q/k/v/out, with its own table
+// row and key offset), passed by value: every (prompt, tile) pair in the
+// order of pair_prompt / pair_tile (heaviest first), times the heads.
+constexpr int kRaggedPrompts = 16;
+constexpr int kRaggedTiles = 256;
+struct RaggedItems {
+  int prompts, pairs;
+  int first_row[kRaggedPrompts], n[kRaggedPrompts], offset[kRaggedPrompts];
+  const int* table[kRaggedPrompts];
+  unsigned char pair_prompt[kRaggedTiles];
+  unsigned short pair_tile[kRaggedTiles];
+  __device__ __forceinline__ int64_t count(const QueryArgs& a) const { return int64_t(pairs) * a.g.heads; }
+  __device__ __forceinline__ PfItem get(int64_t item, const QueryArgs& a) const {
+    const int p = int(item / a.g.heads);
+    const int r = pair_prompt[p];
+    PfItem it;
+    it.tile = pair_tile[p];
+    it.head = int(item - int64_t(p) * a.g.heads);
+    it.nq = n[r];
+    it.offset = offset[r];
+    it.q0 = int64_t(first_row[r]) * a.q_r + it.head * a.q_h;
+    it.o0 = int64_t(first_row[r]) * a.o_r + it.head * a.o_h;
+    it.table_row = table[r];
+    return it;
+  }
+};
+
+template <int DT, int D, class Items>
+__global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a, Items items) {
   using T = typename Elem<DT>::T;
   using V8 = typename Mfma<DT>::v8;
   constexpr int KS = kPfKeys;
@@ -982,35 +1041,33 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
   const int lane = tid & (kWave - 1);
   const int grp = lane >> 4;  // 0..3
   const int col = lane & 15;  // this lane's query within its wave's 16
-  const int tiles = (a.nq + kPfQueries - 1) / kPfQueries;
-  const int64_t bh_count = a.items / tiles;
   const T* qp = static_cast<const T*>(a.q);
   T* out = static_cast<T*>(a.out);
   const int win_keys = kPfWindowPages << g.log2_page;
 
-  for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
-    // Longest (last) query tiles first.
-    const int tile = tiles - 1 - int(item / bh_count);
-    const int64_t bh = item - int64_t(tiles - 1 - tile) * bh_count;
-    const int b = int(bh / g.heads), head = int(bh - int64_t(b) * g.heads);
-    const int* table_row = a.table + int64_t(b) * g.columns;
+  const int64_t n_items = items.count(a);
+  for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const PfItem it = items.get(item, a);
+    const int tile = it.tile, head = it.head;
+    const int* table_row = it.table_row;
+    const int nq = it.nq, offset = it.offset, nk = it.offset + it.nq;
 
     // B operand of S^T = K Q^T: dims [32*ds + 8*grp, +8) of query q0 + col.
     const int q0 = tile * kPfQueries + wave * 16;
     const int qi = q0 + col;
-    const bool q_ok = qi < a.nq;
+    const bool q_ok = qi < nq;
     V8 qv[DS];
     {
-      const T* row = qp + b * a.q_b + head * a.q_h + (q_ok ? qi : 0) * a.q_r;
+      const T* row = qp + it.q0 + (q_ok ? qi : 0) * a.q_r;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds)
         qv[ds] = __builtin_bit_cast(V8, *global_view(reinterpret_cast<const u32x4*>(row + 32 * ds + 8 * grp)));
     }
-    const int qpos = a.offset + qi;
-    const bool wave_live = q0 < a.nq;
-    const int wave_last = a.offset + (q0 + 15 < a.nq ? q0 + 15 : a.nq - 1);
-    const int tile_q = (tile + 1) * kPfQueries - 1 < a.nq ? (tile + 1) * kPfQueries - 1 : a.nq - 1;
-    const int kend = a.offset + tile_q + 1 < a.nk ? a.offset + tile_q + 1 : a.nk;
+    const int qpos = offset + qi;
+    const bool wave_live = q0 < nq;
+    const int wave_last = offset + (q0 + 15 < nq ? q0 + 15 : nq - 1);
+    const int tile_q = (tile + 1) * kPfQueries - 1 < nq ? (tile + 1) * kPfQueries - 1 : nq - 1;
+    const int kend = offset + tile_q + 1 < nk ? offset + tile_q + 1 : nk;
 
     float m = -INFINITY, l = 0.f;
     floatx4 o[DT16];
@@ -1025,7 +1082,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
     // branch waits for them before the block in between is computed.
     u32x4 kx[NC], vx[NC];
     int kstate[NC];  // 0 = loaded, 1 = missing page, 2 = past the window
-    const T* dummy = qp + b * a.q_b + head * a.q_h + (q_ok ? qi : 0) * a.q_r;
+    const T* dummy = qp + it.q0 + (q_ok ? qi : 0) * a.q_r;
     auto stage_load = [&](int k0, int w0, int w1) {
 #pragma unroll
       for (int n = 0; n < NC; ++n) {
@@ -1086,7 +1143,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
         }
         // Causal / length mask, only for blocks that reach past the wave's
         // first query or past kend (a wave-uniform test).
-        if (k0 + KS - 1 > a.offset + q0 || k0 + KS > kend) {
+        if (k0 + KS - 1 > offset + q0 || k0 + KS > kend) {
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
@@ -1156,7 +1213,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a) {
     l += lane_swap32(l);
     // O^T lane layout: dims dt*16 + 4*grp + i of query qi.
     if (q_ok) {
-      T* orow = out + b * a.o_b + head * a.o_h + qi * a.o_r;
+      T* orow = out + it.o0 + qi * a.o_r;
 #pragma unroll
       for (int dt = 0; dt < DT16; ++dt) {
         const T r0 = from_f32<DT>(finalize(o[dt][0], l)), r1 = from_f32<DT>(finalize(o[dt][1], l));
@@ -1192,6 +1249,41 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     T* kp = const_cast<T*>(base) + (pos & (g.page_size - 1)) * dim + col;
     T* vp = kp + g.kind_stride;
     const int64_t src = b * a.src_b + head * a.src_h + pos_in * a.src_r + col;
+    if constexpr (VEC) {
+      *global_view(reinterpret_cast<u32x4*>(kp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k) + src));
+      *global_view(reinterpret_cast<u32x4*>(vp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v) + src));
+    } else {
+      *kp = static_cast<const T*>(a.k)[src];
+      *vp = static_cast<const T*>(a.v)[src];
+    }
+  }
+}
+
+// Append of prompts of different lengths (RaggedItems): the K/V of token row
+// t (elements t * src_r + head * src_h of k and v) go to position
+// offset[p] + (t - first_row[p]) of prompt p's pages; rows whose page is
+// missing are skipped, as in append_kernel.
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void append_ragged_kernel(AppendArgs a, RaggedItems r) {
+  using T = typename Elem<DT>::T;
+  constexpr int E = VEC ? per16<DT>() : 1;
+  const Geometry& g = a.g;
+  const int dim = g.dim;
+  const int per_row = dim / E;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < a.vectors;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t row = i / per_row;  // t * heads + head
+    const int col = int(i - row * per_row) * E;
+    const int64_t t = row / g.heads;
+    const int head = int(row - t * g.heads);
+    int p = 0;
+    while (p + 1 < r.prompts && t >= r.first_row[p + 1]) ++p;
+    const int64_t pos = int64_t(r.offset[p]) + (t - r.first_row[p]);
+    const T* base = page_base<T>(a.slabs, r.table[p], pos >> g.log2_page, g, head);
+    if (!base) continue;
+    T* kp = const_cast<T*>(base) + (pos & (g.page_size - 1)) * dim + col;
+    T* vp = kp + g.kind_stride;
+    const int64_t src = t * a.src_r + head * a.src_h + col;
     if constexpr (VEC) {
       *global_view(reinterpret_cast<u32x4*>(kp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k) + src));
       *global_view(reinterpret_cast<u32x4*>(vp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v) + src));
@@ -1414,11 +1506,11 @@ hipError_t launch_query(QueryArgs& a, int dtype) {
     a.items = int64_t(a.batch) * h * ((a.nq + kPfQueries - 1) / kPfQueries);
     const int blocks = grid_for(a.items);
     if (dtype == kF16) {
-      if (d == 64) prefill_kernel<kF16, 64><<<blocks, kThreads>>>(a);
-      else prefill_kernel<kF16, 128><<<blocks, kThreads>>>(a);
+      if (d == 64) prefill_kernel<kF16, 64, UniformItems><<<blocks, kThreads>>>(a, UniformItems{});
+      else prefill_kernel<kF16, 128, UniformItems><<<blocks, kThreads>>>(a, UniformItems{});
     } else {
-      if (d == 64) prefill_kernel<kBF16, 64><<<blocks, kThreads>>>(a);
-      else prefill_kernel<kBF16, 128><<<blocks, kThreads>>>(a);
+      if (d == 64) prefill_kernel<kBF16, 64, UniformItems><<<blocks, kThreads>>>(a, UniformItems{});
+      else prefill_kernel<kBF16, 128, UniformItems><<<blocks, kThreads>>>(a, UniformItems{});
     }
     return hipGetLastError();
   }
@@ -1500,6 +1592,119 @@ int mt_paged_prefill(void* out, const void* q, const void* k, const void* v, con
   a.q_b = int64_t(n) * qkv_stride; a.q_h = d; a.q_r = qkv_stride;
   a.o_b = int64_t(n) * out_stride; a.o_h = d; a.o_r = out_stride;
   return launch_query(a, dtype);
+}
+
+int mt_paged_prefill_ragged(void* out, const void* q, const void* k, const void* v,
+                            const uint64_t* slabs, const int* const* tables, const int* tokens,
+                            const int* offsets, int requests, int h, int d, int page_size,
+                            int pages_per_slab, int num_slabs, int columns, int layer, int layers,
+                            int dtype, int qkv_stride, int out_stride) {
+  if (!out || !q || !k || !v || !slabs || !tables || !tokens || !offsets || requests < 1 || h < 1 ||
+      d < 1 || dtype < 0 || dtype > 2)
+    return hipErrorInvalidValue;
+  const int64_t hd = int64_t(h) * d;
+  if (qkv_stride == 0) qkv_stride = int(hd);
+  if (out_stride == 0) out_stride = int(hd);
+  if (qkv_stride < hd || out_stride < hd) return hipErrorInvalidValue;
+  int64_t total = 0;
+  for (int r = 0; r < requests; ++r) {
+    if (!tables[r] || tokens[r] < 1 || offsets[r] < 0 || int64_t(offsets[r]) + tokens[r] > INT32_MAX ||
+        !paged_shape(1, h, tokens[r], offsets[r] + tokens[r], d, page_size, pages_per_slab, num_slabs,
+                     columns, layer, layers, offsets[r]))
+      return hipErrorInvalidValue;
+    total += tokens[r];
+  }
+  if (total * qkv_stride > INT32_MAX || total * out_stride > INT32_MAX) return hipErrorInvalidValue;
+  const size_t e = dtype == kF32 ? 4 : 2;
+  auto rows16 = [&](int64_t x) { return (x * int64_t(e)) % 16 == 0; };
+  const bool mfma = dtype != kF32 && (d == 64 || d == 128) && aligned16(out) && aligned16(q) &&
+                    aligned16(k) && aligned16(v) && rows16(qkv_stride) && rows16(out_stride) && rows16(d);
+  if (!mfma) {
+    // Shapes the matrix-core kernel does not take: one call per prompt.
+    int64_t first = 0;
+    for (int r = 0; r < requests; ++r) {
+      const int st = mt_paged_prefill(static_cast<char*>(out) + size_t(first) * out_stride * e,
+                                      static_cast<const char*>(q) + size_t(first) * qkv_stride * e,
+                                      static_cast<const char*>(k) + size_t(first) * qkv_stride * e,
+                                      static_cast<const char*>(v) + size_t(first) * qkv_stride * e, slabs,
+                                      tables[r], 1, h, tokens[r], d, page_size, pages_per_slab, num_slabs,
+                                      columns, layer, layers, offsets[r], dtype, qkv_stride, out_stride);
+      if (st) return st;
+      first += tokens[r];
+    }
+    return hipSuccess;
+  }
+  const Geometry g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
+  // Chunks of at most kRaggedPrompts prompts and kRaggedTiles query tiles.
+  int r0 = 0;
+  int64_t row0 = 0;
+  while (r0 < requests) {
+    RaggedItems it{};
+    int r1 = r0, pairs = 0;
+    int64_t rows = 0;
+    while (r1 < requests && r1 - r0 < kRaggedPrompts &&
+           pairs + (tokens[r1] + kPfQueries - 1) / kPfQueries <= kRaggedTiles) {
+      const int p = r1 - r0;
+      it.first_row[p] = int(rows);
+      it.n[p] = tokens[r1];
+      it.offset[p] = offsets[r1];
+      it.table[p] = tables[r1];
+      pairs += (tokens[r1] + kPfQueries - 1) / kPfQueries;
+      rows += tokens[r1];
+      ++r1;
+    }
+    if (r1 == r0) return hipErrorInvalidValue;  // one prompt with more tiles than a launch takes
+    it.prompts = r1 - r0;
+    it.pairs = pairs;
+    // (prompt, tile) pairs, the tiles that attend the most keys first.
+    std::vector<std::pair<int, int>> order;
+    for (int p = 0; p < it.prompts; ++p)
+      for (int t = 0; t * kPfQueries < it.n[p]; ++t) order.push_back({p, t});
+    std::stable_sort(order.begin(), order.end(), [&](const std::pair<int, int>& x, const std::pair<int, int>& y) {
+      auto keys = [&](const std::pair<int, int>& z) {
+        const int last = (z.second + 1) * kPfQueries < it.n[z.first] ? (z.second + 1) * kPfQueries : it.n[z.first];
+        return it.offset[z.first] + last;
+      };
+      return keys(x) > keys(y);
+    });
+    for (int i = 0; i < pairs; ++i) {
+      it.pair_prompt[i] = static_cast<unsigned char>(order[i].first);
+      it.pair_tile[i] = static_cast<unsigned short>(order[i].second);
+    }
+    const size_t qoff = size_t(row0) * qkv_stride * e, ooff = size_t(row0) * out_stride * e;
+    AppendArgs ap{};
+    ap.k = static_cast<const char*>(k) + qoff;
+    ap.v = static_cast<const char*>(v) + qoff;
+    ap.slabs = slabs;
+    ap.g = g;
+    ap.src_h = d;
+    ap.src_r = qkv_stride;
+    ap.vectors = rows * h * (d / int(16 / e));
+    const int ablocks = int((ap.vectors + 255) / 256 < 65536 * 16 ? (ap.vectors + 255) / 256 : 65536 * 16);
+    QueryArgs a{};
+    a.out = static_cast<char*>(out) + ooff;
+    a.q = static_cast<const char*>(q) + qoff;
+    a.slabs = slabs;
+    a.g = g;
+    a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
+    a.q_h = d; a.q_r = qkv_stride;
+    a.o_h = d; a.o_r = out_stride;
+    const int blocks = grid_for(int64_t(pairs) * h);
+    if (dtype == kF16) {
+      append_ragged_kernel<kF16, true><<<ablocks, 256>>>(ap, it);
+      if (d == 64) prefill_kernel<kF16, 64, RaggedItems><<<blocks, kThreads>>>(a, it);
+      else prefill_kernel<kF16, 128, RaggedItems><<<blocks, kThreads>>>(a, it);
+    } else {
+      append_ragged_kernel<kBF16, true><<<ablocks, 256>>>(ap, it);
+      if (d == 64) prefill_kernel<kBF16, 64, RaggedItems><<<blocks, kThreads>>>(a, it);
+      else prefill_kernel<kBF16, 128, RaggedItems><<<blocks, kThreads>>>(a, it);
+    }
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    r0 = r1;
+    row0 += rows;
+  }
+  return hipSuccess;
 }
 
 int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v,

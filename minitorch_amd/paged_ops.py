@@ -45,6 +45,20 @@ def paged_prefill(out, q, k, v, slab_table, block_table, *, b, h, n, d, page_siz
          columns, layer, layers, offset, dtype_code(dtype), qkv_stride, out_stride)
 
 
+def paged_prefill_ragged(out, q, k, v, slab_table, tables, tokens, offsets, *, h, d, page_size, pages_per_slab,
+                         num_slabs, columns, layer, layers, dtype, qkv_stride=0, out_stride=0):
+    """``mt_paged_prefill_ragged``: ``paged_prefill`` for prompts of different
+    lengths in one call; ``tables`` (device pointers to each prompt's table
+    row), ``tokens`` and ``offsets`` are per prompt, rows token-major and
+    concatenated in prompt order."""
+    r = len(tokens)
+    if not (len(tables) == len(offsets) == r):
+        raise ValueError('tables, tokens and offsets need one entry per prompt')
+    call(paged_library(), 'mt_paged_prefill_ragged', [P] * 8 + [I] * 12,
+         out, q, k, v, slab_table, (P * r)(*tables), (I * r)(*tokens), (I * r)(*offsets), r, h, d,
+         page_size, pages_per_slab, num_slabs, columns, layer, layers, dtype_code(dtype), qkv_stride, out_stride)
+
+
 def paged_decode_batch(out, q, k, v, slab_table, block_table, offsets, *, b, h, d, page_size,
                        pages_per_slab, num_slabs, columns, layer, layers, dtype):
     """``mt_paged_decode_batch`` (reference src/paged_attention_kernel.cu:121-137)."""

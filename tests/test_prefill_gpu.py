@@ -186,3 +186,66 @@ def test_paged_prefill_token_major_equals_append_then_attention(dtype, n):
     po.image_append(image, case.table, case.columns, k, v, 0, offset=offset)
     ref = po.image_paged_attention(image, CODES[dtype], case.table, case.columns, q, 0, offset, offset + n)
     assert_attention_close(out2.to_numpy(), ref, dtype)
+
+
+def run_ragged(dtype, d, tokens, offsets, *, page_size=16, h=3, seed=0, pps=4):
+    """mt_paged_prefill_ragged over prompts of `tokens` rows at `offsets`
+    against the oracle: each prompt's K/V appended to its own pages (whole
+    pool image bit for bit) and its causal attention (tolerances of
+    tests/tolerances.py)."""
+    r = len(tokens)
+    lengths = [o + n for o, n in zip(offsets, tokens)]
+    pages = sum(-(-length // page_size) for length in lengths) + 3
+    case = make_decode_case(seed, batch=r, heads=h, dim=d, page_size=page_size, lengths=lengths,
+                            pool_pages=-(-pages // pps) * pps, pages_per_slab=pps, dtype=dtype)
+    total, hd = sum(tokens), h * d
+    rng = np.random.default_rng(seed)
+    qkv = po.encode(rng.standard_normal((total, 3 * hd), dtype=np.float32), CODES[dtype])
+    dev = DevicePagedCase(case)
+    fused = DeviceTensor(qkv.shape, dtype)
+    runtime().h2d(fused.ptr, qkv)
+    out = DeviceTensor((total, hd), dtype)
+    item = 4 if dtype == 'float32' else 2
+    tables = [dev.block_table.ptr + 4 * i * case.columns for i in range(r)]
+    paged_ops.paged_prefill_ragged(out.ptr, fused.ptr, fused.ptr + hd * item, fused.ptr + 2 * hd * item,
+                                   dev.slab_table.ptr, tables, tokens, offsets, h=h, d=d, page_size=page_size,
+                                   pages_per_slab=pps, num_slabs=case.num_slabs, columns=case.columns,
+                                   layer=0, layers=1, dtype=dtype, qkv_stride=3 * hd, out_stride=hd)
+    runtime().synchronize()
+    image = case.image.copy()
+    got = out.to_numpy()
+    first = 0
+    for i, (n, off) in enumerate(zip(tokens, offsets)):
+        rows = qkv[first:first + n]
+        heads = lambda blk: np.ascontiguousarray(rows[:, blk * hd:(blk + 1) * hd].reshape(1, n, h, d)
+                                                 .transpose(0, 2, 1, 3))
+        table = case.table[i:i + 1]
+        po.image_append(image, table, case.columns, heads(1), heads(2), 0, offset=off)
+        ref = po.image_paged_attention(image, CODES[dtype], table, case.columns, heads(0), 0, off, off + n)
+        mine = got[first:first + n].reshape(1, n, h, d).transpose(0, 2, 1, 3)
+        assert_attention_close(mine, ref, dtype, context=f'prompt {i} n={n} offset={off}')
+        first += n
+    assert np.array_equal(dev.pool_image().view(np.uint8), image.view(np.uint8)), 'append differs'
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+@pytest.mark.parametrize('dim', [64, 128])
+def test_prefill_ragged_prompts(dtype, dim):
+    # one launch: prompts of 1..130 tokens, tiles cut at 64, some at an offset
+    run_ragged(dtype, dim, [1, 5, 16, 63, 64, 65, 130], [0, 7, 0, 100, 0, 33, 0], seed=dim)
+
+
+@pytest.mark.parametrize('page_size', [8, 32])
+def test_prefill_ragged_page_sizes(page_size):
+    run_ragged('bfloat16', 64, [40, 9, 77], [3, 0, 50], page_size=page_size, seed=page_size)
+
+
+def test_prefill_ragged_more_prompts_than_one_launch_takes():
+    # 20 prompts: two launches of at most 16 prompts each
+    rng = np.random.default_rng(3)
+    tokens = [int(n) for n in rng.integers(1, 90, 20)]
+    run_ragged('float16', 64, tokens, [int(o) for o in rng.integers(0, 40, 20)], h=2, seed=3)
+
+
+def test_prefill_ragged_fp32_takes_the_per_prompt_path():
+    run_ragged('float32', 64, [17, 3, 40], [0, 12, 5], h=2, seed=4)
