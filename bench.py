@@ -305,6 +305,46 @@ def bench_prefill_shape(heads, dtype, lengths, steps, warmup, seed):
                 frac=flops / per_round / 1e12 / PEAK_MFMA_TFLOPS)
 
 
+def bench_prefill_ragged(heads, dtype, lengths, steps, warmup, seed, per_call=16):
+    """Mean time per prompt of mt_paged_prefill_ragged (append + causal
+    attention) over the same prompts, ``per_call`` prompts per call
+    (token-major rows of one fused QKV buffer, as the batched prefill loop
+    passes them)."""
+    from minitorch_amd.workloads import make_decode_case, _normal
+    from minitorch_amd.runtime import DeviceTensor
+    from minitorch_amd.dtypes import dtype_code
+    dim, page = 64, 16
+    lengths = np.asarray(lengths, np.int64)
+    pages = int(((lengths + page - 1) // page).sum())
+    case = make_decode_case(seed, batch=len(lengths), heads=heads, dim=dim, page_size=page,
+                            lengths=lengths, pool_pages=-(-pages // 16) * 16, pages_per_slab=16,
+                            dtype=dtype)
+    dev = DevicePagedCase(case)
+    hd, total = heads * dim, int(lengths.sum())
+    qkv = DeviceTensor((total, 3 * hd), dtype)
+    rt = runtime()
+    rt.h2d(qkv.ptr, _normal(np.random.default_rng([seed, 7]), (total, 3 * hd), dtype))
+    out = DeviceTensor((total, hd), dtype)
+    fn = paged_ops.paged_library().mt_paged_prefill_ragged
+    fn.argtypes, fn.restype = [P] * 8 + [I] * 12, I
+    calls, row = [], 0
+    for c0 in range(0, len(lengths), per_call):
+        sel = range(c0, min(c0 + per_call, len(lengths)))
+        n = [int(lengths[i]) for i in sel]
+        tables = (P * len(n))(*[dev.block_table.ptr + 4 * i * case.columns for i in sel])
+        item = 2
+        calls.append((out.ptr + row * hd * item, qkv.ptr + row * 3 * hd * item,
+                      qkv.ptr + (row * 3 * hd + hd) * item, qkv.ptr + (row * 3 * hd + 2 * hd) * item,
+                      dev.slab_table.ptr, tables, (I * len(n))(*n), (I * len(n))(*([0] * len(n))), len(n), heads,
+                      dim, page, case.pages_per_slab, case.num_slabs, case.columns, 0, 1, dtype_code(dtype),
+                      3 * hd, hd))
+        row += sum(n)
+    per_round = time_launches(fn, calls, steps * len(calls), warmup * len(calls)) * len(calls)
+    flops = sum(prefill_flops(int(n), heads, dim) for n in lengths)
+    return dict(prompts=len(lengths), prompts_per_call=per_call, us_per_prompt=per_round / len(lengths) * 1e6,
+                tflops=flops / per_round / 1e12, frac=flops / per_round / 1e12 / PEAK_MFMA_TFLOPS)
+
+
 def prefill_cpu_baseline(heads, dtype, lengths, seed, seconds):
     """The C oracle's causal paged attention (oracle_paged_attention) over the
     same prompts and pages as :func:`bench_prefill_shape`, one prompt per call,
@@ -361,7 +401,9 @@ def bench_prefill(args):
     mt_paged_attention) on the prompt shapes of configs 3 and 4: config 3's
     first 64 prompts (U{32..512}, 12 heads, fp16) and 64 config-4 contexts
     (lognormal median 256, clipped [16, 1024], 16 heads, bf16), one request per
-    call as the batcher admits them, plus single 512- and 1024-token prompts."""
+    call as the batcher admits them, plus single 512- and 1024-token prompts;
+    and the same prompts through mt_paged_prefill_ragged, 16 per call (append
+    included), as the batched prefill loop issues them."""
     from minitorch_amd.e2e import config3_trace, config4_lengths
     steps, warmup = max(1, args.steps // 20), max(1, args.warmup // 10)
     c3 = [len(p) for _, _, p, _ in config3_trace(args.seed)[:64]]
@@ -370,6 +412,8 @@ def bench_prefill(args):
     r4 = bench_prefill_shape(16, 'bfloat16', c4, steps, warmup, args.seed)
     r512 = bench_prefill_shape(12, 'float16', [512], steps * 20, warmup * 10, args.seed)
     r1024 = bench_prefill_shape(16, 'bfloat16', [1024], steps * 20, warmup * 10, args.seed)
+    rr3 = bench_prefill_ragged(12, 'float16', c3, steps, warmup, args.seed)
+    rr4 = bench_prefill_ragged(16, 'bfloat16', c4, steps, warmup, args.seed)
     return {'metric': 'causal paged prefill attention TFLOP/s (1 GPU)', 'value': r3['tflops'],
             'unit': 'TFLOP/s', 'n_gpus': 1, 'steps': steps, 'warmup': warmup,
             'ms_per_step': r3['us_per_prefill'] * r3['prompts'] / 1e3, 'higher_is_better': True,
@@ -380,6 +424,7 @@ def bench_prefill(args):
                          'unit': 'TFLOP/s', 'frac': r3['frac'], 'traffic': None},
             'config3_prompts_fp16': r3, 'config4_contexts_bf16': r4, 'prompt512_h12_fp16': r512,
             'prompt1024_h16_bf16': r1024,
+            'config3_prompts_fp16_ragged16': rr3, 'config4_contexts_bf16_ragged16': rr4,
             'cpu_baseline': None if args.no_cpu_baseline else prefill_cpu_baseline(
                 12, 'float16', c3, args.seed, args.cpu_seconds)}
 
