@@ -113,6 +113,14 @@ def decode_work_list(lengths, heads, split_tokens, compute_units):
     entries of the next ("snake" order). The rows with more than one split
     follow the pairs.
     """
+    if len(lengths) <= 32 and all(0 < int(n) <= split_tokens for n in lengths):
+        # one split per row (the common small decode batch): the same list in
+        # plain Python, cheaper than numpy at this size
+        return _small_work_list([int(n) for n in lengths], heads, compute_units)
+    return _numpy_work_list(lengths, heads, split_tokens, compute_units)
+
+
+def _numpy_work_list(lengths, heads, split_tokens, compute_units):
     L = np.asarray(lengths, np.int64)
     nsplit = np.maximum(1, -(-L // split_tokens))
     rows = np.repeat(np.arange(len(L)), nsplit)
@@ -126,6 +134,22 @@ def decode_work_list(lengths, heads, split_tokens, compute_units):
     merge = np.flatnonzero(nsplit > 1)
     work = np.concatenate([np.stack([rows[order], splits[order]], 1).ravel(), merge])
     return work.astype(np.int32), len(order), len(merge)
+
+
+def _small_work_list(lengths, heads, compute_units):
+    """decode_work_list for rows of one split each: rows longest first
+    (stable, ties by row), every other pass of compute_units // heads rows
+    reversed; no merge rows."""
+    lpt = sorted(range(len(lengths)), key=lambda r: -lengths[r])
+    per = max(1, compute_units // max(1, heads))
+    order = []
+    for k, i in enumerate(range(0, len(lpt), per)):
+        chunk = lpt[i:i + per]
+        order += chunk[::-1] if k % 2 else chunk
+    work = np.empty(2 * len(order), np.int32)
+    work[0::2] = order
+    work[1::2] = 0
+    return work, len(order), 0
 
 
 def embedding_gather(dst, weights, ids, tokens, vocab, dim):
