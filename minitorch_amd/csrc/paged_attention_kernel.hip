@@ -1653,7 +1653,19 @@ int mt_paged_prefill_ragged(void* out, const void* q, const void* k, const void*
       rows += tokens[r1];
       ++r1;
     }
-    if (r1 == r0) return hipErrorInvalidValue;  // one prompt with more tiles than a launch takes
+    if (r1 == r0) {
+      // One prompt with more query tiles than a launch describes: on its own.
+      const size_t qo = size_t(row0) * qkv_stride * e;
+      const int st = mt_paged_prefill(static_cast<char*>(out) + size_t(row0) * out_stride * e,
+                                      static_cast<const char*>(q) + qo, static_cast<const char*>(k) + qo,
+                                      static_cast<const char*>(v) + qo, slabs, tables[r0], 1, h, tokens[r0], d,
+                                      page_size, pages_per_slab, num_slabs, columns, layer, layers,
+                                      offsets[r0], dtype, qkv_stride, out_stride);
+      if (st) return st;
+      row0 += tokens[r0];
+      ++r0;
+      continue;
+    }
     it.prompts = r1 - r0;
     it.pairs = pairs;
     // (prompt, tile) pairs, the tiles that attend the most keys first.

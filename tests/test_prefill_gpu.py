@@ -249,3 +249,39 @@ def test_prefill_ragged_more_prompts_than_one_launch_takes():
 
 def test_prefill_ragged_fp32_takes_the_per_prompt_path():
     run_ragged('float32', 64, [17, 3, 40], [0, 12, 5], h=2, seed=4)
+
+
+def test_prefill_ragged_prompt_longer_than_one_launch_describes():
+    # a prompt of more than 256 query tiles (16400 tokens) is prefilled on its
+    # own; the result equals one mt_paged_prefill call per prompt bit for bit
+    tokens, offsets, h, d, page = [20, 16400, 33], [5, 0, 0], 1, 64, 32
+    lengths = [o + n for o, n in zip(offsets, tokens)]
+    pages = sum(-(-x // page) for x in lengths) + 4
+    case = make_decode_case(61, batch=3, heads=h, dim=d, page_size=page, lengths=lengths,
+                            pool_pages=-(-pages // 8) * 8, pages_per_slab=8, dtype='bfloat16')
+    total, hd = sum(tokens), h * d
+    qkv = po.encode(np.random.default_rng(61).standard_normal((total, 3 * hd), dtype=np.float32), po.BF16)
+    outs, images = [], []
+    for ragged in (True, False):
+        dev = DevicePagedCase(case)
+        fused = DeviceTensor(qkv.shape, 'bfloat16')
+        runtime().h2d(fused.ptr, qkv)
+        out = DeviceTensor((total, hd), 'bfloat16')
+        common = dict(h=h, d=d, page_size=page, pages_per_slab=8, num_slabs=case.num_slabs,
+                      columns=case.columns, layer=0, layers=1, dtype='bfloat16', qkv_stride=3 * hd, out_stride=hd)
+        tables = [dev.block_table.ptr + 4 * i * case.columns for i in range(3)]
+        if ragged:
+            paged_ops.paged_prefill_ragged(out.ptr, fused.ptr, fused.ptr + 2 * hd, fused.ptr + 4 * hd,
+                                           dev.slab_table.ptr, tables, tokens, offsets, **common)
+        else:
+            row = 0
+            for i, (n, off) in enumerate(zip(tokens, offsets)):
+                base = fused.ptr + row * 3 * hd * 2
+                paged_ops.paged_prefill(out.ptr + row * hd * 2, base, base + 2 * hd, base + 4 * hd,
+                                        dev.slab_table.ptr, tables[i], b=1, n=n, offset=off, **common)
+                row += n
+        runtime().synchronize()
+        outs.append(out.raw_numpy())
+        images.append(dev.pool_image())
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(images[0].view(np.uint8), images[1].view(np.uint8))
