@@ -811,6 +811,12 @@ struct QueryArgs {
   // Element strides of q and out per request, head and query: [b, h, nq, d]
   // by default, [b, nq, row] for head-interleaved token rows.
   int64_t q_b, q_h, q_r, o_b, o_h, o_r;
+  // The prompt's own K/V rows (strides of q), or null. When set (prefill
+  // kernel only), keys at or past the offset are read from these rows and the
+  // workgroup of each query tile writes its tokens' K/V to their pages, which
+  // replaces a separate append.
+  const void* k;
+  const void* v;
 };
 
 // Causal paged attention for nq >= 1 queries per (request, head)
@@ -1019,7 +1025,7 @@ struct RaggedItems {
   }
 };
 
-template <int DT, int D, class Items>
+template <int DT, int D, class Items, bool FUSED>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a, Items items) {
   using T = typename Elem<DT>::T;
   using V8 = typename Mfma<DT>::v8;
@@ -1082,7 +1088,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a, Items it
     // branch waits for them before the block in between is computed.
     u32x4 kx[NC], vx[NC];
     int kstate[NC];  // 0 = loaded, 1 = missing page, 2 = past the window
+    T* wpage[NC];    // page address a staged key of this tile is also written to, or null
     const T* dummy = qp + it.q0 + (q_ok ? qi : 0) * a.q_r;
+    // FUSED: keys [offset, nk) come from the prompt's own K/V rows, and this
+    // workgroup writes the keys of its own queries, [own0, kend), to the pages.
+    const T* krows = FUSED ? static_cast<const T*>(a.k) + it.q0 : nullptr;
+    const T* vrows = FUSED ? static_cast<const T*>(a.v) + it.q0 : nullptr;
+    const int own0 = offset + tile * kPfQueries;
     auto stage_load = [&](int k0, int w0, int w1) {
 #pragma unroll
       for (int n = 0; n < NC; ++n) {
@@ -1091,10 +1103,20 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a, Items it
         const int key = k0 + kr;
         const T* page = key < w1 ? s_page[(key - w0) >> g.log2_page] : nullptr;
         kstate[n] = key >= w1 ? 2 : (page ? 0 : 1);
-        const T* kp = page ? page + (key & (g.page_size - 1)) * D + part * 8 : dummy;
-        const int64_t vstep = page ? g.kind_stride : 0;
-        kx[n] = *global_view(reinterpret_cast<const u32x4*>(kp));
-        vx[n] = *global_view(reinterpret_cast<const u32x4*>(kp + vstep));
+        const T* pk = page ? page + (key & (g.page_size - 1)) * D + part * 8 : nullptr;
+        if constexpr (FUSED) {
+          const bool fresh = key >= offset && key < w1;
+          const T* kp = fresh ? krows + int64_t(key - offset) * a.q_r + part * 8 : (pk ? pk : dummy);
+          const T* vp = fresh ? vrows + int64_t(key - offset) * a.q_r + part * 8 : (pk ? pk + g.kind_stride : dummy);
+          wpage[n] = fresh && pk && key >= own0 ? const_cast<T*>(pk) : nullptr;
+          kx[n] = *global_view(reinterpret_cast<const u32x4*>(kp));
+          vx[n] = *global_view(reinterpret_cast<const u32x4*>(vp));
+        } else {
+          const T* kp = pk ? pk : dummy;
+          const int64_t vstep = pk ? g.kind_stride : 0;
+          kx[n] = *global_view(reinterpret_cast<const u32x4*>(kp));
+          vx[n] = *global_view(reinterpret_cast<const u32x4*>(kp + vstep));
+        }
       }
     };
     auto stage_store = [&]() {
@@ -1111,6 +1133,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a, Items it
         for (int j = 0; j < 4; ++j) {
           s_vt[part * 8 + 2 * j][kr] = static_cast<T>(vw[j] & 0xffffu);
           s_vt[part * 8 + 2 * j + 1][kr] = static_cast<T>(vw[j] >> 16);
+        }
+        if constexpr (FUSED) {
+          if (wpage[n]) {  // a key of this tile's own tokens: its page copy
+            *global_view(reinterpret_cast<u32x4*>(wpage[n])) = kx[n];
+            *global_view(reinterpret_cast<u32x4*>(wpage[n] + g.kind_stride)) = vx[n];
+          }
         }
       }
     };
@@ -1249,41 +1277,6 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     T* kp = const_cast<T*>(base) + (pos & (g.page_size - 1)) * dim + col;
     T* vp = kp + g.kind_stride;
     const int64_t src = b * a.src_b + head * a.src_h + pos_in * a.src_r + col;
-    if constexpr (VEC) {
-      *global_view(reinterpret_cast<u32x4*>(kp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k) + src));
-      *global_view(reinterpret_cast<u32x4*>(vp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v) + src));
-    } else {
-      *kp = static_cast<const T*>(a.k)[src];
-      *vp = static_cast<const T*>(a.v)[src];
-    }
-  }
-}
-
-// Append of prompts of different lengths (RaggedItems): the K/V of token row
-// t (elements t * src_r + head * src_h of k and v) go to position
-// offset[p] + (t - first_row[p]) of prompt p's pages; rows whose page is
-// missing are skipped, as in append_kernel.
-template <int DT, bool VEC>
-__global__ __launch_bounds__(256) void append_ragged_kernel(AppendArgs a, RaggedItems r) {
-  using T = typename Elem<DT>::T;
-  constexpr int E = VEC ? per16<DT>() : 1;
-  const Geometry& g = a.g;
-  const int dim = g.dim;
-  const int per_row = dim / E;
-  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < a.vectors;
-       i += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t row = i / per_row;  // t * heads + head
-    const int col = int(i - row * per_row) * E;
-    const int64_t t = row / g.heads;
-    const int head = int(row - t * g.heads);
-    int p = 0;
-    while (p + 1 < r.prompts && t >= r.first_row[p + 1]) ++p;
-    const int64_t pos = int64_t(r.offset[p]) + (t - r.first_row[p]);
-    const T* base = page_base<T>(a.slabs, r.table[p], pos >> g.log2_page, g, head);
-    if (!base) continue;
-    T* kp = const_cast<T*>(base) + (pos & (g.page_size - 1)) * dim + col;
-    T* vp = kp + g.kind_stride;
-    const int64_t src = t * a.src_r + head * a.src_h + col;
     if constexpr (VEC) {
       *global_view(reinterpret_cast<u32x4*>(kp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.k) + src));
       *global_view(reinterpret_cast<u32x4*>(vp)) = *global_view(reinterpret_cast<const u32x4*>(static_cast<const T*>(a.v) + src));
@@ -1491,9 +1484,20 @@ hipError_t launch_append(AppendArgs& a, int dtype) {
   return hipGetLastError();
 }
 
+// Whether launch_query runs the matrix-core prefill kernel: fp16/bf16,
+// head_dim 64/128, 16-byte aligned rows and at least kPfMinQueries queries.
+bool prefill_kernel_takes(const QueryArgs& a, int dtype) {
+  const int d = a.g.dim;
+  const int esize = dtype == kF32 ? 4 : 2;
+  auto rows16 = [&](int64_t x) { return (x * esize) % 16 == 0; };
+  return (d == 64 || d == 128) && dtype != kF32 && a.nq >= kPfMinQueries && aligned16(a.out) &&
+         aligned16(a.q) && rows16(a.q_b) && rows16(a.q_h) && rows16(a.q_r) && rows16(a.o_b) &&
+         rows16(a.o_h) && rows16(a.o_r);
+}
+
 // Causal attention launch for any q/out strides: the matrix-core prefill
-// kernel for fp16/bf16, head_dim 64/128, 16-byte aligned rows and at least
-// kPfMinQueries queries; the per-query kernel otherwise.
+// kernel where prefill_kernel_takes, the per-query kernel otherwise (which
+// reads every key from the pages: a.k must then be null).
 hipError_t launch_query(QueryArgs& a, int dtype) {
   const int d = a.g.dim;
   const int esize = dtype == kF32 ? 4 : 2;
@@ -1502,18 +1506,23 @@ hipError_t launch_query(QueryArgs& a, int dtype) {
                    rows16(a.q_h) && rows16(a.q_r) && rows16(a.o_b) && rows16(a.o_h) && rows16(a.o_r);
   a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
   const int h = a.g.heads;
-  if (vec && dtype != kF32 && a.nq >= kPfMinQueries) {
+  if (prefill_kernel_takes(a, dtype)) {
     a.items = int64_t(a.batch) * h * ((a.nq + kPfQueries - 1) / kPfQueries);
     const int blocks = grid_for(a.items);
+#define MT_PREFILL(DT, D)                                                                   \
+  if (a.k) prefill_kernel<DT, D, UniformItems, true><<<blocks, kThreads>>>(a, UniformItems{});   \
+  else prefill_kernel<DT, D, UniformItems, false><<<blocks, kThreads>>>(a, UniformItems{});
     if (dtype == kF16) {
-      if (d == 64) prefill_kernel<kF16, 64, UniformItems><<<blocks, kThreads>>>(a, UniformItems{});
-      else prefill_kernel<kF16, 128, UniformItems><<<blocks, kThreads>>>(a, UniformItems{});
+      if (d == 64) { MT_PREFILL(kF16, 64) }
+      else { MT_PREFILL(kF16, 128) }
     } else {
-      if (d == 64) prefill_kernel<kBF16, 64, UniformItems><<<blocks, kThreads>>>(a, UniformItems{});
-      else prefill_kernel<kBF16, 128, UniformItems><<<blocks, kThreads>>>(a, UniformItems{});
+      if (d == 64) { MT_PREFILL(kBF16, 64) }
+      else { MT_PREFILL(kBF16, 128) }
     }
+#undef MT_PREFILL
     return hipGetLastError();
   }
+  if (a.k) return hipErrorInvalidValue;
   a.items = int64_t(a.batch) * h * ((a.nq + kWaves - 1) / kWaves);
   const int blocks = grid_for(a.items);
 #define MT_QUERY(DT)                                                                   \
@@ -1555,7 +1564,7 @@ int mt_paged_attention(void* out, const void* q, const uint64_t* slabs, const in
                    offset))
     return hipErrorInvalidValue;
   if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
-  QueryArgs a;
+  QueryArgs a{};
   a.out = out; a.q = q; a.slabs = slabs; a.table = table;
   a.batch = b; a.nq = nq; a.nk = nk; a.offset = offset;
   a.g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
@@ -1579,18 +1588,24 @@ int mt_paged_prefill(void* out, const void* q, const void* k, const void* v, con
                    layers, offset))
     return hipErrorInvalidValue;
   if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
+  QueryArgs a{};
+  a.out = out; a.q = q; a.slabs = slabs; a.table = table;
+  a.batch = b; a.nq = n; a.nk = offset + n; a.offset = offset;
+  a.g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
+  a.q_b = int64_t(n) * qkv_stride; a.q_h = d; a.q_r = qkv_stride;
+  a.o_b = int64_t(n) * out_stride; a.o_h = d; a.o_r = out_stride;
+  if (prefill_kernel_takes(a, dtype) && aligned16(k) && aligned16(v)) {
+    // The prefill kernel reads the new keys from k/v and writes them to
+    // their pages itself: no separate append.
+    a.k = k; a.v = v;
+    return launch_query(a, dtype);
+  }
   AppendArgs ap;
   ap.k = k; ap.v = v; ap.slabs = slabs; ap.table = table; ap.batch = b; ap.n = n; ap.offset = offset;
-  ap.g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
+  ap.g = a.g;
   ap.src_b = int64_t(n) * qkv_stride; ap.src_h = d; ap.src_r = qkv_stride;
   hipError_t e = launch_append(ap, dtype);
   if (e != hipSuccess) return e;
-  QueryArgs a;
-  a.out = out; a.q = q; a.slabs = slabs; a.table = table;
-  a.batch = b; a.nq = n; a.nk = offset + n; a.offset = offset;
-  a.g = ap.g;
-  a.q_b = int64_t(n) * qkv_stride; a.q_h = d; a.q_r = qkv_stride;
-  a.o_b = int64_t(n) * out_stride; a.o_h = d; a.o_r = out_stride;
   return launch_query(a, dtype);
 }
 
@@ -1684,18 +1699,11 @@ int mt_paged_prefill_ragged(void* out, const void* q, const void* k, const void*
       it.pair_tile[i] = static_cast<unsigned short>(order[i].second);
     }
     const size_t qoff = size_t(row0) * qkv_stride * e, ooff = size_t(row0) * out_stride * e;
-    AppendArgs ap{};
-    ap.k = static_cast<const char*>(k) + qoff;
-    ap.v = static_cast<const char*>(v) + qoff;
-    ap.slabs = slabs;
-    ap.g = g;
-    ap.src_h = d;
-    ap.src_r = qkv_stride;
-    ap.vectors = rows * h * (d / int(16 / e));
-    const int ablocks = int((ap.vectors + 255) / 256 < 65536 * 16 ? (ap.vectors + 255) / 256 : 65536 * 16);
     QueryArgs a{};
     a.out = static_cast<char*>(out) + ooff;
     a.q = static_cast<const char*>(q) + qoff;
+    a.k = static_cast<const char*>(k) + qoff;  // the kernel appends the prompts' K/V itself
+    a.v = static_cast<const char*>(v) + qoff;
     a.slabs = slabs;
     a.g = g;
     a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
@@ -1703,13 +1711,11 @@ int mt_paged_prefill_ragged(void* out, const void* q, const void* k, const void*
     a.o_h = d; a.o_r = out_stride;
     const int blocks = grid_for(int64_t(pairs) * h);
     if (dtype == kF16) {
-      append_ragged_kernel<kF16, true><<<ablocks, 256>>>(ap, it);
-      if (d == 64) prefill_kernel<kF16, 64, RaggedItems><<<blocks, kThreads>>>(a, it);
-      else prefill_kernel<kF16, 128, RaggedItems><<<blocks, kThreads>>>(a, it);
+      if (d == 64) prefill_kernel<kF16, 64, RaggedItems, true><<<blocks, kThreads>>>(a, it);
+      else prefill_kernel<kF16, 128, RaggedItems, true><<<blocks, kThreads>>>(a, it);
     } else {
-      append_ragged_kernel<kBF16, true><<<ablocks, 256>>>(ap, it);
-      if (d == 64) prefill_kernel<kBF16, 64, RaggedItems><<<blocks, kThreads>>>(a, it);
-      else prefill_kernel<kBF16, 128, RaggedItems><<<blocks, kThreads>>>(a, it);
+      if (d == 64) prefill_kernel<kBF16, 64, RaggedItems, true><<<blocks, kThreads>>>(a, it);
+      else prefill_kernel<kBF16, 128, RaggedItems, true><<<blocks, kThreads>>>(a, it);
     }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;

@@ -285,3 +285,50 @@ def test_prefill_ragged_prompt_longer_than_one_launch_describes():
         images.append(dev.pool_image())
     assert np.array_equal(outs[0], outs[1])
     assert np.array_equal(images[0].view(np.uint8), images[1].view(np.uint8))
+
+
+@pytest.mark.parametrize('entry', ['prefill', 'ragged'])
+def test_fused_append_with_missing_page_equals_append_then_attention(entry):
+    # The matrix-core prefill reads the new keys from the K/V rows and writes
+    # them to their pages itself. A missing page (table hole, out-of-pool
+    # page) must still be skipped by the write and read as NaN, exactly as
+    # mt_paged_append followed by mt_paged_attention does: bitwise equal
+    # outputs (NaN rows included) and pool images.
+    b, h, d, n, offset, page = 2, 2, 64, 70, 9, 16
+    case = prefill_case(71, batch=b, heads=h, dim=d, page_size=page, nk=offset + n, dtype='bfloat16')
+    case.table[0, 2] = -1          # keys 32..47 of request 0 (new tokens)
+    case.table[1, 4] = 10 ** 6     # keys 64..78 of request 1
+    rng = np.random.default_rng(71)
+    qkv = po.encode(rng.standard_normal((b, n, 3 * h * d), dtype=np.float32), po.BF16)
+    heads = lambda blk: np.ascontiguousarray(qkv[:, :, blk * h * d:(blk + 1) * h * d]
+                                             .reshape(b, n, h, d).transpose(0, 2, 1, 3))
+    q, k, v = heads(0), heads(1), heads(2)
+    common = dict(page_size=page, pages_per_slab=case.pages_per_slab, num_slabs=case.num_slabs,
+                  columns=case.columns, layer=0, layers=1, dtype='bfloat16')
+    one, two = DevicePagedCase(case), DevicePagedCase(case)
+    fused = DeviceTensor(qkv.shape, 'bfloat16')
+    runtime().h2d(fused.ptr, qkv)
+    out1 = DeviceTensor((b, n, h * d), 'bfloat16')
+    if entry == 'prefill':
+        paged_ops.paged_prefill(out1.ptr, fused.ptr, fused.ptr + h * d * 2, fused.ptr + 2 * h * d * 2,
+                                one.slab_table.ptr, one.block_table.ptr, b=b, h=h, n=n, d=d, offset=offset,
+                                qkv_stride=3 * h * d, out_stride=h * d, **common)
+    else:
+        tables = [one.block_table.ptr + 4 * i * case.columns for i in range(b)]
+        paged_ops.paged_prefill_ragged(out1.ptr, fused.ptr, fused.ptr + h * d * 2, fused.ptr + 2 * h * d * 2,
+                                       one.slab_table.ptr, tables, [n] * b, [offset] * b, h=h, d=d,
+                                       qkv_stride=3 * h * d, out_stride=h * d, **common)
+    qd, kd, vd = (DeviceTensor(x.shape, 'bfloat16') for x in (q, k, v))
+    for t, x in ((qd, q), (kd, k), (vd, v)):
+        runtime().h2d(t.ptr, x)
+    out2 = DeviceTensor(q.shape, 'bfloat16')
+    paged_ops.paged_append(kd.ptr, vd.ptr, two.slab_table.ptr, two.block_table.ptr, b=b, h=h, n=n, d=d,
+                           offset=offset, **common)
+    paged_ops.paged_attention(out2.ptr, qd.ptr, two.slab_table.ptr, two.block_table.ptr, b=b, h=h, nq=n,
+                              nk=offset + n, d=d, offset=offset, **common)
+    runtime().synchronize()
+    assert np.array_equal(one.pool_image().view(np.uint8), two.pool_image().view(np.uint8))
+    got1 = out1.raw_numpy().reshape(b, n, h, d).transpose(0, 2, 1, 3)
+    got2 = out2.raw_numpy()
+    assert np.array_equal(got1, got2)
+    assert np.isnan(out2.to_numpy()).any()   # the holes are attended
