@@ -214,3 +214,47 @@ def test_prefill_layers_rejects_invalid_arguments():
     assert call(dtype=5) == 1
     assert call(logits=8, head=None) == 1         # logits need the head weight
     assert call(att=None) == 1
+
+
+def test_ragged_prefill_entries_reject_invalid_arguments():
+    # validation only: every call below returns before any device work
+    lib = library('paged_attention_kernel')
+    f = lib.mt_paged_prefill_ragged
+    f.argtypes, f.restype = [P] * 8 + [I] * 12, I
+    tables = (P * 2)(8, 8)
+
+    def call(tokens=(5, 7), offsets=(0, 3), requests=2, h=3, d=64, page=16, dtype=1, qkv_stride=0,
+             out_stride=0, tabs=tables, layer=0):
+        return f(8, 8, 8, 8, 8, tabs, (I * 2)(*tokens), (I * 2)(*offsets), requests, h, d, page, 4, 4, 8,
+                 layer, 1, dtype, qkv_stride, out_stride)
+    assert call(tokens=(5, 0)) == 1             # an empty prompt
+    assert call(offsets=(0, -1)) == 1           # negative offset
+    assert call(tokens=(5, 200)) == 1           # beyond columns * page_size
+    assert call(requests=0) == 1
+    assert call(page=12) == 1
+    assert call(dtype=3) == 1
+    assert call(qkv_stride=100) == 1            # < h * d
+    assert call(layer=1) == 1                   # layer >= layers
+    assert call(tabs=(P * 2)(8, None)) == 1     # a null table row
+    assert f(None, 8, 8, 8, 8, tables, (I * 2)(5, 7), (I * 2)(0, 0), 2, 3, 64, 16, 4, 4, 8, 0, 1, 1, 0, 0) == 1
+
+    lib = library('model_kernels')
+    g = lib.mt_prefill_layers_ragged
+    g.argtypes = [P, P, I, P, P, P, P, P, P, I, I, P, I, I, ct.c_float, I, I, P, Z, P]
+    g.restype = I
+    layer = _Layer(*([8] * 12))
+    atts = (_Prefill * 2)(_Prefill(8, 8, 16, 4, 4, 8, 1, 0), _Prefill(8, 8, 16, 4, 4, 8, 1, 0))
+    need = lib.mt_decoder_scratch_bytes
+    need.argtypes, need.restype = [I, I, I], Z
+    scratch = need(12, 64, 1)
+
+    def layers_call(tokens=(5, 7), requests=2, scratch_bytes=scratch, heads=2, att=atts):
+        return g(8, ct.byref(layer), 1, 8, 8, 8, 8, 8, 8, 10, requests, (I * 2)(*tokens), 64, heads, 1e-5, 1, 1,
+                 8, scratch_bytes, att)
+    assert layers_call(tokens=(5, 0)) == 1            # an empty prompt
+    assert layers_call(scratch_bytes=scratch - 1) == 1
+    assert layers_call(heads=3) == 1                  # d % heads
+    assert layers_call(requests=0) == 1
+    assert layers_call(att=None) == 1
+    other = (_Prefill * 2)(_Prefill(8, 8, 16, 4, 4, 8, 1, 0), _Prefill(8, 8, 32, 4, 4, 8, 1, 0))
+    assert layers_call(att=other) == 1                # prompts of different pools
