@@ -46,7 +46,13 @@ struct Plan {
   int candidates = 0;
   int calls = 0;
   bool ok = false;
+  bool tunable = false;
 };
+
+// One-off shapes (prefill row counts, which batched prefills make nearly
+// unique) keep at most this many cached plans; beyond it they are all
+// released and rebuilt on demand. Tuned shapes (the decode step's) stay.
+constexpr int kMaxOneOffPlans = 256;
 
 // A hipBLASLt handle, a 64 MiB workspace and the plans (descriptors plus the
 // chosen algorithm) per GEMM shape, created on first use.
@@ -58,6 +64,7 @@ struct Blas {
   size_t workspace_bytes = size_t(64) << 20;
   std::mutex mutex;
   std::map<std::tuple<int, int, int, int, int, int, int, int, int>, Plan> plans;
+  int oneoff_plans = 0;
   // Algorithm per problem class of the one-off shapes (rows rounded up to a
   // multiple of kRowBucket, any row stride): the heuristic's first choice for
   // the class's largest row count.
@@ -229,7 +236,24 @@ int gemm(Blas* blas, void* out, const void* a, const void* b, const void* bias, 
   if (lda == 0) lda = k;  // elements between consecutive rows of a
   std::lock_guard<std::mutex> lock(blas->mutex);
   auto key = std::make_tuple(m, n, k, transb, dtype, out_dtype, bias ? 1 : 0, epilogue, lda);
+  if (!tunable && blas->oneoff_plans >= kMaxOneOffPlans && !blas->plans.count(key)) {
+    for (auto it = blas->plans.begin(); it != blas->plans.end();) {
+      if (!it->second.tunable) {
+        release_plan(it->second);
+        it = blas->plans.erase(it);
+      } else {
+        ++it;
+      }
+    }
+    blas->oneoff_plans = 0;
+  }
   Plan& p = blas->plans[key];
+  if (p.ok && tunable && !p.tunable) {
+    // First built for a one-off call (one class algorithm, never timed): a
+    // repeating shape rebuilds it with the heuristic's candidates to time.
+    release_plan(p);
+    --blas->oneoff_plans;
+  }
   if (!p.ok) {
     // On failure the partial plan is released so a later call can retry.
     const int st = make_plan(blas, p, m, n, k, transb, dtype, out_dtype, bias, epilogue, tunable, lda);
@@ -238,6 +262,8 @@ int gemm(Blas* blas, void* out, const void* a, const void* b, const void* bias, 
       blas->plans.erase(key);
       return st;
     }
+    p.tunable = tunable;
+    if (!tunable) ++blas->oneoff_plans;
   }
   if (tunable && ++p.calls == kTuneAfterCalls && p.candidates > 1 && blas->tune) {
     if (bias)
