@@ -7,6 +7,7 @@ goes to ``cuda_kernels/paged_attention_kernel.so`` or
 ``cuda_kernels/inference_kernels.so``.
 """
 import ctypes as ct
+from functools import lru_cache
 import numpy as np
 from .runtime import library, call, P, I, Z, DeviceTensor, runtime
 from .dtypes import dtype_code
@@ -67,16 +68,20 @@ def paged_decode_batch(out, q, k, v, slab_table, block_table, offsets, *, b, h, 
          num_slabs, columns, layer, layers, dtype_code(dtype))
 
 
+@lru_cache(maxsize=4096)
 def decode_workspace_bytes(*, b, h, page_size, columns, split_tokens=0):
-    """Workspace size for ``mt_paged_decode_split`` (0 when no row can split)."""
+    """Workspace size for ``mt_paged_decode_split`` (0 when no row can split);
+    a pure function of its arguments, memoized."""
     out = ct.c_size_t()
     call(paged_library(), 'mt_paged_decode_workspace_bytes', [I] * 5 + [ct.POINTER(ct.c_size_t)],
          b, h, page_size, columns, split_tokens, ct.byref(out))
     return out.value
 
 
+@lru_cache(maxsize=4096)
 def split_tokens_for(*, page_size, columns, requested=0):
-    """Split length the decode uses for a table of ``columns`` pages."""
+    """Split length the decode uses for a table of ``columns`` pages; a pure
+    function of its arguments, memoized."""
     out = ct.c_int()
     call(paged_library(), 'mt_paged_decode_split_tokens', [I, I, I, ct.POINTER(ct.c_int)],
          page_size, columns, requested, ct.byref(out))
