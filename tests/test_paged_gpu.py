@@ -257,24 +257,36 @@ def test_config5_full_size_bench_case(page_size):
     # lognormal(ln 256, 1.2) clipped to [1, 8192], the hash-filled device pool,
     # the library's split length and the longest-first work list. Every row
     # is checked against the C oracle and the whole pool image bit for bit.
+    full_size_against_c_oracle(config5_lengths(0, 512), 25, page_size, expect_merges=True)
+
+
+def test_config4_attention_shape_full_size():
+    # The decode attention of a config-4 step (128 rows, 16 heads, bf16,
+    # contexts lognormal median 256 clipped to [16, 1024], page 16), as the
+    # end-to-end loop launches it once per layer.
+    from minitorch_amd.e2e import config4_lengths
+    full_size_against_c_oracle(config4_lengths(np.random.default_rng([0, 4]), 128), 16, 16, expect_merges=False)
+
+
+def full_size_against_c_oracle(lengths, heads, page_size, expect_merges):
     import ctypes as ct
     from minitorch_amd.workloads import DeviceRaggedCase
     from minitorch_amd.dtypes import decode_host
     from oracle import c_oracle
     lib = c_oracle.library()
     rt = runtime()
-    lengths = config5_lengths(0, 512)
-    case = DeviceRaggedCase(0, batch=512, heads=25, dim=64, page_size=page_size, lengths=lengths,
+    b = len(lengths)
+    case = DeviceRaggedCase(0, batch=b, heads=heads, dim=64, page_size=page_size, lengths=lengths,
                             dtype='bfloat16')
     kw = case.kwargs()
     image = case.pool.download(np.uint16)
     q, k, v = (t.raw_numpy() for t in (case.q, case.k, case.v))
     split = paged_ops.split_tokens_for(page_size=page_size, columns=case.columns)
-    ws_bytes = paged_ops.decode_workspace_bytes(b=512, h=25, page_size=page_size, columns=case.columns,
+    ws_bytes = paged_ops.decode_workspace_bytes(b=b, h=heads, page_size=page_size, columns=case.columns,
                                                 split_tokens=split)
     ws = RawDeviceBuffer(max(ws_bytes, 4))
-    work, items, merges = paged_ops.decode_work_list(case.lengths, 25, split, rt.compute_units())
-    assert merges > 0 and case.lengths.max() > 1024  # the split reduction runs
+    work, items, merges = paged_ops.decode_work_list(case.lengths, heads, split, rt.compute_units())
+    assert (merges > 0) == expect_merges  # the split reduction runs for config 5
     order = RawDeviceBuffer(4 * len(work))
     order.upload(work)
     paged_ops.paged_decode_split(case.out.ptr, case.q.ptr, case.k.ptr, case.v.ptr, case.slab_table.ptr,
@@ -291,11 +303,11 @@ def test_config5_full_size_bench_case(page_size):
     out = np.zeros_like(q)
     status = lib.oracle_paged_decode_batch(out.ctypes.data, q.ctypes.data, k.ctypes.data, v.ctypes.data,
                                            slabs.ctypes.data, table.ctypes.data, offsets.ctypes.data,
-                                           512, 25, 64, page_size, case.pages_per_slab, case.num_slabs,
+                                           b, heads, 64, page_size, case.pages_per_slab, case.num_slabs,
                                            case.columns, 0, 1, c_oracle.CODES['bfloat16'], 0)
     assert status == 0
     ref = decode_host(out, 'bfloat16').reshape(got.shape)
-    assert_attention_close(got, ref, 'bfloat16', context=f'config 5 P={page_size}')
+    assert_attention_close(got, ref, 'bfloat16', context=f'B={b} H={heads} P={page_size}')
     assert np.array_equal(after, image), 'append differs from the oracle'
 
 
