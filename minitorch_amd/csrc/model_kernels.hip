@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256) void residual_layernorm_wave_kernel(void* out,
                                                                       int has_residual) {
   using T = typename Elem<DT>::T;
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
   if (row >= rows) return;
   const int nj = width >> 8;
   float* xr = x + int64_t(row) * width;
@@ -490,13 +490,17 @@ bool wave_rows(const void* out, const float* x, const void* y, const float* gamm
 }
 
 template <int DT>
+#ifndef MT_LN_ROWS_PER_BLOCK
+#define MT_LN_ROWS_PER_BLOCK 4
+#endif
 void launch_wave_rows(void* out, float* x, const void* y, const float* gamma, const float* beta,
                       int rows, int width, float eps) {
-  const int blocks = (rows + 3) / 4;
+  constexpr int R = MT_LN_ROWS_PER_BLOCK;  // one wave per row
+  const int blocks = (rows + R - 1) / R;
   if (width <= 1024)
-    residual_layernorm_wave_kernel<DT, 4><<<blocks, 256>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr);
+    residual_layernorm_wave_kernel<DT, 4><<<blocks, 64 * R>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr);
   else
-    residual_layernorm_wave_kernel<DT, 8><<<blocks, 256>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr);
+    residual_layernorm_wave_kernel<DT, 8><<<blocks, 64 * R>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr);
 }
 
 hipError_t layernorm(void* out, const float* x, const float* gamma, const float* beta, int rows,
