@@ -407,3 +407,41 @@ def test_gemm_plan_cache_sweep_keeps_results():
     prompt = rng.integers(0, model.n_vocab, 20).tolist()
     assert generate(model, prompt, 6) == go.greedy(model.state, prompt, 6, n_head=model.n_head,
                                                    n_layer=model.n_layer)[0]
+
+
+def test_distilgpt2_shape_batched_prefill_fp16():
+    # DistilGPT-2 shapes (d 768, 12 heads, vocab 50257) in fp16: prompts of
+    # 33..500 tokens prefilled together (one ragged launch per layer, the K/V
+    # append inside the attention kernel) give the logits of one prefill call
+    # each within 1 % of their range, and decode alike afterwards; a batcher
+    # admitting 4 prompts per step completes every request and drains the pool.
+    from minitorch_amd.paged_kv_cache import KVPagePool
+    model = DecoderLM(n_vocab=50257, n_embd=768, n_head=12, n_layer=6, n_positions=1024, seed=5)
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, 50257, n) for n in (33, 100, 257, 500)]
+    with autocast('float16'):
+        outs = []
+        for batched in (False, True):
+            pool = KVPagePool(model, page_size=16, max_bytes=512 * 1024 ** 2, pages_per_slab=16)
+            caches = [model.create_kv_cache(1, len(p) + 2, page_size=16, page_pool=pool) for p in prompts]
+            if batched:
+                logits = model.prefill_batch(prompts, caches).to_numpy()[:, 0]
+            else:
+                logits = np.stack([model.prefill(DeviceTensor.from_numpy(p[None].astype(np.float32)), c)[0]
+                                   .to_numpy()[0, 0] for p, c in zip(prompts, caches)])
+            ids = logits.argmax(axis=1)
+            step = model.decode_batch(DeviceTensor.from_numpy(ids[:, None].astype(np.float32)), caches)
+            outs.append((logits.astype(np.float64), step.to_numpy()[:, 0].astype(np.float64)))
+            for c in caches:
+                c.close()
+            pool.close()
+    for a, b in zip(outs[0], outs[1]):
+        assert np.abs(a - b).max() <= 0.01 * (a.max() - a.min())
+    trace = [(0, f'p{i}', rng.integers(0, 50257, int(n)).tolist(), 5) for i, n in enumerate((40, 90, 33, 300, 64, 120))]
+    batcher, steps = run_trace(model, trace, precision='fp16', max_batch_size=6, budget_pages=2000,
+                               max_prefills_per_step=4)
+    assert max(len(s['prefill_request_ids']) for s in steps) == 4
+    assert all(batcher.requests[t[1]].state == 'completed' and len(batcher.requests[t[1]].output_ids) == 5
+               for t in trace)
+    assert steps[-1]['kv_pool_used_pages'] == 0
+    batcher.close()
