@@ -817,6 +817,9 @@ struct QueryArgs {
   // replaces a separate append.
   const void* k;
   const void* v;
+  // Key-split prefill: per (slot, head, query of the tile) max, denominator
+  // and D accumulators of one split's keys, merged by prefill_merge_kernel.
+  float* partials;
 };
 
 // Causal paged attention for nq >= 1 queries per (request, head)
@@ -974,7 +977,11 @@ struct PfItem {
   int tile, head, nq, offset;
   int64_t q0, o0;
   const int* table_row;
+  int kb0, kb1;  // key blocks [kb0, kb1) of the tile's keys that this item attends
+  int slot;      // partials slot of a split tile, -1: the item writes the output rows
 };
+
+constexpr int kAllKeyBlocks = 1 << 24;
 
 // The uniform batch of QueryArgs (b requests of nq queries at one offset):
 // items ordered by tile, last (longest) tiles first.
@@ -993,6 +1000,7 @@ struct UniformItems {
     it.q0 = b * a.q_b + it.head * a.q_h;
     it.o0 = b * a.o_b + it.head * a.o_h;
     it.table_row = a.table + int64_t(b) * a.g.columns;
+    it.kb0 = 0; it.kb1 = kAllKeyBlocks; it.slot = -1;
     return it;
   }
 };
@@ -1021,6 +1029,32 @@ struct RaggedItems {
     it.q0 = int64_t(first_row[r]) * a.q_r + it.head * a.q_h;
     it.o0 = int64_t(first_row[r]) * a.o_r + it.head * a.o_h;
     it.table_row = table[r];
+    it.kb0 = 0; it.kb1 = kAllKeyBlocks; it.slot = -1;
+    return it;
+  }
+};
+
+// One request (QueryArgs with batch 1) whose long query tiles have their
+// keys split over several workgroups: (tile, key blocks [kb0, kb1), slot)
+// per pair, heaviest first, times the heads. A tile with one split writes its
+// output; the splits of the others write partials for prefill_merge_kernel.
+constexpr int kSplitPairs = 256;
+struct SplitItems {
+  int pairs;
+  unsigned short tile[kSplitPairs], kb0[kSplitPairs], kb1[kSplitPairs];
+  short slot[kSplitPairs];
+  __device__ __forceinline__ int64_t count(const QueryArgs& a) const { return int64_t(pairs) * a.g.heads; }
+  __device__ __forceinline__ PfItem get(int64_t item, const QueryArgs& a) const {
+    const int p = int(item / a.g.heads);
+    PfItem it;
+    it.tile = tile[p];
+    it.head = int(item - int64_t(p) * a.g.heads);
+    it.nq = a.nq;
+    it.offset = a.offset;
+    it.q0 = it.head * a.q_h;
+    it.o0 = it.head * a.o_h;
+    it.table_row = a.table;
+    it.kb0 = kb0[p]; it.kb1 = kb1[p]; it.slot = slot[p];
     return it;
   }
 };
@@ -1142,8 +1176,11 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a, Items it
         }
       }
     };
-    for (int w0 = 0; w0 < kend; w0 += win_keys) {
-      const int w1 = w0 + win_keys < kend ? w0 + win_keys : kend;
+    // This item's keys: blocks [kb0, kb1) of [0, kend).
+    const int kstart = it.kb0 * KS;
+    const int kstop = it.kb1 >= (kend + KS - 1) / KS ? kend : it.kb1 * KS;
+    for (int w0 = kstart; w0 < kstop; w0 += win_keys) {
+      const int w1 = w0 + win_keys < kstop ? w0 + win_keys : kstop;
       const int npg = (w1 - w0 + g.page_size - 1) >> g.log2_page;
       __syncthreads();
       for (int j = tid; j < npg; j += kThreads)
@@ -1239,8 +1276,18 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a, Items it
     // The query's denominator is the sum over its four lanes.
     l += lane_swap16(l);
     l += lane_swap32(l);
+    if (q_ok && it.slot >= 0) {
+      // A split of the tile's keys: (max, denominator, accumulators) in
+      // base-2 units for prefill_merge_kernel.
+      float* part = a.partials + ((int64_t(it.slot) * g.heads + head) * kPfQueries + wave * 16 + col) * (D + 2);
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[2 + dt * 16 + 4 * grp + i] = o[dt][i];
+      if (grp == 0) { part[0] = m; part[1] = l; }
+    }
     // O^T lane layout: dims dt*16 + 4*grp + i of query qi.
-    if (q_ok) {
+    if (q_ok && it.slot < 0) {
       T* orow = out + it.o0 + qi * a.o_r;
 #pragma unroll
       for (int dt = 0; dt < DT16; ++dt) {
@@ -1251,6 +1298,48 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a, Items it
       }
     }
   }
+}
+
+// Merge of a split prefill (one request): for each split tile, every query's
+// outputs from its splits' (max, denominator, accumulators) by the log-sum-exp
+// rule, with the finalize rule of the unsplit kernel (a NaN denominator stays
+// NaN, a zero one gives 0). One workgroup per (tile, head), four threads per
+// query, D/4 dims each.
+struct PrefillMerge {
+  int tiles;
+  unsigned short tile[kSplitPairs], first_slot[kSplitPairs];
+  unsigned char splits[kSplitPairs];
+};
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(QueryArgs a, PrefillMerge mg) {
+  using T = typename Elem<DT>::T;
+  constexpr int DQ = D / 4;
+  const int t = int(blockIdx.x / unsigned(a.g.heads));
+  const int head = int(blockIdx.x - unsigned(t) * a.g.heads);
+  if (t >= mg.tiles) return;
+  const int q = threadIdx.x >> 2, c0 = (threadIdx.x & 3) * DQ;
+  const int qi = mg.tile[t] * kPfQueries + q;
+  if (qi >= a.nq) return;
+  const int n = mg.splits[t];
+  auto part = [&](int s) {
+    return a.partials + ((int64_t(mg.first_slot[t] + s) * a.g.heads + head) * kPfQueries + q) * (D + 2);
+  };
+  float M = -INFINITY;
+  for (int s = 0; s < n; ++s) M = fmaxf(M, part(s)[0]);
+  float L = 0.f, acc[DQ];
+#pragma unroll
+  for (int j = 0; j < DQ; ++j) acc[j] = 0.f;
+  for (int s = 0; s < n; ++s) {
+    const float* p = part(s);
+    const float w = p[0] == -INFINITY ? 0.f : fast_exp2(p[0] - M);
+    L = fmaf(p[1], w, L);  // a NaN denominator (missing page) poisons the sum
+#pragma unroll
+    for (int j = 0; j < DQ; ++j) acc[j] = fmaf(p[2 + c0 + j], w, acc[j]);
+  }
+  T* orow = static_cast<T*>(a.out) + head * a.o_h + int64_t(qi) * a.o_r + c0;
+#pragma unroll
+  for (int j = 0; j < DQ; ++j) orow[j] = from_f32<DT>(finalize(acc[j], L));
 }
 
 // Multi-token append at a common offset (reference paged_append with
@@ -1495,6 +1584,66 @@ bool prefill_kernel_takes(const QueryArgs& a, int dtype) {
          rows16(a.o_h) && rows16(a.o_r);
 }
 
+// Key-split prefill of one request whose query tiles give at most one
+// workgroup per compute unit and whose last tile walks many key blocks: each tile's keys are cut
+// into splits of B blocks (B chosen for about two workgroups per compute
+// unit), every split a workgroup, the splits then merged. Returns
+// hipErrorNotSupported when the shape is better served unsplit.
+hipError_t launch_split_prefill(QueryArgs& a, int dtype) {
+  const int h = a.g.heads, d = a.g.dim;
+  const int tiles = (a.nq + kPfQueries - 1) / kPfQueries;
+  const int cus = device_compute_units();
+  auto blocks_of = [&](int t) {
+    const int64_t last = int64_t(a.offset) + std::min(int64_t(t + 1) * kPfQueries, int64_t(a.nq));
+    return int((std::min<int64_t>(last, a.nk) + kPfKeys - 1) / kPfKeys);
+  };
+  if (a.batch != 1 || cus < 1 || int64_t(tiles) * h > cus || blocks_of(tiles - 1) < 6)
+    return hipErrorNotSupported;
+  int64_t total = 0;
+  for (int t = 0; t < tiles; ++t) total += blocks_of(t);
+  const int B = std::max<int>(2, int((total * h + 2 * cus - 1) / (2 * cus)));
+  SplitItems it{};
+  PrefillMerge mg{};
+  int pairs = 0, slots = 0;
+  for (int t = tiles - 1; t >= 0; --t) {  // heaviest tiles first
+    const int nb = blocks_of(t), n = (nb + B - 1) / B;
+    if (pairs + n > kSplitPairs || n > 255 || nb > 65535) return hipErrorNotSupported;
+    if (n > 1) {
+      mg.tile[mg.tiles] = static_cast<unsigned short>(t);
+      mg.first_slot[mg.tiles] = static_cast<unsigned short>(slots);
+      mg.splits[mg.tiles] = static_cast<unsigned char>(n);
+      ++mg.tiles;
+    }
+    for (int s = 0; s < n; ++s) {
+      it.tile[pairs] = static_cast<unsigned short>(t);
+      it.kb0[pairs] = static_cast<unsigned short>(s * B);
+      it.kb1[pairs] = static_cast<unsigned short>(std::min(nb, (s + 1) * B));
+      it.slot[pairs] = static_cast<short>(n > 1 ? slots++ : -1);
+      ++pairs;
+    }
+  }
+  if (mg.tiles == 0) return hipErrorNotSupported;
+  it.pairs = pairs;
+  void* ws = nullptr;
+  const int e = library_workspace(size_t(slots) * h * kPfQueries * (d + 2) * sizeof(float), &ws);
+  if (e != hipSuccess) return hipError_t(e);
+  a.partials = static_cast<float*>(ws);
+  const int blocks = grid_for(int64_t(pairs) * h);
+#define MT_SPLIT(DT, D)                                                                        \
+  if (a.k) prefill_kernel<DT, D, SplitItems, true><<<blocks, kThreads>>>(a, it);              \
+  else prefill_kernel<DT, D, SplitItems, false><<<blocks, kThreads>>>(a, it);                 \
+  prefill_merge_kernel<DT, D><<<unsigned(mg.tiles * h), 256>>>(a, mg);
+  if (dtype == kF16) {
+    if (d == 64) { MT_SPLIT(kF16, 64) }
+    else { MT_SPLIT(kF16, 128) }
+  } else {
+    if (d == 64) { MT_SPLIT(kBF16, 64) }
+    else { MT_SPLIT(kBF16, 128) }
+  }
+#undef MT_SPLIT
+  return hipGetLastError();
+}
+
 // Causal attention launch for any q/out strides: the matrix-core prefill
 // kernel where prefill_kernel_takes, the per-query kernel otherwise (which
 // reads every key from the pages: a.k must then be null).
@@ -1507,6 +1656,8 @@ hipError_t launch_query(QueryArgs& a, int dtype) {
   a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
   const int h = a.g.heads;
   if (prefill_kernel_takes(a, dtype)) {
+    const hipError_t split = launch_split_prefill(a, dtype);
+    if (split != hipErrorNotSupported) return split;
     a.items = int64_t(a.batch) * h * ((a.nq + kPfQueries - 1) / kPfQueries);
     const int blocks = grid_for(a.items);
 #define MT_PREFILL(DT, D)                                                                   \

@@ -332,3 +332,59 @@ def test_fused_append_with_missing_page_equals_append_then_attention(entry):
     got2 = out2.raw_numpy()
     assert np.array_equal(got1, got2)
     assert np.isnan(out2.to_numpy()).any()   # the holes are attended
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+@pytest.mark.parametrize('dim', [64, 128])
+@pytest.mark.parametrize('nq,offset,page_size', [(1024, 0, 16), (700, 333, 32), (300, 2000, 8)])
+def test_prefill_long_single_prompt_key_splits(dtype, dim, nq, offset, page_size):
+    # One request of a few heads with a long context: its query tiles leave
+    # most compute units idle, so their keys are split over workgroups and
+    # merged (log-sum-exp). Against the oracle, through both entries: causal
+    # attention over appended pages, and the fused append + attention.
+    case = prefill_case(80 + nq, batch=1, heads=2, dim=dim, page_size=page_size, nk=offset + nq, dtype=dtype,
+                        pages_per_slab=8)
+    run_prefill(case, nq, offset + nq, offset, seed=nq)
+    run_fused_single(case, nq, offset, seed=nq)
+
+
+def run_fused_single(case, n, offset, seed=0):
+    """mt_paged_prefill of one request on token-major fused QKV rows (the
+    kernel appends the K/V itself) against the oracle's append + attention:
+    pool image bit for bit, attention within tolerance."""
+    dtype, h, d = case.dtype, case.heads, case.dim
+    hd = h * d
+    rng = np.random.default_rng(seed)
+    qkv = po.encode(rng.standard_normal((1, n, 3 * hd), dtype=np.float32), CODES[dtype])
+    dev = DevicePagedCase(case)
+    fused = DeviceTensor(qkv.shape, dtype)
+    runtime().h2d(fused.ptr, qkv)
+    out = DeviceTensor((1, n, hd), dtype)
+    item = 4 if dtype == 'float32' else 2
+    paged_ops.paged_prefill(out.ptr, fused.ptr, fused.ptr + hd * item, fused.ptr + 2 * hd * item,
+                            dev.slab_table.ptr, dev.block_table.ptr, b=1, h=h, n=n, d=d, page_size=case.page_size,
+                            pages_per_slab=case.pages_per_slab, num_slabs=case.num_slabs, columns=case.columns,
+                            layer=case.layer, layers=case.layers, offset=offset, dtype=dtype,
+                            qkv_stride=3 * hd, out_stride=hd)
+    runtime().synchronize()
+    heads = lambda blk: np.ascontiguousarray(qkv[:, :, blk * hd:(blk + 1) * hd].reshape(1, n, h, d)
+                                             .transpose(0, 2, 1, 3))
+    image = case.image.copy()
+    po.image_append(image, case.table, case.columns, heads(1), heads(2), case.layer, offset=offset)
+    ref = po.image_paged_attention(image, CODES[dtype], case.table, case.columns, heads(0), case.layer,
+                                   offset, offset + n)
+    got = out.to_numpy().reshape(1, n, h, d).transpose(0, 2, 1, 3)
+    assert_attention_close(got, ref, dtype, context=f'fused n={n} offset={offset}')
+    assert np.array_equal(dev.pool_image().view(np.uint8), image.view(np.uint8)), 'append differs'
+
+
+def test_prefill_key_splits_with_missing_pages():
+    # holes inside the split key range: the queries that attend them are NaN,
+    # the others are not (the merge keeps a NaN denominator)
+    nq, offset = 900, 50
+    case = prefill_case(91, batch=1, heads=2, dim=64, page_size=16, nk=offset + nq, dtype='bfloat16',
+                        pages_per_slab=8)
+    case.table[0, 10] = -1          # keys 160..175
+    case.table[0, 40] = 10 ** 6     # keys 640..655
+    got, ref = run_prefill(case, nq, offset + nq, offset, seed=9)
+    assert np.isnan(ref[0, :, 160 - offset:]).all() and not np.isnan(ref[0, :, :160 - offset]).any()
