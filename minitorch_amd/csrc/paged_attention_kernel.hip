@@ -817,10 +817,15 @@ struct QueryArgs {
   // replaces a separate append.
   const void* k;
   const void* v;
-  // Key-split prefill: per (slot, head, query of the tile) max, denominator
-  // and D accumulators of one split's keys, merged by prefill_merge_kernel.
+  // Key-split prefill: per (slot, head, query of the tile) D accumulators,
+  // max and denominator of one split's keys, merged by prefill_merge_kernel.
   float* partials;
 };
+
+// Floats per query in the key-split partials: D accumulators, then max and
+// denominator, padded so every row starts 16-byte aligned.
+template <int D>
+constexpr int pf_part_row() { return D + 4; }
 
 // Causal paged attention for nq >= 1 queries per (request, head)
 // (reference paged_forward with offsets == nullptr, src/paged_attention_kernel.cu:35-85):
@@ -1279,12 +1284,11 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a, Items it
     if (q_ok && it.slot >= 0) {
       // A split of the tile's keys: (max, denominator, accumulators) in
       // base-2 units for prefill_merge_kernel.
-      float* part = a.partials + ((int64_t(it.slot) * g.heads + head) * kPfQueries + wave * 16 + col) * (D + 2);
+      float* part = a.partials + ((int64_t(it.slot) * g.heads + head) * kPfQueries + wave * 16 + col) * pf_part_row<D>();
 #pragma unroll
       for (int dt = 0; dt < DT16; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) part[2 + dt * 16 + 4 * grp + i] = o[dt][i];
-      if (grp == 0) { part[0] = m; part[1] = l; }
+        *reinterpret_cast<float4*>(part + dt * 16 + 4 * grp) = float4{o[dt][0], o[dt][1], o[dt][2], o[dt][3]};
+      if (grp == 0) *reinterpret_cast<float2*>(part + D) = float2{m, l};
     }
     // O^T lane layout: dims dt*16 + 4*grp + i of query qi.
     if (q_ok && it.slot < 0) {
@@ -1304,7 +1308,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(QueryArgs a, Items it
 // outputs from its splits' (max, denominator, accumulators) by the log-sum-exp
 // rule, with the finalize rule of the unsplit kernel (a NaN denominator stays
 // NaN, a zero one gives 0). One workgroup per (tile, head), four threads per
-// query, D/4 dims each.
+// query, each taking every fourth 16-byte chunk of the row; one online pass
+// over the splits, unrolled so that several splits' loads are in flight.
 struct PrefillMerge {
   int tiles;
   unsigned short tile[kSplitPairs], first_slot[kSplitPairs];
@@ -1314,32 +1319,48 @@ struct PrefillMerge {
 template <int DT, int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(QueryArgs a, PrefillMerge mg) {
   using T = typename Elem<DT>::T;
-  constexpr int DQ = D / 4;
+  constexpr int R = pf_part_row<D>(), C = D / 16;
   const int t = int(blockIdx.x / unsigned(a.g.heads));
   const int head = int(blockIdx.x - unsigned(t) * a.g.heads);
   if (t >= mg.tiles) return;
-  const int q = threadIdx.x >> 2, c0 = (threadIdx.x & 3) * DQ;
+  const int q = threadIdx.x >> 2, sub = threadIdx.x & 3;
   const int qi = mg.tile[t] * kPfQueries + q;
   if (qi >= a.nq) return;
   const int n = mg.splits[t];
-  auto part = [&](int s) {
-    return a.partials + ((int64_t(mg.first_slot[t] + s) * a.g.heads + head) * kPfQueries + q) * (D + 2);
-  };
-  float M = -INFINITY;
-  for (int s = 0; s < n; ++s) M = fmaxf(M, part(s)[0]);
-  float L = 0.f, acc[DQ];
+  const float* base = a.partials + ((int64_t(mg.first_slot[t]) * a.g.heads + head) * kPfQueries + q) * R;
+  const int64_t step = int64_t(a.g.heads) * kPfQueries * R;
+  float M = -INFINITY, L = 0.f;
+  float4 acc[C];
 #pragma unroll
-  for (int j = 0; j < DQ; ++j) acc[j] = 0.f;
+  for (int c = 0; c < C; ++c) acc[c] = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
   for (int s = 0; s < n; ++s) {
-    const float* p = part(s);
-    const float w = p[0] == -INFINITY ? 0.f : fast_exp2(p[0] - M);
-    L = fmaf(p[1], w, L);  // a NaN denominator (missing page) poisons the sum
+    const float* p = base + s * step;
+    const float2 ml = *reinterpret_cast<const float2*>(p + D);
+    float4 x[C];
 #pragma unroll
-    for (int j = 0; j < DQ; ++j) acc[j] = fmaf(p[2 + c0 + j], w, acc[j]);
+    for (int c = 0; c < C; ++c) x[c] = *reinterpret_cast<const float4*>(p + 4 * (sub + 4 * c));
+    const float Mn = fmaxf(M, ml.x);
+    const float wo = M == -INFINITY ? 0.f : fast_exp2(M - Mn);
+    const float wn = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - Mn);
+    L = fmaf(L, wo, ml.y * wn);  // a NaN denominator (missing page) poisons the sum
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      acc[c].x = fmaf(acc[c].x, wo, x[c].x * wn);
+      acc[c].y = fmaf(acc[c].y, wo, x[c].y * wn);
+      acc[c].z = fmaf(acc[c].z, wo, x[c].z * wn);
+      acc[c].w = fmaf(acc[c].w, wo, x[c].w * wn);
+    }
+    M = Mn;
   }
-  T* orow = static_cast<T*>(a.out) + head * a.o_h + int64_t(qi) * a.o_r + c0;
+  T* orow = static_cast<T*>(a.out) + head * a.o_h + int64_t(qi) * a.o_r;
 #pragma unroll
-  for (int j = 0; j < DQ; ++j) orow[j] = from_f32<DT>(finalize(acc[j], L));
+  for (int c = 0; c < C; ++c) {
+    const T r0 = from_f32<DT>(finalize(acc[c].x, L)), r1 = from_f32<DT>(finalize(acc[c].y, L));
+    const T r2 = from_f32<DT>(finalize(acc[c].z, L)), r3 = from_f32<DT>(finalize(acc[c].w, L));
+    *reinterpret_cast<uint2*>(orow + 4 * (sub + 4 * c)) =
+        uint2{uint32_t(r0) | (uint32_t(r1) << 16), uint32_t(r2) | (uint32_t(r3) << 16)};
+  }
 }
 
 // Multi-token append at a common offset (reference paged_append with
@@ -1625,7 +1646,7 @@ hipError_t launch_split_prefill(QueryArgs& a, int dtype) {
   if (mg.tiles == 0) return hipErrorNotSupported;
   it.pairs = pairs;
   void* ws = nullptr;
-  const int e = library_workspace(size_t(slots) * h * kPfQueries * (d + 2) * sizeof(float), &ws);
+  const int e = library_workspace(size_t(slots) * h * kPfQueries * (d + 4) * sizeof(float), &ws);
   if (e != hipSuccess) return hipError_t(e);
   a.partials = static_cast<float*>(ws);
   const int blocks = grid_for(int64_t(pairs) * h);
