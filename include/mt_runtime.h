@@ -52,6 +52,28 @@ int mt_host_alloc(void** p, size_t bytes);
 int mt_host_free(void* p);
 /* p[0:n] = v (fp32). Replaces reference mt_fill (src/cuda_runtime.cu:54-57). */
 int mt_fill(float* p, int n, float v);
+/* p[0:n] uniform in [0, 1), a deterministic function of (seed, index): the
+ * SplitMix64 output function of seed * 0x9E3779B97F4A7C15 + index, top 24
+ * bits. Same range and contract as the reference, not cuRAND's Philox stream.
+ * Replaces reference mt_random (src/cuda_runtime.cu:37-44,58-61). */
+int mt_random(float* p, int n, unsigned long long seed);
+/* out[i] = 1 if i % classes == (int)ids[i / classes] else 0, i < size (the
+ * id truncated toward zero; NaN reads as 0, out-of-range ids saturate).
+ * Replaces reference mt_one_hot (src/cuda_runtime.cu:45-48,62-65). */
+int mt_one_hot(float* out, const float* ids, int size, int classes);
+/* width == 0: out[i] = i; else out[i] = -3.402823466e38 if
+ * i % width > i / width, else 0 (causal mask rows).
+ * Replaces reference mt_sequence (src/cuda_runtime.cu:49-52,66-69). */
+int mt_sequence(float* out, int size, int width);
+/* hipBLASLt handle and row-major fp32 GEMM out[m,n] = a[m,k] @ b[k,n],
+ * forwarded to model_kernels.so (include/mt_model.h) found next to this
+ * library, so one handle serves both; hipErrorSharedObjectInitFailed (303)
+ * when that library is missing.
+ * Replace reference mt_blas_create / mt_blas_destroy / mt_gemm
+ * (src/cuda_runtime.cu:22-30). */
+int mt_blas_create(void** handle);
+int mt_blas_destroy(void* handle);
+int mt_gemm(void* handle, float* out, const float* a, const float* b, int m, int n, int k);
 /* Fill `words` 32-bit words with `value` by a kernel (graph-capturable,
  * unlike a memset node). No reference counterpart. */
 int mt_fill_words(void* p, size_t words, unsigned int value);

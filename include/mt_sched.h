@@ -77,18 +77,18 @@ int mt_pool_release_rows(MT_POOL_ARGS, const int* slots, int rows, int keep, int
  * `limit` pops); new_page[i] = that page or -1; offsets[i] = committed length;
  * positions[i] = (float)offsets[i]; cu_seqlens[0..b] = exclusive prefix sum
  * of offsets[i] + 1; table [b, columns] = each row's pages, -1 beyond them.
- * Replaces reference PagedDecodeBatch.prepare (minitorch/paged_decode.py:303-317). */
+ * Replaces reference PagedDecodeBatch.prepare (minitorch/paged_decode.py:40-54). */
 int mt_sched_decode_prepare(MT_POOL_ARGS, const int* slots, int b, int columns, int page_size,
                             int limit, int* table, int* offsets, float* positions,
                             int* cu_seqlens, int* new_page);
 
 /* lengths[slots[i]] += tokens. Replaces the length update of reference
- * CacheBase.commit_append (minitorch/kv_cache.py:343-348). */
+ * CacheBase.commit_append (minitorch/kv_cache.py:142-147). */
 int mt_sched_add_length(MT_POOL_ARGS, const int* slots, int b, int tokens);
 
 /* Return the pages taken by mt_sched_decode_prepare (new_page >= 0), in row
  * order. Replaces reference PagedDecodeBatch.__exit__'s aborts
- * (minitorch/paged_decode.py:351-353). */
+ * (minitorch/paged_decode.py:88-90). */
 int mt_sched_decode_abort(MT_POOL_ARGS, const int* slots, int b, const int* new_page);
 
 #undef MT_POOL_ARGS

@@ -4,7 +4,11 @@
 // otherwise the hipError_t value, whose numbering matches the CUDA codes the
 // reference's Python checks: 1 = invalid value, 2 = out of memory).
 #include <hip/hip_runtime.h>
+#include <dlfcn.h>
+#include <climits>
 #include <cstdint>
+#include <mutex>
+#include <string>
 
 namespace {
 
@@ -43,9 +47,66 @@ __global__ __launch_bounds__(256) void fill_random_kernel(void* out, int64_t n, 
   }
 }
 
+// Uniform float in [0, 1) from (seed, index): the SplitMix64 output function
+// (Steele, Lea and Flood, "Fast splittable pseudorandom number generators",
+// OOPSLA 2014) applied to seed * golden-ratio increment + index, top 24 bits.
+// This is this library's own stream; it is not cuRAND's Philox sequence.
+__device__ __forceinline__ float unit_uniform(unsigned long long seed, unsigned long long i) {
+  unsigned long long z = seed * 0x9E3779B97F4A7C15ull + i;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return float(z >> 40) * (1.0f / 16777216.0f);
+}
+
+__global__ __launch_bounds__(256) void random_kernel(float* out, int64_t n, unsigned long long seed) {
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+    out[i] = unit_uniform(seed, (unsigned long long)i);
+}
+
+// float -> int as a truncating hardware conversion does it: NaN gives 0,
+// values beyond the int range saturate.
+__device__ __forceinline__ int to_int_saturating(float f) {
+  if (isnan(f)) return 0;
+  if (f >= 2147483648.0f) return INT_MAX;
+  if (f <= -2147483648.0f) return INT_MIN;
+  return int(f);
+}
+
+__global__ __launch_bounds__(256) void one_hot_kernel(float* out, const float* ids, int64_t size, int classes) {
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < size; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t row = i / classes;
+    out[i] = int64_t(to_int_saturating(ids[row])) == i - row * classes ? 1.f : 0.f;
+  }
+}
+
+__global__ __launch_bounds__(256) void sequence_kernel(float* out, int64_t size, int width) {
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < size; i += int64_t(gridDim.x) * blockDim.x) {
+    if (width) out[i] = (i % width > i / width) ? -3.402823466e38f : 0.f;
+    else out[i] = float(i);
+  }
+}
+
 int blocks_for(int64_t n) {
   const int64_t b = (n + 255) / 256;
   return int(b < (1 << 20) ? b : (1 << 20));
+}
+
+// The hipBLASLt handle and GEMM live in model_kernels.so (built next to this
+// library); the runtime's BLAS symbols forward to it, so a handle created
+// through either library is valid for both.
+void* blas_symbol(const char* name) {
+  static std::once_flag once;
+  static void* lib = nullptr;
+  std::call_once(once, [] {
+    Dl_info info{};
+    if (!dladdr(reinterpret_cast<void*>(&blas_symbol), &info) || !info.dli_fname) return;
+    std::string path(info.dli_fname);
+    const size_t slash = path.rfind('/');
+    path = (slash == std::string::npos ? std::string(".") : path.substr(0, slash)) + "/model_kernels.so";
+    lib = dlopen(path.c_str(), RTLD_NOW | RTLD_LOCAL);
+  });
+  return lib ? dlsym(lib, name) : nullptr;
 }
 
 }  // namespace
@@ -91,6 +152,51 @@ int mt_fill(float* p, int n, float v) {
   if (n < 0) return hipErrorInvalidValue;
   if (n) fill_kernel<<<blocks_for(n), 256>>>(p, n, v);
   return hipGetLastError();
+}
+
+// out[0:n] uniform in [0, 1) from `seed` (reference mt_random,
+// src/cuda_runtime.cu:37-44,58-61). Deterministic per (seed, index); the
+// stream is this library's own, not cuRAND's.
+int mt_random(float* p, int n, unsigned long long seed) {
+  if (n < 0 || (!p && n)) return hipErrorInvalidValue;
+  if (n) random_kernel<<<blocks_for(n), 256>>>(p, n, seed);
+  return hipGetLastError();
+}
+
+// out[i] = 1 where i % classes == int(ids[i / classes]), else 0, for `size`
+// outputs (reference mt_one_hot, src/cuda_runtime.cu:45-48,62-65).
+int mt_one_hot(float* out, const float* ids, int size, int classes) {
+  if (size < 0 || (size && (!out || !ids || classes < 1))) return hipErrorInvalidValue;
+  if (size) one_hot_kernel<<<blocks_for(size), 256>>>(out, ids, size, classes);
+  return hipGetLastError();
+}
+
+// width == 0: out[i] = i; else the causal mask of rows of `width`:
+// -3.402823466e38 where i % width > i / width, else 0 (reference
+// mt_sequence, src/cuda_runtime.cu:49-52,66-69).
+int mt_sequence(float* out, int size, int width) {
+  if (size < 0 || width < 0 || (!out && size)) return hipErrorInvalidValue;
+  if (size) sequence_kernel<<<blocks_for(size), 256>>>(out, size, width);
+  return hipGetLastError();
+}
+
+// Replace reference mt_blas_create / mt_blas_destroy / mt_gemm
+// (src/cuda_runtime.cu:22-30): forwarded to model_kernels.so's hipBLASLt
+// implementation. hipErrorSharedObjectInitFailed if that library is absent.
+int mt_blas_create(void** handle) {
+  auto f = reinterpret_cast<int (*)(void**)>(blas_symbol("mt_blas_create"));
+  return f ? f(handle) : hipErrorSharedObjectInitFailed;
+}
+
+int mt_blas_destroy(void* handle) {
+  auto f = reinterpret_cast<int (*)(void*)>(blas_symbol("mt_blas_destroy"));
+  return f ? f(handle) : hipErrorSharedObjectInitFailed;
+}
+
+int mt_gemm(void* handle, float* out, const float* a, const float* b, int m, int n, int k) {
+  auto f = reinterpret_cast<int (*)(void*, float*, const float*, const float*, int, int, int)>(
+      blas_symbol("mt_gemm"));
+  return f ? f(handle, out, a, b, m, n, k) : hipErrorSharedObjectInitFailed;
 }
 
 // Fill `words` 32-bit words with a bit pattern: a small kernel rather than a

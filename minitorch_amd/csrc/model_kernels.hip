@@ -575,7 +575,7 @@ hipError_t gather_rows(void* out, const void* in, const int* rows, int count, si
   if (row_bytes % 4) return hipErrorInvalidValue;
   const int64_t words = int64_t(row_bytes / 4);
   for (int c0 = 0; c0 < count; c0 += kGatherRows) {
-    GatherRows g;
+    GatherRows g{};
     g.count = count - c0 < kGatherRows ? count - c0 : kGatherRows;
     for (int i = 0; i < g.count; ++i) g.row[i] = rows[c0 + i];
     const dim3 grid(unsigned((words + 255) / 256), unsigned(g.count));

@@ -1410,7 +1410,7 @@ bool paged_shape(int b, int h, int nq, int nk, int d, int page_size, int pps, in
 }
 
 Geometry make_geometry(int h, int d, int page_size, int pps, int num_slabs, int columns, int layer) {
-  Geometry g;
+  Geometry g{};
   g.heads = h; g.dim = d; g.page_size = page_size;
   g.log2_page = page_size == 8 ? 3 : page_size == 16 ? 4 : 5;
   g.pps = pps; g.num_slabs = num_slabs; g.columns = columns; g.layer = layer;
@@ -1441,6 +1441,21 @@ int choose_split(int64_t cap, int requested) {
 size_t workspace_bytes_for(int64_t bh, int nsplit_max) {
   // (max, denominator, accumulator[128]) per (row, head, split)
   return size_t(bh) * nsplit_max * (128 + 2) * sizeof(float);
+}
+
+// Whether the decode runs its 16-byte-load kernel for these operands.
+bool decode_vec(int d, int dtype, const void* out, const void* q, const void* k, const void* v,
+                int64_t qkv_stride) {
+  return (d == 64 || d == 128) && aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v) &&
+         (qkv_stride * (dtype == kF32 ? 4 : 2)) % 16 == 0;
+}
+
+// Bytes of split partials a decode launch writes: (max, denominator,
+// accumulator[D]) per (row, head, split), D being the kernel's head-dim
+// template (64 for the 16-byte kernel at d = 64, else 128).
+size_t partial_bytes(int64_t bh, int64_t nsplit_max, bool vec, int d) {
+  const int dt = (vec && d == 64) ? 64 : 128;
+  return size_t(bh) * size_t(nsplit_max) * size_t(dt + 2) * sizeof(float);
 }
 
 // Compute units of the current device (cached per device).
@@ -1525,29 +1540,36 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
                work_items > int64_t(b) * nsplit_max))
     return hipErrorInvalidValue;
   if (work && work_items == 0) return hipSuccess;
-  if (nsplit_max > 1 && (!workspace || workspace_bytes < workspace_bytes_for(bh, int(nsplit_max))))
+  const int64_t stride = qkv_stride ? qkv_stride : int64_t(h) * d;
+  const bool vec = decode_vec(d, dtype, out, q, k, v, stride);
+  if (nsplit_max > 1 && (!workspace || workspace_bytes < partial_bytes(bh, nsplit_max, vec, d)))
     return hipErrorInvalidValue;
-  DecodeArgs a;
+  DecodeArgs a{};
   a.out = out; a.q = q; a.k = k; a.v = v; a.slabs = slabs; a.table = table; a.offsets = offsets;
   a.batch = b; a.split_tokens = S; a.nsplit_max = int(nsplit_max);
   a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
   a.items = work ? int64_t(work_items) * h : bh * nsplit_max;
   a.g = make_geometry(h, d, page_size, pps, num_slabs, columns, layer);
   a.partials = static_cast<float*>(workspace);
-  a.qkv_stride = qkv_stride ? qkv_stride : int64_t(h) * d;
+  a.qkv_stride = stride;
   a.work = work;
   a.work_items = work ? work_items : 0;
   a.merge_rows = work ? merge_rows : 0;
-  const bool vec = (d == 64 || d == 128) && aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v) &&
-                   (a.qkv_stride * (dtype == kF32 ? 4 : 2)) % 16 == 0;
   if (dtype == kF32) return launch_decode_dt<kF32>(a, a.items, vec, d, unroll, waves);
   if (dtype == kF16) return launch_decode_dt<kF16>(a, a.items, vec, d, unroll, waves);
   if (dtype == kBF16) return launch_decode_dt<kBF16>(a, a.items, vec, d, unroll, waves);
   return hipErrorInvalidValue;
 }
 
-// Library-owned decode workspace for the reference entry point, which has no
-// workspace argument: grown on demand, kept per device until the process ends.
+// Library-owned split workspace of the reference entry points, which have no
+// workspace argument (mt_paged_decode_batch for tables longer than one split,
+// the key-split prefill of mt_paged_attention / mt_paged_prefill). One buffer
+// per device, kept until the process ends. It grows stream-ordered on the
+// null stream, where every launch of this library runs: hipMallocAsync for
+// the larger buffer and hipFreeAsync for the old one, which is released only
+// after the work queued before it, so growing neither synchronizes the device
+// nor blocks the host. Callers that cannot allocate use mt_paged_decode_split
+// with their own workspace.
 std::mutex g_ws_mutex;
 std::vector<std::pair<void*, size_t>> g_ws;
 
@@ -1559,14 +1581,16 @@ int library_workspace(size_t bytes, void** out) {
   if (g_ws.size() <= size_t(dev)) g_ws.resize(dev + 1, {nullptr, 0});
   auto& slot = g_ws[dev];
   if (slot.second < bytes) {
-    if (slot.first) {
-      e = hipFree(slot.first);  // synchronizes the device before release
-      if (e != hipSuccess) return e;
-      slot = {nullptr, 0};
-    }
     void* p = nullptr;
-    e = hipMalloc(&p, bytes);
-    if (e != hipSuccess) return e;
+    e = hipMallocAsync(&p, bytes, nullptr);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();  // the caller reports the status; keep it off the next launch
+      return e;
+    }
+    if (slot.first) {
+      e = hipFreeAsync(slot.first, nullptr);
+      if (e != hipSuccess) return e;
+    }
     slot = {p, bytes};
   }
   *out = slot.first;
@@ -1646,8 +1670,9 @@ hipError_t launch_split_prefill(QueryArgs& a, int dtype) {
   if (mg.tiles == 0) return hipErrorNotSupported;
   it.pairs = pairs;
   void* ws = nullptr;
-  const int e = library_workspace(size_t(slots) * h * kPfQueries * (d + 4) * sizeof(float), &ws);
-  if (e != hipSuccess) return hipError_t(e);
+  // Without room for the partials the prompt runs unsplit.
+  if (library_workspace(size_t(slots) * h * kPfQueries * (d + 4) * sizeof(float), &ws) != hipSuccess)
+    return hipErrorNotSupported;
   a.partials = static_cast<float*>(ws);
   const int blocks = grid_for(int64_t(pairs) * h);
 #define MT_SPLIT(DT, D)                                                                        \
@@ -1721,7 +1746,7 @@ int mt_paged_append(const void* k, const void* v, const uint64_t* slabs, const i
                    layers, offset))
     return hipErrorInvalidValue;
   if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
-  AppendArgs a;
+  AppendArgs a{};
   a.k = k; a.v = v; a.slabs = slabs; a.table = table; a.batch = b; a.n = n; a.offset = offset;
   a.g = make_geometry(h, d, page_size, pages_per_slab, num_slabs, columns, layer);
   a.src_b = int64_t(h) * n * d; a.src_h = int64_t(n) * d; a.src_r = d;
@@ -1772,7 +1797,7 @@ int mt_paged_prefill(void* out, const void* q, const void* k, const void* v, con
     a.k = k; a.v = v;
     return launch_query(a, dtype);
   }
-  AppendArgs ap;
+  AppendArgs ap{};
   ap.k = k; ap.v = v; ap.slabs = slabs; ap.table = table; ap.batch = b; ap.n = n; ap.offset = offset;
   ap.g = a.g;
   ap.src_b = int64_t(n) * qkv_stride; ap.src_h = d; ap.src_r = qkv_stride;

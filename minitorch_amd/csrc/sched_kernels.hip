@@ -2,7 +2,7 @@
 //
 // The reference keeps the page free list, per-cache page lists, block tables
 // and decode offsets on the host and uploads them every step
-// (minitorch/paged_kv_cache.py:71-103,171-189; minitorch/paged_decode.py:303-317).
+// (minitorch/paged_kv_cache.py:71-103,171-189; minitorch/paged_decode.py:40-54).
 // Here they live in one device "pool state" blob and are updated by small
 // single-workgroup kernels on the null stream, so admitting, stepping and
 // finishing requests never reads device memory back. Page IDs follow the
@@ -13,7 +13,7 @@
 //     of the older free pages, then all `count` pages are popped
 //     (paged_kv_cache.py:78-89) -- "bulk" pops, used by prepare_append(n);
 //   * a decode step acquires one page per row that needs it, row by row, each
-//     as its own pop of one page (paged_decode.py:307-309 calling
+//     as its own pop of one page (paged_decode.py:44-46 calling
 //     paged_kv_cache.py:171-186) -- "sequential" pops;
 //   * releases push pages in the given order (paged_kv_cache.py:96-103).
 // The state blob layout is computed by pool_layout() and exported through
@@ -40,7 +40,7 @@ struct Layout {
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 Layout pool_layout(int max_pages, int max_slabs, int max_slots, int max_cols) {
-  Layout l;
+  Layout l{};
   size_t o = 0;
   l.header = o; o = align256(o + sizeof(Header));
   l.stack = o; o = align256(o + size_t(max_pages) * 4);
@@ -71,7 +71,7 @@ Pool make_pool(void* state, int max_pages, int max_slabs, int max_slots, int max
                unsigned long long pool_base, unsigned long long slab_bytes) {
   const Layout l = pool_layout(max_pages, max_slabs, max_slots, max_cols);
   char* s = static_cast<char*>(state);
-  Pool p;
+  Pool p{};
   p.h = reinterpret_cast<Header*>(s + l.header);
   p.stack = reinterpret_cast<int*>(s + l.stack);
   p.issued = reinterpret_cast<unsigned*>(s + l.issued);

@@ -126,7 +126,7 @@ class PagedDecodeBatch:
         self.cu_seqlens = _DeviceView(ws.buffer, int(ws.offsets[4]), 4 * (b + 1))
         self.work = _DeviceView(ws.buffer, int(ws.offsets[1]), 4 * len(work))
         self.position_ids = DeviceTensor((b, 1), 'float32', buffer=ws.buffer, byte_offset=int(ws.offsets[3]))
-        # Host half, row by row like the reference (paged_decode.py:307-309):
+        # Host half, row by row like the reference (paged_decode.py:44-46):
         # the row whose page would exceed the budget raises MemoryError.
         pops = 0
         for cache, need in zip(self.caches, needs):

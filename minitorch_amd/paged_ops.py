@@ -1,7 +1,7 @@
 """Thin Python wrappers over the paged-attention and token-I/O C-ABI.
 
 Argument order and meaning follow the reference's ctypes call sites
-(minitorch/paged_kv_cache.py:205-221, minitorch/paged_decode.py:328-332,
+(minitorch/paged_kv_cache.py:205-221, minitorch/paged_decode.py:65-69,
 minitorch/kv_cache.py:35,52, minitorch/pretrained_gpt2.py:30-31). Every call
 goes to ``cuda_kernels/paged_attention_kernel.so`` or
 ``cuda_kernels/inference_kernels.so``.

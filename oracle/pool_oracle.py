@@ -14,7 +14,7 @@ Followed line by line:
   (:171-189), abort releasing only the new pages (:228-234), close releasing
   every row's pages row by row (:125-131);
 * PagedDecodeBatch.prepare: offsets, columns and the [B, columns] table
-  (minitorch/paged_decode.py:296-317);
+  (minitorch/paged_decode.py:17-54);
 * ContinuousBatcher: submit (minitorch/continuous_batching.py:84-106),
   decode-before-admit step with FIFO head-of-line blocking, the
   prefill_token_budget exemption of the first prefill, reserved-page
@@ -152,7 +152,7 @@ class CacheOracle:
 def decode_batch_metadata(caches):
     """PagedDecodeBatch metadata for batch-1 caches in batch order:
     (offsets, columns, table [B][columns]) after every cache's prepare_append(1)
-    (minitorch/paged_decode.py:296-317). Mutates the caches' page lists."""
+    (minitorch/paged_decode.py:17-54). Mutates the caches' page lists."""
     page_size = caches[0].pool.page_size
     offsets = [c.length for c in caches]
     columns = max((c.length + 1 + page_size - 1) // page_size for c in caches)

@@ -150,6 +150,54 @@ def test_error_strings():
     assert lib.mt_error(1)
 
 
+# The reference's CudaRuntime binds exactly these names from cuda_runtime.so
+# (minitorch/cuda_storage.py:29-40), then mt_error (:41-42), and calls
+# mt_blas_create at start-up (:43-45).
+REFERENCE_RUNTIME_SIGNATURES = {
+    'mt_malloc': [ct.POINTER(P), Z], 'mt_free': [P],
+    'mt_copy': [P, P, Z, I], 'mt_sync': [], 'mt_fill': [P, I, ct.c_float],
+    'mt_random': [P, I, ct.c_ulonglong], 'mt_one_hot': [P, P, I, I],
+    'mt_sequence': [P, I, I], 'mt_blas_create': [ct.POINTER(P)],
+    'mt_blas_destroy': [P], 'mt_gemm': [P, P, P, P, I, I, I],
+    'mt_event_create': [ct.POINTER(P)], 'mt_event_record': [P],
+    'mt_event_elapsed': [ct.POINTER(ct.c_float), P, P], 'mt_event_destroy': [P],
+}
+
+
+def test_runtime_binds_the_reference_signature_table():
+    # The reference's binding loop, run against a fresh handle of this build's
+    # cuda_runtime.so: every getattr succeeds and each symbol is a function of
+    # this library (not only reachable through another one).
+    lib = ct.CDLL(str(ROOT / 'minitorch_amd' / 'cuda_kernels' / 'cuda_runtime.so'))
+    for name, args in REFERENCE_RUNTIME_SIGNATURES.items():
+        f = getattr(lib, name)
+        f.argtypes, f.restype = args, I
+    lib.mt_error.argtypes, lib.mt_error.restype = [I], ct.c_char_p
+    out = subprocess.run(['nm', '-D', '--defined-only',
+                          str(ROOT / 'minitorch_amd' / 'cuda_kernels' / 'cuda_runtime.so')],
+                         capture_output=True, text=True, check=True).stdout
+    defined = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = sorted(set(REFERENCE_RUNTIME_SIGNATURES) - defined)
+    assert not missing, missing
+
+
+def test_runtime_generators_reject_invalid_arguments():
+    # Host-side checks only (no launch reaches a device).
+    lib = library('cuda_runtime')
+    for name, args in REFERENCE_RUNTIME_SIGNATURES.items():
+        f = getattr(lib, name)
+        f.argtypes, f.restype = args, I
+    assert lib.mt_random(None, -1, 0) == 1
+    assert lib.mt_random(None, 4, 0) == 1
+    assert lib.mt_one_hot(8, 8, -1, 3) == 1
+    assert lib.mt_one_hot(8, 8, 6, 0) == 1
+    assert lib.mt_one_hot(8, None, 6, 3) == 1
+    assert lib.mt_sequence(8, -1, 0) == 1
+    assert lib.mt_sequence(8, 4, -2) == 1
+    assert lib.mt_sequence(None, 4, 2) == 1
+    assert lib.mt_gemm(None, 8, 8, 8, 1, 1, 1) == 1
+
+
 def test_paged_prefill_rejects_invalid_arguments():
     lib = library('paged_attention_kernel')
     f = lib.mt_paged_prefill

@@ -103,7 +103,7 @@ def test_cache_prepare_distributes_one_acquire_over_rows():
 
 
 def test_decode_metadata_hand_example():
-    # paged_decode.py:296-317: offsets = lengths, columns = max ceil((len+1)/P),
+    # paged_decode.py:17-54: offsets = lengths, columns = max ceil((len+1)/P),
     # each cache prepare_append(1) in batch order, table padded with -1.
     p = PoolOracle(page_bytes=PAGE, max_bytes=100 * PAGE, page_size=16, pages_per_slab=4)
     caches = []

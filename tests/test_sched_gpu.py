@@ -262,7 +262,7 @@ def test_decode_budget_exhaustion_aborts_like_reference():
 
 def decode_batch_metadata_with_abort(caches):
     """Reference PagedDecodeBatch.prepare + __exit__ on failure
-    (minitorch/paged_decode.py:303-309,351-353)."""
+    (minitorch/paged_decode.py:44-46,88-90)."""
     prepared = []
     try:
         for c in caches:
