@@ -40,8 +40,10 @@ int mt_paged_attention(void* out, const void* q, const uint64_t* slabs, const in
  * committed lengths. Appends k/v at position offsets[i] of request i, then
  * attends its offsets[i] + 1 keys. One fused append + attention launch, plus
  * a split-reduction launch when the table is longer than one context split;
- * the split partials live in a library-owned device workspace (allocated on
- * first need, grown on demand, kept until the process ends).
+ * the split partials live in a library-owned device workspace, one per
+ * device, kept until the process ends and grown stream-ordered on the null
+ * stream (hipMallocAsync / hipFreeAsync, no device synchronization) when a
+ * table needs more; status 2 if it cannot grow.
  * Replaces reference mt_paged_decode_batch (src/paged_attention_kernel.cu:121-137). */
 int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v,
                           const uint64_t* slabs, const int* table, const int* offsets, int b,
