@@ -50,6 +50,31 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
                           int h, int d, int page_size, int pages_per_slab, int num_slabs,
                           int columns, int layer, int layers, int dtype);
 
+/* Bytes of device memory mt_paged_decode_batch_noalloc keeps for split
+ * partials: a fixed array in the library, one copy per device, held until
+ * the process ends. */
+#define MT_PAGED_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* mt_paged_decode_batch that allocates nothing: same arguments, kernels and
+ * results, but the split partials of tables longer than one split (1024
+ * tokens) live in the library's fixed device array of
+ * MT_PAGED_NOALLOC_SCRATCH_BYTES instead of a workspace that may grow. It
+ * returns 1 (invalid value) before any launch when the partials,
+ * b * h * ceil(columns * page_size / split) * (d' + 2) * 4 bytes (d' = 64 for
+ * 16-byte-aligned operands at d = 64, else 128), exceed that size; tables of
+ * at most 1024 tokens need none (mt_paged_decode_workspace_bytes with
+ * split_tokens 0 gives an upper bound). Calls on one device share the array: calls
+ * that overlap (different streams) race; calls in stream order do not. The
+ * first call on a device looks the array's device address up
+ * (hipGetSymbolAddress) and keeps it; no call allocates or frees.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops and harnesses
+ * that forbid hipMalloc). */
+int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const void* v,
+                                  const uint64_t* slabs, const int* table, const int* offsets,
+                                  int b, int h, int d, int page_size, int pages_per_slab,
+                                  int num_slabs, int columns, int layer, int layers, int dtype);
+
 /* Bytes of workspace mt_paged_decode_split needs (0 when no row can be split).
  * split_tokens = 0 selects the automatic split length.
  * No reference counterpart: the split-context reduction is new in this build. */

@@ -1597,6 +1597,40 @@ int library_workspace(size_t bytes, void** out) {
   return hipSuccess;
 }
 
+// Split partials of mt_paged_decode_batch_noalloc: a fixed device array, so
+// that entry point allocates nothing. Every call on a device shares that
+// device's copy. The decode writes every partial of a split row before the
+// merge reads it, so nothing carries over between calls and nothing needs
+// clearing; calls that overlap on one device (other streams) would race.
+}  // namespace
+
+static __device__ __align__(256) float scratch[MT_PAGED_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = MT_PAGED_NOALLOC_SCRATCH_BYTES;
+
+// Device address of `scratch` on the current device, looked up once per
+// device (the host-side name of the array is not a device address).
+int scratch_address(void** out) {
+  static std::mutex mutex;
+  static std::vector<void*> addresses;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mutex);
+  if (addresses.size() <= size_t(dev)) addresses.resize(dev + 1, nullptr);
+  if (!addresses[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    addresses[dev] = p;
+  }
+  *out = addresses[dev];
+  return hipSuccess;
+}
+
 // Launch of the append kernel for any source strides; the 16-byte path needs
 // 16-byte aligned rows.
 hipError_t launch_append(AppendArgs& a, int dtype) {
@@ -1944,6 +1978,32 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, S, 0, kDefaultWaves, 0,
                        nullptr, 0, 0, ws, ws_bytes);
+}
+
+int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const void* v,
+                                  const uint64_t* slabs, const int* table, const int* offsets,
+                                  int b, int h, int d, int page_size, int pages_per_slab,
+                                  int num_slabs, int columns, int layer, int layers, int dtype) {
+  if (!out || !q || !k || !v || !slabs || !table || !offsets ||
+      !paged_shape(b, h, 1, 1, d, page_size, pages_per_slab, num_slabs, columns, layer, layers, 0) ||
+      int64_t(columns) * page_size > INT32_MAX)
+    return hipErrorInvalidValue;
+  if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
+  const int64_t cap = int64_t(columns) * page_size;
+  const int S = choose_split(cap, 0);
+  const int64_t nsplit_max = (cap + S - 1) / S;
+  void* ws = nullptr;
+  if (nsplit_max > 1) {
+    // Split partials beyond the fixed array are refused, before any launch.
+    const bool vec = decode_vec(d, dtype, out, q, k, v, int64_t(h) * d);
+    if (partial_bytes(int64_t(b) * h, nsplit_max, vec, d) > kNoAllocScratchBytes)
+      return hipErrorInvalidValue;
+    const int e = scratch_address(&ws);
+    if (e != hipSuccess) return e;
+  }
+  return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
+                       num_slabs, columns, layer, layers, dtype, S, 0, kDefaultWaves, 0,
+                       nullptr, 0, 0, ws, nsplit_max > 1 ? kNoAllocScratchBytes : 0);
 }
 
 int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, int split_tokens,
