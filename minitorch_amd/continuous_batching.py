@@ -168,6 +168,14 @@ class ContinuousBatcher:
             if request.eos_token_id is None and request.generated >= request.max_new_tokens:
                 self._finish(request, 'completed', 'length')
 
+    @staticmethod
+    def _ended_early(request):
+        """Ended by cancel, an early finish or a failure rather than by its own
+        tokens: nothing is delivered to it afterwards, as the reference emits
+        nothing after a cancel (minitorch/continuous_batching.py:117-122)."""
+        return request.state in ('cancelled', 'failed') or (
+            request.state == 'completed' and request.finish_reason not in ('length', 'eos'))
+
     def _drain(self, keep=0, block=True):
         """Deliver arrived tokens in issue order, leaving ``keep`` read-backs
         in flight; without ``block`` only those already complete."""
@@ -180,6 +188,8 @@ class ContinuousBatcher:
             self._inflight.popleft()
             arrival = self.clock()
             for request, token in zip(requests, tokens):
+                if self._ended_early(request):
+                    continue  # cancelled, finished or failed while the token was in flight
                 finish = request.eos_token_id is not None
                 events.append(self._deliver(request, int(token), arrival, finish))
         return events

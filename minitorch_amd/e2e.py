@@ -13,6 +13,7 @@ with a seeded 5 % probability (or when it reaches its capacity) by a fresh
 prefilled one, exercising page free/reuse. Decode tokens/s counts decode
 steps only.
 """
+import math
 import time
 import numpy as np
 
@@ -37,6 +38,15 @@ def config3_trace(seed=0, requests=256, rate=32.0, vocab=50257, n_positions=1024
         new = int(min(rng.geometric(1.0 / 128), n_positions - n + 1))
         out.append((float(arrivals[i]), f'r{i}', prompt, new))
     return out
+
+
+def config3_step_trace(seed=0, step_seconds=1e-3, **kwargs):
+    """``config3_trace`` on a step-indexed clock: one scheduler step stands for
+    ``step_seconds`` and an arrival at t seconds becomes step
+    floor(t / step_seconds). Replaying it submits request i just before that
+    step runs, so decisions do not depend on wall-clock timing."""
+    return [(int(math.floor(a / step_seconds)), rid, prompt, new)
+            for a, rid, prompt, new in config3_trace(seed, **kwargs)]
 
 
 def _progress(message):

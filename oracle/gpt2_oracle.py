@@ -136,6 +136,32 @@ def decode_step(state, caches, ids, *, n_head, n_layer, eps=1e-5, dtype=np.float
     return x @ g['transformer.wte.weight'].T
 
 
+def greedy_cached(state, prompts, steps, *, n_head, n_layer, eps=1e-5, dtype=np.float64):
+    """``greedy`` for several prompts at once through ``prefill_cache`` and
+    batched ``decode_step`` (each row's math is the full forward's, so the
+    tokens equal ``greedy``'s): ``steps[i]`` tokens after ``prompts[i]``.
+    Returns (tokens, margins), one list per prompt."""
+    g = _cast(state, dtype)
+    caches, out, margins = [], [], []
+    for prompt, n in zip(prompts, steps):
+        cache, last = prefill_cache(g, prompt, n_head=n_head, n_layer=n_layer, capacity=len(prompt) + n,
+                                    eps=eps, dtype=dtype)
+        top = np.argsort(last)[-2:]
+        caches.append(cache)
+        out.append([int(np.argmax(last))])
+        margins.append([float(last[top[1]] - last[top[0]])])
+    while True:
+        rows = [i for i, n in enumerate(steps) if len(out[i]) < n]
+        if not rows:
+            return out, margins
+        logits = decode_step(g, [caches[i] for i in rows], [out[i][-1] for i in rows], n_head=n_head,
+                             n_layer=n_layer, eps=eps, dtype=dtype)
+        for i, row in zip(rows, logits):
+            top = np.argsort(row)[-2:]
+            out[i].append(int(np.argmax(row)))
+            margins[i].append(float(row[top[1]] - row[top[0]]))
+
+
 def _cast(state, dtype):
     if all(np.asarray(v).dtype == dtype for v in state.values()):
         return state

@@ -60,3 +60,18 @@ def test_cached_decode_step_equals_full_forward(dtype, tol):
             assert np.abs(logits[r] - full).max() <= tol * np.abs(full).max(), r
             s.append(int(np.argmax(full)))
     assert [c['length'] for c in caches] == [len(s) - 1 for s in seqs]
+
+
+def test_greedy_cached_equals_greedy():
+    # The batched KV-cached greedy (used for long end-to-end traces) gives the
+    # full-recompute greedy's tokens and margins for prompts of different
+    # lengths and output counts.
+    state = init_gpt2_state(n_vocab=61, n_embd=32, n_layer=2, n_positions=64, seed=9)
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, 61, n).tolist() for n in (1, 5, 13)]
+    steps = [6, 1, 9]
+    tokens, margins = go.greedy_cached(state, prompts, steps, n_head=4, n_layer=2)
+    for p, n, t, m in zip(prompts, steps, tokens, margins):
+        ref, ref_m = go.greedy(state, p, n, n_head=4, n_layer=2)
+        assert t == ref
+        assert np.allclose(m, ref_m, rtol=1e-9, atol=1e-12)

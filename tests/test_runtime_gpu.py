@@ -52,9 +52,11 @@ def test_token_readback_in_order():
 
 def test_sync_free_batcher_cancel_and_finish_in_flight():
     # Cancel and finish requests right after steps that left their tokens in
-    # flight: the pages come back, every delivered token belongs to a step
-    # before the cancel/finish, and the tokens delivered equal the synchronous
-    # loop's prefix for those requests.
+    # flight: the pages come back, nothing is delivered to those requests
+    # after the cancel/finish (their in-flight tokens are dropped, as the
+    # reference emits nothing after a cancel), what they did receive is a
+    # prefix of the synchronous loop's tokens, and every other request gets
+    # exactly the synchronous loop's tokens.
     from minitorch_amd.model import DecoderLM
     from minitorch_amd.continuous_batching import ContinuousBatchingEngine
     model = DecoderLM(n_vocab=256, n_embd=64, n_head=2, n_layer=2, n_positions=128, seed=3)
@@ -68,23 +70,31 @@ def test_sync_free_batcher_cancel_and_finish_in_flight():
             eng.admit(rid, p, max_new_tokens=20)
         for _ in range(6):
             eng.step()
+        at_end = {rid: len(eng.requests[rid].output_ids) for rid in ('r0', 'r1')}
         eng.cancel('r0')
         eng.finish('r1')
+        late = []
         while eng.has_work:
-            eng.step()
+            late += [e['request_id'] for e in eng.step()]
         out = {rid: (r.state, r.finish_reason, list(r.output_ids)) for rid, r in eng.requests.items()}
         stats = eng.pool.memory_stats()
         eng.close()
-        return out, stats
+        return out, stats, late, at_end
 
-    sync, s_stats = run(False)
-    fb, f_stats = run(True)
+    sync, s_stats, s_late, s_end = run(False)
+    fb, f_stats, f_late, f_end = run(True)
     assert s_stats['kv_pool_used_pages'] == 0 and f_stats['kv_pool_used_pages'] == 0
     assert fb['r0'][:2] == ('cancelled', 'cancelled') and fb['r1'][:2] == ('completed', 'finished')
+    for late, end, out in ((s_late, s_end, sync), (f_late, f_end, fb)):
+        assert 'r0' not in late and 'r1' not in late
+        assert all(len(out[rid][2]) == end[rid] for rid in ('r0', 'r1'))
+    assert f_end['r0'] < s_end['r0']                    # a token was in flight and was dropped
     for rid in prompts:
-        # same states and the same tokens, including those generated before the
-        # cancel/finish but delivered after it in the sync-free loop
-        assert fb[rid] == sync[rid], rid
+        if rid in ('r0', 'r1'):
+            assert fb[rid][:2] == sync[rid][:2]
+            assert fb[rid][2] == sync[rid][2][:len(fb[rid][2])], rid
+        else:
+            assert fb[rid] == sync[rid], rid
 
 
 def _reference_runtime():
