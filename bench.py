@@ -9,11 +9,16 @@ resident in HBM before the timed region. To measure cold-cache HBM bandwidth,
 steps rotate over ``--pools`` disjoint copies of the pool, tables and Q/K/V
 (6 x ~113 MB touched per cycle, beyond the 256 MB Infinity Cache).
 
-Prints one JSON line: decode tokens/s (B tokens per step / mean step time from
-HIP events around the K timed steps), the roofline of the decode kernel
-(algorithmic bytes per launch / mean launch time vs 8 TB/s) and the CPU
-baseline (the C restatement in oracle/, OpenMP on the host cores, on a
-bounded sample of the same workload).
+Prints one JSON line: the op-level rate (B requests per step / mean step time
+from HIP events around the K timed steps; one layer's fused append + attention,
+not a whole-model rate), the roofline of the decode kernel (algorithmic bytes
+per launch / mean launch time vs 8 TB/s) and the CPU baseline (the C
+restatement in oracle/, OpenMP on the host cores, on a bounded sample of the
+same workload); then, under ``config1`` and ``e2e``, config 1's launch time
+beside its CPU time and the end-to-end decode tokens/s of configs 3
+(DistilGPT-2 fp16 trace, by the reference's formula and over busy steps) and 4
+(GPT-2-medium bf16 steady state, ms per decode step), each with its CPU
+baseline. ``--no-e2e`` skips those.
 """
 import argparse
 import ctypes as ct
@@ -468,49 +473,140 @@ def e2e_cpu_baseline(model, lengths, seconds, seed):
                 host=dict(nproc=os.cpu_count(), cpu_model=host_cpu_model()))
 
 
-def bench_e2e(args):
+def e2e_config3(args, loops=('sync', 'sync-free')):
+    """Config 3 end to end: the 256-request DistilGPT-2 trace (fp16) replayed by
+    wall clock through the batcher. Reports decode tokens/s by the reference's
+    formula (generated tokens / (end - start), arrival gaps included,
+    project/benchmark_continuous_batching.py:122) and as busy-step tokens/s
+    (decode tokens / time of the steps that ran), per loop."""
     from minitorch_amd import model as model_mod, e2e
+    model = model_mod.distilgpt2(seed=args.seed)
+    trace = e2e.config3_trace(args.seed)
+    warm = e2e.config3_trace(args.seed + 1, requests=8, rate=1000.0)
+    r = {}
+    if 'sync' in loops:
+        e2e.run_config3(model, warm, precision='fp16', report_every=0)
+        r = e2e.run_config3(model, trace, precision='fp16')
+    if 'sync-free' in loops:
+        # the same trace through the sync-free loop (device-side token feedback)
+        e2e.run_config3(model, warm, precision='fp16', token_feedback=True, report_every=0)
+        r['sync_free'] = e2e.run_config3(model, trace, precision='fp16', token_feedback=True)
+    if not args.no_cpu_baseline:
+        # the trace's mean decode batch, mid-generation contexts of its first requests
+        batch = max(1, int(round((r.get('sync_free') or r).get('mean_decode_batch_size', 2))))
+        r['cpu_baseline'] = e2e_cpu_baseline(model, [len(p) + 64 for _, _, p, _ in trace[:batch]],
+                                             args.cpu_seconds, args.seed)
+    r['workload'] = ('config 3: continuous batching, random-init DistilGPT-2 (6 layers, d 768, 12 heads, vocab '
+                     '50257), fp16, 256 Poisson requests at 32 req/s, prompts U[32,512], outputs geometric mean '
+                     '128, greedy, EOS off, 16384 pages of 16 tokens, FIFO, max_batch_size 256')
+    return r
+
+
+def e2e_config4(args, loops=('sync', 'sync-free')):
+    """Config 4 end to end: 128 concurrent GPT-2-medium (bf16) requests, 5 %
+    replaced per step. Reports decode tokens/s and ms per decode step (whole
+    24-layer model step with the tied head, tokens to the host) and the whole
+    loop's rate including the replacement prefills, per loop."""
+    from minitorch_amd import model as model_mod, e2e
+    model = model_mod.gpt2_medium(seed=args.seed)
+    kw = dict(seed=args.seed, steps=max(10, min(args.steps, 40)), warmup=max(2, min(args.warmup, 5)),
+              replace_rate=args.replace_rate, batch_prefills=not args.prefill_each)
+    r = e2e.run_config4(model, **kw) if 'sync' in loops else {}
+    if 'sync-free' in loops:
+        r['sync_free'] = e2e.run_config4(model, **kw, token_feedback=True)
+    if not args.no_cpu_baseline:
+        r['cpu_baseline'] = e2e_cpu_baseline(model, e2e.config4_lengths(np.random.default_rng([args.seed, 4]), 128),
+                                             args.cpu_seconds, args.seed)
+    r['workload'] = ('config 4: steady state of 128 requests, random-init GPT-2-medium (24 layers, d 1024, 16 '
+                     'heads), bf16, contexts lognormal(median 256, sigma 1.2) clipped [16,1024], page 16, '
+                     f'{args.replace_rate:.0%} replaced per step')
+    return r
+
+
+def config1_times(args):
+    """Config 1 (4 requests, L = {7, 33, 64, 120}, 12 heads, fp32): one
+    mt_paged_decode_batch launch on the GPU (HIP events, mean of many) and the
+    C restatement's decode step on the host (median, 1 and up to 16 threads)."""
+    from minitorch_amd.workloads import config1_case
+    case = config1_case(args.seed)
+    dev = DevicePagedCase(case)
+    fn = paged_ops.paged_library().mt_paged_decode_batch
+    fn.argtypes, fn.restype = [P] * 7 + [I] * 10, I
+    from minitorch_amd.dtypes import dtype_code
+    kw = dev.kwargs()
+    call = (dev.out.ptr, dev.q.ptr, dev.k.ptr, dev.v.ptr, dev.slab_table.ptr, dev.block_table.ptr,
+            dev.offsets.ptr, kw['b'], kw['h'], kw['d'], kw['page_size'], kw['pages_per_slab'], kw['num_slabs'],
+            kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype']))
+    per = time_launches(fn, [call], 200, 20)
+    out = dict(workload='config 1: B=4, L={7,33,64,120}, H=12, D=64, P=16, fp32, 64-page pool',
+               gpu_us_per_launch=per * 1e6)
+    if args.no_cpu_baseline:
+        return out
+    try:
+        from oracle import c_oracle
+        lib = c_oracle.library()
+    except Exception as error:  # the oracle library is optional on the GPU box
+        out['cpu_baseline'] = dict(value=None, sample=f'unavailable: {error}')
+        return out
+    host = c_oracle.HostCase(case)
+    threads = min(os.cpu_count() or 1, 16)
+    seconds = min(2.0, args.cpu_seconds)
+    many = timed_steps(lambda: host.run(lib, threads), seconds)
+    one = timed_steps(lambda: host.run(lib, 1), seconds)
+    out['cpu_baseline'] = dict(value=float(np.median(many)) * 1e6, unit='us per step', cores=threads, kind='port',
+                               sample=f'median of {len(many)} config-1 decode steps (append + attention), fp32, '
+                                      f'C restatement, OpenMP over (request, head)',
+                               single_core=dict(value=float(np.median(one)) * 1e6, unit='us per step', cores=1,
+                                                steps=len(one)))
+    return out
+
+
+def bench_e2e(args):
     if args.config == 3:
-        model = model_mod.distilgpt2(seed=args.seed)
-        trace = e2e.config3_trace(args.seed)
-        warm = e2e.config3_trace(args.seed + 1, requests=8, rate=1000.0)
-        r = {}
-        if args.loop in ('both', 'sync'):
-            e2e.run_config3(model, warm, precision='fp16')
-            r = e2e.run_config3(model, trace, precision='fp16')
-        if args.loop in ('both', 'sync-free'):
-            # the same trace through the sync-free loop (device-side token feedback)
-            e2e.run_config3(model, warm, precision='fp16', token_feedback=True)
-            r['sync_free'] = e2e.run_config3(model, trace, precision='fp16', token_feedback=True)
-        if not args.no_cpu_baseline:
-            # the trace's mean decode batch, mid-generation contexts of its first requests
-            batch = max(1, int(round((r.get('sync_free') or r).get('mean_decode_batch_size', 2))))
-            r['cpu_baseline'] = e2e_cpu_baseline(model, [len(p) + 64 for _, _, p, _ in trace[:batch]],
-                                                 args.cpu_seconds, args.seed)
-        value, workload = r.get('busy_decode_tokens_per_sec'), (
-            'config 3: continuous batching, random-init DistilGPT-2 (6 layers, d 768, 12 heads, vocab '
-            '50257), fp16, 256 Poisson requests at 32 req/s, prompts U[32,512], outputs geometric mean '
-            '128, greedy, EOS off, 16384 pages of 16 tokens, FIFO, max_batch_size 256')
-        dtype = 'f16'
+        loops = ('sync', 'sync-free') if args.loop == 'both' else (args.loop,)
+        r = e2e_config3(args, loops)
+        value, dtype = (r.get('busy_decode_tokens_per_sec') or r.get('sync_free', {}).get('busy_step_tokens_per_sec')), 'f16'
     else:
-        model = model_mod.gpt2_medium(seed=args.seed)
-        kw = dict(seed=args.seed, steps=min(args.steps, 40), warmup=min(args.warmup, 5),
-                  replace_rate=args.replace_rate, batch_prefills=not args.prefill_each)
-        r = e2e.run_config4(model, **kw) if args.loop in ('both', 'sync') else {}
-        if args.loop in ('both', 'sync-free'):
-            r['sync_free'] = e2e.run_config4(model, **kw, token_feedback=True)
-        if not args.no_cpu_baseline:
-            r['cpu_baseline'] = e2e_cpu_baseline(model, e2e.config4_lengths(np.random.default_rng([args.seed, 4]), 128),
-                                                 args.cpu_seconds, args.seed)
-        value, workload = r.get('decode_tokens_per_sec'), (
-            'config 4: steady state of 128 requests, random-init GPT-2-medium (24 layers, d 1024, 16 '
-            'heads), bf16, contexts lognormal(median 256, sigma 1.2) clipped [16,1024], page 16, '
-            f'{args.replace_rate:.0%} replaced per step')
-        dtype = 'bf16'
+        loops = ('sync', 'sync-free') if args.loop == 'both' else (args.loop,)
+        r = e2e_config4(args, loops)
+        value, dtype = r.get('decode_tokens_per_sec') or r.get('sync_free', {}).get('loop_tokens_per_sec'), 'bf16'
     return {'metric': 'decode tokens/s (1 GPU), end to end', 'value': value, 'unit': 'tokens/s',
             'n_gpus': 1, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
             'dtype': dtype, 'data': 'synthetic (random-init weights, random token ids)',
-            'config': {'workload': workload}, 'cpu_baseline': r.pop('cpu_baseline', None), 'measurements': r}
+            'config': {'workload': r.pop('workload')}, 'cpu_baseline': r.pop('cpu_baseline', None),
+            'measurements': r}
+
+
+def e2e_summary(r3, r4):
+    """The end-to-end figures of configs 3 and 4 for the default line."""
+    out = {}
+    if r3 is not None:
+        sf = r3.get('sync_free', {})
+        out['config3'] = dict(
+            workload=r3['workload'],
+            decode_tokens_per_sec_reference_formula=r3.get('output_tokens_per_sec'),
+            busy_step_decode_tokens_per_sec=r3.get('busy_step_tokens_per_sec'),
+            busy_decode_tokens_per_sec=r3.get('busy_decode_tokens_per_sec'),
+            sync_free=dict(decode_tokens_per_sec_reference_formula=sf.get('output_tokens_per_sec'),
+                           busy_step_decode_tokens_per_sec=sf.get('busy_step_tokens_per_sec'),
+                           ttft_p50_ms=sf.get('ttft_p50_ms')) if sf else None,
+            elapsed_seconds=r3.get('elapsed_seconds'), generated_tokens=r3.get('generated_tokens'),
+            completed=r3.get('completed'), mean_decode_batch_size=r3.get('mean_decode_batch_size'),
+            ttft_p50_ms=r3.get('ttft_p50_ms'), ttft_p95_ms=r3.get('ttft_p95_ms'),
+            kv_pool_used_pages_after=r3.get('kv_pool_used_pages_after'),
+            cpu_baseline=r3.get('cpu_baseline'))
+    if r4 is not None:
+        sf = r4.get('sync_free', {})
+        out['config4'] = dict(
+            workload=r4['workload'],
+            decode_tokens_per_sec=r4.get('decode_tokens_per_sec'), ms_per_decode_step=r4.get('ms_per_step'),
+            loop_tokens_per_sec=r4.get('loop_tokens_per_sec'), loop_ms_per_step=r4.get('loop_ms_per_step'),
+            sync_free=dict(loop_tokens_per_sec=sf.get('loop_tokens_per_sec'),
+                           loop_ms_per_step=sf.get('loop_ms_per_step')) if sf else None,
+            steps=r4.get('steps'), mean_context_tokens=r4.get('mean_context_tokens'),
+            replaced_requests=r4.get('replaced_requests'), page_reuses=r4.get('page_reuses'),
+            cpu_baseline=r4.get('cpu_baseline'))
+    return out
 
 
 def main():
@@ -543,6 +639,8 @@ def main():
                     help='config 4: fraction of requests replaced per step (0 = decode steps only)')
     ap.add_argument('--prefill', action='store_true',
                     help='op-level causal paged prefill attention on the prompt shapes of configs 3 and 4')
+    ap.add_argument('--no-e2e', action='store_true',
+                    help='default line: skip the end-to-end configs 3 and 4 and config 1')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: this build has no multi-GPU path '
@@ -626,6 +724,9 @@ def main():
         'vs_baseline': None,
         'dtype': 'f16',
         'data': 'synthetic',
+        'value_definition': ('op level: B requests / mean duration of ONE fused KV-append + decode-attention '
+                             'launch over ONE layer (config 2); not a whole-model rate. End-to-end decode '
+                             'tokens/s of full model steps: e2e.config3 / e2e.config4'),
         'config': {
             'workload': 'config 2: op-level paged decode (fused KV append + attention), B=64, '
                         'L~U[128,1024], H=12, D=64, page 16, fp16 K/V, fp32 accumulate, 8192-page '
@@ -652,6 +753,11 @@ def main():
         result['pattern_ceiling'] = pattern_ceiling(case, devs, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         result['cpu_baseline'] = cpu_baseline(case, args.cpu_seconds)
+    del devs, calls, ws, order
+    if not args.no_e2e:
+        print('config 1, then end-to-end configs 3 and 4', file=sys.stderr, flush=True)
+        result['config1'] = config1_times(args)
+        result['e2e'] = e2e_summary(e2e_config3(args), e2e_config4(args))
     print(json.dumps(result), flush=True)
 
 
