@@ -9,13 +9,14 @@
 //
 // Decode attention is a GEMV over paged K/V (about one flop per byte), so it
 // is bound by HBM bandwidth and uses no MFMA. The design:
-//   * one workgroup (4 waves) owns one (request, head, context split);
-//   * a wave covers 16 tokens per step: four lanes per token, each lane owning
-//     head_dim/4 contiguous dims, so one page row-block of one head (2 KiB for
-//     fp16, D = 64) is a single coalesced 16-byte-per-lane load;
-//   * every 4-lane token group keeps its own online-softmax state (running max,
+//   * one workgroup (4 or 8 waves) owns one (request, head, context split);
+//   * a wave covers 8 tokens per step: eight lanes per token, each lane owning
+//     head_dim/8 contiguous dims, so for fp16/bf16 at D = 64 every 16-byte-per-
+//     lane load instruction reads 1 KiB of one page-head block contiguously
+//     (8 whole token rows), non-temporally: each K/V byte is read once;
+//   * every 8-lane token group keeps its own online-softmax state (running max,
 //     denominator, fp32 accumulator), so the stream needs no cross-lane
-//     reduction except the 4-lane dot-product sum; groups, waves and splits are
+//     reduction except the 8-lane dot-product sum; groups, waves and splits are
 //     merged once at the end with the log-sum-exp rule;
 //   * the slab table of a small pool is staged in LDS and each lane resolves
 //     the page of one of its wave's row-blocks before streaming (broadcast with
@@ -39,8 +40,11 @@
 #include <algorithm>
 #include <climits>
 
-#ifndef MT_NT_LOADS
-#define MT_NT_LOADS 0
+// The decode kernel streams every K/V byte of a launch exactly once, so its
+// loads are non-temporal (streamed past the caches). Measured on MI355X
+// (config 2, cold pools): 24.1 -> 21.0 us together with 8 lanes per token.
+#ifndef MT_DECODE_NT_LOADS
+#define MT_DECODE_NT_LOADS 1
 #endif
 #include <cmath>
 #include <mutex>
@@ -64,11 +68,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 #define MT_STAGES 1
 #endif
 constexpr int kStages = MT_STAGES;  // register stages of the K/V stream
-constexpr int kDefaultWaves = 4;     // waves per decode workgroup
+// Lanes per token in the decode kernel: 8 lanes of 8 dims (fp16/bf16, D 64)
+// make each 16-byte-per-lane load instruction one contiguous 1 KiB of a page
+// (8 whole token rows); with 4 lanes of 16 dims an instruction touches every
+// row of the 2 KiB page-row block half each.
 #ifndef MT_DECODE_GROUP
-#define MT_DECODE_GROUP 4
+#define MT_DECODE_GROUP 8
 #endif
-constexpr int kDecodeGroup = MT_DECODE_GROUP;  // lanes per token in the decode kernel
+constexpr int kDecodeGroup = MT_DECODE_GROUP;
+constexpr bool kDecodeNT = MT_DECODE_NT_LOADS != 0;
 // Pools of at most this many slabs have their slab table staged in LDS by the
 // decode kernel, so that page resolution after the block-table read is an LDS
 // read instead of a second dependent global load.
@@ -240,16 +248,15 @@ struct Chunk {
   static constexpr int NV = VEC ? DL * elem_bytes<DT>() / 16 : 1;
   u32x4 raw[VEC ? NV : 1];
   float val[VEC ? 1 : DL];
+  // NTL: non-temporal loads (data read once, not kept in the caches).
+  template <bool NTL = false>
   __device__ __forceinline__ void load(const T* p, int col0, int dim) {
     if constexpr (VEC) {
       const auto* v = global_view(reinterpret_cast<const u32x4*>(p));
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-#if MT_NT_LOADS
-        raw[i] = __builtin_nontemporal_load(v + i);
-#else
-        raw[i] = v[i];
-#endif
+        if constexpr (NTL) raw[i] = __builtin_nontemporal_load(v + i);
+        else raw[i] = v[i];
       }
     } else {
       const auto* g = global_view(p);
@@ -472,8 +479,8 @@ __device__ __forceinline__ void stream_wave(Softmax<D / G, G>& st, const Query<D
       const T* page = reinterpret_cast<const T*>(pb);
       if (valid[u] && page) {
         const T* kp = page + (rel & pmask) * dim + col0;
-        kc[u].load(kp, col0, dim);
-        vc[u].load(kp + g.kind_stride, col0, dim);
+        kc[u].template load<kDecodeNT>(kp, col0, dim);
+        vc[u].template load<kDecodeNT>(kp + g.kind_stride, col0, dim);
       } else {
         kc[u].nan_fill();
         vc[u].nan_fill();
@@ -1471,24 +1478,35 @@ int device_compute_units() {
   return cached[dev];
 }
 
+// Workgroups of decode_kernel<DT, D, VEC, U, kStages, WAVES, G> resident per
+// compute unit (0 if the query fails), looked up once per instantiation.
+template <int DT, int D, bool VEC, int U, int WAVES, int G>
+int decode_occupancy() {
+  static const int per_cu = [] {
+    int n = 0;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<DT, D, VEC, U, kStages, WAVES, G>,
+                                                        WAVES * kWave, 0) == hipSuccess ? n : 0;
+  }();
+  return per_cu;
+}
+
 template <int DT, int D, bool VEC, int WAVES, int G>
 hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
   // Row bytes per lane bound the useful unroll: register stages beyond it spill.
   constexpr int kMaxUnroll = !VEC ? 1 : (D * elem_bytes<DT>() >= 256 ? 2 : 4);
   constexpr int NT = WAVES * kWave;
   if (unroll == 0) {
-    // Automatic: the deepest unroll when the whole grid is resident at its
-    // occupancy (more loads in flight per wave), else unroll 1, whose lower
-    // register count keeps the most workgroups per compute unit.
-    unroll = 1;
-    if constexpr (kMaxUnroll >= 4) {
-      static int per_cu = -1;
-      if (per_cu < 0) {
-        int n = 0;
-        per_cu = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                     &n, decode_kernel<DT, D, VEC, 4, kStages, WAVES, G>, NT, 0) == hipSuccess ? n : 0;
-      }
-      if (blocks <= int64_t(per_cu) * device_compute_units()) unroll = 4;
+    if constexpr (G == 8) {
+      // Two row-blocks per register stage: measured best or within 1 % of
+      // the best at every decode shape of configs 2, 4 and 5.
+      unroll = 2;
+    } else if constexpr (kMaxUnroll >= 4) {
+      // The deepest unroll when the whole grid is resident at its
+      // occupancy (more loads in flight per wave), else unroll 1, whose
+      // lower register count keeps the most workgroups per compute unit.
+      unroll = blocks <= int64_t(decode_occupancy<DT, D, VEC, 4, WAVES, G>()) * device_compute_units() ? 4 : 1;
+    } else {
+      unroll = 1;
     }
   }
   // Requests between the supported values round down (3 -> 2, 5+ -> 4).
@@ -1508,10 +1526,21 @@ hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
   return hipGetLastError();
 }
 
+// waves 0 = automatic: 8-wave workgroups when the whole grid is resident at
+// their occupancy (a (row, head) streamed by 8 waves finishes its longest
+// rows sooner; config 2: 21.0 us vs 21.9 us with 4), else 4 (more
+// workgroups per compute unit for grids of several residency rounds;
+// config 5: 256 us vs 267 us with 8).
 template <int DT, int D, bool VEC>
 hipError_t launch_decode_t(const DecodeArgs& a, int64_t blocks, int unroll, int waves) {
-  if (waves == 8) return launch_decode_w<DT, D, VEC, 8, kDecodeGroup>(a, blocks, unroll);
-  return launch_decode_w<DT, D, VEC, 4, kDecodeGroup>(a, blocks, unroll);
+  constexpr int G = kDecodeGroup;
+  if (waves == 0) {
+    constexpr int U8 = VEC && G == 8 ? 2 : 1;
+    waves = blocks <= int64_t(decode_occupancy<DT, D, VEC, U8, 8, G>()) * device_compute_units() ? 8 : 4;
+  }
+  if (a.split_tokens % ((kWave / G) * waves) != 0) waves = 4;
+  if (waves == 8) return launch_decode_w<DT, D, VEC, 8, G>(a, blocks, unroll);
+  return launch_decode_w<DT, D, VEC, 4, G>(a, blocks, unroll);
 }
 
 template <int DT>
@@ -1531,8 +1560,7 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   if (work && split_tokens <= 0) return hipErrorInvalidValue;
   const int S = choose_split(cap, split_tokens);
   if (S < 64 || S % 64 != 0 || S > kMaxSplitTokens) return hipErrorInvalidValue;
-  if (waves != 4 && waves != 8) return hipErrorInvalidValue;
-  if (S % ((kWave / kDecodeGroup) * waves) != 0) waves = 4;
+  if (waves != 0 && waves != 4 && waves != 8) return hipErrorInvalidValue;
   const int64_t nsplit_max = (cap + S - 1) / S;
   const int64_t bh = int64_t(b) * h;
   if (nsplit_max > INT_MAX) return hipErrorInvalidValue;
@@ -1976,7 +2004,7 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
     if (e != hipSuccess) return e;
   }
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
-                       num_slabs, columns, layer, layers, dtype, S, 0, kDefaultWaves, 0,
+                       num_slabs, columns, layer, layers, dtype, S, 0, 0, 0,
                        nullptr, 0, 0, ws, ws_bytes);
 }
 
@@ -2002,7 +2030,7 @@ int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const
     if (e != hipSuccess) return e;
   }
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
-                       num_slabs, columns, layer, layers, dtype, S, 0, kDefaultWaves, 0,
+                       num_slabs, columns, layer, layers, dtype, S, 0, 0, 0,
                        nullptr, 0, 0, ws, nsplit_max > 1 ? kNoAllocScratchBytes : 0);
 }
 
@@ -2045,7 +2073,7 @@ int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v
   if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, split_tokens,
-                       unroll, waves == 0 ? kDefaultWaves : waves, qkv_stride,
+                       unroll, waves, qkv_stride,
                        work, work_items, merge_rows, workspace, workspace_bytes);
 }
 
