@@ -115,7 +115,7 @@ int mt_residual_layernorm(void* out, float* x, const void* y, const float* gamma
 size_t mt_decoder_scratch_bytes(int rows, int d, int dtype);
 
 /* The layer loop of one batched decode step, all launches issued from here on
- * the null stream: for each layer, LayerNorm (fused with the previous
+ * the default stream: for each layer, LayerNorm (fused with the previous
  * residual add), fused QKV GEMM, paged decode attention
  * (mt_paged_decode_split reading q/k/v as column blocks of the QKV output),
  * out-projection, residual add + LayerNorm, fc GEMM + GELU, proj GEMM; after
@@ -134,7 +134,7 @@ int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
                       const mt_decode_attention* att);
 
 /* The layer loop of a prefill of n tokens for each of batch requests, all
- * launches issued from here on the null stream: as mt_decoder_layers, with
+ * launches issued from here on the default stream: as mt_decoder_layers, with
  * rows = batch * n token rows (x [rows, d] fp32, updated in place; h [rows, d]
  * in dtype) and, per layer, mt_paged_prefill appending K/V at att->offset and
  * computing causal attention, with q/k/v read as column blocks of the fused

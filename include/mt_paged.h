@@ -5,7 +5,8 @@
  * src/paged_attention_kernel.cu): every entry returns an int status, 0 on
  * success, otherwise a hipError_t value (1 = invalid value, 2 = out of
  * memory); pointers are device addresses; dtype 0 = float32, 1 = float16,
- * 2 = bfloat16; launches go to the null stream and never synchronize.
+ * 2 = bfloat16; launches go to the calling thread's default stream (the
+ * libraries are built with per-thread default streams) and never synchronize.
  *
  * Slab layout: [layers][2 (K,V)][pages_per_slab][heads][page_size][head_dim];
  * physical page p is slot p % pages_per_slab of slab p / pages_per_slab, whose
@@ -74,6 +75,13 @@ int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const
                                   const uint64_t* slabs, const int* table, const int* offsets,
                                   int b, int h, int d, int page_size, int pages_per_slab,
                                   int num_slabs, int columns, int layer, int layers, int dtype);
+
+/* Number of launches since the library was loaded in which
+ * mt_paged_attention / mt_paged_prefill split one long prompt's keys over
+ * workgroups (query tiles x heads <= compute units, >= 6 key blocks in the
+ * last tile). A diagnostic, e.g. for tests that must exercise that path.
+ * No reference counterpart. */
+int mt_paged_prefill_key_splits(long long* launches);
 
 /* Bytes of workspace mt_paged_decode_split needs (0 when no row can be split).
  * split_tokens = 0 selects the automatic split length.

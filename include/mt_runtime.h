@@ -1,6 +1,8 @@
 /* Device runtime of the boundary: C-ABI of
  * minitorch_amd/cuda_kernels/cuda_runtime.so. Device 0 (the current HIP
- * device), null stream. Status convention as in mt_paged.h.
+ * device), the calling thread's default stream (the libraries are built with
+ * per-thread default streams; one host thread sees the reference's legacy
+ * null-stream ordering). Status convention as in mt_paged.h.
  */
 #ifndef MT_RUNTIME_H
 #define MT_RUNTIME_H
@@ -16,13 +18,13 @@ int mt_free(void* p);
 /* kind: 0 host->host, 1 host->device, 2 device->host, 3 device->device,
  * 4 inferred. Replaces reference mt_copy (src/cuda_runtime.cu:10-12). */
 int mt_copy(void* dst, const void* src, size_t bytes, int kind);
-/* Asynchronous copy on the null stream. No reference counterpart. */
+/* Asynchronous copy on the default stream. No reference counterpart. */
 int mt_copy_async(void* dst, const void* src, size_t bytes, int kind);
 /* Replaces reference mt_sync (src/cuda_runtime.cu:13). */
 int mt_sync(void);
 /* Replaces reference mt_error (src/cuda_runtime.cu:14). */
 const char* mt_error(int code);
-/* Events on the null stream; elapsed waits for the second event.
+/* Events on the default stream; elapsed waits for the second event.
  * Replace reference mt_event_* (src/cuda_runtime.cu:15-21). */
 int mt_event_create(void** e);
 int mt_event_record(void* e);
@@ -46,6 +48,16 @@ int mt_compute_units(int* n);
  * without the decode's work. No reference counterpart. */
 int mt_chunk_read(const unsigned long long* chunks, int count, int chunk_bytes, int blocks,
                   unsigned* sink);
+/* Graph capture of the calling thread's default stream (where every entry of
+ * these libraries launches): mt_graph_begin starts a thread-local capture;
+ * mt_graph_end ends it and instantiates the graph (*exec; null and the
+ * capture discarded on failure); mt_graph_launch replays it on the same
+ * stream; mt_graph_destroy releases it. Used to replay a decode step whose
+ * shapes are fixed. No reference counterpart. */
+int mt_graph_begin(void);
+int mt_graph_end(void** exec);
+int mt_graph_launch(void* exec);
+int mt_graph_destroy(void* exec);
 /* Pinned host memory (hipHostMalloc) for asynchronous uploads.
  * No reference counterpart. */
 int mt_host_alloc(void** p, size_t bytes);

@@ -4,7 +4,7 @@
  * The reference keeps the page free list, per-cache page lists, block tables
  * and decode offsets on the host (minitorch/paged_kv_cache.py:27-263,
  * minitorch/paged_decode.py:10-93) and uploads them every step. Here they live
- * in one device "pool state" blob updated by kernels on the null stream, with
+ * in one device "pool state" blob updated by kernels on the calling thread's default stream, with
  * page IDs identical to the reference's allocator: LIFO pops, new slabs'
  * page IDs pushed in reverse order on top of older free pages before a pop
  * that finds too few free pages, releases pushed in the given order.

@@ -32,6 +32,10 @@ HIPCC_FLAGS = [
     '-O3', '-std=c++17', '-fPIC', '-shared', f'--offload-arch={ARCH}',
     # Packed-fp32 VALU forms are kept out of every kernel.
     '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+    # Launches and stream-0 API calls go to the calling thread's default
+    # stream, which (unlike the legacy null stream) can be captured into a
+    # graph; every library shares it.
+    '-fgpu-default-stream=per-thread',
     '-Wno-unused-command-line-argument',
 ]
 

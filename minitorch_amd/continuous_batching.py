@@ -17,7 +17,9 @@ delivers one step later (a step returns the events of the tokens that
 arrived during it; a step that admits requests waits for all its tokens, so
 first tokens are not delayed). Scheduling decisions, pages and tokens are the same as in
 the synchronous mode; a step whose batch has a request with an EOS token
-waits for its tokens, since finishing then depends on their values.
+waits for its tokens, since finishing then depends on their values. With
+``graph=True`` as well, each decode step's device work is replayed from a HIP
+graph captured per batch size (``DecoderLM.decode_greedy(graph=True)``).
 """
 from collections import deque
 from contextlib import nullcontext
@@ -65,7 +67,7 @@ class ContinuousBatcher:
 
     def __init__(self, model, *, max_batch_size=4, page_size=16, kv_budget_bytes=256 * 1024 ** 2,
                  pages_per_slab=4, precision='fp32', max_prefills_per_step=1,
-                 prefill_token_budget=512, clock=time.perf_counter, token_feedback=False):
+                 prefill_token_budget=512, clock=time.perf_counter, token_feedback=False, graph=False):
         for value in (max_batch_size, max_prefills_per_step, prefill_token_budget):
             if type(value) is not int or value < 1:
                 raise ValueError('Positive integer batch size and prefill limits required')
@@ -87,7 +89,10 @@ class ContinuousBatcher:
         self.iteration = 0
         self.last_step = None
         self.closed = False
+        if graph and not token_feedback:
+            raise ValueError('graph replay needs the sync-free loop (token_feedback=True)')
         self.token_feedback = bool(token_feedback)
+        self.graph = bool(graph)
         self._readback = TokenReadback(max_prefills_per_step + 4) if self.token_feedback else None
         self._inflight = deque()  # (readback ticket, requests) in issue order
 
@@ -207,7 +212,7 @@ class ContinuousBatcher:
             if decode_ids and self.token_feedback:
                 batch = [self.active[rid] for rid in decode_ids]
                 try:
-                    ids = self.model.decode_greedy([r.cache for r in batch])
+                    ids = self.model.decode_greedy([r.cache for r in batch], graph=self.graph)
                     self.peak_used_pages = max(self.peak_used_pages, self.pool.used_pages)
                     self._issue(batch, ids)
                     if any(r.eos_token_id is not None for r in batch):

@@ -1,5 +1,8 @@
 // Device runtime of the boundary: allocation, copies, synchronization, error
-// strings and events on device 0's null stream, with the reference's symbol
+// strings and events on the calling thread's default stream of device 0 (the
+// libraries are built with per-thread default streams, so that a decode step
+// can be captured into a graph; with one host thread this orders work exactly
+// as the reference's legacy null stream does), with the reference's symbol
 // names and status convention (src/cuda_runtime.cu:7-21; status 0 = success,
 // otherwise the hipError_t value, whose numbering matches the CUDA codes the
 // reference's Python checks: 1 = invalid value, 2 = out of memory).
@@ -143,6 +146,42 @@ int mt_compute_units(int* n) {
   if (e != hipSuccess) return e;
   return hipDeviceGetAttribute(n, hipDeviceAttributeMultiprocessorCount, dev);
 }
+// Graph capture of the calling thread's default stream, where the libraries
+// of this build launch everything (they are built with per-thread default
+// streams; the legacy null stream cannot be captured). Thread-local mode:
+// an allocation or synchronization issued by this thread inside the capture
+// fails instead of being recorded.
+int mt_graph_begin() { return hipStreamBeginCapture(hipStreamPerThread, hipStreamCaptureModeThreadLocal); }
+
+// Ends the capture begun by mt_graph_begin and instantiates it; on any
+// failure the capture is still ended (and discarded) and *exec is null.
+int mt_graph_end(void** exec) {
+  if (!exec) return hipErrorInvalidValue;
+  *exec = nullptr;
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(hipStreamPerThread, &graph);
+  if (e != hipSuccess) {
+    if (graph) hipGraphDestroy(graph);
+    return e;
+  }
+  hipGraphExec_t x = nullptr;
+  e = hipGraphInstantiate(&x, graph, nullptr, nullptr, 0);
+  hipGraphDestroy(graph);
+  if (e != hipSuccess) return e;
+  *exec = x;
+  return hipSuccess;
+}
+
+int mt_graph_launch(void* exec) {
+  if (!exec) return hipErrorInvalidValue;
+  return hipGraphLaunch(static_cast<hipGraphExec_t>(exec), hipStreamPerThread);
+}
+
+int mt_graph_destroy(void* exec) {
+  if (!exec) return hipErrorInvalidValue;
+  return hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec));
+}
+
 // Pinned host memory for asynchronous uploads (allocated, never registered).
 int mt_host_alloc(void** p, size_t bytes) { return hipHostMalloc(p, bytes, hipHostMallocDefault); }
 int mt_host_free(void* p) { return hipHostFree(p); }

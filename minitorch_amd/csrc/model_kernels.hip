@@ -94,6 +94,12 @@ enum Epilogue : int { kEpiNone = 0, kEpiGelu = 1 };
 // timing, which would otherwise stall serving.
 constexpr size_t kFlushBytes = size_t(256) << 20;
 
+// Whether work issued now is being captured into a graph (per-thread stream).
+bool stream_capturing() {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(hipStreamPerThread, &status) == hipSuccess && status != hipStreamCaptureStatusNone;
+}
+
 int pick_fastest(Blas* blas, Plan& p, const hipblasLtMatmulHeuristicResult_t* heur, int count,
                  void* out, const void* a, const void* b) {
   if (count == 1) { p.algo = heur[0].algo; return 0; }
@@ -110,16 +116,16 @@ int pick_fastest(Blas* blas, Plan& p, const hipblasLtMatmulHeuristicResult_t* he
   for (int i = 0; i < count; ++i) {
     auto run = [&]() {
       return hipblasLtMatmul(blas->handle, p.desc, &alpha, b, p.la, a, p.lb, &beta, out, p.lc, out,
-                             p.lc, &heur[i].algo, blas->workspace, blas->workspace_bytes, nullptr);
+                             p.lc, &heur[i].algo, blas->workspace, blas->workspace_bytes, hipStreamPerThread);
     };
     if (run() != HIPBLAS_STATUS_SUCCESS) continue;  // warm-up; unusable candidates drop out
     float total = 0.f;
     bool ok = true;
     for (int r = 0; r < 2 && ok; ++r) {
-      if (blas->flush) ok = hipMemsetAsync(blas->flush, r, kFlushBytes, nullptr) == hipSuccess;
-      hipEventRecord(start, nullptr);
+      if (blas->flush) ok = hipMemsetAsync(blas->flush, r, kFlushBytes, hipStreamPerThread) == hipSuccess;
+      hipEventRecord(start, hipStreamPerThread);
       ok = ok && run() == HIPBLAS_STATUS_SUCCESS;
-      hipEventRecord(stop, nullptr);
+      hipEventRecord(stop, hipStreamPerThread);
       float ms = 0.f;
       ok = ok && hipEventSynchronize(stop) == hipSuccess && hipEventElapsedTime(&ms, start, stop) == hipSuccess;
       total += ms;
@@ -265,7 +271,9 @@ int gemm(Blas* blas, void* out, const void* a, const void* b, const void* bias, 
     p.tunable = tunable;
     if (!tunable) ++blas->oneoff_plans;
   }
-  if (tunable && ++p.calls == kTuneAfterCalls && p.candidates > 1 && blas->tune) {
+  // No timing (events, synchronization, cache flushes) inside a stream
+  // capture: a captured step keeps the algorithm chosen so far.
+  if (tunable && !stream_capturing() && ++p.calls == kTuneAfterCalls && p.candidates > 1 && blas->tune) {
     if (bias)
       hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
     const int e = pick_fastest(blas, p, p.heur, p.candidates, out, a, b);
@@ -276,7 +284,7 @@ int gemm(Blas* blas, void* out, const void* a, const void* b, const void* bias, 
   const float alpha = 1.f, beta = 0.f;
   return blas_status(hipblasLtMatmul(blas->handle, p.desc, &alpha, b, p.la, a, p.lb, &beta, out,
                                      p.lc, out, p.lc, &p.algo, blas->workspace,
-                                     blas->workspace_bytes, nullptr));
+                                     blas->workspace_bytes, hipStreamPerThread));
 }
 
 int blocks_for(int64_t n, int threads = 256) {

@@ -38,6 +38,7 @@
 #include "mt_device.h"
 #include "../../include/mt_paged.h"
 #include <algorithm>
+#include <atomic>
 #include <climits>
 
 // The decode kernel streams every K/V byte of a launch exactly once, so its
@@ -1593,7 +1594,8 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
 // workspace argument (mt_paged_decode_batch for tables longer than one split,
 // the key-split prefill of mt_paged_attention / mt_paged_prefill). One buffer
 // per device, kept until the process ends. It grows stream-ordered on the
-// null stream, where every launch of this library runs: hipMallocAsync for
+// calling thread's default stream, where every launch of this library runs
+// (the libraries are built with per-thread default streams): hipMallocAsync for
 // the larger buffer and hipFreeAsync for the old one, which is released only
 // after the work queued before it, so growing neither synchronizes the device
 // nor blocks the host. Callers that cannot allocate use mt_paged_decode_split
@@ -1610,13 +1612,13 @@ int library_workspace(size_t bytes, void** out) {
   auto& slot = g_ws[dev];
   if (slot.second < bytes) {
     void* p = nullptr;
-    e = hipMallocAsync(&p, bytes, nullptr);
+    e = hipMallocAsync(&p, bytes, hipStreamPerThread);
     if (e != hipSuccess) {
       (void)hipGetLastError();  // the caller reports the status; keep it off the next launch
       return e;
     }
     if (slot.first) {
-      e = hipFreeAsync(slot.first, nullptr);
+      e = hipFreeAsync(slot.first, hipStreamPerThread);
       if (e != hipSuccess) return e;
     }
     slot = {p, bytes};
@@ -1691,6 +1693,9 @@ bool prefill_kernel_takes(const QueryArgs& a, int dtype) {
          rows16(a.o_h) && rows16(a.o_r);
 }
 
+// Launches that took the key-split prefill path (a diagnostic for tests).
+std::atomic<long long> g_key_split_launches{0};
+
 // Key-split prefill of one request whose query tiles give at most one
 // workgroup per compute unit and whose last tile walks many key blocks: each tile's keys are cut
 // into splits of B blocks (B chosen for about two workgroups per compute
@@ -1749,7 +1754,9 @@ hipError_t launch_split_prefill(QueryArgs& a, int dtype) {
     else { MT_SPLIT(kBF16, 128) }
   }
 #undef MT_SPLIT
-  return hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) g_key_split_launches.fetch_add(1, std::memory_order_relaxed);
+  return e;
 }
 
 // Causal attention launch for any q/out strides: the matrix-core prefill
@@ -2032,6 +2039,12 @@ int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, S, 0, 0, 0,
                        nullptr, 0, 0, ws, nsplit_max > 1 ? kNoAllocScratchBytes : 0);
+}
+
+int mt_paged_prefill_key_splits(long long* launches) {
+  if (!launches) return hipErrorInvalidValue;
+  *launches = g_key_split_launches.load(std::memory_order_relaxed);
+  return hipSuccess;
 }
 
 int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, int split_tokens,

@@ -4,7 +4,7 @@
 // and decode offsets on the host and uploads them every step
 // (minitorch/paged_kv_cache.py:71-103,171-189; minitorch/paged_decode.py:40-54).
 // Here they live in one device "pool state" blob and are updated by small
-// single-workgroup kernels on the null stream, so admitting, stepping and
+// single-workgroup kernels on the default stream, so admitting, stepping and
 // finishing requests never reads device memory back. Page IDs follow the
 // reference's host allocator exactly:
 //   * the free list is a LIFO stack; pops take the top;
@@ -274,6 +274,9 @@ __global__ __launch_bounds__(kThreads) void decode_prepare_kernel(Pool p, const 
   __shared__ int s_red;
   if (threadIdx.x == 0) s_red = 0;
   const int F = p.h->top, opened = p.h->slabs_opened, pps = p.pages_per_slab;
+  // limit -1: the pages the budget has left, read from the pool header on
+  // the device (so that a captured step needs no host-computed budget).
+  if (limit < 0) limit = p.max_pages - p.h->leased;
   __syncthreads();
   int need_base = 0, seq_base = 0, reused = 0, last_rank = -1;
   for (int base = 0; base < b; base += blockDim.x) {
@@ -441,7 +444,7 @@ int mt_sched_decode_prepare(MT_POOL_ARGS, const int* slots, int b, int columns, 
                             int limit, int* table, int* offsets, float* positions,
                             int* cu_seqlens, int* new_page) {
   MT_POOL_CHECK
-  if (!slots || b < 1 || columns < 1 || columns > max_cols || limit < 0 || !table || !offsets ||
+  if (!slots || b < 1 || columns < 1 || columns > max_cols || limit < -1 || !table || !offsets ||
       !positions || !cu_seqlens || !new_page || !(page_size == 8 || page_size == 16 || page_size == 32) ||
       int64_t(b) * columns > INT32_MAX)
     return hipErrorInvalidValue;

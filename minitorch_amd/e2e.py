@@ -56,7 +56,7 @@ def _progress(message):
 
 def run_config3(model, trace, *, precision='fp16', max_batch_size=256, page_size=16, kv_pages=16384,
                 max_prefills_per_step=1, prefill_token_budget=512, clock=time.perf_counter,
-                report_every=200, token_feedback=False):
+                report_every=200, token_feedback=False, graph=False):
     """Replay a config-3 trace through the batcher. ``busy_step_tokens_per_sec``
     is decode tokens over the wall time of the steps (decode, prefill and
     scheduling, idle gaps between arrivals excluded), comparable between the
@@ -69,7 +69,7 @@ def run_config3(model, trace, *, precision='fp16', max_batch_size=256, page_size
                                 kv_budget_bytes=kv_pages * page_bytes, precision=precision,
                                 max_prefills_per_step=max_prefills_per_step,
                                 prefill_token_budget=prefill_token_budget, clock=clock,
-                                token_feedback=token_feedback)
+                                token_feedback=token_feedback, graph=graph)
     pending = list(trace)
     steps = []
     start = clock()
@@ -93,7 +93,7 @@ def run_config3(model, trace, *, precision='fp16', max_batch_size=256, page_size
     step_seconds = sum(s['step_seconds'] for s in steps)
     ttft = [r.ttft_seconds for r in batcher.requests.values() if r.ttft_seconds is not None]
     result = dict(
-        token_feedback=token_feedback,
+        token_feedback=token_feedback, graph=graph,
         generated_tokens=generated, elapsed_seconds=elapsed,
         output_tokens_per_sec=generated / elapsed,
         busy_decode_tokens_per_sec=(decode_tokens / decode_seconds if decode_seconds and not token_feedback
@@ -116,7 +116,8 @@ def config4_lengths(rng, n):
 
 
 def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_rate=0.05,
-                precision='bf16', page_size=16, kv_pages=None, token_feedback=False, batch_prefills=True):
+                precision='bf16', page_size=16, kv_pages=None, token_feedback=False, batch_prefills=True,
+                graph=False):
     """Steady-state decode throughput; returns a dict of measurements.
 
     ``decode_tokens_per_sec`` (synchronous loop only) times each step's decode
@@ -175,7 +176,7 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
                 rt.synchronize()
                 loop0 = time.perf_counter()
             if token_feedback:
-                model.decode_greedy(caches)
+                model.decode_greedy(caches, graph=graph)
                 if step >= warmup:
                     tokens += len(caches)
             else:
@@ -208,7 +209,7 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
         for c in caches:
             c.close()
         pool.close()
-    return dict(token_feedback=token_feedback, batch_prefills=batch_prefills,
+    return dict(token_feedback=token_feedback, graph=graph, batch_prefills=batch_prefills,
                 decode_tokens_per_sec=tokens / decode_seconds if decode_seconds else None,
                 decode_seconds=decode_seconds, loop_tokens_per_sec=tokens / loop_seconds,
                 loop_seconds=loop_seconds, steps=steps, concurrent=concurrent,

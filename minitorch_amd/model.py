@@ -342,15 +342,93 @@ class DecoderLM:
         may have different context lengths (reference modules_transformer.py:373-390)."""
         return self._decode_batch(idx, caches, greedy=False)
 
-    def decode_greedy(self, caches, idx=None):
+    def decode_greedy(self, caches, idx=None, *, graph=False):
         """``decode_batch`` with greedy selection on the device, for the
         sync-free decode loop: the input token of each row is ``idx`` or, when
         None, the last token its cache slot holds in the pool (written by the
         previous step's selection); the chosen tokens are written back there
         and returned as fp32 IDs [B, 1] on the device. Nothing waits for the
         device. No reference counterpart (the reference reads every step's
-        tokens on the host, minitorch/continuous_batching.py:143,146)."""
+        tokens on the host, minitorch/continuous_batching.py:143,146).
+
+        With ``graph`` (and ``idx`` None) the step's device work (page pops
+        and metadata, embeddings, the layer loop, the greedy selection and the
+        length commit) is replayed from a HIP graph captured for the batch
+        size; the first ``GRAPH_WARMUP`` steps of a batch size run eagerly, so
+        that the projections' hipBLASLt algorithms are chosen (and timed)
+        outside any capture. The returned IDs then live in the captured step's
+        buffer and are overwritten by its next replay."""
+        if graph and idx is None:
+            return self._decode_greedy_graph(caches)
         return self._decode_batch(idx, caches, greedy=True)
+
+    def _decode_greedy_graph(self, caches):
+        from .paged_decode import PagedDecodeBatch
+        rt = runtime()
+        with PagedDecodeBatch(self, None, caches) as batch:
+            batch.prepare(graph=True)
+            pool, b, dtype, ws = batch.pool, batch.batch_size, batch.dtype, batch._ws
+            w = self._weights(dtype)
+            att = batch.attention_metadata()
+            deps = (w, self.blas(), ws.buffer, ws.partials, pool.slot_tokens, pool.state)
+            step = ws.graphs.get(b)
+            if step is not None and not step.matches(deps):
+                step.close()
+                del ws.graphs[b]
+                step = None
+            if step is None and ws.eager_steps.get(b, 0) < GRAPH_WARMUP:
+                ws.eager_steps[b] = ws.eager_steps.get(b, 0) + 1
+                batch.prepare_device()
+                ids = self._issue_decode(batch, w, att, _StepBuffers(model_library(), b, self.n_embd,
+                                                                     self.n_vocab, dtype))
+                batch.mark_layers_written()
+                batch.commit()
+                return ids
+            if step is None:
+                step = ws.graphs[b] = self._capture_decode(batch, w, att, deps)
+            rt.check(rt.lib.mt_graph_launch(step.exec))
+            batch._device_prepared = True
+            batch.mark_layers_written()
+            batch.commit(device=False)
+            return step.buffers.ids
+
+    def _capture_decode(self, batch, w, att, deps):
+        """Capture the device work of one decode step into a graph (nothing
+        runs until it is launched)."""
+        rt = runtime()
+        buffers = _StepBuffers(model_library(), batch.batch_size, self.n_embd, self.n_vocab, batch.dtype)
+        exec_ptr = P()
+        rt.check(rt.lib.mt_graph_begin())
+        try:
+            batch.prepare_device()
+            self._issue_decode(batch, w, att, buffers)
+            batch.commit_device()
+        except Exception:
+            rt.lib.mt_graph_end(ct.byref(exec_ptr))     # ends and discards the capture
+            if exec_ptr.value:
+                rt.lib.mt_graph_destroy(exec_ptr)
+            raise
+        finally:
+            batch._device_prepared = False              # nothing has run yet
+        rt.check(rt.lib.mt_graph_end(ct.byref(exec_ptr)))
+        return _CapturedStep(exec_ptr.value, buffers, deps)
+
+    def _issue_decode(self, batch, w, att, buffers):
+        """The device work of a sync-free decode step after its metadata:
+        embeddings of each slot's last token, the native layer loop with the
+        tied head, and the greedy selection with token feedback, into
+        ``buffers``; returns the IDs."""
+        b, d, dtype, pool = batch.batch_size, self.n_embd, batch.dtype, batch.pool
+        paged_ops.embed_tokens(buffers.x.ptr, w.wte.ptr, w.wpe.ptr, None, batch.position_ids.ptr, b,
+                               self.n_vocab, self.n_positions, d, slot_tokens=pool.slot_tokens.ptr,
+                               slots=batch.device_slots.ptr, num_slots=pool.max_slots)
+        call(model_library(), 'mt_decoder_layers', [P, P, I, P, P, P, P, P, P, I, I, I, I, F, I, I, P, ct.c_size_t, P],
+             self.blas().handle, w.layer_array, self.n_layer, buffers.x.ptr, buffers.h.ptr, w.ln_f[0].ptr,
+             w.ln_f[1].ptr, w.head.ptr, buffers.logits.ptr, self.n_vocab, b, d, self.n_head, self.ln_eps,
+             dtype_code(dtype), 1 if FUSED_GELU else 0, buffers.scratch.ptr, buffers.scratch_bytes, ct.byref(att))
+        paged_ops.row_argmax_feedback(buffers.ids.ptr, pool.slot_tokens.ptr, batch.device_slots.ptr,
+                                      pool.max_slots, buffers.logits.ptr, b, self.n_vocab, dtype)
+        return buffers.ids
 
     def _decode_batch(self, idx, caches, greedy):
         from .paged_decode import PagedDecodeBatch
@@ -379,6 +457,39 @@ class DecoderLM:
                                               pool.max_slots, logits.ptr, b, self.n_vocab, dtype)
             batch.commit()
             return ids if greedy else logits
+
+
+# Eager steps of a batch size before its decode step is captured: the
+# decoder loop times its projections' algorithms on the third call of a shape.
+GRAPH_WARMUP = 3
+
+
+class _CapturedStep:
+    """A captured decode step: the instantiated graph, the device buffers it
+    writes, and the objects whose memory it reads (kept alive, and compared
+    before each replay)."""
+
+    def __init__(self, exec_ptr, buffers, deps):
+        self.exec, self.buffers, self.deps = exec_ptr, buffers, deps
+
+    def matches(self, deps):
+        return len(deps) == len(self.deps) and all(a is b for a, b in zip(deps, self.deps))
+
+    def close(self):
+        if self.exec:
+            rt = runtime()
+            rt.check(rt.lib.mt_graph_destroy(self.exec))
+            self.exec = None
+
+
+class _StepBuffers:
+    def __init__(self, lib, b, d, n_vocab, dtype):
+        self.x = DeviceTensor((b, d), 'float32')
+        self.h = DeviceTensor((b, d), dtype)
+        self.scratch_bytes = _scratch_bytes(lib, b, d, dtype)
+        self.scratch = DeviceTensor(((self.scratch_bytes + 3) // 4,), 'float32')
+        self.logits = DeviceTensor((b, 1, n_vocab), dtype)
+        self.ids = DeviceTensor((b, 1), 'float32')
 
 
 def _scratch_bytes(lib, rows, d, dtype):

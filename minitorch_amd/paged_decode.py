@@ -16,8 +16,26 @@ from .runtime import RawDeviceBuffer, PinnedHostBuffer, DeviceTensor, runtime, P
 from . import paged_ops
 
 
+# Rows a graph-mode workspace is sized for (more when a batch is larger).
+GRAPH_ROWS = 256
+
+
+def _padded_work_list(work, items, merges, b, cap, split_tokens):
+    """A decode work list padded to the fixed length of a captured step:
+    b x ceil(cap / split) (row, split) entries, then b merge rows when a row
+    can span several splits; padding entries are -1 (skipped by the kernels)."""
+    nsplit_max = -(-cap // split_tokens)
+    items_pad, merges_pad = b * nsplit_max, (b if nsplit_max > 1 else 0)
+    out = np.full(2 * items_pad + merges_pad, -1, np.int32)
+    out[:2 * items] = work[:2 * items]
+    out[2 * items_pad:2 * items_pad + merges] = work[2 * items:2 * items + merges]
+    return out, items_pad, merges_pad
+
+
 class _DecodeWorkspace:
-    """Per-pool device buffers for decode metadata, grown on demand."""
+    """Per-pool device buffers for decode metadata, grown on demand, and the
+    captured decode steps (graphs) that use them: a graph holds their device
+    addresses, so every graph is released when a buffer is reallocated."""
 
     def __init__(self):
         self.rows = self.cols = self.work = 0
@@ -25,10 +43,18 @@ class _DecodeWorkspace:
         self.stagings = None
         self.partials = None
         self.partial_bytes = 0
+        self.graphs = {}          # batch size -> captured step
+        self.eager_steps = {}     # batch size -> eager steps run in graph mode
+
+    def release_graphs(self):
+        for step in self.graphs.values():
+            step.close()
+        self.graphs.clear()
 
     def ensure(self, rows, cols, work):
         if rows <= self.rows and cols <= self.cols and work <= self.work and self.buffer is not None:
             return
+        self.release_graphs()
         self.rows, self.cols, self.work = max(rows, self.rows), max(cols, self.cols), max(work, self.work)
         r, c = self.rows, self.cols
         # slots | work list | offsets | positions | cu_seqlens | new_page | table
@@ -48,6 +74,7 @@ class _DecodeWorkspace:
 
     def ensure_partials(self, nbytes):
         if nbytes > self.partial_bytes:
+            self.release_graphs()
             self.partials = RawDeviceBuffer(nbytes)
             self.partial_bytes = nbytes
         return self.partials.ptr if nbytes else None
@@ -57,7 +84,7 @@ class _DecodeWorkspace:
 
 
 class PagedDecodeBatch:
-    """Batched projections plus per-row paged attention on the null stream.
+    """Batched projections plus per-row paged attention on the default stream.
 
     Owns only transient metadata; the child caches keep their pages and
     committed lengths. A failed execution aborts every participating cache.
@@ -88,25 +115,49 @@ class PagedDecodeBatch:
         self._prepared, self._written_layers = [], set()
         self._committed = False
         self._device_prepared = False
+        self._graph = False
         self.last_attention_path = 'paged_batch_decode'
 
-    def _workspace(self, work_len):
+    def _workspace(self, work_len, rows=None):
         ws = getattr(self.pool, '_decode_workspace', None)
         if ws is None:
             ws = self.pool._decode_workspace = _DecodeWorkspace()
-        ws.ensure(self.batch_size, self.columns, work_len)
+        ws.ensure(rows or self.batch_size, self.columns, work_len)
         return ws
 
-    def prepare(self):
+    def prepare(self, *, graph=False):
+        """Upload the batch's slots and work list, then build the step's
+        metadata on the device and update the host mirrors.
+
+        With ``graph`` the metadata takes the fixed shapes a captured step
+        replays with: the table is [B, pool.max_cols] (the split length
+        follows from it), the work list is padded to B x (most splits a row
+        can have) entries, plus B merge rows when rows can split, with -1
+        rows that the kernels skip, the page budget is read from the pool
+        header on the device, and the workspace is sized for ``GRAPH_ROWS``
+        rows so that batches up to that size share it. The device half is
+        then left to ``prepare_device``, which the caller issues inside the
+        capture (or before replaying one)."""
         if self._prepared or self._committed:
             raise ValueError('Decode batch already executed')
         pool, b = self.pool, self.batch_size
+        self._graph = graph
+        if graph:
+            self.columns = pool.max_cols
+        heads = max(h for h, _ in self.layout)
         # Work list: every (row, split) longest first, balanced over the
         # compute units; the kernel writes each row to its own output row.
         self.split_tokens = paged_ops.split_tokens_for(page_size=pool.page_size, columns=self.columns)
         work, self.work_items, self.merge_rows = paged_ops.decode_work_list(
-            self.offsets + 1, max(h for h, _ in self.layout), self.split_tokens, runtime().compute_units())
-        ws = self._workspace(len(work))
+            self.offsets + 1, heads, self.split_tokens, runtime().compute_units())
+        rows = None
+        if graph:
+            rows = max(b, GRAPH_ROWS)
+            work, self.work_items, self.merge_rows = _padded_work_list(
+                work, self.work_items, self.merge_rows, b, self.columns * pool.page_size, self.split_tokens)
+            reserve = len(_padded_work_list(work[:0], 0, 0, rows, self.columns * pool.page_size,
+                                            self.split_tokens)[0])
+        ws = self._workspace(reserve if graph else len(work), rows)
         slots = np.array([c.slot for c in self.caches], np.int32)
         needs = (self.offsets % pool.page_size) == 0
         avail = pool.max_pages - pool._leased_count
@@ -115,11 +166,10 @@ class PagedDecodeBatch:
         w0 = int(ws.offsets[1]) // 4
         upload[w0:w0 + len(work)] = work
         ws.staging.upload_async(ws.ptr(0), upload[:w0 + len(work)])
-        pool._call('mt_sched_decode_prepare', [P, I, I, I, I, P, P, P, P, P],
-                   ws.ptr(0), b, self.columns, pool.page_size, avail, ws.ptr(6), ws.ptr(2),
-                   ws.ptr(3), ws.ptr(4), ws.ptr(5))
-        self._device_prepared = True
         self._ws = ws
+        self._limit = -1 if graph else avail
+        if not graph:
+            self.prepare_device()
         self.table = _DeviceView(ws.buffer, int(ws.offsets[6]), 4 * b * self.columns)
         self.device_slots = _DeviceView(ws.buffer, int(ws.offsets[0]), 4 * b)
         self.device_offsets = _DeviceView(ws.buffer, int(ws.offsets[2]), 4 * b)
@@ -127,7 +177,8 @@ class PagedDecodeBatch:
         self.work = _DeviceView(ws.buffer, int(ws.offsets[1]), 4 * len(work))
         self.position_ids = DeviceTensor((b, 1), 'float32', buffer=ws.buffer, byte_offset=int(ws.offsets[3]))
         # Host half, row by row like the reference (paged_decode.py:44-46):
-        # the row whose page would exceed the budget raises MemoryError.
+        # the row whose page would exceed the budget raises MemoryError (in
+        # graph mode before any device work of the step).
         pops = 0
         for cache, need in zip(self.caches, needs):
             self._prepared.append(cache)
@@ -138,6 +189,15 @@ class PagedDecodeBatch:
             if need:
                 pool._mirror_sequential_pops(1)
                 pops += 1
+
+    def prepare_device(self):
+        """``mt_sched_decode_prepare``: each row's new page from the device
+        free list, and the table, offsets, positions and cu_seqlens."""
+        ws, pool = self._ws, self.pool
+        pool._call('mt_sched_decode_prepare', [P, I, I, I, I, P, P, P, P, P],
+                   ws.ptr(0), self.batch_size, self.columns, pool.page_size, self._limit, ws.ptr(6), ws.ptr(2),
+                   ws.ptr(3), ws.ptr(4), ws.ptr(5))
+        self._device_prepared = True
 
     def decode_attention(self, layer, q, k, v):
         if self.table is None or layer in self._written_layers or not 0 <= layer < len(self.layout):
@@ -176,9 +236,16 @@ class PagedDecodeBatch:
         heads = max(h for h, _ in self.layout)
         partial_bytes = paged_ops.decode_workspace_bytes(b=self.batch_size, h=heads, page_size=pool.page_size,
                                                          columns=self.columns, split_tokens=self.split_tokens)
+        if self._graph:
+            # sized for the workspace's rows, so that batch sizes share it
+            partial_bytes = paged_ops.decode_workspace_bytes(b=self._ws.rows, h=heads, page_size=pool.page_size,
+                                                             columns=self.columns, split_tokens=self.split_tokens)
         partials = self._ws.ensure_partials(partial_bytes)
+        # A captured step must see pages of slabs opened after the capture:
+        # it bounds page IDs by the whole budget's slabs (all allocated).
+        slabs = pool.max_slabs if self._graph else pool.num_slabs
         return DecodeAttentionStruct(pool.slab_table.ptr, self.table.ptr, self.device_offsets.ptr,
-                                     pool.page_size, pool.pages_per_slab, pool.num_slabs, self.columns,
+                                     pool.page_size, pool.pages_per_slab, slabs, self.columns,
                                      len(self.layout), self.split_tokens, self.work.ptr, self.work_items,
                                      self.merge_rows, partials, partial_bytes)
 
@@ -190,12 +257,19 @@ class PagedDecodeBatch:
                 cache._written_layers.add(layer)
                 cache.last_attention_path = self.last_attention_path
 
-    def commit(self):
+    def commit_device(self):
+        """``mt_sched_add_length``: every row's committed length + 1 on the device."""
+        self.pool._call('mt_sched_add_length', [P, I, I], self._ws.ptr(0), self.batch_size, 1)
+
+    def commit(self, *, device=True):
+        """Commit every cache; ``device=False`` when the device half
+        (``commit_device``) ran already, inside a captured step."""
         if len(self._written_layers) != len(self.layout):
             raise ValueError('Cannot commit incomplete decode batch')
         if any(c._pending_tokens != 1 or len(c._written_layers) != len(c.layout) for c in self.caches):
             raise ValueError('Decode transaction modified during execution')
-        self.pool._call('mt_sched_add_length', [P, I, I], self._ws.ptr(0), self.batch_size, 1)
+        if device:
+            self.commit_device()
         for cache in self.caches:
             cache.commit_append(device=False)
         self._committed = True

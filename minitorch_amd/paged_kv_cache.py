@@ -253,6 +253,9 @@ class KVPagePool:
             return
         if self._leased_count:
             raise ValueError('Cannot close page pool while caches own pages')
+        ws = getattr(self, '_decode_workspace', None)
+        if ws is not None:
+            ws.release_graphs()      # captured decode steps hold this pool's addresses
         self._slabs.clear()
         self._free_issued.clear()
         for buffer in (self.kv, self.state, self.slot_ids, self._scratch, self._slot_tokens):

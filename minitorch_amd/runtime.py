@@ -1,7 +1,7 @@
 """Device runtime over the C-ABI: library loading, buffers, typed device arrays.
 
 Mirrors the reference's FFI layer (minitorch/cuda_storage.py:14-147,258-271;
-minitorch/cuda_resident_ops.py:33-47): one device, the null stream, ctypes
+minitorch/cuda_resident_ops.py:33-47): one device, one stream (the calling thread's default stream, where the libraries launch; the reference's legacy null stream), ctypes
 ``call(lib, name, argtypes, *args)`` that raises ``RuntimeError('CUDA: ...')``
 on a nonzero status, byte buffers for metadata and slabs, and events.
 Everything runs in ``cuda_kernels/*.so`` built from ``csrc/*.hip``; there is
@@ -47,6 +47,8 @@ class HipRuntime:
             'mt_device_count': [ct.POINTER(I)], 'mt_compute_units': [ct.POINTER(I)],
             'mt_host_alloc': [ct.POINTER(P), Z], 'mt_host_free': [P],
             'mt_fill_random': [P, ct.c_longlong, ct.c_ulonglong, I],
+            'mt_graph_begin': [], 'mt_graph_end': [ct.POINTER(P)], 'mt_graph_launch': [P],
+            'mt_graph_destroy': [P],
         }
         for name, args in signatures.items():
             f = getattr(self.lib, name)
@@ -89,7 +91,7 @@ class HipRuntime:
     def h2d(self, dst, array):
         """Copy a host array to device memory. Arrays up to STAGED_UPLOAD_BYTES
         are copied into pinned staging memory and uploaded asynchronously on
-        the null stream (stream-ordered before any later launch or read-back),
+        the default stream (stream-ordered before any later launch or read-back),
         so a small upload does not wait for the work already queued; larger
         ones use a blocking copy."""
         a = np.ascontiguousarray(array)
@@ -180,7 +182,7 @@ class CachingAllocator:
     hipFree synchronizes the device, so per-step tensors must not be freed to
     the driver. Blocks are rounded up to 256 bytes below 1 MiB and to powers of
     two above it (the reference's MemoryPool, minitorch/memory_pool.py:24-83,
-    uses powers of two). On the single null stream, a block released by the
+    uses powers of two). On the single stream, a block released by the
     host may be reused at once: later kernels run after every kernel that used
     the block before.
     """
@@ -284,7 +286,7 @@ class PinnedHostBuffer:
 
     def upload_async(self, dst, array):
         """Copy ``array`` into this staging buffer and enqueue its upload to ``dst``
-        on the null stream. Before overwriting the staging memory it waits for
+        on the default stream. Before overwriting the staging memory it waits for
         the previous upload from it to have run (normally long finished)."""
         a = np.ascontiguousarray(array)
         if a.nbytes > self.nbytes:

@@ -388,3 +388,41 @@ def test_prefill_key_splits_with_missing_pages():
     case.table[0, 40] = 10 ** 6     # keys 640..655
     got, ref = run_prefill(case, nq, offset + nq, offset, seed=9)
     assert np.isnan(ref[0, :, 160 - offset:]).all() and not np.isnan(ref[0, :, :160 - offset]).any()
+
+
+def key_split_launches():
+    import ctypes as ct
+    f = paged_ops.paged_library().mt_paged_prefill_key_splits
+    f.argtypes, f.restype = [ct.POINTER(ct.c_longlong)], ct.c_int
+    n = ct.c_longlong()
+    assert f(ct.byref(n)) == 0
+    return n.value
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+@pytest.mark.parametrize('heads,dim', [(12, 64), (16, 64), (12, 128), (16, 128)])
+def test_prefill_key_split_at_model_head_counts(heads, dim, dtype):
+    # The shapes the split is for: a 1024-token prompt of DistilGPT-2 (12
+    # heads; 16 tiles x 12 heads, B = 4 key blocks per split) and GPT-2-medium
+    # (16 heads; 256 workgroups, an odd B = 5), at head_dim 64 and 128, through
+    # mt_paged_attention (pages) and mt_paged_prefill (fused append); each
+    # must take the key-split path, checked with the library's counter.
+    nq = 1024
+    case = prefill_case(90 + heads + dim, batch=1, heads=heads, dim=dim, page_size=16, nk=nq, dtype=dtype,
+                        pages_per_slab=8)
+    before = key_split_launches()
+    run_prefill(case, nq, nq, 0, seed=heads + dim)
+    assert key_split_launches() == before + 1, 'mt_paged_attention did not split the keys'
+    run_fused_single(case, nq, 0, seed=heads + dim)
+    assert key_split_launches() == before + 2, 'mt_paged_prefill did not split the keys'
+
+
+def test_prefill_above_the_split_limit_stays_unsplit():
+    # 25 heads x 16 query tiles = 400 workgroups > 256 compute units: the
+    # prompt already fills the GPU, so it runs unsplit (and still matches)
+    nq, heads = 1024, 25
+    case = prefill_case(97, batch=1, heads=heads, dim=64, page_size=16, nk=nq, dtype='bfloat16', pages_per_slab=8)
+    before = key_split_launches()
+    run_prefill(case, nq, nq, 0, seed=97)
+    run_fused_single(case, nq, 0, seed=97)
+    assert key_split_launches() == before
