@@ -491,6 +491,9 @@ def e2e_config3(args, loops=('sync', 'sync-free')):
         # the same trace through the sync-free loop (device-side token feedback)
         e2e.run_config3(model, warm, precision='fp16', token_feedback=True, report_every=0)
         r['sync_free'] = e2e.run_config3(model, trace, precision='fp16', token_feedback=True)
+        # and with each decode step replayed from a HIP graph (one per batch size)
+        e2e.run_config3(model, warm, precision='fp16', token_feedback=True, graph=True, report_every=0)
+        r['graph'] = e2e.run_config3(model, trace, precision='fp16', token_feedback=True, graph=True)
     if not args.no_cpu_baseline:
         # the trace's mean decode batch, mid-generation contexts of its first requests
         batch = max(1, int(round((r.get('sync_free') or r).get('mean_decode_batch_size', 2))))
@@ -514,6 +517,8 @@ def e2e_config4(args, loops=('sync', 'sync-free')):
     r = e2e.run_config4(model, **kw) if 'sync' in loops else {}
     if 'sync-free' in loops:
         r['sync_free'] = e2e.run_config4(model, **kw, token_feedback=True)
+        # the sync-free loop with each decode step replayed from a HIP graph
+        r['graph'] = e2e.run_config4(model, **kw, token_feedback=True, graph=True)
     if not args.no_cpu_baseline:
         r['cpu_baseline'] = e2e_cpu_baseline(model, e2e.config4_lengths(np.random.default_rng([args.seed, 4]), 128),
                                              args.cpu_seconds, args.seed)
@@ -581,7 +586,7 @@ def e2e_summary(r3, r4):
     """The end-to-end figures of configs 3 and 4 for the default line."""
     out = {}
     if r3 is not None:
-        sf = r3.get('sync_free', {})
+        sf, gr = r3.get('sync_free', {}), r3.get('graph', {})
         out['config3'] = dict(
             workload=r3['workload'],
             decode_tokens_per_sec_reference_formula=r3.get('output_tokens_per_sec'),
@@ -590,19 +595,27 @@ def e2e_summary(r3, r4):
             sync_free=dict(decode_tokens_per_sec_reference_formula=sf.get('output_tokens_per_sec'),
                            busy_step_decode_tokens_per_sec=sf.get('busy_step_tokens_per_sec'),
                            ttft_p50_ms=sf.get('ttft_p50_ms')) if sf else None,
+            graph=dict(decode_tokens_per_sec_reference_formula=gr.get('output_tokens_per_sec'),
+                       busy_step_decode_tokens_per_sec=gr.get('busy_step_tokens_per_sec'),
+                       ttft_p50_ms=gr.get('ttft_p50_ms'), completed=gr.get('completed')) if gr else None,
             elapsed_seconds=r3.get('elapsed_seconds'), generated_tokens=r3.get('generated_tokens'),
             completed=r3.get('completed'), mean_decode_batch_size=r3.get('mean_decode_batch_size'),
             ttft_p50_ms=r3.get('ttft_p50_ms'), ttft_p95_ms=r3.get('ttft_p95_ms'),
             kv_pool_used_pages_after=r3.get('kv_pool_used_pages_after'),
             cpu_baseline=r3.get('cpu_baseline'))
     if r4 is not None:
-        sf = r4.get('sync_free', {})
+        sf, gr = r4.get('sync_free', {}), r4.get('graph', {})
         out['config4'] = dict(
             workload=r4['workload'],
             decode_tokens_per_sec=r4.get('decode_tokens_per_sec'), ms_per_decode_step=r4.get('ms_per_step'),
             loop_tokens_per_sec=r4.get('loop_tokens_per_sec'), loop_ms_per_step=r4.get('loop_ms_per_step'),
             sync_free=dict(loop_tokens_per_sec=sf.get('loop_tokens_per_sec'),
-                           loop_ms_per_step=sf.get('loop_ms_per_step')) if sf else None,
+                           loop_ms_per_step=sf.get('loop_ms_per_step'),
+                           decode_ms_per_step=sf.get('ms_per_step')) if sf else None,
+            graph=dict(decode_tokens_per_sec=gr.get('decode_tokens_per_sec'),
+                       decode_ms_per_step=gr.get('ms_per_step'),
+                       loop_tokens_per_sec=gr.get('loop_tokens_per_sec'),
+                       loop_ms_per_step=gr.get('loop_ms_per_step')) if gr else None,
             steps=r4.get('steps'), mean_context_tokens=r4.get('mean_context_tokens'),
             replaced_requests=r4.get('replaced_requests'), page_reuses=r4.get('page_reuses'),
             cpu_baseline=r4.get('cpu_baseline'))

@@ -20,7 +20,7 @@ import numpy as np
 from .continuous_batching import ContinuousBatcher
 from .kv_cache import greedy_token
 from .paged_kv_cache import KVPagePool
-from .runtime import DeviceTensor, runtime
+from .runtime import DeviceTensor, CudaEvent, runtime
 from .amp import autocast
 
 
@@ -120,8 +120,10 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
                 graph=False):
     """Steady-state decode throughput; returns a dict of measurements.
 
-    ``decode_tokens_per_sec`` (synchronous loop only) times each step's decode
-    up to its tokens on the host. ``loop_tokens_per_sec`` times the whole
+    ``decode_tokens_per_sec`` times each step's decode: in the synchronous
+    loop up to its tokens on the host (wall clock), in the sync-free loop
+    between events recorded on the stream before and after it (gaps the host
+    leaves in the stream included). ``loop_tokens_per_sec`` times the whole
     timed loop (decode steps plus the replacement prefills, synchronized only
     at its start and end), which is comparable between the synchronous loop
     and the sync-free one (``token_feedback``: tokens stay on the device as
@@ -168,7 +170,7 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
             new, first = admit([draw() for _ in range(min(32, concurrent - c0))])
             caches += new
             last += first
-        decode_seconds, tokens, replaced, context = 0.0, 0, 0, []
+        decode_seconds, tokens, replaced, context, step_events = 0.0, 0, 0, [], []
         loop0 = None
         for step in range(warmup + steps):
             context.append(sum(c.length + 1 for c in caches))
@@ -176,8 +178,15 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
                 rt.synchronize()
                 loop0 = time.perf_counter()
             if token_feedback:
+                if step >= warmup:
+                    # events around the decode step: its time on the device,
+                    # host-induced gaps included, replacement prefills not
+                    e0, e1 = CudaEvent(), CudaEvent()
+                    e0.record()
                 model.decode_greedy(caches, graph=graph)
                 if step >= warmup:
+                    e1.record()
+                    step_events.append((e0, e1))
                     tokens += len(caches)
             else:
                 ids = DeviceTensor.from_numpy(np.array(last, np.float32)[:, None])
@@ -205,6 +214,8 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
                 replaced += len(slots)
         rt.synchronize()
         loop_seconds = time.perf_counter() - loop0
+        if step_events:
+            decode_seconds = sum(e1.seconds_since(e0) for e0, e1 in step_events)
         stats = pool.memory_stats()
         for c in caches:
             c.close()
