@@ -250,10 +250,11 @@ int mt_fill_words(void* p, size_t words, unsigned int value) {
 // hash of (seed, index), uniform in [-2, 2): synthetic K/V for large pools.
 // Reads `count` chunks of `chunk_bytes` (a multiple of 1 KiB) whose addresses
 // are listed in `chunks`, each wave taking chunks wave, wave + waves, ...,
-// and XORs what it read into sink[0] only if the XOR equals a sentinel (so the
-// loads cannot be dropped and nothing is written in practice). A measuring
-// kernel: the bandwidth of exactly the K/V access pattern of a decode step,
-// with no address arithmetic, math or merging.
+// with non-temporal 16-byte loads (as the decode kernel reads K/V), and XORs
+// what it read into sink[0] only if the XOR equals a sentinel (so the loads
+// cannot be dropped and nothing is written in practice). A measuring kernel:
+// the bandwidth of exactly the K/V access pattern of a decode step, with no
+// address arithmetic, math or merging.
 __global__ __launch_bounds__(256) void chunk_read_kernel(const unsigned long long* chunks, int count,
                                                           int vec_per_chunk, unsigned* sink) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(256) void chunk_read_kernel(const unsigned long lon
   for (int c = wave; c < count; c += waves) {
     const auto* p = reinterpret_cast<const __attribute__((address_space(1))) u32x4*>(chunks[c]);
     for (int v = lane; v < vec_per_chunk; v += 64) {
-      const u32x4 x = p[v];
+      const u32x4 x = __builtin_nontemporal_load(p + v);  // as the decode kernel loads K/V
       acc ^= x.x ^ x.y ^ x.z ^ x.w;
     }
   }
