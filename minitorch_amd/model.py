@@ -376,7 +376,14 @@ class DecoderLM:
                 step.close()
                 del ws.graphs[b]
                 step = None
-            if step is None and ws.eager_steps.get(b, 0) < GRAPH_WARMUP:
+            if step is None and ws.eager_steps.get(b, 0) >= GRAPH_WARMUP and b not in ws.uncapturable:
+                try:
+                    step = ws.graphs[b] = self._capture_decode(batch, w, att, deps)
+                except RuntimeError:
+                    # this batch size keeps running eagerly (the capture was
+                    # ended and discarded; nothing of it ran)
+                    ws.uncapturable.add(b)
+            if step is None:
                 ws.eager_steps[b] = ws.eager_steps.get(b, 0) + 1
                 batch.prepare_device()
                 ids = self._issue_decode(batch, w, att, _StepBuffers(model_library(), b, self.n_embd,
@@ -384,8 +391,6 @@ class DecoderLM:
                 batch.mark_layers_written()
                 batch.commit()
                 return ids
-            if step is None:
-                step = ws.graphs[b] = self._capture_decode(batch, w, att, deps)
             rt.check(rt.lib.mt_graph_launch(step.exec))
             batch._device_prepared = True
             batch.mark_layers_written()

@@ -45,6 +45,7 @@ class _DecodeWorkspace:
         self.partial_bytes = 0
         self.graphs = {}          # batch size -> captured step
         self.eager_steps = {}     # batch size -> eager steps run in graph mode
+        self.uncapturable = set()  # batch sizes whose capture failed: eager from then on
 
     def release_graphs(self):
         for step in self.graphs.values():

@@ -125,3 +125,21 @@ def test_graph_distilgpt2_shape_replays():
     for k in range(steps):
         assert np.array_equal(eager[0][k], graph[0][k]), f'step {k}'
         assert eager[1][k] == graph[1][k], f'step {k}: pages differ'
+
+
+def test_failed_capture_falls_back_to_eager_steps(monkeypatch):
+    # A capture that fails (forced from the host here) leaves that batch size
+    # running eagerly, with the eager loop's tokens and pages.
+    model = tiny(seed=49)
+
+    def refuse(*args, **kwargs):
+        raise RuntimeError('CUDA: operation not permitted when stream is capturing')
+
+    steps = GRAPH_WARMUP + 4
+    eager = steady_loop(model, False, steps, seed=49)
+    monkeypatch.setattr(model, '_capture_decode', refuse)
+    fallback = steady_loop(model, True, steps, seed=49)
+    assert fallback[3] == 0
+    for k in range(steps):
+        assert np.array_equal(eager[0][k], fallback[0][k]), f'step {k}'
+        assert eager[1][k] == fallback[1][k]
