@@ -111,6 +111,29 @@ int mt_gemm_epilogue(void* handle, void* out, const void* a, const void* b, cons
 int mt_residual_layernorm(void* out, float* x, const void* y, const float* gamma, const float* beta,
                           int rows, int width, float eps, int dtype);
 
+/* Decode projection on the matrix cores for fp16/bf16 (dtype 1/2):
+ * out = epilogue(x[m, k] @ w[n, k]^T) with fp32 accumulation, for
+ * 1 <= m <= 256 rows. epilogue 0: + bias[n] (bias in dtype, may be null),
+ * out [m, n] in dtype; 1: + bias, then tanh GELU in fp32, out in dtype;
+ * 2: out [splits, m, n] fp32 partial sums over `splits` (1, 2, 4 or 8)
+ * equal k ranges, no bias (epilogues 0 and 1 take splits = 1). Requires n a
+ * multiple of 16, k a multiple of 128 * splits, x and w 16-byte aligned, out
+ * 8-byte (16-byte for epilogue 2) aligned; hipErrorInvalidValue otherwise.
+ * Weights are read once per call. No reference counterpart (the reference's
+ * Linear, minitorch/modules_basic.py:132-149, calls cuBLAS). */
+int mt_decode_projection(void* out, const void* x, const void* w, const void* bias, int m, int n, int k,
+                         int splits, int epilogue, int dtype);
+
+/* x[r, :] += bias + sum_s partials[s, r, :] (fp32), then out[r, :] =
+ * LayerNorm(x[r, :]) in dtype (1 or 2): the residual add and LayerNorm after
+ * a split projection (mt_decode_projection epilogue 2), as
+ * mt_residual_layernorm. width a multiple of 256, at most 2048; 1 <= splits
+ * <= 8. No reference counterpart (minitorch/modules_transformer.py:272-282
+ * with the projection's split-k reduction folded in). */
+int mt_residual_layernorm_partials(void* out, float* x, const float* partials, int splits, const void* bias,
+                                   const float* gamma, const float* beta, int rows, int width, float eps,
+                                   int dtype);
+
 /* Scratch bytes mt_decoder_layers needs for `rows` tokens of width d. */
 size_t mt_decoder_scratch_bytes(int rows, int d, int dtype);
 
@@ -123,8 +146,14 @@ size_t mt_decoder_scratch_bytes(int rows, int d, int dtype);
  * (final_gamma/final_beta). x [rows, d] fp32 is the residual stream, updated
  * in place; h [rows, d] in dtype receives the final LayerNorm output and,
  * when logits is not null, logits [rows, vocab] = h @ head_weight^T (the tied
- * head, head_weight [vocab, d]). The projections of this loop choose their
- * hipBLASLt algorithm by timing (cold caches) on the third call of a shape.
+ * head, head_weight [vocab, d]). For fp16/bf16 the layer projections run on
+ * mt_decode_projection where it takes their shapes: the QKV and fc
+ * projections for rows <= 16, the out- and proj-projections (as split-k
+ * partial sums reduced by mt_residual_layernorm_partials, d a multiple of
+ * 256) for rows <= 32. Larger batches, fp32, other shapes and
+ * MT_DECODE_PROJECTIONS=0 in the environment use hipBLASLt, which chooses its
+ * algorithm by timing (cold caches) on the third call of a shape, as does the
+ * tied head.
  * Replaces the reference's per-op layer loop of DecoderLM.decode_batch
  * (minitorch/modules_transformer.py:373-390,258-284). */
 int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,

@@ -444,6 +444,349 @@ __global__ __launch_bounds__(256) void gelu_kernel(void* x, int64_t n) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode projections on the matrix cores: out[m, n] = x[m, :] . w[n, :] for
+// the few rows of a decode step (m <= kProjMaxRows) against weights stored
+// [n, k] (fp16/bf16, fp32 accumulation). At these row counts a projection
+// moves a few MB (the weights, read once) through short chains of dependent
+// loads, so the kernel is built for memory-level parallelism: many waves,
+// each with a short k range whose loads are all issued before its first
+// MFMA, instead of long per-wave k loops that wait one memory latency per
+// step.
+//
+// C^T = W X^T on v_mfma_f32_16x16x32: A = 16 weight rows, B = 16 activation
+// rows, both contiguous along k and loaded 16 bytes per lane straight from
+// global memory; lane (c, g) ends up holding C^T[4g + i][c], i.e. 4
+// consecutive features of one row. A workgroup owns 16 features, up to 128
+// rows (blockIdx.z selects the block of 128) and k range blockIdx.y of
+// `splits`; its WK waves (blockDim.x / 64) split that range into kc-wide
+// pieces of at most SMAX 32-wide steps, and their sums meet in LDS. Weights
+// are read with non-temporal loads (a step's weights do not fit the caches);
+// the activations, which every workgroup reads, stay cached.
+//
+// Epilogues: kProjBias: + bias (type T) -> T; kProjGelu: + bias, tanh GELU
+// in fp32 -> T; kProjPartials: the fp32 sums of split blockIdx.y into
+// out[split][m][n] (no bias), which residual_layernorm_partials_kernel adds
+// into the residual stream together with the bias.
+constexpr int kProjMaxRows = 256;
+constexpr int kProjMaxSplits = 8;
+constexpr int kProjMaxWaves = 16;
+constexpr int kProjRowBlock = 128;  // rows per workgroup (8 tiles of 16)
+// Row counts up to which the decode step uses this kernel rather than
+// hipBLASLt (measured on MI355X, captured DistilGPT-2 and GPT-2-medium decode
+// steps): every compute unit takes in all m * k activation bytes of an
+// unsplit projection, which from 32 rows on costs as much as hipBLASLt's
+// tiling; the split projections plus their LayerNorm reduction stay ahead to
+// 32 rows and fall behind by 64.
+constexpr int kProjDirectRows = 16;
+constexpr int kProjSplitRows = 32;
+enum ProjEpilogue : int { kProjBias = 0, kProjGelu = 1, kProjPartials = 2 };
+
+struct ProjArgs {
+  void* out;
+  const void* x;
+  const void* w;
+  const void* bias;
+  int m, n, k;
+  int kc;  // k per wave: k / (splits * waves), a multiple of 32, at most 32 * SMAX
+};
+
+__device__ __forceinline__ float gelu_tanh(float v) {
+  const float c = 0.7978845608028654f;
+  return 0.5f * v * (1.f + tanhf(c * (v + 0.044715f * v * v * v)));
+}
+
+// Steps of 32 a wave may hold in flight: 2 with 8 row tiles (the loads and
+// accumulators then fill the 128 registers a 16-wave workgroup allows), 4
+// with fewer.
+template <int MT>
+constexpr int proj_max_steps() { return MT >= 8 ? 2 : 4; }
+
+template <int DT, int MT, int EPI>
+__global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
+  using T = typename Elem<DT>::T;
+  using V8 = typename Mfma<DT>::v8;
+  constexpr int SMAX = proj_max_steps<MT>();
+  constexpr int NL = 1 + MT;  // 16-byte loads per lane and step
+  extern __shared__ floatx4 red[];  // [waves][MT][64]
+  const int waves = int(blockDim.x >> 6);
+  const int wave = int(threadIdx.x >> 6), lane = int(threadIdx.x & 63);
+  const int col = lane & 15, grp = lane >> 4;
+  const int f0 = int(blockIdx.x) * 16;
+  const int r0 = int(blockIdx.z) * kProjRowBlock;
+  const int k0 = (int(blockIdx.y) * waves + wave) * p.kc + 8 * grp;
+  const int steps = p.kc >> 5;
+  const T* w = static_cast<const T*>(p.w) + int64_t(f0 + col) * p.k + k0;
+  const T* x = static_cast<const T*>(p.x);
+  int xoff[MT];  // element offsets of this lane's activation rows (rows past m repeat row m - 1)
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int row = r0 + 16 * t + col < p.m ? r0 + 16 * t + col : p.m - 1;
+    xoff[t] = row * p.k + k0;
+  }
+  u32x4 buf[SMAX][NL];
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    if (s < steps) {
+      buf[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + 32 * s));
+#pragma unroll
+      for (int t = 0; t < MT; ++t) buf[s][1 + t] = *global_view(reinterpret_cast<const u32x4*>(x + xoff[t] + 32 * s));
+    }
+  }
+  floatx4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    if (s < steps) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        acc[t] = Mfma<DT>::run(__builtin_bit_cast(V8, buf[s][0]), __builtin_bit_cast(V8, buf[s][1 + t]), acc[t]);
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < MT; ++t) red[(wave * MT + t) * 64 + lane] = acc[t];
+  __syncthreads();
+  for (int t = wave; t < MT; t += waves) {
+    floatx4 a = red[t * 64 + lane];
+    for (int v = 1; v < waves; ++v) {
+      const floatx4 b = red[(v * MT + t) * 64 + lane];
+      a[0] += b[0]; a[1] += b[1]; a[2] += b[2]; a[3] += b[3];
+    }
+    const int row = r0 + 16 * t + col;
+    if (row >= p.m) continue;
+    const int feat = f0 + 4 * grp;
+    float v[4] = {a[0], a[1], a[2], a[3]};
+    if constexpr (EPI == kProjPartials) {
+      float* o = static_cast<float*>(p.out) + (int64_t(blockIdx.y) * p.m + row) * p.n + feat;
+      *reinterpret_cast<float4*>(o) = float4{v[0], v[1], v[2], v[3]};
+    } else {
+      if (p.bias) {
+        const uint2 b = *reinterpret_cast<const uint2*>(static_cast<const T*>(p.bias) + feat);
+        v[0] += to_f32<DT>(T(b.x & 0xffffu)); v[1] += to_f32<DT>(T(b.x >> 16));
+        v[2] += to_f32<DT>(T(b.y & 0xffffu)); v[3] += to_f32<DT>(T(b.y >> 16));
+      }
+      if constexpr (EPI == kProjGelu) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = gelu_tanh(v[i]);
+      }
+      T* o = static_cast<T*>(p.out) + int64_t(row) * p.n + feat;
+      *reinterpret_cast<uint2*>(o) =
+          uint2{uint32_t(from_f32<DT>(v[0])) | (uint32_t(from_f32<DT>(v[1])) << 16),
+                uint32_t(from_f32<DT>(v[2])) | (uint32_t(from_f32<DT>(v[3])) << 16)};
+    }
+  }
+}
+
+// x[r, :] += bias + sum over the S splits of partials[s, r, :] (fp32);
+// out[r, :] = LayerNorm(x[r, :]) in T. One wave per row, as
+// residual_layernorm_wave_kernel; every load of a row (x, bias, the S
+// partials, which other XCDs wrote) is issued before the first add.
+template <int DT, int NJ, int S>
+__global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* out, float* x, const float* part,
+                                                                          const void* bias, const float* gamma,
+                                                                          const float* beta, int rows, int width,
+                                                                          float eps) {
+  using T = typename Elem<DT>::T;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nj = width >> 8;
+  float* xr = x + int64_t(row) * width;
+  const int64_t split_stride = int64_t(rows) * width;
+  const float* pr = part + int64_t(row) * width;
+  float4 v[NJ], q[NJ][S];
+  uint2 b[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (j < nj) {
+      const int c = 256 * j + 4 * lane;
+      v[j] = *reinterpret_cast<const float4*>(xr + c);
+      b[j] = bias ? *reinterpret_cast<const uint2*>(static_cast<const T*>(bias) + c) : uint2{0u, 0u};
+#pragma unroll
+      for (int s = 0; s < S; ++s) q[j][s] = *reinterpret_cast<const float4*>(pr + s * split_stride + c);
+    }
+  }
+  float sum = 0.f, sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (j >= nj) break;
+    const int c = 256 * j + 4 * lane;
+    v[j].x += to_f32<DT>(T(b[j].x & 0xffffu)); v[j].y += to_f32<DT>(T(b[j].x >> 16));
+    v[j].z += to_f32<DT>(T(b[j].y & 0xffffu)); v[j].w += to_f32<DT>(T(b[j].y >> 16));
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      v[j].x += q[j][s].x; v[j].y += q[j][s].y; v[j].z += q[j][s].z; v[j].w += q[j][s].w;
+    }
+    *reinterpret_cast<float4*>(xr + c) = v[j];
+    sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    sq += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    sum += __shfl_xor(sum, off);
+    sq += __shfl_xor(sq, off);
+  }
+  const float mean = sum / width;
+  const float var = fmaxf(sq / width - mean * mean, 0.f) + eps;
+  const float inv = 1.f / sqrtf(var);
+  T* o = static_cast<T*>(out) + int64_t(row) * width;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (j >= nj) break;
+    const int c = 256 * j + 4 * lane;
+    const float4 g = *reinterpret_cast<const float4*>(gamma + c);
+    const float4 b = *reinterpret_cast<const float4*>(beta + c);
+    const float r0 = g.x * ((v[j].x - mean) * inv) + b.x;
+    const float r1 = g.y * ((v[j].y - mean) * inv) + b.y;
+    const float r2 = g.z * ((v[j].z - mean) * inv) + b.z;
+    const float r3 = g.w * ((v[j].w - mean) * inv) + b.w;
+    *reinterpret_cast<uint2*>(o + c) =
+        uint2{uint32_t(from_f32<DT>(r0)) | (uint32_t(from_f32<DT>(r1)) << 16),
+              uint32_t(from_f32<DT>(r2)) | (uint32_t(from_f32<DT>(r3)) << 16)};
+  }
+}
+
+bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; }
+
+// Row tiles of 16 a workgroup holds for m rows (m > 128 takes blocks of 128).
+int proj_row_tiles(int m) { return m <= 16 ? 1 : m <= 32 ? 2 : m <= 64 ? 4 : 8; }
+
+// Waves per workgroup for a k range of `range` per split: the most (at most
+// kProjMaxWaves) that leave each wave a whole number of 32-wide steps, at most
+// as many as it can hold in flight; 0 if none does.
+int proj_waves(int range, int mt) {
+  const int smax = mt >= 8 ? proj_max_steps<8>() : proj_max_steps<4>();
+  for (int wv = kProjMaxWaves; wv >= 1; --wv)
+    if (range % (32 * wv) == 0 && range / (32 * wv) <= smax) return wv;
+  return 0;
+}
+
+// Whether the decode projection kernel takes out = epi(x [m, k] @ w[n, k]^T):
+// fp16/bf16, m <= kProjMaxRows, n a multiple of 16, k split into `splits`
+// ranges that some wave count divides into short whole-step pieces, 16-byte
+// aligned rows.
+bool projection_ok(const void* out, const void* x, const void* w, const void* bias, int m, int n, int k,
+                   int splits, int epilogue, int dtype) {
+  if (dtype != kF16 && dtype != kBF16) return false;
+  if (m < 1 || m > kProjMaxRows || n < 16 || n % 16 || k < 32) return false;
+  if (splits != 1 && splits != 2 && splits != 4 && splits != 8) return false;
+  if (epilogue < 0 || epilogue > kProjPartials || (epilogue != kProjPartials && splits != 1)) return false;
+  if (k % splits || proj_waves(k / splits, proj_row_tiles(m)) == 0) return false;
+  if (int64_t(m) * k > INT32_MAX || int64_t(n) * k > INT32_MAX || int64_t(splits) * m * n > INT32_MAX) return false;
+  return out && x && w && aligned(x, 16) && aligned(w, 16) && aligned(out, epilogue == kProjPartials ? 16 : 8) &&
+         (!bias || aligned(bias, 8));
+}
+
+// MT_DECODE_PROJECTIONS=0 sends the decode step's projections to hipBLASLt.
+bool decode_projections_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("MT_DECODE_PROJECTIONS");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
+// Splits of k for an [m, n] x [n, k] projection whose partial sums are
+// reduced downstream: the fewest that give at least one workgroup per compute
+// unit (n / 16 feature tiles per split), while the projection kernel still
+// takes each split's range.
+int projection_splits(int m, int n, int k) {
+  static const int cus = [] {
+    int dev = 0, c = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c < 1)
+      c = 256;
+    return c;
+  }();
+  const int tiles = n / 16 * ((m + kProjRowBlock - 1) / kProjRowBlock);
+  const int mt = proj_row_tiles(m);
+  auto takes = [&](int s) { return k % s == 0 && proj_waves(k / s, mt) > 0; };
+  int s = 1;
+  while (s < kProjMaxSplits && !takes(s)) s *= 2;
+  while (s < kProjMaxSplits && int64_t(tiles) * s < cus && takes(2 * s)) s *= 2;
+  return s;
+}
+
+template <int DT, int MT, int EPI>
+void launch_projection_mt(ProjArgs a, int splits) {
+  const int waves = proj_waves(a.k / splits, MT);
+  a.kc = a.k / (splits * waves);
+  const dim3 grid(unsigned(a.n / 16), unsigned(splits), unsigned((a.m + kProjRowBlock - 1) / kProjRowBlock));
+  projection_kernel<DT, MT, EPI><<<grid, 64 * waves, size_t(waves) * MT * 64 * sizeof(floatx4)>>>(a);
+}
+
+template <int DT, int EPI>
+void launch_projection_epi(const ProjArgs& a, int splits) {
+  const int mt = proj_row_tiles(a.m);
+  if (mt == 1) launch_projection_mt<DT, 1, EPI>(a, splits);
+  else if (mt == 2) launch_projection_mt<DT, 2, EPI>(a, splits);
+  else if (mt == 4) launch_projection_mt<DT, 4, EPI>(a, splits);
+  else launch_projection_mt<DT, 8, EPI>(a, splits);
+}
+
+// Caller has checked projection_ok.
+hipError_t projection(void* out, const void* x, const void* w, const void* bias, int m, int n, int k, int splits,
+                      int epilogue, int dtype) {
+  ProjArgs a{};
+  a.out = out; a.x = x; a.w = w; a.bias = bias;
+  a.m = m; a.n = n; a.k = k;
+  if (dtype == kF16) {
+    if (epilogue == kProjBias) launch_projection_epi<kF16, kProjBias>(a, splits);
+    else if (epilogue == kProjGelu) launch_projection_epi<kF16, kProjGelu>(a, splits);
+    else launch_projection_epi<kF16, kProjPartials>(a, splits);
+  } else {
+    if (epilogue == kProjBias) launch_projection_epi<kBF16, kProjBias>(a, splits);
+    else if (epilogue == kProjGelu) launch_projection_epi<kBF16, kProjGelu>(a, splits);
+    else launch_projection_epi<kBF16, kProjPartials>(a, splits);
+  }
+  return hipGetLastError();
+}
+
+// Whether residual_layernorm_partials takes the row shape (width a multiple of
+// 256, at most 2048, 16-byte aligned rows).
+bool partials_ln_ok(const void* out, const float* x, const float* part, const void* bias, const float* gamma,
+                    const float* beta, int width, int dtype) {
+  return (dtype == kF16 || dtype == kBF16) && width % 256 == 0 && width <= 2048 && aligned(x, 16) &&
+         aligned(part, 16) && aligned(gamma, 16) && aligned(beta, 16) && aligned(out, 8) && (!bias || aligned(bias, 8));
+}
+
+template <int DT, int S>
+void launch_partials_ln(void* out, float* x, const float* part, const void* bias, const float* gamma,
+                        const float* beta, int rows, int width, float eps) {
+  constexpr int R = 4;  // rows (waves) per workgroup
+  const int blocks = (rows + R - 1) / R;
+  if (width <= 1024)
+    residual_layernorm_partials_kernel<DT, 4, S><<<blocks, 64 * R>>>(out, x, part, bias, gamma, beta, rows, width, eps);
+  else
+    residual_layernorm_partials_kernel<DT, 8, S><<<blocks, 64 * R>>>(out, x, part, bias, gamma, beta, rows, width, eps);
+}
+
+template <int DT>
+void launch_partials_ln_dt(void* out, float* x, const float* part, int splits, const void* bias, const float* gamma,
+                           const float* beta, int rows, int width, float eps) {
+  switch (splits) {
+    case 1: launch_partials_ln<DT, 1>(out, x, part, bias, gamma, beta, rows, width, eps); break;
+    case 2: launch_partials_ln<DT, 2>(out, x, part, bias, gamma, beta, rows, width, eps); break;
+    case 3: launch_partials_ln<DT, 3>(out, x, part, bias, gamma, beta, rows, width, eps); break;
+    case 4: launch_partials_ln<DT, 4>(out, x, part, bias, gamma, beta, rows, width, eps); break;
+    case 5: launch_partials_ln<DT, 5>(out, x, part, bias, gamma, beta, rows, width, eps); break;
+    case 6: launch_partials_ln<DT, 6>(out, x, part, bias, gamma, beta, rows, width, eps); break;
+    case 7: launch_partials_ln<DT, 7>(out, x, part, bias, gamma, beta, rows, width, eps); break;
+    default: launch_partials_ln<DT, 8>(out, x, part, bias, gamma, beta, rows, width, eps); break;
+  }
+}
+
+// Caller has checked partials_ln_ok and 1 <= splits <= kProjMaxSplits.
+hipError_t residual_layernorm_partials(void* out, float* x, const float* part, int splits, const void* bias,
+                                       const float* gamma, const float* beta, int rows, int width, float eps,
+                                       int dtype) {
+  if (dtype == kF16) launch_partials_ln_dt<kF16>(out, x, part, splits, bias, gamma, beta, rows, width, eps);
+  else launch_partials_ln_dt<kBF16>(out, x, part, splits, bias, gamma, beta, rows, width, eps);
+  return hipGetLastError();
+}
+
 // x[i] += y[i] with fp32 x (the residual stream) and y in its own type.
 template <int DT>
 __global__ __launch_bounds__(256) void residual_kernel(float* x, const void* y, int64_t n) {
@@ -743,12 +1086,29 @@ int mt_residual_layernorm(void* out, float* x, const void* y, const float* gamma
   return residual_layernorm(out, x, y, gamma, beta, rows, width, eps, dtype);
 }
 
+int mt_decode_projection(void* out, const void* x, const void* w, const void* bias, int m, int n, int k,
+                         int splits, int epilogue, int dtype) {
+  if (!projection_ok(out, x, w, bias, m, n, k, splits, epilogue, dtype)) return hipErrorInvalidValue;
+  return projection(out, x, w, bias, m, n, k, splits, epilogue, dtype);
+}
+
+int mt_residual_layernorm_partials(void* out, float* x, const float* partials, int splits, const void* bias,
+                                   const float* gamma, const float* beta, int rows, int width, float eps,
+                                   int dtype) {
+  if (!out || !x || !partials || !gamma || !beta || rows < 1 || splits < 1 || splits > kProjMaxSplits ||
+      int64_t(splits) * rows * width > INT32_MAX || !partials_ln_ok(out, x, partials, bias, gamma, beta, width, dtype))
+    return hipErrorInvalidValue;
+  return residual_layernorm_partials(out, x, partials, splits, bias, gamma, beta, rows, width, eps, dtype);
+}
+
 size_t mt_decoder_scratch_bytes(int rows, int d, int dtype) {
   if (rows < 1 || d < 1 || !dtype_ok(dtype)) return 0;
   const size_t e = dtype == kF32 ? 4 : 2;
-  // qkv [rows, 3d] | attention [rows, d] | projection [rows, d] | mlp [rows, 4d], each 256-aligned
+  // qkv [rows, 3d] | attention [rows, d] | projection [rows, d] | mlp [rows, 4d] | (fp16/bf16 and
+  // rows <= kProjSplitRows) fp32 split partials [kProjMaxSplits, rows, d], each 256-aligned
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-  return al(size_t(rows) * 3 * d * e) + 2 * al(size_t(rows) * d * e) + al(size_t(rows) * 4 * d * e);
+  const size_t partials = dtype != kF32 && rows <= kProjSplitRows ? al(size_t(kProjMaxSplits) * rows * d * 4) : 0;
+  return al(size_t(rows) * 3 * d * e) + 2 * al(size_t(rows) * d * e) + al(size_t(rows) * 4 * d * e) + partials;
 }
 
 int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
@@ -769,24 +1129,47 @@ int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
   char* attn = qkv + al(size_t(rows) * 3 * d * e);
   char* proj = attn + al(size_t(rows) * d * e);
   char* mlp = proj + al(size_t(rows) * d * e);
+  float* partials = dtype != kF32 && rows <= kProjSplitRows
+                        ? reinterpret_cast<float*>(mlp + al(size_t(rows) * 4 * d * e)) : nullptr;
   const int hd = d / heads;
+  const bool own = decode_projections_enabled();
+  // out = epi(in @ wt^T + b): the decode projection kernel where it takes
+  // the shape, else hipBLASLt.
+  auto project = [&](void* out, const void* in, const void* wt, const void* b, int n, int k, int epi) -> int {
+    if (own && rows <= kProjDirectRows && projection_ok(out, in, wt, b, rows, n, k, 1, epi, dtype))
+      return projection(out, in, wt, b, rows, n, k, 1, epi, dtype);
+    if (epi == kProjGelu) return gemm_gelu(blas, out, in, wt, b, rows, n, k, dtype, fused_gelu != 0, true, 1);
+    return gemm(blas, out, in, wt, b, rows, n, k, 1, dtype, dtype, kEpiNone, true);
+  };
+  // x += in @ wt^T + b, then h = LayerNorm(x): split-k partial sums that the
+  // LayerNorm kernel adds up, or one projection and residual_layernorm.
+  auto project_residual = [&](const void* in, const void* wt, const void* b, int k, const float* g,
+                              const float* be) -> int {
+    const int s = projection_splits(rows, d, k);
+    if (own && partials && rows <= kProjSplitRows &&
+        projection_ok(partials, in, wt, nullptr, rows, d, k, s, kProjPartials, dtype) &&
+        partials_ln_ok(h, x, partials, b, g, be, d, dtype)) {
+      const int st = projection(partials, in, wt, nullptr, rows, d, k, s, kProjPartials, dtype);
+      return st ? st : residual_layernorm_partials(h, x, partials, s, b, g, be, rows, d, eps, dtype);
+    }
+    const int st = project(proj, in, wt, b, d, k, kProjBias);
+    return st ? st : residual_layernorm(h, x, proj, g, be, rows, d, eps, dtype);
+  };
   int st = layernorm(h, x, layers[0].ln1_gamma, layers[0].ln1_beta, rows, d, eps, dtype);
   for (int i = 0; i < n_layer && !st; ++i) {
     const mt_decoder_layer& L = layers[i];
-    if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 1, dtype, dtype, kEpiNone, true))) break;
+    if ((st = project(qkv, h, L.w_qkv, L.b_qkv, 3 * d, d, kProjBias))) break;
     if ((st = mt_paged_decode_split(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, att->slabs,
                                     att->table, att->offsets, rows, heads, hd, att->page_size,
                                     att->pages_per_slab, att->num_slabs, att->columns, i, att->layers,
                                     dtype, att->split_tokens, 0, 0, 3 * d, att->work, att->work_items,
                                     att->merge_rows, att->partials, att->partial_bytes)))
       break;
-    if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 1, dtype, dtype, kEpiNone, true))) break;
-    if ((st = residual_layernorm(h, x, proj, L.ln2_gamma, L.ln2_beta, rows, d, eps, dtype))) break;
-    if ((st = gemm_gelu(blas, mlp, h, L.w_fc, L.b_fc, rows, 4 * d, d, dtype, fused_gelu != 0, true, 1))) break;
-    if ((st = gemm(blas, proj, mlp, L.w_proj, L.b_proj, rows, d, 4 * d, 1, dtype, dtype, kEpiNone, true))) break;
+    if ((st = project_residual(attn, L.w_o, L.b_o, d, L.ln2_gamma, L.ln2_beta))) break;
+    if ((st = project(mlp, h, L.w_fc, L.b_fc, 4 * d, d, kProjGelu))) break;
     const bool last = i + 1 == n_layer;
-    st = residual_layernorm(h, x, proj, last ? final_gamma : layers[i + 1].ln1_gamma,
-                            last ? final_beta : layers[i + 1].ln1_beta, rows, d, eps, dtype);
+    st = project_residual(mlp, L.w_proj, L.b_proj, 4 * d, last ? final_gamma : layers[i + 1].ln1_gamma,
+                          last ? final_beta : layers[i + 1].ln1_beta);
   }
   // Tied head: logits [rows, vocab] = h @ head_weight^T (head_weight [vocab, d]).
   if (!st && logits)

@@ -97,4 +97,26 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* global_view(T* p
   return (__attribute__((address_space(1))) T*)(p);
 }
 
+// v_mfma_f32_16x16x32 (fp16/bf16 in, fp32 accumulate). Lane l (column
+// c = l % 16, group g = l / 16) supplies A[c][8g .. 8g+7] and B[8g .. 8g+7][c]
+// and holds C[4g + i][c], i < 4.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+struct Mfma;
+template <>
+struct Mfma<kF16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ floatx4 run(const v8& a, const v8& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<kBF16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ floatx4 run(const v8& a, const v8& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
 }  // namespace mt

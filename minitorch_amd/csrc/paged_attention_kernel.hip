@@ -922,25 +922,6 @@ constexpr int kPfWindowPages = 512;  // page bases resolved into LDS at a time
 #endif
 constexpr int kPfMinQueries = MT_PREFILL_MIN_QUERIES;  // fewer queries use query_kernel
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-template <int DT>
-struct Mfma;
-template <>
-struct Mfma<kF16> {
-  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
-  static __device__ __forceinline__ floatx4 run(const v8& a, const v8& b, const floatx4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma<kBF16> {
-  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
-  static __device__ __forceinline__ floatx4 run(const v8& a, const v8& b, const floatx4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-
 // x of lane l ^ 16 and of lane l ^ 32, combined with x by the caller: the
 // permlane swaps exchange rows of 16 (32) lanes between two registers, so
 // after swapping two copies of x, lane l holds x[l] in one and x[l ^ 16]

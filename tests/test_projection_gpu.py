@@ -1,0 +1,175 @@
+"""GPU parity of the decode projection kernel (mt_decode_projection) and of
+the residual + LayerNorm that reduces its split partial sums
+(mt_residual_layernorm_partials), against float64 numpy on the same rounded
+operands.
+
+Tolerances: the fp32 partial sums may differ from the fp64 product by the fp32
+accumulation error, bounded here by 1e-5 * sum_k |x||w| (a dropped or doubled
+term is of order |x||w| and fails it at these k); a rounded output may differ
+by half a unit in the last place of its type at |ref| + that bound, plus the
+bound itself. The decoder-level effect (tokens of the captured and eager
+steps, logits against the fp64 GPT-2 oracle) is covered by the model tests.
+"""
+import numpy as np
+import pytest
+
+from minitorch_amd.model import model_library
+from minitorch_amd.runtime import DeviceTensor, call, P, I, F
+from minitorch_amd.dtypes import dtype_code
+
+pytestmark = pytest.mark.gpu
+
+PROJ = [P, P, P, P, I, I, I, I, I, I]
+LN_PARTIALS = [P, P, P, I, P, P, P, I, I, F, I]
+MANT = {'bfloat16': 7, 'float16': 10}
+
+
+def host(t):
+    return np.asarray(t.to_numpy(), np.float64)
+
+
+def rounded(a, dtype):
+    t = DeviceTensor.from_numpy(np.asarray(a, np.float32), dtype)
+    return t, host(t)
+
+
+def half_ulp(v, dtype):
+    """Half the spacing of dtype's values at |v| (normal range)."""
+    e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -14)))
+    return 0.5 * 2.0 ** (e - MANT[dtype])
+
+
+def gelu64(x):
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+CASES = [
+    # m, n, k, splits, epilogue
+    (1, 64, 128, 1, 0),
+    (16, 256, 256, 1, 1),
+    (17, 768, 768, 2, 2),
+    (37, 384, 256, 1, 1),
+    (64, 128, 1024, 8, 2),
+    (128, 3072, 1024, 1, 0),
+    (128, 1024, 1024, 4, 2),
+    (128, 4096, 1024, 1, 1),
+    (128, 1024, 4096, 8, 2),
+    (200, 2304, 768, 1, 0),
+    (256, 768, 3072, 4, 2),
+    (150, 1024, 4096, 4, 2),
+]
+
+
+@pytest.mark.parametrize('dtype', ['bfloat16', 'float16'])
+@pytest.mark.parametrize('m,n,k,splits,epilogue', CASES)
+def test_decode_projection(dtype, m, n, k, splits, epilogue):
+    rng = np.random.default_rng([m, n, k, splits, epilogue])
+    x = rng.standard_normal((m, k))
+    w = rng.standard_normal((n, k)) * 0.05
+    b = rng.standard_normal(n) * 0.5
+    X, xr = rounded(x, dtype)
+    W, wr = rounded(w, dtype)
+    B, br = rounded(b, dtype)
+    bound = 1e-5 * (np.abs(xr) @ np.abs(wr).T) + 1e-7
+    prod = xr @ wr.T
+    if epilogue == 2:
+        out = DeviceTensor((splits, m, n), 'float32')
+        call(model_library(), 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, 0, m, n, k, splits, 2,
+             dtype_code(dtype))
+        got = host(out)
+        kc = k // splits
+        for s in range(splits):
+            ref = xr[:, s * kc:(s + 1) * kc] @ wr[:, s * kc:(s + 1) * kc].T
+            assert np.all(np.abs(got[s] - ref) <= bound), f'split {s}: {np.max(np.abs(got[s] - ref) / bound)}'
+        assert np.all(np.abs(got.sum(axis=0) - prod) <= bound)
+        return
+    out = DeviceTensor((m, n), dtype)
+    call(model_library(), 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, B.ptr, m, n, k, 1, epilogue,
+         dtype_code(dtype))
+    pre = prod + br
+    if epilogue == 1:
+        ref = gelu64(pre)
+        err = bound * 1.2 + 1e-6   # |gelu'| <= 1.13
+    else:
+        ref = pre
+        err = bound
+    got = host(out)
+    tol = half_ulp(np.abs(ref) + err, dtype) + err
+    assert np.all(np.abs(got - ref) <= tol), float(np.max(np.abs(got - ref) / tol))
+
+
+@pytest.mark.parametrize('dtype', ['bfloat16', 'float16'])
+def test_decode_projection_without_bias(dtype):
+    rng = np.random.default_rng(7)
+    m, n, k = 5, 512, 384
+    X, xr = rounded(rng.standard_normal((m, k)), dtype)
+    W, wr = rounded(rng.standard_normal((n, k)) * 0.05, dtype)
+    out = DeviceTensor((m, n), dtype)
+    call(model_library(), 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, 0, m, n, k, 1, 0, dtype_code(dtype))
+    ref = xr @ wr.T
+    err = 1e-5 * (np.abs(xr) @ np.abs(wr).T) + 1e-7
+    assert np.all(np.abs(host(out) - ref) <= half_ulp(np.abs(ref) + err, dtype) + err)
+
+
+def test_decode_projection_rejects_unsupported_shapes():
+    X = DeviceTensor((300, 1024), 'bfloat16')
+    W = DeviceTensor((1024, 1024), 'bfloat16')
+    out = DeviceTensor((8, 300, 1024), 'float32')
+    lib, bf = model_library(), dtype_code('bfloat16')
+    bad = [
+        (257, 1024, 1024, 1, 0, bf),    # more rows than the kernel takes
+        (4, 40, 1024, 1, 0, bf),        # n not a multiple of 16
+        (4, 1024, 100, 1, 0, bf),       # k not a multiple of 32
+        (4, 1024, 1024, 3, 2, bf),      # splits not a power of two
+        (4, 1024, 1024, 16, 2, bf),     # more than 8 splits
+        (4, 1024, 96, 2, 2, bf),        # a split's k range not a whole number of 32-wide steps
+        (128, 1024, 4096, 1, 0, bf),    # k range too long for the waves of one workgroup
+        (4, 1024, 1024, 2, 0, bf),      # a split needs the partial-sum epilogue
+        (4, 1024, 1024, 1, 3, bf),      # no such epilogue
+        (4, 1024, 1024, 1, 0, 0),       # fp32 is not taken
+        (0, 1024, 1024, 1, 0, bf),
+    ]
+    for m, n, k, s, e, d in bad:
+        with pytest.raises(RuntimeError):
+            call(lib, 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, 0, m, n, k, s, e, d)
+    with pytest.raises(RuntimeError):  # misaligned activations
+        call(lib, 'mt_decode_projection', PROJ, out.ptr, X.ptr + 2, W.ptr, 0, 4, 1024, 1024, 1, 0, bf)
+
+
+@pytest.mark.parametrize('dtype', ['bfloat16', 'float16'])
+@pytest.mark.parametrize('width,splits,bias', [(1024, 4, True), (768, 1, True), (2048, 8, False), (1024, 2, False),
+                                               (768, 3, True)])
+def test_residual_layernorm_partials(dtype, width, splits, bias):
+    rng = np.random.default_rng([width, splits])
+    rows = 37
+    x = (rng.standard_normal((rows, width)) * 3 + 1).astype(np.float32)
+    part = rng.standard_normal((splits, rows, width)).astype(np.float32)
+    g = rng.standard_normal(width).astype(np.float32)
+    be = rng.standard_normal(width).astype(np.float32)
+    X = DeviceTensor.from_numpy(x, 'float32')
+    Pt = DeviceTensor.from_numpy(part, 'float32')
+    Bv, bv = rounded(rng.standard_normal(width), dtype)
+    G, Bt = DeviceTensor.from_numpy(g, 'float32'), DeviceTensor.from_numpy(be, 'float32')
+    out = DeviceTensor((rows, width), dtype)
+    call(model_library(), 'mt_residual_layernorm_partials', LN_PARTIALS, out.ptr, X.ptr, Pt.ptr, splits,
+         Bv.ptr if bias else 0, G.ptr, Bt.ptr, rows, width, 1e-5, dtype_code(dtype))
+    xs = x.astype(np.float64) + part.astype(np.float64).sum(axis=0) + (bv if bias else 0.0)
+    assert np.allclose(host(X), xs, rtol=1e-6, atol=1e-5)
+    mean = xs.mean(axis=1, keepdims=True)
+    var = np.maximum((xs ** 2).mean(axis=1, keepdims=True) - mean ** 2, 0) + 1e-5
+    ref = g * ((xs - mean) / np.sqrt(var)) + be
+    err = 1e-5 * (np.abs(g) * np.abs((xs - mean) / np.sqrt(var)) + 1)
+    assert np.all(np.abs(host(out) - ref) <= half_ulp(np.abs(ref) + err, dtype) + err)
+
+
+def test_residual_layernorm_partials_rejects():
+    X = DeviceTensor((4, 1000), 'float32')
+    Pt = DeviceTensor((9, 4, 1000), 'float32')
+    G = DeviceTensor((1000,), 'float32')
+    out = DeviceTensor((4, 1000), 'bfloat16')
+    lib = model_library()
+    for rows, width, splits, d in [(4, 1000, 1, 2), (4, 768, 9, 2), (4, 768, 0, 2), (4, 768, 1, 0), (0, 768, 1, 2),
+                                   (4, 2304, 1, 2)]:
+        with pytest.raises(RuntimeError):
+            call(lib, 'mt_residual_layernorm_partials', LN_PARTIALS, out.ptr, X.ptr, Pt.ptr, splits, 0, G.ptr,
+                 G.ptr, rows, width, 1e-5, d)
