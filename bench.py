@@ -473,6 +473,92 @@ def e2e_cpu_baseline(model, lengths, seconds, seed):
                 host=dict(nproc=os.cpu_count(), cpu_model=host_cpu_model()))
 
 
+def bench_projections(args):
+    """Decode projections of DistilGPT-2 (fp16) and GPT-2-medium (bf16) at a
+    few batch sizes: the matrix-core projection kernel (mt_decode_projection,
+    with the split the decoder loop chooses for the out- and proj-projections)
+    against hipBLASLt (mt_gemm_ex with bias), each over enough distinct copies
+    of the weights (>= 512 MiB) that every launch reads them from HBM, the
+    launches of one kind captured in a HIP graph and replayed; microseconds
+    per launch."""
+    from minitorch_amd.model import model_library, DecoderLM
+    from minitorch_amd.runtime import DeviceTensor, call
+    from minitorch_amd.dtypes import dtype_code
+    rt = runtime()
+    lib = model_library()
+    proj_args = [P, P, P, P, I, I, I, I, I, I]
+    gemm_args = [P, P, P, P, P, I, I, I, I, I, I]
+    blas = DecoderLM(n_vocab=16, n_embd=16, n_head=1, n_layer=1, n_positions=4).blas()
+
+    def filled(shape, seed, dtype):
+        t = DeviceTensor(shape, dtype)
+        rt.check(rt.lib.mt_fill_random(t.ptr, int(np.prod(shape)), seed, dtype_code(dtype)))
+        return t
+
+    def waves_ok(rng, mt):
+        smax = 2 if mt >= 8 else 4
+        return any(rng % (32 * w) == 0 and rng // (32 * w) <= smax for w in range(16, 0, -1))
+
+    def splits(m, n, k):
+        # the decoder loop's choice (projection_splits in csrc/model_kernels.hip)
+        mt = 1 if m <= 16 else 2 if m <= 32 else 4 if m <= 64 else 8
+        tiles, s = n // 16 * ((m + 127) // 128), 1
+        while s < 8 and not (k % s == 0 and waves_ok(k // s, mt)):
+            s *= 2
+        while s < 8 and tiles * s < rt.compute_units() and k % (2 * s) == 0 and waves_ok(k // (2 * s), mt):
+            s *= 2
+        return s
+
+    def graph_time(launch, reps=5):
+        launch()
+        rt.synchronize()
+        rt.check(rt.lib.mt_graph_begin())
+        launch()
+        ex = ct.c_void_p()
+        rt.check(rt.lib.mt_graph_end(ct.byref(ex)))
+        rt.check(rt.lib.mt_graph_launch(ex))
+        rt.synchronize()
+        e0, e1 = CudaEvent(), CudaEvent()
+        e0.record()
+        for _ in range(reps):
+            rt.check(rt.lib.mt_graph_launch(ex))
+        e1.record()
+        e1.synchronize()
+        rt.check(rt.lib.mt_graph_destroy(ex))
+        return e1.seconds_since(e0) / reps
+
+    rows = []
+    for name, d, dtype, ms in (('distilgpt2', 768, 'float16', (2, 16, 64)),
+                               ('gpt2-medium', 1024, 'bfloat16', (2, 16, 64, 128))):
+        code = dtype_code(dtype)
+        for m in ms:
+            x = filled((m, 4 * d), 1, dtype)
+            bias = filled((4 * d,), 2, dtype)
+            out = DeviceTensor((8, m, 4 * d), 'float32')
+            for kind, n, k, epi in (('qkv', 3 * d, d, 0), ('out', d, d, 2), ('fc', 4 * d, d, 1),
+                                    ('proj', d, 4 * d, 2)):
+                sp = splits(m, n, k) if epi == 2 else 1
+                copies = max(8, -(-(512 << 20) // (n * k * 2)))
+                ws = [filled((n, k), 100 + i, dtype) for i in range(copies)]
+
+                def own():
+                    for w in ws:
+                        call(lib, 'mt_decode_projection', proj_args, out.ptr, x.ptr, w.ptr,
+                             0 if epi == 2 else bias.ptr, m, n, k, sp, epi, code)
+
+                def hipblaslt():
+                    for w in ws:
+                        call(lib, 'mt_gemm_ex', gemm_args, blas.handle, out.ptr, x.ptr, w.ptr, bias.ptr, m, n, k, 1,
+                             code, code)
+                t_own, t_blas = graph_time(own) / copies, graph_time(hipblaslt) / copies
+                rows.append(dict(model=name, rows=m, projection=kind, n=n, k=k, splits=sp,
+                                 epilogue=('bias', 'bias+gelu', 'split partials')[epi],
+                                 own_us=round(t_own * 1e6, 2), hipblaslt_us=round(t_blas * 1e6, 2)))
+                print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+                del ws
+    return dict(metric='decode projection time (us per launch, cold weights)', projections=rows)
+
+
 def e2e_config3(args, loops=('sync', 'sync-free')):
     """Config 3 end to end: the 256-request DistilGPT-2 trace (fp16) replayed by
     wall clock through the batcher. Reports decode tokens/s by the reference's
@@ -511,19 +597,24 @@ def e2e_config4(args, loops=('sync', 'sync-free')):
     24-layer model step with the tied head, tokens to the host) and the whole
     loop's rate including the replacement prefills, per loop."""
     from minitorch_amd import model as model_mod, e2e
-    model = model_mod.gpt2_medium(seed=args.seed)
+    distil = args.model == 'distilgpt2'
+    model = model_mod.distilgpt2(seed=args.seed) if distil else model_mod.gpt2_medium(seed=args.seed)
     kw = dict(seed=args.seed, steps=max(10, min(args.steps, 40)), warmup=max(2, min(args.warmup, 5)),
-              replace_rate=args.replace_rate, batch_prefills=not args.prefill_each)
+              replace_rate=args.replace_rate, batch_prefills=not args.prefill_each, concurrent=args.concurrent,
+              precision='fp16' if distil else 'bf16')
     r = e2e.run_config4(model, **kw) if 'sync' in loops else {}
     if 'sync-free' in loops:
         r['sync_free'] = e2e.run_config4(model, **kw, token_feedback=True)
         # the sync-free loop with each decode step replayed from a HIP graph
         r['graph'] = e2e.run_config4(model, **kw, token_feedback=True, graph=True)
     if not args.no_cpu_baseline:
-        r['cpu_baseline'] = e2e_cpu_baseline(model, e2e.config4_lengths(np.random.default_rng([args.seed, 4]), 128),
-                                             args.cpu_seconds, args.seed)
-    r['workload'] = ('config 4: steady state of 128 requests, random-init GPT-2-medium (24 layers, d 1024, 16 '
-                     'heads), bf16, contexts lognormal(median 256, sigma 1.2) clipped [16,1024], page 16, '
+        r['cpu_baseline'] = e2e_cpu_baseline(
+            model, e2e.config4_lengths(np.random.default_rng([args.seed, 4]), args.concurrent),
+            args.cpu_seconds, args.seed)
+    arch = ('DistilGPT-2 (6 layers, d 768, 12 heads), fp16' if distil
+            else 'GPT-2-medium (24 layers, d 1024, 16 heads), bf16')
+    r['workload'] = (f'config 4: steady state of {args.concurrent} requests, random-init {arch}, contexts '
+                     'lognormal(median 256, sigma 1.2) clipped [16,1024], page 16, '
                      f'{args.replace_rate:.0%} replaced per step')
     return r
 
@@ -574,7 +665,8 @@ def bench_e2e(args):
     else:
         loops = ('sync', 'sync-free') if args.loop == 'both' else (args.loop,)
         r = e2e_config4(args, loops)
-        value, dtype = r.get('decode_tokens_per_sec') or r.get('sync_free', {}).get('loop_tokens_per_sec'), 'bf16'
+        value = r.get('decode_tokens_per_sec') or r.get('sync_free', {}).get('loop_tokens_per_sec')
+        dtype = 'f16' if args.model == 'distilgpt2' else 'bf16'
     return {'metric': 'decode tokens/s (1 GPU), end to end', 'value': value, 'unit': 'tokens/s',
             'n_gpus': 1, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
             'dtype': dtype, 'data': 'synthetic (random-init weights, random token ids)',
@@ -652,6 +744,11 @@ def main():
                     help='config 4: fraction of requests replaced per step (0 = decode steps only)')
     ap.add_argument('--prefill', action='store_true',
                     help='op-level causal paged prefill attention on the prompt shapes of configs 3 and 4')
+    ap.add_argument('--model', choices=('gpt2-medium', 'distilgpt2'), default='gpt2-medium',
+                    help='config 4: the model of the steady state (DistilGPT-2 runs in fp16, GPT-2-medium in bf16)')
+    ap.add_argument('--concurrent', type=int, default=128, help='config 4: requests decoded every step')
+    ap.add_argument('--projections', action='store_true',
+                    help='time the decode projections (projection kernel vs hipBLASLt) at several batch sizes')
     ap.add_argument('--no-e2e', action='store_true',
                     help='default line: skip the end-to-end configs 3 and 4 and config 1')
     args = ap.parse_args()
@@ -676,6 +773,9 @@ def main():
         return
     if args.prefill:
         print(json.dumps(bench_prefill(args)), flush=True)
+        return
+    if args.projections:
+        print(json.dumps(bench_projections(args)), flush=True)
         return
     if args.config in (3, 4):
         print(json.dumps(bench_e2e(args)), flush=True)
