@@ -124,6 +124,23 @@ int mt_residual_layernorm(void* out, float* x, const void* y, const float* gamma
 int mt_decode_projection(void* out, const void* x, const void* w, const void* bias, int m, int n, int k,
                          int splits, int epilogue, int dtype);
 
+/* mt_decode_projection (epilogue 0 or 1, one split) whose activations are
+ * LayerNorm(x_in + part_bias + sum_s partials[s]) for rows r < m: v[r, :] =
+ * x_in[r, :] + part_bias + sum over s < splits of partials[s, r, :] (fp32;
+ * splits 0, 1, 2 or 4; 0 means no partials and no part_bias), h = gamma *
+ * ((v - mean) * rsqrt(var + eps)) + beta with one-pass mean and variance as
+ * mt_residual_layernorm, rounded to dtype, out = epilogue(h @ w[n, k]^T +
+ * bias); x_out[r, :] = v[r, :] (x_out must not be x_in). 1 <= m <= 16, k a
+ * multiple of 256 up to 1024, n a multiple of 16, 16-byte aligned
+ * x_in/x_out/partials/gamma/beta/w, 8-byte aligned out/bias/part_bias;
+ * hipErrorInvalidValue otherwise. The residual add and LayerNorm of a decode
+ * step fused into the QKV and fc projections for small batches. No reference
+ * counterpart (minitorch/modules_transformer.py:272-282 around the Linear of
+ * minitorch/modules_basic.py:132-149). */
+int mt_decode_projection_ln(void* out, const float* x_in, float* x_out, const float* partials, int splits,
+                            const void* part_bias, const float* gamma, const float* beta, float eps, const void* w,
+                            const void* bias, int m, int n, int k, int epilogue, int dtype);
+
 /* x[r, :] += bias + sum_s partials[s, r, :] (fp32), then out[r, :] =
  * LayerNorm(x[r, :]) in dtype (1 or 2): the residual add and LayerNorm after
  * a split projection (mt_decode_projection epilogue 2), as
@@ -150,7 +167,9 @@ size_t mt_decoder_scratch_bytes(int rows, int d, int dtype);
  * mt_decode_projection where it takes their shapes: the QKV and fc
  * projections for rows <= 16, the out- and proj-projections (as split-k
  * partial sums reduced by mt_residual_layernorm_partials, d a multiple of
- * 256) for rows <= 32. Larger batches, fp32, other shapes and
+ * 256) for rows <= 32; for rows <= 8 and d <= 1024 the residual add and
+ * LayerNorm move into the QKV and fc projections (mt_decode_projection_ln,
+ * the residual stream alternating between x and a scratch copy). Larger batches, fp32, other shapes and
  * MT_DECODE_PROJECTIONS=0 in the environment use hipBLASLt, which chooses its
  * algorithm by timing (cold caches) on the third call of a shape, as does the
  * tied head.

@@ -498,7 +498,27 @@ struct ProjArgs {
   const void* bias;
   int m, n, k;
   int kc;  // k per wave: k / (splits * waves), a multiple of 32, at most 32 * SMAX
+  // LayerNorm prologue (projection_kernel with PS >= 0): the activations are
+  // LayerNorm(x_in + part_bias + sum of the PS partial rows part[s, r, :]),
+  // computed by every workgroup; workgroup (0, 0, 0) writes the sum to x_out.
+  const float* x_in;
+  float* x_out;
+  const float* part;
+  const void* part_bias;
+  const float* gamma;
+  const float* beta;
+  float eps;
 };
+
+// Rows up to which the decode step fuses the residual add and LayerNorm into
+// the QKV and fc projections (every workgroup re-reads m * d * (4 + 4 splits)
+// bytes, which outweighs the saved launch beyond a few rows), and the largest
+// width the prologue takes.
+#ifndef MT_PROJ_FUSED_ROWS
+#define MT_PROJ_FUSED_ROWS 8
+#endif
+constexpr int kProjFusedRows = MT_PROJ_FUSED_ROWS;
+constexpr int kProjFusedMaxWidth = 1024;
 
 __device__ __forceinline__ float gelu_tanh(float v) {
   const float c = 0.7978845608028654f;
@@ -511,13 +531,87 @@ __device__ __forceinline__ float gelu_tanh(float v) {
 template <int MT>
 constexpr int proj_max_steps() { return MT >= 8 ? 2 : 4; }
 
-template <int DT, int MT, int EPI>
+// LayerNorm prologue of projection_kernel (PS >= 0, one row tile): pass 1
+// spreads the m x k sums v = x_in + part_bias + sum_s part[s] over all
+// threads (every load in flight at once) into vbuf, and gamma/beta into gb;
+// pass 2 takes one wave per row for the mean and variance (one-pass, as the
+// LayerNorm kernels) and writes the normalized rows in T to the activation
+// tile xt (row stride xs).
+template <int DT, int PS>
+__device__ __forceinline__ void ln_prologue(const ProjArgs& p, float* vbuf, float* gb, typename Elem<DT>::T* xt,
+                                            int xs, int wave, int waves, int lane) {
+  using T = typename Elem<DT>::T;
+  const int tid = int(threadIdx.x), nt = int(blockDim.x);
+  const int k4 = p.k >> 2;
+  const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
+  for (int i = tid; i < p.m * k4; i += nt) {
+    const int r = i / k4, c = 4 * (i - r * k4);
+    float4 v = *reinterpret_cast<const float4*>(p.x_in + r * p.k + c);
+    if constexpr (PS > 0) {
+      float4 q[PS];
+#pragma unroll
+      for (int s = 0; s < PS; ++s) q[s] = *reinterpret_cast<const float4*>(p.part + (s * p.m + r) * p.k + c);
+      const uint2 b = p.part_bias ? *reinterpret_cast<const uint2*>(static_cast<const T*>(p.part_bias) + c)
+                                  : uint2{0u, 0u};
+      v.x += to_f32<DT>(T(b.x & 0xffffu)); v.y += to_f32<DT>(T(b.x >> 16));
+      v.z += to_f32<DT>(T(b.y & 0xffffu)); v.w += to_f32<DT>(T(b.y >> 16));
+#pragma unroll
+      for (int s = 0; s < PS; ++s) { v.x += q[s].x; v.y += q[s].y; v.z += q[s].z; v.w += q[s].w; }
+    }
+    *reinterpret_cast<float4*>(vbuf + r * p.k + c) = v;
+    if (writer) *reinterpret_cast<float4*>(p.x_out + r * p.k + c) = v;
+  }
+  for (int i = tid; i < k4; i += nt) {
+    *reinterpret_cast<float4*>(gb + 4 * i) = *reinterpret_cast<const float4*>(p.gamma + 4 * i);
+    *reinterpret_cast<float4*>(gb + p.k + 4 * i) = *reinterpret_cast<const float4*>(p.beta + 4 * i);
+  }
+  __syncthreads();
+  const int nj = p.k >> 8;
+  for (int r = wave; r < p.m; r += waves) {
+    float sum = 0.f, sq = 0.f;
+    for (int j = 0; j < nj; ++j) {
+      const float4 v = *reinterpret_cast<const float4*>(vbuf + r * p.k + 256 * j + 4 * lane);
+      sum += (v.x + v.y) + (v.z + v.w);
+      sq += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      sum += __shfl_xor(sum, off);
+      sq += __shfl_xor(sq, off);
+    }
+    const float mean = sum / p.k;
+    const float var = fmaxf(sq / p.k - mean * mean, 0.f) + p.eps;
+    const float inv = 1.f / sqrtf(var);
+    for (int j = 0; j < nj; ++j) {
+      const int c = 256 * j + 4 * lane;
+      const float4 v = *reinterpret_cast<const float4*>(vbuf + r * p.k + c);
+      const float4 g = *reinterpret_cast<const float4*>(gb + c);
+      const float4 b = *reinterpret_cast<const float4*>(gb + p.k + c);
+      const float r0 = g.x * ((v.x - mean) * inv) + b.x;
+      const float r1 = g.y * ((v.y - mean) * inv) + b.y;
+      const float r2 = g.z * ((v.z - mean) * inv) + b.z;
+      const float r3 = g.w * ((v.w - mean) * inv) + b.w;
+      *reinterpret_cast<uint2*>(xt + r * xs + c) =
+          uint2{uint32_t(from_f32<DT>(r0)) | (uint32_t(from_f32<DT>(r1)) << 16),
+                uint32_t(from_f32<DT>(r2)) | (uint32_t(from_f32<DT>(r3)) << 16)};
+    }
+  }
+  __syncthreads();
+}
+
+// PS < 0: activations read from p.x. PS >= 0 (one row tile, one split): the
+// activations come from the LayerNorm prologue through LDS; the weight loads
+// are issued before it, so their HBM latency overlaps it.
+template <int DT, int MT, int EPI, int PS = -1>
 __global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
   using T = typename Elem<DT>::T;
   using V8 = typename Mfma<DT>::v8;
   constexpr int SMAX = proj_max_steps<MT>();
   constexpr int NL = 1 + MT;  // 16-byte loads per lane and step
-  extern __shared__ floatx4 red[];  // [waves][MT][64]
+  constexpr bool LN = PS >= 0;
+  static_assert(!LN || MT == 1, "the LayerNorm prologue takes one row tile");
+  // [waves][MT][64] sums | LN: v [m][k] fp32, gamma/beta [2][k] fp32, tile [16][k + 8] T
+  extern __shared__ floatx4 red[];
   const int waves = int(blockDim.x >> 6);
   const int wave = int(threadIdx.x >> 6), lane = int(threadIdx.x & 63);
   const int col = lane & 15, grp = lane >> 4;
@@ -534,12 +628,27 @@ __global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
     xoff[t] = row * p.k + k0;
   }
   u32x4 buf[SMAX][NL];
+  if constexpr (LN) {
+    float* vbuf = reinterpret_cast<float*>(red + waves * 64);
+    float* gb = vbuf + p.m * p.k;
+    T* xt = reinterpret_cast<T*>(gb + 2 * p.k);
+    const int xs = p.k + 8;
 #pragma unroll
-  for (int s = 0; s < SMAX; ++s) {
-    if (s < steps) {
-      buf[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + 32 * s));
+    for (int s = 0; s < SMAX; ++s)
+      if (s < steps) buf[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + 32 * s));
+    ln_prologue<DT, PS>(p, vbuf, gb, xt, xs, wave, waves, lane);
+    const int row = col < p.m ? col : p.m - 1;
 #pragma unroll
-      for (int t = 0; t < MT; ++t) buf[s][1 + t] = *global_view(reinterpret_cast<const u32x4*>(x + xoff[t] + 32 * s));
+    for (int s = 0; s < SMAX; ++s)
+      if (s < steps) buf[s][1] = *reinterpret_cast<const u32x4*>(xt + row * xs + k0 + 32 * s);
+  } else {
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      if (s < steps) {
+        buf[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + 32 * s));
+#pragma unroll
+        for (int t = 0; t < MT; ++t) buf[s][1 + t] = *global_view(reinterpret_cast<const u32x4*>(x + xoff[t] + 32 * s));
+      }
     }
   }
   floatx4 acc[MT];
@@ -733,6 +842,62 @@ void launch_projection_epi(const ProjArgs& a, int splits) {
   else if (mt == 2) launch_projection_mt<DT, 2, EPI>(a, splits);
   else if (mt == 4) launch_projection_mt<DT, 4, EPI>(a, splits);
   else launch_projection_mt<DT, 8, EPI>(a, splits);
+}
+
+// Whether the LayerNorm-prologue projection takes out = epi(LayerNorm(x_in +
+// part_bias + sum of splits partial rows) @ w^T): fp16/bf16, 1 <= m <= 16,
+// one split, k a multiple of 256 up to kProjFusedMaxWidth, partial splits
+// 0, 1, 2 or 4 (0: no partials and no part_bias), x_out distinct from x_in.
+bool projection_ln_ok(const void* out, const float* x_in, const float* x_out, const float* part, int splits,
+                      const void* part_bias, const float* gamma, const float* beta, const void* w,
+                      const void* bias, int m, int n, int k, int epilogue, int dtype) {
+  if (dtype != kF16 && dtype != kBF16) return false;
+  if (m < 1 || m > 16 || n < 16 || n % 16 || k < 256 || k % 256 || k > kProjFusedMaxWidth) return false;
+  if (epilogue != kProjBias && epilogue != kProjGelu) return false;
+  if (splits != 0 && splits != 1 && splits != 2 && splits != 4) return false;
+  if ((splits == 0) != (part == nullptr) || (splits == 0 && part_bias)) return false;
+  if (proj_waves(k, 1) == 0 || int64_t(n) * k > INT32_MAX) return false;
+  if (!out || !x_in || !x_out || x_in == x_out || !gamma || !beta || !w) return false;
+  return aligned(out, 8) && aligned(x_in, 16) && aligned(x_out, 16) && (!part || aligned(part, 16)) &&
+         (!part_bias || aligned(part_bias, 8)) && aligned(gamma, 16) && aligned(beta, 16) && aligned(w, 16) &&
+         (!bias || aligned(bias, 8));
+}
+
+template <int DT, int EPI, int PS>
+void launch_projection_ln_ps(const ProjArgs& a) {
+  const int waves = proj_waves(a.k, 1);
+  ProjArgs b = a;
+  b.kc = a.k / waves;
+  const size_t lds = size_t(waves) * 64 * sizeof(floatx4) + sizeof(float) * (size_t(a.m) * a.k + 2 * a.k) +
+                     sizeof(typename Elem<DT>::T) * 16 * size_t(a.k + 8);
+  projection_kernel<DT, 1, EPI, PS><<<dim3(unsigned(a.n / 16), 1, 1), 64 * waves, lds>>>(b);
+}
+
+template <int DT, int EPI>
+void launch_projection_ln_epi(const ProjArgs& a, int splits) {
+  if (splits == 0) launch_projection_ln_ps<DT, EPI, 0>(a);
+  else if (splits == 1) launch_projection_ln_ps<DT, EPI, 1>(a);
+  else if (splits == 2) launch_projection_ln_ps<DT, EPI, 2>(a);
+  else launch_projection_ln_ps<DT, EPI, 4>(a);
+}
+
+// Caller has checked projection_ln_ok.
+hipError_t projection_ln(void* out, const float* x_in, float* x_out, const float* part, int splits,
+                         const void* part_bias, const float* gamma, const float* beta, float eps, const void* w,
+                         const void* bias, int m, int n, int k, int epilogue, int dtype) {
+  ProjArgs a{};
+  a.out = out; a.w = w; a.bias = bias;
+  a.m = m; a.n = n; a.k = k;
+  a.x_in = x_in; a.x_out = x_out; a.part = part; a.part_bias = part_bias;
+  a.gamma = gamma; a.beta = beta; a.eps = eps;
+  if (dtype == kF16) {
+    if (epilogue == kProjBias) launch_projection_ln_epi<kF16, kProjBias>(a, splits);
+    else launch_projection_ln_epi<kF16, kProjGelu>(a, splits);
+  } else {
+    if (epilogue == kProjBias) launch_projection_ln_epi<kBF16, kProjBias>(a, splits);
+    else launch_projection_ln_epi<kBF16, kProjGelu>(a, splits);
+  }
+  return hipGetLastError();
 }
 
 // Caller has checked projection_ok.
@@ -1098,6 +1263,16 @@ int mt_decode_projection(void* out, const void* x, const void* w, const void* bi
   return projection(out, x, w, bias, m, n, k, splits, epilogue, dtype);
 }
 
+int mt_decode_projection_ln(void* out, const float* x_in, float* x_out, const float* partials, int splits,
+                            const void* part_bias, const float* gamma, const float* beta, float eps, const void* w,
+                            const void* bias, int m, int n, int k, int epilogue, int dtype) {
+  if (!projection_ln_ok(out, x_in, x_out, partials, splits, part_bias, gamma, beta, w, bias, m, n, k, epilogue,
+                        dtype))
+    return hipErrorInvalidValue;
+  return projection_ln(out, x_in, x_out, partials, splits, part_bias, gamma, beta, eps, w, bias, m, n, k, epilogue,
+                       dtype);
+}
+
 int mt_residual_layernorm_partials(void* out, float* x, const float* partials, int splits, const void* bias,
                                    const float* gamma, const float* beta, int rows, int width, float eps,
                                    int dtype) {
@@ -1114,7 +1289,10 @@ size_t mt_decoder_scratch_bytes(int rows, int d, int dtype) {
   // rows <= kProjSplitRows) fp32 split partials [kProjMaxSplits, rows, d], each 256-aligned
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
   const size_t partials = dtype != kF32 && rows <= kProjSplitRows ? al(size_t(kProjMaxSplits) * rows * d * 4) : 0;
-  return al(size_t(rows) * 3 * d * e) + 2 * al(size_t(rows) * d * e) + al(size_t(rows) * 4 * d * e) + partials;
+  // (fp16/bf16 and rows <= kProjFusedRows) | second residual stream [rows, d] fp32
+  const size_t stream = dtype != kF32 && rows <= kProjFusedRows ? al(size_t(rows) * d * 4) : 0;
+  return al(size_t(rows) * 3 * d * e) + 2 * al(size_t(rows) * d * e) + al(size_t(rows) * 4 * d * e) + partials +
+         stream;
 }
 
 int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
@@ -1139,6 +1317,61 @@ int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
                         ? reinterpret_cast<float*>(mlp + al(size_t(rows) * 4 * d * e)) : nullptr;
   const int hd = d / heads;
   const bool own = decode_projections_enabled();
+  float* xb = partials && rows <= kProjFusedRows
+                  ? reinterpret_cast<float*>(reinterpret_cast<char*>(partials) +
+                                             al(size_t(kProjMaxSplits) * rows * d * 4))
+                  : nullptr;
+  auto attention = [&](int i) -> int {
+    return mt_paged_decode_split(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, att->slabs, att->table,
+                                 att->offsets, rows, heads, hd, att->page_size, att->pages_per_slab,
+                                 att->num_slabs, att->columns, i, att->layers, dtype, att->split_tokens, 0, 0,
+                                 3 * d, att->work, att->work_items, att->merge_rows, att->partials,
+                                 att->partial_bytes);
+  };
+  // A few rows: the residual add and LayerNorm run inside the QKV and fc
+  // projections (LayerNorm prologue), the residual stream alternating between
+  // x and xb, and the out- and proj-projections leave split partial sums:
+  // five kernels per layer and one LayerNorm (the final one) per step.
+  if (own && xb) {
+    auto fused_splits = [&](int k) {
+      for (int sp = 4; sp >= 1; sp /= 2)
+        if (projection_ok(partials, attn, layers[0].w_o, nullptr, rows, d, k, sp, kProjPartials, dtype)) return sp;
+      return 0;
+    };
+    const int so = fused_splits(d), sp = fused_splits(4 * d);
+    bool ok = so > 0 && sp > 0 && partials_ln_ok(h, x, partials, layers[n_layer - 1].b_proj, final_gamma, final_beta,
+                                                 d, dtype);
+    for (int i = 0; i < n_layer && ok; ++i) {
+      const mt_decoder_layer& L = layers[i];
+      ok = projection_ln_ok(qkv, x, xb, i ? partials : nullptr, i ? sp : 0, i ? layers[i - 1].b_proj : nullptr,
+                            L.ln1_gamma, L.ln1_beta, L.w_qkv, L.b_qkv, rows, 3 * d, d, kProjBias, dtype) &&
+           projection_ok(partials, attn, L.w_o, nullptr, rows, d, d, so, kProjPartials, dtype) &&
+           projection_ln_ok(mlp, xb, x, partials, so, L.b_o, L.ln2_gamma, L.ln2_beta, L.w_fc, L.b_fc, rows, 4 * d,
+                            d, kProjGelu, dtype) &&
+           projection_ok(partials, mlp, L.w_proj, nullptr, rows, d, 4 * d, sp, kProjPartials, dtype);
+    }
+    if (ok) {
+      int st = 0;
+      for (int i = 0; i < n_layer && !st; ++i) {
+        const mt_decoder_layer& L = layers[i];
+        if ((st = projection_ln(qkv, x, xb, i ? partials : nullptr, i ? sp : 0, i ? layers[i - 1].b_proj : nullptr,
+                                L.ln1_gamma, L.ln1_beta, eps, L.w_qkv, L.b_qkv, rows, 3 * d, d, kProjBias, dtype)))
+          break;
+        if ((st = attention(i))) break;
+        if ((st = projection(partials, attn, L.w_o, nullptr, rows, d, d, so, kProjPartials, dtype))) break;
+        if ((st = projection_ln(mlp, xb, x, partials, so, L.b_o, L.ln2_gamma, L.ln2_beta, eps, L.w_fc, L.b_fc, rows,
+                                4 * d, d, kProjGelu, dtype)))
+          break;
+        st = projection(partials, mlp, L.w_proj, nullptr, rows, d, 4 * d, sp, kProjPartials, dtype);
+      }
+      if (!st)
+        st = residual_layernorm_partials(h, x, partials, sp, layers[n_layer - 1].b_proj, final_gamma, final_beta,
+                                         rows, d, eps, dtype);
+      if (!st && logits)
+        st = gemm(blas, logits, h, head_weight, nullptr, rows, vocab, d, 1, dtype, dtype, kEpiNone, true);
+      return st;
+    }
+  }
   // out = epi(in @ wt^T + b): the decode projection kernel where it takes
   // the shape, else hipBLASLt.
   auto project = [&](void* out, const void* in, const void* wt, const void* b, int n, int k, int epi) -> int {
@@ -1165,12 +1398,7 @@ int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
   for (int i = 0; i < n_layer && !st; ++i) {
     const mt_decoder_layer& L = layers[i];
     if ((st = project(qkv, h, L.w_qkv, L.b_qkv, 3 * d, d, kProjBias))) break;
-    if ((st = mt_paged_decode_split(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, att->slabs,
-                                    att->table, att->offsets, rows, heads, hd, att->page_size,
-                                    att->pages_per_slab, att->num_slabs, att->columns, i, att->layers,
-                                    dtype, att->split_tokens, 0, 0, 3 * d, att->work, att->work_items,
-                                    att->merge_rows, att->partials, att->partial_bytes)))
-      break;
+    if ((st = attention(i))) break;
     if ((st = project_residual(attn, L.w_o, L.b_o, d, L.ln2_gamma, L.ln2_beta))) break;
     if ((st = project(mlp, h, L.w_fc, L.b_fc, 4 * d, d, kProjGelu))) break;
     const bool last = i + 1 == n_layer;

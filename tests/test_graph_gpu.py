@@ -116,12 +116,15 @@ def test_graph_batcher_matches_eager_batcher():
     assert graph[2] == eager[2]
 
 
-def test_graph_distilgpt2_shape_replays():
-    # DistilGPT-2 shapes (d 768, 12 heads, vocab 50257) in fp16, 16 requests
+@pytest.mark.parametrize('concurrent', [4, 16])
+def test_graph_distilgpt2_shape_replays(concurrent):
+    # DistilGPT-2 shapes (d 768, 12 heads, vocab 50257) in fp16; 4 requests
+    # take the decode loop with the LayerNorm inside the QKV and fc
+    # projections, 16 the one with separate residual LayerNorm kernels
     model = DecoderLM(n_vocab=50257, n_embd=768, n_head=12, n_layer=6, n_positions=1024, seed=45)
     steps = GRAPH_WARMUP + 6
-    eager = steady_loop(model, False, steps, seed=45, concurrent=16, dtype='float16', replace=0.1)
-    graph = steady_loop(model, True, steps, seed=45, concurrent=16, dtype='float16', replace=0.1)
+    eager = steady_loop(model, False, steps, seed=45, concurrent=concurrent, dtype='float16', replace=0.1)
+    graph = steady_loop(model, True, steps, seed=45, concurrent=concurrent, dtype='float16', replace=0.1)
     for k in range(steps):
         assert np.array_equal(eager[0][k], graph[0][k]), f'step {k}'
         assert eager[1][k] == graph[1][k], f'step {k}: pages differ'

@@ -449,12 +449,13 @@ def test_distilgpt2_shape_batched_prefill_fp16():
 
 
 @pytest.mark.parametrize('precision', ['fp16', 'bf16'])
-@pytest.mark.parametrize('batch', [3, 20, 40])
+@pytest.mark.parametrize('batch', [3, 8, 20, 40])
 def test_low_precision_batched_decode_near_oracle(precision, batch):
-    # d = 256: fp16/bf16 decode steps of 3 rows run every layer projection on
-    # the matrix-core projection kernel (out- and proj-projections as split-k
-    # partial sums reduced in the residual LayerNorm), 20 rows only the split
-    # ones, 40 rows none (hipBLASLt). Each row's logits against the fp64 numpy
+    # d = 256: fp16/bf16 decode steps of 3 and 8 rows run every layer
+    # projection on the matrix-core projection kernel, with the residual add
+    # and LayerNorm inside the QKV and fc projections and the out- and
+    # proj-projections as split-k partial sums; 20 rows only the split ones
+    # (reduced in the residual LayerNorm kernel), 40 rows none (hipBLASLt). Each row's logits against the fp64 numpy
     # GPT-2 on its own sequence, within 2 % of the logits' range as above.
     model = tiny(seed=19, d=256, heads=4)
     rng = np.random.default_rng([19, batch])

@@ -173,3 +173,63 @@ def test_residual_layernorm_partials_rejects():
         with pytest.raises(RuntimeError):
             call(lib, 'mt_residual_layernorm_partials', LN_PARTIALS, out.ptr, X.ptr, Pt.ptr, splits, 0, G.ptr,
                  G.ptr, rows, width, 1e-5, d)
+
+
+PROJ_LN = [P, P, P, P, I, P, P, P, F, P, P, I, I, I, I, I]
+
+
+@pytest.mark.parametrize('dtype', ['bfloat16', 'float16'])
+@pytest.mark.parametrize('m,n,k,splits,epilogue', [(1, 2304, 768, 0, 0), (2, 3072, 768, 4, 1), (8, 4096, 1024, 2, 1),
+                                                    (5, 3072, 1024, 1, 0), (16, 256, 256, 4, 0)])
+def test_decode_projection_layernorm_prologue(dtype, m, n, k, splits, epilogue):
+    rng = np.random.default_rng([m, n, k, splits, epilogue, 1])
+    x = (rng.standard_normal((m, k)) * 2 + 0.5).astype(np.float32)
+    part = rng.standard_normal((max(splits, 1), m, k)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    be = (0.1 * rng.standard_normal(k)).astype(np.float32)
+    X, Xo = DeviceTensor.from_numpy(x, 'float32'), DeviceTensor((m, k), 'float32')
+    Pt = DeviceTensor.from_numpy(part, 'float32')
+    PB, pb = rounded(rng.standard_normal(k) * 0.5, dtype)
+    G, Bt = DeviceTensor.from_numpy(g, 'float32'), DeviceTensor.from_numpy(be, 'float32')
+    W, wr = rounded(rng.standard_normal((n, k)) * 0.05, dtype)
+    B, br = rounded(rng.standard_normal(n) * 0.5, dtype)
+    out = DeviceTensor((m, n), dtype)
+    call(model_library(), 'mt_decode_projection_ln', PROJ_LN, out.ptr, X.ptr, Xo.ptr, Pt.ptr if splits else 0,
+         splits, PB.ptr if splits else 0, G.ptr, Bt.ptr, 1e-5, W.ptr, B.ptr, m, n, k, epilogue, dtype_code(dtype))
+    v = x.astype(np.float64) + (part.astype(np.float64).sum(axis=0) + pb if splits else 0.0)
+    assert np.allclose(host(Xo), v, rtol=1e-6, atol=1e-5)
+    assert np.array_equal(X.to_numpy(), x)
+    mean = v.mean(axis=1, keepdims=True)
+    var = np.maximum((v ** 2).mean(axis=1, keepdims=True) - mean ** 2, 0) + 1e-5
+    hn = g * ((v - mean) / np.sqrt(var)) + be
+    # h is rounded to dtype from an fp32 computation: within one unit in the
+    # last place of the fp64 value; that unit, carried through |w|, plus the
+    # fp32 accumulation bound
+    h_err = 2 * half_ulp(np.abs(hn) + 1e-4, dtype) + 1e-5
+    pre = hn @ wr.T + br
+    err = np.abs(h_err) @ np.abs(wr).T + 1e-5 * (np.abs(hn) @ np.abs(wr).T) + 1e-6
+    if epilogue == 1:
+        ref, err = gelu64(pre), err * 1.2 + 1e-6
+    else:
+        ref = pre
+    got = host(out)
+    tol = half_ulp(np.abs(ref) + err, dtype) + err
+    assert np.all(np.abs(got - ref) <= tol), float(np.max(np.abs(got - ref) / tol))
+
+
+def test_decode_projection_layernorm_prologue_rejects():
+    X, Xo = DeviceTensor((16, 1280), 'float32'), DeviceTensor((16, 1280), 'float32')
+    Pt = DeviceTensor((4, 16, 1280), 'float32')
+    G = DeviceTensor((1280,), 'float32')
+    W = DeviceTensor((1024, 1280), 'bfloat16')
+    out = DeviceTensor((16, 1024), 'bfloat16')
+    lib, bf = model_library(), dtype_code('bfloat16')
+
+    def run(x_out=Xo.ptr, part=Pt.ptr, splits=4, part_bias=0, m=4, n=1024, k=1024, epi=0, d=bf):
+        call(lib, 'mt_decode_projection_ln', PROJ_LN, out.ptr, X.ptr, x_out, part, splits, part_bias, G.ptr, G.ptr,
+             1e-5, W.ptr, 0, m, n, k, epi, d)
+    run()  # valid
+    for kw in [dict(x_out=X.ptr), dict(k=1280), dict(k=640), dict(splits=3), dict(splits=0), dict(part=0),
+               dict(part=0, splits=0, part_bias=G.ptr), dict(m=17), dict(m=0), dict(n=40), dict(epi=2), dict(d=0)]:
+        with pytest.raises(RuntimeError):
+            run(**kw)
