@@ -102,7 +102,7 @@ int mt_paged_decode_split_tokens(int page_size, int columns, int requested, int*
  * v, so that they can be column blocks of one fused [b, 3*h*d] projection
  * output; 0 = h*d, contiguous; out is always contiguous), and an optional
  * work list built by the caller from the
- * context lengths it knows on the host (device int32): work_items pairs
+ * context lengths it knows on the host (device int32, 8-byte aligned): work_items pairs
  * (row, split), in the order they should be scheduled (e.g. longest first),
  * followed by merge_rows row indices, the rows with more than one split. A
  * work list requires an explicit split_tokens and must hold every (row,

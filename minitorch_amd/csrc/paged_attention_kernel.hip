@@ -573,11 +573,14 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
   for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
     int split, b, head;
     if (a.work) {
+      // (row, split) read as one 8-byte load: the workgroup's first dependent
+      // round trip.
       const int64_t w = item / g.heads;
       head = int(item - w * g.heads);
-      b = a.work[2 * w];
-      split = a.work[2 * w + 1];
-      if (b < 0 || b >= a.batch || split < 0 || split >= a.nsplit_max) continue;
+      const uint64_t e = reinterpret_cast<const uint64_t*>(a.work)[w];
+      b = int(uint32_t(e));
+      split = int(uint32_t(e >> 32));
+      if (!((unsigned(b) < unsigned(a.batch)) & (unsigned(split) < unsigned(a.nsplit_max)))) continue;
     } else {
       split = int(item / bh_count);
       const int64_t bhi = item - int64_t(split) * bh_count;
@@ -586,15 +589,10 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
     }
     const int64_t bh = int64_t(b) * g.heads + head;
 
-    // Loads that do not depend on the context length are issued first: the
-    // offset, the query, the new token's K/V (wave 0) and the table entry of
-    // each of this wave's page slots.
-    const int offset = a.offsets[b];
-    Query<DT, D, VEC, G> qv;
-    const int64_t qrow = int64_t(b) * a.qkv_stride + int64_t(head) * dim;  // q, k, v row
-    qv.load(qp + qrow, col0, dim, a.qscale);
-    T new_k{}, new_v{};
-    if (tid < dim) { new_k = kin[qrow + tid]; new_v = vin[qrow + tid]; }
+    // Loads that do not depend on the context length are issued first, all
+    // in one round trip: the table entry of each of this wave's page slots
+    // (the next link of the chain to the K/V loads), the query, the new
+    // token's K/V (wave 0) and the offset.
     const int* table_row = a.table + int64_t(b) * g.columns;
     const int t0i = split * a.split_tokens;
     const int slot_i = lane >> sub_shift;
@@ -602,6 +600,12 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
     const int64_t slot_logical = (int64_t(t0i) + slot_tok) >> g.log2_page;
     int physical = -1;
     if (slot_i < rb_per_wave && slot_logical < g.columns) physical = table_row[slot_logical];
+    Query<DT, D, VEC, G> qv;
+    const int64_t qrow = int64_t(b) * a.qkv_stride + int64_t(head) * dim;  // q, k, v row
+    qv.load(qp + qrow, col0, dim, a.qscale);
+    T new_k{}, new_v{};
+    if (tid < dim) { new_k = kin[qrow + tid]; new_v = vin[qrow + tid]; }
+    const int offset = a.offsets[b];
 
     const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
     T* orow = out + bh * dim;
@@ -1547,7 +1551,7 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   const int64_t bh = int64_t(b) * h;
   if (nsplit_max > INT_MAX) return hipErrorInvalidValue;
   if (work && (work_items < 0 || merge_rows < 0 || merge_rows > b ||
-               work_items > int64_t(b) * nsplit_max))
+               work_items > int64_t(b) * nsplit_max || (reinterpret_cast<uintptr_t>(work) & 7u)))
     return hipErrorInvalidValue;
   if (work && work_items == 0) return hipSuccess;
   const int64_t stride = qkv_stride ? qkv_stride : int64_t(h) * d;
