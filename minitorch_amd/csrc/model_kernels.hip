@@ -452,6 +452,8 @@ __global__ __launch_bounds__(256) void gelu_kernel(void* x, int64_t n) {
 #define MT_LN_ROWS_PER_BLOCK 2
 #endif
 constexpr int kLnRowsPerBlock = MT_LN_ROWS_PER_BLOCK;
+static_assert(kLnRowsPerBlock >= 1 && kLnRowsPerBlock * 64 <= 256,
+              "the one-wave-per-row LayerNorm kernels are built for at most 256 threads per workgroup");
 
 // ---------------------------------------------------------------------------
 // Decode projections on the matrix cores: out[m, n] = x[m, :] . w[n, :] for
