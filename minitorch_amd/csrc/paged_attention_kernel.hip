@@ -1007,6 +1007,9 @@ struct UniformItems {
 // rows [first_row[r], first_row[r] + n[r]) of q/k/v/out, with its own table
 // row and key offset), passed by value: every (prompt, tile) pair in the
 // order of pair_prompt / pair_tile (heaviest first), times the heads.
+#ifndef MT_RAGGED_KEY_SPLIT
+#define MT_RAGGED_KEY_SPLIT 1
+#endif
 constexpr int kRaggedPrompts = 16;
 constexpr int kRaggedTiles = 256;
 struct RaggedItems {
@@ -1015,6 +1018,10 @@ struct RaggedItems {
   const int* table[kRaggedPrompts];
   unsigned char pair_prompt[kRaggedTiles];
   unsigned short pair_tile[kRaggedTiles];
+  // Key blocks [kb0, kb1) of the pair's tile and its partials slot (-1: the
+  // pair covers all of the tile's keys and writes the output rows).
+  unsigned short pair_kb0[kRaggedTiles], pair_kb1[kRaggedTiles];
+  short pair_slot[kRaggedTiles];
   __device__ __forceinline__ int64_t count(const QueryArgs& a) const { return int64_t(pairs) * a.g.heads; }
   __device__ __forceinline__ PfItem get(int64_t item, const QueryArgs& a) const {
     const int p = int(item / a.g.heads);
@@ -1027,7 +1034,9 @@ struct RaggedItems {
     it.q0 = int64_t(first_row[r]) * a.q_r + it.head * a.q_h;
     it.o0 = int64_t(first_row[r]) * a.o_r + it.head * a.o_h;
     it.table_row = table[r];
-    it.kb0 = 0; it.kb1 = kAllKeyBlocks; it.slot = -1;
+    it.slot = pair_slot[p];
+    it.kb0 = it.slot >= 0 ? pair_kb0[p] : 0;
+    it.kb1 = it.slot >= 0 ? pair_kb1[p] : kAllKeyBlocks;
     return it;
   }
 };
@@ -1309,18 +1318,23 @@ struct PrefillMerge {
   unsigned char splits[kSplitPairs];
 };
 
+// Key splits of ragged prompts: per split tile, its first output row (in the
+// launch's rows), its valid queries, first partials slot and split count.
+struct RaggedMerge {
+  int tiles;
+  int row0[kSplitPairs];
+  unsigned short nq[kSplitPairs], first_slot[kSplitPairs];
+  unsigned char splits[kSplitPairs];
+};
+
+// Query q of a split tile: log-sum-exp merge of the n partials from slot
+// first_slot on, written to orow (256 threads: 64 queries x 4 column groups).
 template <int DT, int D>
-__global__ __launch_bounds__(256) void prefill_merge_kernel(QueryArgs a, PrefillMerge mg) {
+__device__ __forceinline__ void merge_query(const QueryArgs& a, int head, int q, int sub, int first_slot, int n,
+                                            typename Elem<DT>::T* orow) {
   using T = typename Elem<DT>::T;
   constexpr int R = pf_part_row<D>(), C = D / 16;
-  const int t = int(blockIdx.x / unsigned(a.g.heads));
-  const int head = int(blockIdx.x - unsigned(t) * a.g.heads);
-  if (t >= mg.tiles) return;
-  const int q = threadIdx.x >> 2, sub = threadIdx.x & 3;
-  const int qi = mg.tile[t] * kPfQueries + q;
-  if (qi >= a.nq) return;
-  const int n = mg.splits[t];
-  const float* base = a.partials + ((int64_t(mg.first_slot[t]) * a.g.heads + head) * kPfQueries + q) * R;
+  const float* base = a.partials + ((int64_t(first_slot) * a.g.heads + head) * kPfQueries + q) * R;
   const int64_t step = int64_t(a.g.heads) * kPfQueries * R;
   float M = -INFINITY, L = 0.f;
   float4 acc[C];
@@ -1346,7 +1360,6 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(QueryArgs a, Prefill
     }
     M = Mn;
   }
-  T* orow = static_cast<T*>(a.out) + head * a.o_h + int64_t(qi) * a.o_r;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const T r0 = from_f32<DT>(finalize(acc[c].x, L)), r1 = from_f32<DT>(finalize(acc[c].y, L));
@@ -1354,6 +1367,35 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(QueryArgs a, Prefill
     *reinterpret_cast<uint2*>(orow + 4 * (sub + 4 * c)) =
         uint2{uint32_t(r0) | (uint32_t(r1) << 16), uint32_t(r2) | (uint32_t(r3) << 16)};
   }
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(QueryArgs a, PrefillMerge mg) {
+  using T = typename Elem<DT>::T;
+  const int t = int(blockIdx.x / unsigned(a.g.heads));
+  const int head = int(blockIdx.x - unsigned(t) * a.g.heads);
+  if (t >= mg.tiles) return;
+  const int q = threadIdx.x >> 2, sub = threadIdx.x & 3;
+  const int qi = mg.tile[t] * kPfQueries + q;
+  if (qi >= a.nq) return;
+  T* orow = static_cast<T*>(a.out) + head * a.o_h + int64_t(qi) * a.o_r;
+  merge_query<DT, D>(a, head, q, sub, mg.first_slot[t], mg.splits[t], orow);
+}
+
+// Kernel arguments stay within the 4 KiB kernarg limit.
+static_assert(sizeof(QueryArgs) + sizeof(RaggedItems) <= 4096, "ragged prefill arguments");
+static_assert(sizeof(QueryArgs) + sizeof(RaggedMerge) <= 4096, "ragged merge arguments");
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void ragged_merge_kernel(QueryArgs a, RaggedMerge mg) {
+  using T = typename Elem<DT>::T;
+  const int t = int(blockIdx.x / unsigned(a.g.heads));
+  const int head = int(blockIdx.x - unsigned(t) * a.g.heads);
+  if (t >= mg.tiles) return;
+  const int q = threadIdx.x >> 2, sub = threadIdx.x & 3;
+  if (q >= mg.nq[t]) return;
+  T* orow = static_cast<T*>(a.out) + head * a.o_h + (int64_t(mg.row0[t]) + q) * a.o_r;
+  merge_query<DT, D>(a, head, q, sub, mg.first_slot[t], mg.splits[t], orow);
 }
 
 // Multi-token append at a common offset (reference paged_append with
@@ -1945,9 +1987,70 @@ int mt_paged_prefill_ragged(void* out, const void* q, const void* k, const void*
       };
       return keys(x) > keys(y);
     });
+    // Key splits: a tile whose keys span more blocks than its share of the
+    // launch (all pairs' key blocks times the heads over two workgroups per
+    // compute unit, at least 2) is cut into pieces of at most that many
+    // blocks, merged afterwards by ragged_merge_kernel. Only when the longest
+    // tile has at least 6 blocks, as for one prompt (launch_split_prefill).
+    auto blocks_of = [&](const std::pair<int, int>& z) {
+      const int last = (z.second + 1) * kPfQueries < it.n[z.first] ? (z.second + 1) * kPfQueries : it.n[z.first];
+      return (it.offset[z.first] + last + kPfKeys - 1) / kPfKeys;
+    };
+    int64_t total_blocks = 0;
+    int max_blocks = 0;
+    for (const auto& z : order) {
+      total_blocks += blocks_of(z);
+      max_blocks = std::max(max_blocks, blocks_of(z));
+    }
+    const int cus = device_compute_units();
+    int B = std::max<int>(2, int((total_blocks * h + 2 * cus - 1) / (2 * std::max(cus, 1))));
+    auto pieces = [&](int B) {
+      int64_t c = 0;
+      for (const auto& z : order) c += (blocks_of(z) + B - 1) / B;
+      return c;
+    };
+    while (pieces(B) > kRaggedTiles) ++B;
+    bool split = MT_RAGGED_KEY_SPLIT && cus > 0 && max_blocks >= 6 && max_blocks > B && max_blocks <= 65535;
+    struct Piece { int p, t, kb0, kb1, slot; };
+    std::vector<Piece> list;
+    RaggedMerge mg{};
+    int slots = 0;
+    if (split) {
+      for (const auto& z : order) {
+        const int nb = blocks_of(z), n = (nb + B - 1) / B;
+        if (n > 1) {
+          mg.row0[mg.tiles] = it.first_row[z.first] + z.second * kPfQueries;
+          mg.nq[mg.tiles] = static_cast<unsigned short>(std::min(kPfQueries, it.n[z.first] - z.second * kPfQueries));
+          mg.first_slot[mg.tiles] = static_cast<unsigned short>(slots);
+          mg.splits[mg.tiles] = static_cast<unsigned char>(n);
+          ++mg.tiles;
+        }
+        for (int j = 0; j < n; ++j)
+          list.push_back({z.first, z.second, j * B, std::min(nb, (j + 1) * B), n > 1 ? slots++ : -1});
+      }
+      // Heaviest pieces first.
+      std::stable_sort(list.begin(), list.end(),
+                       [](const Piece& x, const Piece& y) { return x.kb1 - x.kb0 > y.kb1 - y.kb0; });
+    } else {
+      for (const auto& z : order) list.push_back({z.first, z.second, 0, blocks_of(z), -1});
+    }
+    void* ws = nullptr;
+    // Without room for the partials the launch runs unsplit.
+    if (split && (mg.tiles > kSplitPairs || slots > 32767 ||
+                  library_workspace(size_t(slots) * h * kPfQueries * (d + 4) * sizeof(float), &ws) != hipSuccess)) {
+      split = false;
+      list.clear();
+      mg = RaggedMerge{};
+      for (const auto& z : order) list.push_back({z.first, z.second, 0, blocks_of(z), -1});
+    }
+    pairs = int(list.size());
+    it.pairs = pairs;
     for (int i = 0; i < pairs; ++i) {
-      it.pair_prompt[i] = static_cast<unsigned char>(order[i].first);
-      it.pair_tile[i] = static_cast<unsigned short>(order[i].second);
+      it.pair_prompt[i] = static_cast<unsigned char>(list[i].p);
+      it.pair_tile[i] = static_cast<unsigned short>(list[i].t);
+      it.pair_kb0[i] = static_cast<unsigned short>(list[i].kb0);
+      it.pair_kb1[i] = static_cast<unsigned short>(list[i].kb1);
+      it.pair_slot[i] = static_cast<short>(list[i].slot);
     }
     const size_t qoff = size_t(row0) * qkv_stride * e, ooff = size_t(row0) * out_stride * e;
     QueryArgs a{};
@@ -1960,6 +2063,7 @@ int mt_paged_prefill_ragged(void* out, const void* q, const void* k, const void*
     a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
     a.q_h = d; a.q_r = qkv_stride;
     a.o_h = d; a.o_r = out_stride;
+    a.partials = static_cast<float*>(ws);
     const int blocks = grid_for(int64_t(pairs) * h);
     if (dtype == kF16) {
       if (d == 64) prefill_kernel<kF16, 64, RaggedItems, true><<<blocks, kThreads>>>(a, it);
@@ -1968,8 +2072,19 @@ int mt_paged_prefill_ragged(void* out, const void* q, const void* k, const void*
       if (d == 64) prefill_kernel<kBF16, 64, RaggedItems, true><<<blocks, kThreads>>>(a, it);
       else prefill_kernel<kBF16, 128, RaggedItems, true><<<blocks, kThreads>>>(a, it);
     }
+    if (split) {
+      const unsigned mblocks = unsigned(mg.tiles * h);
+      if (dtype == kF16) {
+        if (d == 64) ragged_merge_kernel<kF16, 64><<<mblocks, 256>>>(a, mg);
+        else ragged_merge_kernel<kF16, 128><<<mblocks, 256>>>(a, mg);
+      } else {
+        if (d == 64) ragged_merge_kernel<kBF16, 64><<<mblocks, 256>>>(a, mg);
+        else ragged_merge_kernel<kBF16, 128><<<mblocks, 256>>>(a, mg);
+      }
+    }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
+    if (split) g_key_split_launches.fetch_add(1, std::memory_order_relaxed);
     r0 = r1;
     row0 += rows;
   }

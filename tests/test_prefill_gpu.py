@@ -426,3 +426,22 @@ def test_prefill_above_the_split_limit_stays_unsplit():
     run_prefill(case, nq, nq, 0, seed=97)
     run_fused_single(case, nq, 0, seed=97)
     assert key_split_launches() == before
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+@pytest.mark.parametrize('dim', [64, 128])
+def test_prefill_ragged_key_splits(dtype, dim):
+    # A replacement batch of config-4 shape (16 heads): one long prompt among
+    # short ones. The long prompt's last tiles span more key blocks than their
+    # share of the launch, so their keys are split over workgroups and merged;
+    # every prompt against the oracle and the pool image bit for bit.
+    tokens, offsets = [1000, 60, 130, 5, 300], [0, 0, 20, 7, 0]
+    before = key_split_launches()
+    run_ragged(dtype, dim, tokens, offsets, h=16, seed=dim + 1)
+    assert key_split_launches() == before + 1, 'the ragged launch did not split the keys'
+
+
+def test_prefill_ragged_short_prompts_stay_unsplit():
+    before = key_split_launches()
+    run_ragged('bfloat16', 64, [1, 5, 16, 63, 64, 65, 130], [0, 7, 0, 100, 0, 33, 0], h=16, seed=5)
+    assert key_split_launches() == before
