@@ -273,7 +273,7 @@ def test_config4_gpt2_medium_pages_reuse_and_attention():
                                      pages_per_slab=pool.pages_per_slab, num_slabs=pool.num_slabs,
                                      columns=columns, layer=layer, layers=model.n_layer, dtype='bfloat16')
         runtime().synchronize()
-        assert_attention_close(dout.to_numpy(), ref, 'bfloat16', context='config 4 layer 7')
+        assert_attention_close(dout.to_numpy(), ref, 'bfloat16', context='config 4 layer 7', ref_rounded=True)
         assert np.array_equal(_layer_block(pool, layer), host.image), 'append into the live pool differs'
 
         for c, o in zip(caches, shadows):
