@@ -57,6 +57,10 @@ CASES = [
     (200, 2304, 768, 1, 0),
     (256, 768, 3072, 4, 2),
     (150, 1024, 4096, 4, 2),
+    # more than 32 rows with 8 splits
+    (150, 1024, 4096, 8, 2),
+    (40, 768, 3072, 8, 2),
+    (128, 1024, 1024, 8, 2),
 ]
 
 
