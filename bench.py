@@ -477,7 +477,10 @@ def bench_projections(args):
     """Decode projections of DistilGPT-2 (fp16) and GPT-2-medium (bf16) at a
     few batch sizes: the matrix-core projection kernel (mt_decode_projection,
     with the split the decoder loop chooses for the out- and proj-projections)
-    against hipBLASLt (mt_gemm_ex with bias), each over enough distinct copies
+    on row-major operands and on fragment-tiled ones (the weights, and the
+    activations of qkv, fc and proj; fc also writes its output tiled, as in the
+    decoder loop) against hipBLASLt
+    (mt_gemm_ex with bias), each over enough distinct copies
     of the weights (>= 512 MiB) that every launch reads them from HBM, the
     launches of one kind captured in a HIP graph and replayed; microseconds
     per launch."""
@@ -486,7 +489,7 @@ def bench_projections(args):
     from minitorch_amd.dtypes import dtype_code
     rt = runtime()
     lib = model_library()
-    proj_args = [P, P, P, P, I, I, I, I, I, I]
+    proj_args = [P, P, P, P, I, I, I, I, I, I, I]
     gemm_args = [P, P, P, P, P, I, I, I, I, I, I]
     blas = DecoderLM(n_vocab=16, n_embd=16, n_head=1, n_layer=1, n_positions=4).blas()
 
@@ -495,17 +498,22 @@ def bench_projections(args):
         rt.check(rt.lib.mt_fill_random(t.ptr, int(np.prod(shape)), seed, dtype_code(dtype)))
         return t
 
-    def waves_ok(rng, mt):
-        smax = 2 if mt >= 8 else 4
+    def waves_ok(rng, q):
+        smax = 2 if q >= 8 else 4
         return any(rng % (32 * w) == 0 and rng // (32 * w) <= smax for w in range(16, 0, -1))
 
     def splits(m, n, k):
-        # the decoder loop's choice (projection_splits in csrc/model_kernels.hip)
-        mt = 1 if m <= 16 else 2 if m <= 32 else 4 if m <= 64 else 8
-        tiles, s = n // 16 * ((m + 127) // 128), 1
-        while s < 8 and not (k % s == 0 and waves_ok(k // s, mt)):
+        # the decoder loop's choice (proj_tiles and projection_splits in csrc/model_kernels.hip)
+        if m <= 32:
+            mt, nt = (1 if m <= 16 else 2), 1
+        elif n % 32 == 0:
+            mt, nt = (2 if m <= 64 else 4), 2
+        else:
+            mt, nt = (4 if m <= 64 else 8), 1
+        tiles, s = n // (16 * nt) * -(-m // (16 * mt)), 1
+        while s < 8 and not (k % s == 0 and waves_ok(k // s, mt * nt)):
             s *= 2
-        while s < 8 and tiles * s < rt.compute_units() and k % (2 * s) == 0 and waves_ok(k // (2 * s), mt):
+        while s < 8 and tiles * s < rt.compute_units() and k % (2 * s) == 0 and waves_ok(k // (2 * s), mt * nt):
             s *= 2
         return s
 
@@ -528,11 +536,12 @@ def bench_projections(args):
         return e1.seconds_since(e0) / reps
 
     rows = []
-    for name, d, dtype, ms in (('distilgpt2', 768, 'float16', (2, 16, 64)),
-                               ('gpt2-medium', 1024, 'bfloat16', (2, 16, 64, 128))):
+    for name, d, dtype, ms in (('distilgpt2', 768, 'float16', (2, 16, 64, 128)),
+                               ('gpt2-medium', 1024, 'bfloat16', (2, 16, 32, 64, 128, 256))):
         code = dtype_code(dtype)
         for m in ms:
             x = filled((m, 4 * d), 1, dtype)
+            xt = filled((-(-m // 16) * 16, 4 * d), 3, dtype)  # the tiled layout's padded rows
             bias = filled((4 * d,), 2, dtype)
             out = DeviceTensor((8, m, 4 * d), 'float32')
             for kind, n, k, epi in (('qkv', 3 * d, d, 0), ('out', d, d, 2), ('fc', 4 * d, d, 1),
@@ -541,10 +550,10 @@ def bench_projections(args):
                 copies = max(8, -(-(512 << 20) // (n * k * 2)))
                 ws = [filled((n, k), 100 + i, dtype) for i in range(copies)]
 
-                def own():
+                def own(layout=0):
                     for w in ws:
-                        call(lib, 'mt_decode_projection', proj_args, out.ptr, x.ptr, w.ptr,
-                             0 if epi == 2 else bias.ptr, m, n, k, sp, epi, code)
+                        call(lib, 'mt_decode_projection', proj_args, out.ptr, xt.ptr if layout else x.ptr, w.ptr,
+                             0 if epi == 2 else bias.ptr, m, n, k, sp, epi, code, layout)
 
                 def hipblaslt():
                     for w in ws:
@@ -554,6 +563,9 @@ def bench_projections(args):
                 rows.append(dict(model=name, rows=m, projection=kind, n=n, k=k, splits=sp,
                                  epilogue=('bias', 'bias+gelu', 'split partials')[epi],
                                  own_us=round(t_own * 1e6, 2), hipblaslt_us=round(t_blas * 1e6, 2)))
+                # tiled weights, and tiled activations except for out (attention's row-major output)
+                layout = 4 | (0 if kind == 'out' else 3 if kind == 'fc' else 1)
+                rows[-1]['own_tiled_us'] = round(graph_time(lambda: own(layout)) / copies * 1e6, 2)
                 print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
                 del ws
     return dict(metric='decode projection time (us per launch, cold weights)', projections=rows)

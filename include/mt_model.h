@@ -25,6 +25,10 @@ typedef struct mt_decoder_layer {
   const float* ln2_gamma; const float* ln2_beta;
   const void* w_fc; const void* b_fc;
   const void* w_proj; const void* b_proj;
+  /* The four projection weights again in the fragment-tiled layout of
+   * mt_decode_projection (fp16/bf16 only; null: the decode projections read
+   * the row-major copies above, which hipBLASLt always reads). */
+  const void* w_qkv_tiled; const void* w_o_tiled; const void* w_fc_tiled; const void* w_proj_tiled;
 } mt_decoder_layer;
 
 /* Paged-cache metadata of one decode batch, as mt_paged_decode_split takes it
@@ -117,12 +121,20 @@ int mt_residual_layernorm(void* out, float* x, const void* y, const float* gamma
  * out [m, n] in dtype; 1: + bias, then tanh GELU in fp32, out in dtype;
  * 2: out [splits, m, n] fp32 partial sums over `splits` (1, 2, 4 or 8)
  * equal k ranges, no bias (epilogues 0 and 1 take splits = 1). Requires n a
- * multiple of 16, k a multiple of 128 * splits, x and w 16-byte aligned, out
- * 8-byte (16-byte for epilogue 2) aligned; hipErrorInvalidValue otherwise.
- * Weights are read once per call. No reference counterpart (the reference's
- * Linear, minitorch/modules_basic.py:132-149, calls cuBLAS). */
+ * multiple of 16, k / splits = 32 * s * w for some w <= 16 and s <= 4
+ * (s <= 2 when m > 64), x and w 16-byte aligned, out 8-byte (16-byte for
+ * epilogue 2) aligned; hipErrorInvalidValue otherwise. layout bit 0: x is in
+ * the fragment-tiled layout, bit 1: out (epilogues 0 and 1, n a multiple of
+ * 32) is written in it, bit 2: w [n, k] is in it (fragment_tiled in
+ * minitorch_amd/model.py writes it). That layout stores a 16-bit [rows, width] matrix
+ * (width a multiple of 32) as ceil(rows / 16) * 16 rows: element (r, c) at
+ * ((r / 16) * (width / 32) + c / 32) * 512 + (((c / 8) % 4) * 16 + r % 16) * 8
+ * + c % 8, i.e. each 16 x 32 block as one 1 KB run in the order the matrix
+ * cores take it; rows past m are read and never affect the result. Weights
+ * are read once per call. No reference counterpart (the reference's Linear,
+ * minitorch/modules_basic.py:132-149, calls cuBLAS). */
 int mt_decode_projection(void* out, const void* x, const void* w, const void* bias, int m, int n, int k,
-                         int splits, int epilogue, int dtype);
+                         int splits, int epilogue, int dtype, int layout);
 
 /* mt_decode_projection (epilogue 0 or 1, one split) whose activations are
  * LayerNorm(x_in + part_bias + sum_s partials[s]) for rows r < m: v[r, :] =
@@ -134,22 +146,25 @@ int mt_decode_projection(void* out, const void* x, const void* w, const void* bi
  * multiple of 256 up to 1024, n a multiple of 16, 16-byte aligned
  * x_in/x_out/partials/gamma/beta/w, 8-byte aligned out/bias/part_bias;
  * hipErrorInvalidValue otherwise. The residual add and LayerNorm of a decode
- * step fused into the QKV and fc projections for small batches. No reference
- * counterpart (minitorch/modules_transformer.py:272-282 around the Linear of
+ * step fused into the QKV and fc projections for small batches. layout 0: w
+ * row-major, 4: w in the fragment-tiled layout (mt_decode_projection). No
+ * reference counterpart (minitorch/modules_transformer.py:272-282 around the Linear of
  * minitorch/modules_basic.py:132-149). */
 int mt_decode_projection_ln(void* out, const float* x_in, float* x_out, const float* partials, int splits,
                             const void* part_bias, const float* gamma, const float* beta, float eps, const void* w,
-                            const void* bias, int m, int n, int k, int epilogue, int dtype);
+                            const void* bias, int m, int n, int k, int epilogue, int dtype, int layout);
 
 /* x[r, :] += bias + sum_s partials[s, r, :] (fp32), then out[r, :] =
  * LayerNorm(x[r, :]) in dtype (1 or 2): the residual add and LayerNorm after
  * a split projection (mt_decode_projection epilogue 2), as
  * mt_residual_layernorm. width a multiple of 256, at most 2048; 1 <= splits
- * <= 8. No reference counterpart (minitorch/modules_transformer.py:272-282
- * with the projection's split-k reduction folded in). */
+ * <= 8; layout 0: out [rows, width] row-major, 2: out in the fragment-tiled
+ * layout of mt_decode_projection. No reference counterpart
+ * (minitorch/modules_transformer.py:272-282 with the projection's split-k
+ * reduction folded in). */
 int mt_residual_layernorm_partials(void* out, float* x, const float* partials, int splits, const void* bias,
                                    const float* gamma, const float* beta, int rows, int width, float eps,
-                                   int dtype);
+                                   int dtype, int layout);
 
 /* Scratch bytes mt_decoder_layers needs for `rows` tokens of width d. */
 size_t mt_decoder_scratch_bytes(int rows, int d, int dtype);

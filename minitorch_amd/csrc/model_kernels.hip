@@ -362,6 +362,26 @@ __global__ __launch_bounds__(256) void residual_layernorm_kernel(void* out, floa
     o[i] = from_f32<DT>(gamma[i] * ((row[i] - mean) * inv) + beta[i]);
 }
 
+// Fragment-tiled layout of a 16-bit [rows, width] activation matrix (width a
+// multiple of 32, rows padded to a multiple of 16): the 16 x 32 block of row
+// tile R and column tile K is 1 KB at element ((R * width / 32) + K) * 512,
+// stored in the order lane (c, g) of v_mfma_f32_16x16x32 takes it as its B
+// operand: row 16 R + c, columns 32 K + 8 g .. 8 g + 7 at element
+// (16 g + c) * 8 of the block. A wave then reads a B fragment as one 1 KB run
+// of consecutive 16-byte lane loads, which the memory pipeline coalesces;
+// from row-major rows the same fragment is 16 separate 64-byte pieces, served
+// at about a third of the rate (MI355X: ~35 against ~110 GB/s per compute
+// unit from L2). kProjXTiled: x is tiled; kProjOutTiled: out (epilogues 0
+// and 1) is written tiled; kProjWTiled: the weights [n, k] are tiled (their
+// A fragments have the same lane order). A tiled buffer holds
+// ceil(rows / 16) * 16 rows; the rows past `rows` are read but never affect a
+// stored result.
+enum ProjLayout : int { kProjXTiled = 1, kProjOutTiled = 2, kProjWTiled = 4 };
+__host__ __device__ __forceinline__ int64_t tiled_offset(int row, int col, int width) {
+  return ((int64_t(row >> 4) * (width >> 5) + (col >> 5)) << 9) + ((((col >> 3) & 3) << 4) + (row & 15)) * 8 +
+         (col & 7);
+}
+
 // The same residual add + LayerNorm with one wave per row, for widths that are
 // a multiple of 256 (at most 256 * NJ): lane l owns columns 4l + 256j of
 // every 256-column block j. All loads of a row (x, y, gamma, beta) are issued
@@ -373,7 +393,7 @@ __global__ __launch_bounds__(256) void residual_layernorm_wave_kernel(void* out,
                                                                       const float* gamma,
                                                                       const float* beta, int rows,
                                                                       int width, float eps,
-                                                                      int has_residual) {
+                                                                      int has_residual, int out_tiled) {
   using T = typename Elem<DT>::T;
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
@@ -412,19 +432,20 @@ __global__ __launch_bounds__(256) void residual_layernorm_wave_kernel(void* out,
   const float mean = sum / width;
   const float var = fmaxf(sq / width - mean * mean, 0.f) + eps;
   const float inv = 1.f / sqrtf(var);
-  T* o = static_cast<T*>(out) + int64_t(row) * width;
+  T* o = static_cast<T*>(out);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     if (j >= nj) break;
     const int c = 256 * j + 4 * lane;
+    const int64_t at = out_tiled ? tiled_offset(row, c, width) : int64_t(row) * width + c;
     const float r0 = g[j].x * ((v[j].x - mean) * inv) + b[j].x;
     const float r1 = g[j].y * ((v[j].y - mean) * inv) + b[j].y;
     const float r2 = g[j].z * ((v[j].z - mean) * inv) + b[j].z;
     const float r3 = g[j].w * ((v[j].w - mean) * inv) + b[j].w;
     if constexpr (DT == kF32) {
-      *reinterpret_cast<float4*>(o + c) = float4{r0, r1, r2, r3};
+      *reinterpret_cast<float4*>(o + at) = float4{r0, r1, r2, r3};
     } else {
-      *reinterpret_cast<uint2*>(o + c) =
+      *reinterpret_cast<uint2*>(o + at) =
           uint2{uint32_t(from_f32<DT>(r0)) | (uint32_t(from_f32<DT>(r1)) << 16),
                 uint32_t(from_f32<DT>(r2)) | (uint32_t(from_f32<DT>(r3)) << 16)};
     }
@@ -468,8 +489,8 @@ static_assert(kLnRowsPerBlock >= 1 && kLnRowsPerBlock * 64 <= 256,
 // C^T = W X^T on v_mfma_f32_16x16x32: A = 16 weight rows, B = 16 activation
 // rows, both contiguous along k and loaded 16 bytes per lane straight from
 // global memory; lane (c, g) ends up holding C^T[4g + i][c], i.e. 4
-// consecutive features of one row. A workgroup owns 16 features, up to 128
-// rows (blockIdx.z selects the block of 128) and k range blockIdx.y of
+// consecutive features of one row. A workgroup owns 16 NT features, 16 MT
+// rows (blockIdx.z selects the row block) and k range blockIdx.y of
 // `splits`; its WK waves (blockDim.x / 64) split that range into kc-wide
 // pieces of at most SMAX 32-wide steps, and their sums meet in LDS. Weights
 // are read with non-temporal loads (a step's weights do not fit the caches);
@@ -482,16 +503,16 @@ static_assert(kLnRowsPerBlock >= 1 && kLnRowsPerBlock * 64 <= 256,
 constexpr int kProjMaxRows = 256;
 constexpr int kProjMaxSplits = 8;
 constexpr int kProjMaxWaves = 16;
-constexpr int kProjRowBlock = 128;  // rows per workgroup (8 tiles of 16)
-// Row counts up to which the decode step uses this kernel rather than
-// hipBLASLt (measured on MI355X, captured DistilGPT-2 and GPT-2-medium decode
-// steps): every compute unit takes in all m * k activation bytes of an
-// unsplit projection, which from 32 rows on costs as much as hipBLASLt's
-// tiling; the split projections plus their LayerNorm reduction stay ahead to
-// 32 rows and fall behind by 64.
+// Row counts up to which a decode step on row-major activations (the layer
+// loop's fallback when neither the fused nor the tiled path takes the shapes)
+// uses this kernel rather than hipBLASLt, measured on MI355X with captured
+// DistilGPT-2 and GPT-2-medium steps: unsplit projections to 16 rows, split
+// ones plus their LayerNorm reduction to 32. The tiled path also takes its
+// out-projection (row-major: attention's output) split up to kProjSplitRows.
 constexpr int kProjDirectRows = 16;
 constexpr int kProjSplitRows = 32;
 enum ProjEpilogue : int { kProjBias = 0, kProjGelu = 1, kProjPartials = 2 };
+
 
 struct ProjArgs {
   void* out;
@@ -500,6 +521,7 @@ struct ProjArgs {
   const void* bias;
   int m, n, k;
   int kc;  // k per wave: k / (splits * waves), a multiple of 32, at most 32 * SMAX
+  int w_tiled;  // w is [n, k] in the fragment-tiled layout
   // LayerNorm prologue (projection_kernel with PS >= 0): the activations are
   // LayerNorm(x_in + part_bias + sum of the PS partial rows part[s, r, :]),
   // computed by every workgroup; workgroup (0, 0, 0) writes the sum to x_out.
@@ -529,7 +551,9 @@ __device__ __forceinline__ float gelu_tanh(float v) {
 
 // Steps of 32 a wave may hold in flight: 2 with 8 row tiles (the loads and
 // accumulators then fill the 128 registers a 16-wave workgroup allows), 4
-// with fewer.
+// with fewer. (4 steps in 8-wave workgroups at 8 row tiles, which halves the
+// cross-wave reduction, measured 4-8 % slower on MI355X: fewer loads in
+// flight per compute unit.)
 template <int MT>
 constexpr int proj_max_steps() { return MT >= 8 ? 2 : 4; }
 
@@ -601,33 +625,58 @@ __device__ __forceinline__ void ln_prologue(const ProjArgs& p, float* vbuf, floa
   __syncthreads();
 }
 
-// PS < 0: activations read from p.x. PS >= 0 (one row tile, one split): the
+// PS < 0: activations read from p.x (row-major, or tiled with LAY &
+// kProjXTiled). PS >= 0 (one row tile, one feature tile, one split): the
 // activations come from the LayerNorm prologue through LDS; the weight loads
-// are issued before it, so their HBM latency overlaps it.
-template <int DT, int MT, int EPI, int PS = -1>
+// are issued before it, so their HBM latency overlaps it. LAY &
+// kProjOutTiled writes out tiled. A workgroup owns NT feature tiles and MT
+// row tiles: each wave's step loads NT weight and MT activation fragments and
+// runs NT * MT MFMAs.
+template <int DT, int MT, int EPI, int PS = -1, int LAY = 0, int NT = 1>
 __global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
   using T = typename Elem<DT>::T;
   using V8 = typename Mfma<DT>::v8;
-  constexpr int SMAX = proj_max_steps<MT>();
-  constexpr int NL = 1 + MT;  // 16-byte loads per lane and step
+  constexpr int SMAX = proj_max_steps<MT * NT>();
+  constexpr int NL = NT + MT;  // 16-byte loads per lane and step
+  constexpr int NQ = NT * MT;  // output tiles
   constexpr bool LN = PS >= 0;
-  static_assert(!LN || MT == 1, "the LayerNorm prologue takes one row tile");
-  // [waves][MT][64] sums | LN: v [m][k] fp32, gamma/beta [2][k] fp32, tile [16][k + 8] T
+  constexpr bool XT = (LAY & kProjXTiled) != 0;
+  constexpr int XSTEP = XT ? 512 : 32;  // elements between a lane's activations of consecutive 32-wide steps
+  static_assert(!LN || (MT == 1 && NT == 1), "the LayerNorm prologue takes one row and one feature tile");
+  static_assert(!LN || LAY == 0, "the LayerNorm prologue reads its activations from LDS");
+  static_assert(EPI != kProjPartials || !(LAY & kProjOutTiled), "split partials are written row-major");
+  // [waves][NQ][64] sums | LN: v [m][k] fp32, gamma/beta [2][k] fp32, tile [16][k + 8] T
   extern __shared__ floatx4 red[];
   const int waves = int(blockDim.x >> 6);
   const int wave = int(threadIdx.x >> 6), lane = int(threadIdx.x & 63);
   const int col = lane & 15, grp = lane >> 4;
-  const int f0 = int(blockIdx.x) * 16;
-  const int r0 = int(blockIdx.z) * kProjRowBlock;
+  const int f0 = int(blockIdx.x) * 16 * NT;
+  const int r0 = int(blockIdx.z) * 16 * MT;
   const int k0 = (int(blockIdx.y) * waves + wave) * p.kc + 8 * grp;
+  const int kt = (k0 - 8 * grp) >> 5;  // the wave's first 32-wide step
   const int steps = p.kc >> 5;
-  const T* w = static_cast<const T*>(p.w) + int64_t(f0 + col) * p.k + k0;
+  // weights [n, k] row-major, or tiled (p.w_tiled) as the activations are
+  const T* w = p.w_tiled ? static_cast<const T*>(p.w) + ((int64_t(f0 >> 4) * (p.k >> 5) + kt) << 9) + lane * 8
+                         : static_cast<const T*>(p.w) + int64_t(f0 + col) * p.k + k0;
+  const int wstep = p.w_tiled ? 512 : 32;  // elements between a lane's weights of consecutive steps
+  const int wtile = p.k << 4;              // and of consecutive feature tiles (16 rows of k in both layouts)
   const T* x = static_cast<const T*>(p.x);
-  int xoff[MT];  // element offsets of this lane's activation rows (rows past m repeat row m - 1)
+  int xoff[MT];  // element offsets of this lane's activations at the first step
+  if constexpr (XT) {
+    // row tiles past the last one repeat it (their columns are never stored)
+    const int last = (p.m - 1) >> 4;
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    const int row = r0 + 16 * t + col < p.m ? r0 + 16 * t + col : p.m - 1;
-    xoff[t] = row * p.k + k0;
+    for (int t = 0; t < MT; ++t) {
+      const int rt = (r0 >> 4) + t < last ? (r0 >> 4) + t : last;
+      xoff[t] = ((rt * (p.k >> 5) + kt) << 9) + lane * 8;
+    }
+  } else {
+    // rows past m repeat row m - 1
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int row = r0 + 16 * t + col < p.m ? r0 + 16 * t + col : p.m - 1;
+      xoff[t] = row * p.k + k0;
+    }
   }
   u32x4 buf[SMAX][NL];
   if constexpr (LN) {
@@ -637,7 +686,7 @@ __global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
     const int xs = p.k + 8;
 #pragma unroll
     for (int s = 0; s < SMAX; ++s)
-      if (s < steps) buf[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + 32 * s));
+      if (s < steps) buf[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + wstep * s));
     ln_prologue<DT, PS>(p, vbuf, gb, xt, xs, wave, waves, lane);
     const int row = col < p.m ? col : p.m - 1;
 #pragma unroll
@@ -647,36 +696,42 @@ __global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
 #pragma unroll
     for (int s = 0; s < SMAX; ++s) {
       if (s < steps) {
-        buf[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + 32 * s));
 #pragma unroll
-        for (int t = 0; t < MT; ++t) buf[s][1 + t] = *global_view(reinterpret_cast<const u32x4*>(x + xoff[t] + 32 * s));
+        for (int f = 0; f < NT; ++f)
+          buf[s][f] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + wtile * f + wstep * s));
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          buf[s][NT + t] = *global_view(reinterpret_cast<const u32x4*>(x + xoff[t] + XSTEP * s));
       }
     }
   }
-  floatx4 acc[MT];
+  floatx4 acc[NQ];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < NQ; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < SMAX; ++s) {
     if (s < steps) {
 #pragma unroll
-      for (int t = 0; t < MT; ++t)
-        acc[t] = Mfma<DT>::run(__builtin_bit_cast(V8, buf[s][0]), __builtin_bit_cast(V8, buf[s][1 + t]), acc[t]);
+      for (int f = 0; f < NT; ++f)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          acc[f * MT + t] = Mfma<DT>::run(__builtin_bit_cast(V8, buf[s][f]), __builtin_bit_cast(V8, buf[s][NT + t]),
+                                          acc[f * MT + t]);
     }
   }
 
 #pragma unroll
-  for (int t = 0; t < MT; ++t) red[(wave * MT + t) * 64 + lane] = acc[t];
+  for (int q = 0; q < NQ; ++q) red[(wave * NQ + q) * 64 + lane] = acc[q];
   __syncthreads();
-  for (int t = wave; t < MT; t += waves) {
-    floatx4 a = red[t * 64 + lane];
+  for (int q = wave; q < NQ; q += waves) {
+    floatx4 a = red[q * 64 + lane];
     for (int v = 1; v < waves; ++v) {
-      const floatx4 b = red[(v * MT + t) * 64 + lane];
+      const floatx4 b = red[(v * NQ + q) * 64 + lane];
       a[0] += b[0]; a[1] += b[1]; a[2] += b[2]; a[3] += b[3];
     }
-    const int row = r0 + 16 * t + col;
+    const int row = r0 + 16 * (q % MT) + col;
     if (row >= p.m) continue;
-    const int feat = f0 + 4 * grp;
+    const int feat = f0 + 16 * (q / MT) + 4 * grp;
     float v[4] = {a[0], a[1], a[2], a[3]};
     if constexpr (EPI == kProjPartials) {
       float* o = static_cast<float*>(p.out) + (int64_t(blockIdx.y) * p.m + row) * p.n + feat;
@@ -691,7 +746,7 @@ __global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = gelu_tanh(v[i]);
       }
-      T* o = static_cast<T*>(p.out) + int64_t(row) * p.n + feat;
+      T* o = static_cast<T*>(p.out) + ((LAY & kProjOutTiled) ? tiled_offset(row, feat, p.n) : int64_t(row) * p.n + feat);
       *reinterpret_cast<uint2*>(o) =
           uint2{uint32_t(from_f32<DT>(v[0])) | (uint32_t(from_f32<DT>(v[1])) << 16),
                 uint32_t(from_f32<DT>(v[2])) | (uint32_t(from_f32<DT>(v[3])) << 16)};
@@ -707,7 +762,7 @@ template <int DT, int NJ, int S>
 __global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* out, float* x, const float* part,
                                                                           const void* bias, const float* gamma,
                                                                           const float* beta, int rows, int width,
-                                                                          float eps) {
+                                                                          float eps, int out_tiled) {
   using T = typename Elem<DT>::T;
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
@@ -751,18 +806,19 @@ __global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* 
   const float mean = sum / width;
   const float var = fmaxf(sq / width - mean * mean, 0.f) + eps;
   const float inv = 1.f / sqrtf(var);
-  T* o = static_cast<T*>(out) + int64_t(row) * width;
+  T* o = static_cast<T*>(out);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     if (j >= nj) break;
     const int c = 256 * j + 4 * lane;
+    const int64_t at = out_tiled ? tiled_offset(row, c, width) : int64_t(row) * width + c;
     const float4 g = *reinterpret_cast<const float4*>(gamma + c);
     const float4 b = *reinterpret_cast<const float4*>(beta + c);
     const float r0 = g.x * ((v[j].x - mean) * inv) + b.x;
     const float r1 = g.y * ((v[j].y - mean) * inv) + b.y;
     const float r2 = g.z * ((v[j].z - mean) * inv) + b.z;
     const float r3 = g.w * ((v[j].w - mean) * inv) + b.w;
-    *reinterpret_cast<uint2*>(o + c) =
+    *reinterpret_cast<uint2*>(o + at) =
         uint2{uint32_t(from_f32<DT>(r0)) | (uint32_t(from_f32<DT>(r1)) << 16),
               uint32_t(from_f32<DT>(r2)) | (uint32_t(from_f32<DT>(r3)) << 16)};
   }
@@ -770,14 +826,28 @@ __global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* 
 
 bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; }
 
-// Row tiles of 16 a workgroup holds for m rows (m > 128 takes blocks of 128).
-int proj_row_tiles(int m) { return m <= 16 ? 1 : m <= 32 ? 2 : m <= 64 ? 4 : 8; }
+// Row tiles (mt) and feature tiles (nt) of 16 a workgroup holds for m rows of
+// an n-feature projection (more rows take several row blocks of 16 mt). Every
+// workgroup takes in (16 mt + 16 nt) k elements for 256 mt nt outputs: from
+// 33 rows on, 32 features (n a multiple of 32) by 32 or 64 rows read a
+// fifth to a third less than 16 features by 64 or 128 rows, with the same
+// number of workgroups.
+struct ProjTiles {
+  int mt, nt;
+};
+ProjTiles proj_tiles(int m, int n) {
+  if (m <= 16) return {1, 1};
+  if (m <= 32) return {2, 1};
+  if (n % 32 == 0) return {m <= 64 ? 2 : 4, 2};
+  return {m <= 64 ? 4 : 8, 1};
+}
 
-// Waves per workgroup for a k range of `range` per split: the most (at most
-// kProjMaxWaves) that leave each wave a whole number of 32-wide steps, at most
-// as many as it can hold in flight; 0 if none does.
-int proj_waves(int range, int mt) {
-  const int smax = mt >= 8 ? proj_max_steps<8>() : proj_max_steps<4>();
+// Waves per workgroup for a k range of `range` per split and q = mt * nt
+// output tiles: the most (at most kProjMaxWaves) that leave each wave a whole
+// number of 32-wide steps, at most as many as it can hold in flight; 0 if none
+// does.
+int proj_waves(int range, int q) {
+  const int smax = q >= 8 ? proj_max_steps<8>() : proj_max_steps<4>();
   for (int wv = kProjMaxWaves; wv >= 1; --wv)
     if (range % (32 * wv) == 0 && range / (32 * wv) <= smax) return wv;
   return 0;
@@ -788,13 +858,17 @@ int proj_waves(int range, int mt) {
 // ranges that some wave count divides into short whole-step pieces, 16-byte
 // aligned rows.
 bool projection_ok(const void* out, const void* x, const void* w, const void* bias, int m, int n, int k,
-                   int splits, int epilogue, int dtype) {
+                   int splits, int epilogue, int dtype, int layout = 0) {
   if (dtype != kF16 && dtype != kBF16) return false;
   if (m < 1 || m > kProjMaxRows || n < 16 || n % 16 || k < 32) return false;
   if (splits != 1 && splits != 2 && splits != 4 && splits != 8) return false;
   if (epilogue < 0 || epilogue > kProjPartials || (epilogue != kProjPartials && splits != 1)) return false;
-  if (k % splits || proj_waves(k / splits, proj_row_tiles(m)) == 0) return false;
-  if (int64_t(m) * k > INT32_MAX || int64_t(n) * k > INT32_MAX || int64_t(splits) * m * n > INT32_MAX) return false;
+  if (layout < 0 || layout > (kProjXTiled | kProjOutTiled | kProjWTiled)) return false;
+  if ((layout & kProjOutTiled) && (epilogue == kProjPartials || n % 32)) return false;
+  const ProjTiles pt = proj_tiles(m, n);
+  if (k % splits || proj_waves(k / splits, pt.mt * pt.nt) == 0) return false;
+  const int64_t mp = (int64_t(m) + 15) / 16 * 16;  // rows of a tiled buffer
+  if (mp * k > INT32_MAX || int64_t(n) * k > INT32_MAX || int64_t(splits) * mp * n > INT32_MAX) return false;
   return out && x && w && aligned(x, 16) && aligned(w, 16) && aligned(out, epilogue == kProjPartials ? 16 : 8) &&
          (!bias || aligned(bias, 8));
 }
@@ -806,6 +880,20 @@ bool decode_projections_enabled() {
     return !(v && v[0] == '0');
   }();
   return on;
+}
+
+// Rows up to which a decode step past the fused rows runs on the projection
+// kernel with tiled activations (MT_DECODE_TILED_ROWS overrides it, 0 turns
+// the tiled path off). Captured GPT-2-medium steps on MI355X: 1.80 against
+// 1.91 ms at 128 rows, 2.86 against 2.72 ms at 256 (hipBLASLt's tiles win
+// there).
+constexpr int kProjTiledRows = 128;
+int decode_tiled_rows() {
+  static const int rows = [] {
+    const char* v = std::getenv("MT_DECODE_TILED_ROWS");
+    return v && *v ? std::atoi(v) : kProjTiledRows;
+  }();
+  return rows;
 }
 
 // Splits of k for an [m, n] x [n, k] projection whose partial sums are
@@ -820,40 +908,66 @@ int projection_splits(int m, int n, int k) {
       c = 256;
     return c;
   }();
-  const int tiles = n / 16 * ((m + kProjRowBlock - 1) / kProjRowBlock);
-  const int mt = proj_row_tiles(m);
-  auto takes = [&](int s) { return k % s == 0 && proj_waves(k / s, mt) > 0; };
+  const ProjTiles pt = proj_tiles(m, n);
+  const int tiles = n / (16 * pt.nt) * ((m + 16 * pt.mt - 1) / (16 * pt.mt));
+  auto takes = [&](int s) { return k % s == 0 && proj_waves(k / s, pt.mt * pt.nt) > 0; };
   int s = 1;
   while (s < kProjMaxSplits && !takes(s)) s *= 2;
   while (s < kProjMaxSplits && int64_t(tiles) * s < cus && takes(2 * s)) s *= 2;
   return s;
 }
 
-template <int DT, int MT, int EPI>
+template <int DT, int MT, int NT, int EPI, int LAY>
 void launch_projection_mt(ProjArgs a, int splits) {
-  const int waves = proj_waves(a.k / splits, MT);
+  const int waves = proj_waves(a.k / splits, MT * NT);
   a.kc = a.k / (splits * waves);
-  const dim3 grid(unsigned(a.n / 16), unsigned(splits), unsigned((a.m + kProjRowBlock - 1) / kProjRowBlock));
-  projection_kernel<DT, MT, EPI><<<grid, 64 * waves, size_t(waves) * MT * 64 * sizeof(floatx4)>>>(a);
+  const dim3 grid(unsigned(a.n / (16 * NT)), unsigned(splits), unsigned((a.m + 16 * MT - 1) / (16 * MT)));
+  projection_kernel<DT, MT, EPI, -1, LAY, NT>
+      <<<grid, 64 * waves, size_t(waves) * MT * NT * 64 * sizeof(floatx4)>>>(a);
+}
+
+template <int DT, int EPI, int LAY>
+void launch_projection_lay(const ProjArgs& a, int splits) {
+  const ProjTiles pt = proj_tiles(a.m, a.n);
+  if (pt.nt == 2) {
+    if (pt.mt == 2) launch_projection_mt<DT, 2, 2, EPI, LAY>(a, splits);
+    else launch_projection_mt<DT, 4, 2, EPI, LAY>(a, splits);
+  } else if (pt.mt == 1) {
+    launch_projection_mt<DT, 1, 1, EPI, LAY>(a, splits);
+  } else if (pt.mt == 2) {
+    launch_projection_mt<DT, 2, 1, EPI, LAY>(a, splits);
+  } else if (pt.mt == 4) {
+    launch_projection_mt<DT, 4, 1, EPI, LAY>(a, splits);
+  } else {
+    launch_projection_mt<DT, 8, 1, EPI, LAY>(a, splits);
+  }
 }
 
 template <int DT, int EPI>
-void launch_projection_epi(const ProjArgs& a, int splits) {
-  const int mt = proj_row_tiles(a.m);
-  if (mt == 1) launch_projection_mt<DT, 1, EPI>(a, splits);
-  else if (mt == 2) launch_projection_mt<DT, 2, EPI>(a, splits);
-  else if (mt == 4) launch_projection_mt<DT, 4, EPI>(a, splits);
-  else launch_projection_mt<DT, 8, EPI>(a, splits);
+void launch_projection_epi(const ProjArgs& a, int splits, int layout) {
+  if constexpr (EPI == kProjPartials) {
+    if (layout & kProjXTiled) launch_projection_lay<DT, EPI, kProjXTiled>(a, splits);
+    else launch_projection_lay<DT, EPI, 0>(a, splits);
+  } else {
+    switch (layout) {
+      case 0: launch_projection_lay<DT, EPI, 0>(a, splits); break;
+      case kProjXTiled: launch_projection_lay<DT, EPI, kProjXTiled>(a, splits); break;
+      case kProjOutTiled: launch_projection_lay<DT, EPI, kProjOutTiled>(a, splits); break;
+      default: launch_projection_lay<DT, EPI, kProjXTiled | kProjOutTiled>(a, splits); break;
+    }
+  }
 }
 
 // Whether the LayerNorm-prologue projection takes out = epi(LayerNorm(x_in +
 // part_bias + sum of splits partial rows) @ w^T): fp16/bf16, 1 <= m <= 16,
 // one split, k a multiple of 256 up to kProjFusedMaxWidth, partial splits
-// 0, 1, 2 or 4 (0: no partials and no part_bias), x_out distinct from x_in.
+// 0, 1, 2 or 4 (0: no partials and no part_bias), x_out distinct from x_in;
+// layout 0 or kProjWTiled.
 bool projection_ln_ok(const void* out, const float* x_in, const float* x_out, const float* part, int splits,
                       const void* part_bias, const float* gamma, const float* beta, const void* w,
-                      const void* bias, int m, int n, int k, int epilogue, int dtype) {
+                      const void* bias, int m, int n, int k, int epilogue, int dtype, int layout = 0) {
   if (dtype != kF16 && dtype != kBF16) return false;
+  if (layout != 0 && layout != kProjWTiled) return false;
   if (m < 1 || m > 16 || n < 16 || n % 16 || k < 256 || k % 256 || k > kProjFusedMaxWidth) return false;
   if (epilogue != kProjBias && epilogue != kProjGelu) return false;
   if (splits != 0 && splits != 1 && splits != 2 && splits != 4) return false;
@@ -886,10 +1000,11 @@ void launch_projection_ln_epi(const ProjArgs& a, int splits) {
 // Caller has checked projection_ln_ok.
 hipError_t projection_ln(void* out, const float* x_in, float* x_out, const float* part, int splits,
                          const void* part_bias, const float* gamma, const float* beta, float eps, const void* w,
-                         const void* bias, int m, int n, int k, int epilogue, int dtype) {
+                         const void* bias, int m, int n, int k, int epilogue, int dtype, int layout = 0) {
   ProjArgs a{};
   a.out = out; a.w = w; a.bias = bias;
   a.m = m; a.n = n; a.k = k;
+  a.w_tiled = layout == kProjWTiled;
   a.x_in = x_in; a.x_out = x_out; a.part = part; a.part_bias = part_bias;
   a.gamma = gamma; a.beta = beta; a.eps = eps;
   if (dtype == kF16) {
@@ -904,18 +1019,20 @@ hipError_t projection_ln(void* out, const float* x_in, float* x_out, const float
 
 // Caller has checked projection_ok.
 hipError_t projection(void* out, const void* x, const void* w, const void* bias, int m, int n, int k, int splits,
-                      int epilogue, int dtype) {
+                      int epilogue, int dtype, int layout = 0) {
   ProjArgs a{};
   a.out = out; a.x = x; a.w = w; a.bias = bias;
   a.m = m; a.n = n; a.k = k;
+  a.w_tiled = (layout & kProjWTiled) != 0;
+  layout &= kProjXTiled | kProjOutTiled;
   if (dtype == kF16) {
-    if (epilogue == kProjBias) launch_projection_epi<kF16, kProjBias>(a, splits);
-    else if (epilogue == kProjGelu) launch_projection_epi<kF16, kProjGelu>(a, splits);
-    else launch_projection_epi<kF16, kProjPartials>(a, splits);
+    if (epilogue == kProjBias) launch_projection_epi<kF16, kProjBias>(a, splits, layout);
+    else if (epilogue == kProjGelu) launch_projection_epi<kF16, kProjGelu>(a, splits, layout);
+    else launch_projection_epi<kF16, kProjPartials>(a, splits, layout);
   } else {
-    if (epilogue == kProjBias) launch_projection_epi<kBF16, kProjBias>(a, splits);
-    else if (epilogue == kProjGelu) launch_projection_epi<kBF16, kProjGelu>(a, splits);
-    else launch_projection_epi<kBF16, kProjPartials>(a, splits);
+    if (epilogue == kProjBias) launch_projection_epi<kBF16, kProjBias>(a, splits, layout);
+    else if (epilogue == kProjGelu) launch_projection_epi<kBF16, kProjGelu>(a, splits, layout);
+    else launch_projection_epi<kBF16, kProjPartials>(a, splits, layout);
   }
   return hipGetLastError();
 }
@@ -930,38 +1047,55 @@ bool partials_ln_ok(const void* out, const float* x, const float* part, const vo
 
 template <int DT, int S>
 void launch_partials_ln(void* out, float* x, const float* part, const void* bias, const float* gamma,
-                        const float* beta, int rows, int width, float eps) {
+                        const float* beta, int rows, int width, float eps, int tiled) {
   constexpr int R = kLnRowsPerBlock;  // rows (waves) per workgroup
   const int blocks = (rows + R - 1) / R;
   if (width <= 1024)
-    residual_layernorm_partials_kernel<DT, 4, S><<<blocks, 64 * R>>>(out, x, part, bias, gamma, beta, rows, width, eps);
+    residual_layernorm_partials_kernel<DT, 4, S>
+        <<<blocks, 64 * R>>>(out, x, part, bias, gamma, beta, rows, width, eps, tiled);
   else
-    residual_layernorm_partials_kernel<DT, 8, S><<<blocks, 64 * R>>>(out, x, part, bias, gamma, beta, rows, width, eps);
+    residual_layernorm_partials_kernel<DT, 8, S>
+        <<<blocks, 64 * R>>>(out, x, part, bias, gamma, beta, rows, width, eps, tiled);
 }
 
 template <int DT>
 void launch_partials_ln_dt(void* out, float* x, const float* part, int splits, const void* bias, const float* gamma,
-                           const float* beta, int rows, int width, float eps) {
+                           const float* beta, int rows, int width, float eps, int tiled) {
   switch (splits) {
-    case 1: launch_partials_ln<DT, 1>(out, x, part, bias, gamma, beta, rows, width, eps); break;
-    case 2: launch_partials_ln<DT, 2>(out, x, part, bias, gamma, beta, rows, width, eps); break;
-    case 3: launch_partials_ln<DT, 3>(out, x, part, bias, gamma, beta, rows, width, eps); break;
-    case 4: launch_partials_ln<DT, 4>(out, x, part, bias, gamma, beta, rows, width, eps); break;
-    case 5: launch_partials_ln<DT, 5>(out, x, part, bias, gamma, beta, rows, width, eps); break;
-    case 6: launch_partials_ln<DT, 6>(out, x, part, bias, gamma, beta, rows, width, eps); break;
-    case 7: launch_partials_ln<DT, 7>(out, x, part, bias, gamma, beta, rows, width, eps); break;
-    default: launch_partials_ln<DT, 8>(out, x, part, bias, gamma, beta, rows, width, eps); break;
+    case 1: launch_partials_ln<DT, 1>(out, x, part, bias, gamma, beta, rows, width, eps, tiled); break;
+    case 2: launch_partials_ln<DT, 2>(out, x, part, bias, gamma, beta, rows, width, eps, tiled); break;
+    case 3: launch_partials_ln<DT, 3>(out, x, part, bias, gamma, beta, rows, width, eps, tiled); break;
+    case 4: launch_partials_ln<DT, 4>(out, x, part, bias, gamma, beta, rows, width, eps, tiled); break;
+    case 5: launch_partials_ln<DT, 5>(out, x, part, bias, gamma, beta, rows, width, eps, tiled); break;
+    case 6: launch_partials_ln<DT, 6>(out, x, part, bias, gamma, beta, rows, width, eps, tiled); break;
+    case 7: launch_partials_ln<DT, 7>(out, x, part, bias, gamma, beta, rows, width, eps, tiled); break;
+    default: launch_partials_ln<DT, 8>(out, x, part, bias, gamma, beta, rows, width, eps, tiled); break;
   }
 }
 
-// Caller has checked partials_ln_ok and 1 <= splits <= kProjMaxSplits.
+// Caller has checked partials_ln_ok and 1 <= splits <= kProjMaxSplits. tiled:
+// out in the fragment-tiled layout (ceil(rows / 16) * 16 rows).
 hipError_t residual_layernorm_partials(void* out, float* x, const float* part, int splits, const void* bias,
                                        const float* gamma, const float* beta, int rows, int width, float eps,
-                                       int dtype) {
-  if (dtype == kF16) launch_partials_ln_dt<kF16>(out, x, part, splits, bias, gamma, beta, rows, width, eps);
-  else launch_partials_ln_dt<kBF16>(out, x, part, splits, bias, gamma, beta, rows, width, eps);
+                                       int dtype, int tiled = 0) {
+  if (dtype == kF16) launch_partials_ln_dt<kF16>(out, x, part, splits, bias, gamma, beta, rows, width, eps, tiled);
+  else launch_partials_ln_dt<kBF16>(out, x, part, splits, bias, gamma, beta, rows, width, eps, tiled);
   return hipGetLastError();
 }
+
+// The weights a decode projection reads: a layer's fragment-tiled copy where
+// it has one (kProjWTiled), else the row-major one.
+struct ProjWeight {
+  const void* w;
+  int layout;
+};
+ProjWeight pick_weight(const void* row_major, const void* tiled) {
+  return tiled ? ProjWeight{tiled, kProjWTiled} : ProjWeight{row_major, 0};
+}
+ProjWeight qkv_weight(const mt_decoder_layer& L) { return pick_weight(L.w_qkv, L.w_qkv_tiled); }
+ProjWeight out_weight(const mt_decoder_layer& L) { return pick_weight(L.w_o, L.w_o_tiled); }
+ProjWeight fc_weight(const mt_decoder_layer& L) { return pick_weight(L.w_fc, L.w_fc_tiled); }
+ProjWeight proj_weight(const mt_decoder_layer& L) { return pick_weight(L.w_proj, L.w_proj_tiled); }
 
 // x[i] += y[i] with fp32 x (the residual stream) and y in its own type.
 template <int DT>
@@ -1018,22 +1152,28 @@ bool wave_rows(const void* out, const float* x, const void* y, const float* gamm
 
 template <int DT>
 void launch_wave_rows(void* out, float* x, const void* y, const float* gamma, const float* beta,
-                      int rows, int width, float eps) {
+                      int rows, int width, float eps, int tiled) {
   constexpr int R = kLnRowsPerBlock;  // one wave per row
   const int blocks = (rows + R - 1) / R;
   if (width <= 1024)
-    residual_layernorm_wave_kernel<DT, 4><<<blocks, 64 * R>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr);
+    residual_layernorm_wave_kernel<DT, 4>
+        <<<blocks, 64 * R>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr, tiled);
   else
-    residual_layernorm_wave_kernel<DT, 8><<<blocks, 64 * R>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr);
+    residual_layernorm_wave_kernel<DT, 8>
+        <<<blocks, 64 * R>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr, tiled);
 }
 
+// tiled: out in the fragment-tiled layout (fp16/bf16, rows that the
+// one-wave-per-row kernel takes; anything else is rejected).
 hipError_t layernorm(void* out, const float* x, const float* gamma, const float* beta, int rows,
-                     int width, float eps, int dtype) {
-  if (wave_rows(out, x, nullptr, gamma, beta, width, dtype)) {
+                     int width, float eps, int dtype, int tiled = 0) {
+  const bool wave = wave_rows(out, x, nullptr, gamma, beta, width, dtype);
+  if (tiled && (!wave || dtype == kF32)) return hipErrorInvalidValue;
+  if (wave) {
     float* xm = const_cast<float*>(x);  // not written without a residual
-    if (dtype == kF32) launch_wave_rows<kF32>(out, xm, nullptr, gamma, beta, rows, width, eps);
-    else if (dtype == kF16) launch_wave_rows<kF16>(out, xm, nullptr, gamma, beta, rows, width, eps);
-    else launch_wave_rows<kBF16>(out, xm, nullptr, gamma, beta, rows, width, eps);
+    if (dtype == kF32) launch_wave_rows<kF32>(out, xm, nullptr, gamma, beta, rows, width, eps, 0);
+    else if (dtype == kF16) launch_wave_rows<kF16>(out, xm, nullptr, gamma, beta, rows, width, eps, tiled);
+    else launch_wave_rows<kBF16>(out, xm, nullptr, gamma, beta, rows, width, eps, tiled);
     return hipGetLastError();
   }
   if (dtype == kF32) layernorm_kernel<kF32><<<rows, 256>>>(out, x, gamma, beta, width, eps);
@@ -1043,11 +1183,13 @@ hipError_t layernorm(void* out, const float* x, const float* gamma, const float*
 }
 
 hipError_t residual_layernorm(void* out, float* x, const void* y, const float* gamma,
-                              const float* beta, int rows, int width, float eps, int dtype) {
-  if (wave_rows(out, x, y, gamma, beta, width, dtype)) {
-    if (dtype == kF32) launch_wave_rows<kF32>(out, x, y, gamma, beta, rows, width, eps);
-    else if (dtype == kF16) launch_wave_rows<kF16>(out, x, y, gamma, beta, rows, width, eps);
-    else launch_wave_rows<kBF16>(out, x, y, gamma, beta, rows, width, eps);
+                              const float* beta, int rows, int width, float eps, int dtype, int tiled = 0) {
+  const bool wave = wave_rows(out, x, y, gamma, beta, width, dtype);
+  if (tiled && (!wave || dtype == kF32)) return hipErrorInvalidValue;
+  if (wave) {
+    if (dtype == kF32) launch_wave_rows<kF32>(out, x, y, gamma, beta, rows, width, eps, 0);
+    else if (dtype == kF16) launch_wave_rows<kF16>(out, x, y, gamma, beta, rows, width, eps, tiled);
+    else launch_wave_rows<kBF16>(out, x, y, gamma, beta, rows, width, eps, tiled);
     return hipGetLastError();
   }
   if (dtype == kF32)
@@ -1260,41 +1402,46 @@ int mt_residual_layernorm(void* out, float* x, const void* y, const float* gamma
 }
 
 int mt_decode_projection(void* out, const void* x, const void* w, const void* bias, int m, int n, int k,
-                         int splits, int epilogue, int dtype) {
-  if (!projection_ok(out, x, w, bias, m, n, k, splits, epilogue, dtype)) return hipErrorInvalidValue;
-  return projection(out, x, w, bias, m, n, k, splits, epilogue, dtype);
+                         int splits, int epilogue, int dtype, int layout) {
+  if (!projection_ok(out, x, w, bias, m, n, k, splits, epilogue, dtype, layout)) return hipErrorInvalidValue;
+  return projection(out, x, w, bias, m, n, k, splits, epilogue, dtype, layout);
 }
 
 int mt_decode_projection_ln(void* out, const float* x_in, float* x_out, const float* partials, int splits,
                             const void* part_bias, const float* gamma, const float* beta, float eps, const void* w,
-                            const void* bias, int m, int n, int k, int epilogue, int dtype) {
+                            const void* bias, int m, int n, int k, int epilogue, int dtype, int layout) {
   if (!projection_ln_ok(out, x_in, x_out, partials, splits, part_bias, gamma, beta, w, bias, m, n, k, epilogue,
-                        dtype))
+                        dtype, layout))
     return hipErrorInvalidValue;
   return projection_ln(out, x_in, x_out, partials, splits, part_bias, gamma, beta, eps, w, bias, m, n, k, epilogue,
-                       dtype);
+                       dtype, layout);
 }
 
 int mt_residual_layernorm_partials(void* out, float* x, const float* partials, int splits, const void* bias,
                                    const float* gamma, const float* beta, int rows, int width, float eps,
-                                   int dtype) {
+                                   int dtype, int layout) {
   if (!out || !x || !partials || !gamma || !beta || rows < 1 || splits < 1 || splits > kProjMaxSplits ||
-      int64_t(splits) * rows * width > INT32_MAX || !partials_ln_ok(out, x, partials, bias, gamma, beta, width, dtype))
+      (layout != 0 && layout != kProjOutTiled) || int64_t(splits) * rows * width > INT32_MAX ||
+      !partials_ln_ok(out, x, partials, bias, gamma, beta, width, dtype))
     return hipErrorInvalidValue;
-  return residual_layernorm_partials(out, x, partials, splits, bias, gamma, beta, rows, width, eps, dtype);
+  return residual_layernorm_partials(out, x, partials, splits, bias, gamma, beta, rows, width, eps, dtype,
+                                     layout == kProjOutTiled);
 }
 
 size_t mt_decoder_scratch_bytes(int rows, int d, int dtype) {
   if (rows < 1 || d < 1 || !dtype_ok(dtype)) return 0;
   const size_t e = dtype == kF32 ? 4 : 2;
-  // qkv [rows, 3d] | attention [rows, d] | projection [rows, d] | mlp [rows, 4d] | (fp16/bf16 and
-  // rows <= kProjSplitRows) fp32 split partials [kProjMaxSplits, rows, d], each 256-aligned
+  const size_t mp = (size_t(rows) + 15) / 16 * 16;  // rows of a tiled buffer
+  const bool low = dtype != kF32;
+  // qkv [rows, 3d] | attention [rows, d] | projection [rows, d] | mlp [mp, 4d] (room for the tiled
+  // layout), then for fp16/bf16 decode batches (rows <= kProjMaxRows): fp32 split partials
+  // [kProjMaxSplits, rows, d], and either (rows <= kProjFusedRows) the second residual stream
+  // [rows, d] fp32 or (more rows) the tiled LayerNorm output [mp, d]; each 256-aligned
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-  const size_t partials = dtype != kF32 && rows <= kProjSplitRows ? al(size_t(kProjMaxSplits) * rows * d * 4) : 0;
-  // (fp16/bf16 and rows <= kProjFusedRows) | second residual stream [rows, d] fp32
-  const size_t stream = dtype != kF32 && rows <= kProjFusedRows ? al(size_t(rows) * d * 4) : 0;
-  return al(size_t(rows) * 3 * d * e) + 2 * al(size_t(rows) * d * e) + al(size_t(rows) * 4 * d * e) + partials +
-         stream;
+  const size_t partials = low && rows <= kProjMaxRows ? al(size_t(kProjMaxSplits) * rows * d * 4) : 0;
+  const size_t stream = low && rows <= kProjFusedRows ? al(size_t(rows) * d * 4) : 0;
+  const size_t ht = low && rows > kProjFusedRows && rows <= kProjMaxRows ? al(mp * d * e) : 0;
+  return al(size_t(rows) * 3 * d * e) + 2 * al(size_t(rows) * d * e) + al(mp * 4 * d * e) + partials + stream + ht;
 }
 
 int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
@@ -1315,14 +1462,15 @@ int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
   char* attn = qkv + al(size_t(rows) * 3 * d * e);
   char* proj = attn + al(size_t(rows) * d * e);
   char* mlp = proj + al(size_t(rows) * d * e);
-  float* partials = dtype != kF32 && rows <= kProjSplitRows
-                        ? reinterpret_cast<float*>(mlp + al(size_t(rows) * 4 * d * e)) : nullptr;
+  const size_t mp = (size_t(rows) + 15) / 16 * 16;
+  const bool low = dtype != kF32 && rows <= kProjMaxRows;
+  char* tail = mlp + al(mp * 4 * d * e);
+  float* partials = low ? reinterpret_cast<float*>(tail) : nullptr;
+  if (low) tail += al(size_t(kProjMaxSplits) * rows * d * 4);
+  float* xb = low && rows <= kProjFusedRows ? reinterpret_cast<float*>(tail) : nullptr;
+  void* ht = low && rows > kProjFusedRows ? tail : nullptr;
   const int hd = d / heads;
   const bool own = decode_projections_enabled();
-  float* xb = partials && rows <= kProjFusedRows
-                  ? reinterpret_cast<float*>(reinterpret_cast<char*>(partials) +
-                                             al(size_t(kProjMaxSplits) * rows * d * 4))
-                  : nullptr;
   auto attention = [&](int i) -> int {
     return mt_paged_decode_split(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, att->slabs, att->table,
                                  att->offsets, rows, heads, hd, att->page_size, att->pages_per_slab,
@@ -1345,26 +1493,29 @@ int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
                                                  d, dtype);
     for (int i = 0; i < n_layer && ok; ++i) {
       const mt_decoder_layer& L = layers[i];
+      const ProjWeight wq = qkv_weight(L), wo = out_weight(L), wf = fc_weight(L), wp = proj_weight(L);
       ok = projection_ln_ok(qkv, x, xb, i ? partials : nullptr, i ? sp : 0, i ? layers[i - 1].b_proj : nullptr,
-                            L.ln1_gamma, L.ln1_beta, L.w_qkv, L.b_qkv, rows, 3 * d, d, kProjBias, dtype) &&
-           projection_ok(partials, attn, L.w_o, nullptr, rows, d, d, so, kProjPartials, dtype) &&
-           projection_ln_ok(mlp, xb, x, partials, so, L.b_o, L.ln2_gamma, L.ln2_beta, L.w_fc, L.b_fc, rows, 4 * d,
-                            d, kProjGelu, dtype) &&
-           projection_ok(partials, mlp, L.w_proj, nullptr, rows, d, 4 * d, sp, kProjPartials, dtype);
+                            L.ln1_gamma, L.ln1_beta, wq.w, L.b_qkv, rows, 3 * d, d, kProjBias, dtype, wq.layout) &&
+           projection_ok(partials, attn, wo.w, nullptr, rows, d, d, so, kProjPartials, dtype, wo.layout) &&
+           projection_ln_ok(mlp, xb, x, partials, so, L.b_o, L.ln2_gamma, L.ln2_beta, wf.w, L.b_fc, rows, 4 * d,
+                            d, kProjGelu, dtype, wf.layout) &&
+           projection_ok(partials, mlp, wp.w, nullptr, rows, d, 4 * d, sp, kProjPartials, dtype, wp.layout);
     }
     if (ok) {
       int st = 0;
       for (int i = 0; i < n_layer && !st; ++i) {
         const mt_decoder_layer& L = layers[i];
+        const ProjWeight wq = qkv_weight(L), wo = out_weight(L), wf = fc_weight(L), wp = proj_weight(L);
         if ((st = projection_ln(qkv, x, xb, i ? partials : nullptr, i ? sp : 0, i ? layers[i - 1].b_proj : nullptr,
-                                L.ln1_gamma, L.ln1_beta, eps, L.w_qkv, L.b_qkv, rows, 3 * d, d, kProjBias, dtype)))
+                                L.ln1_gamma, L.ln1_beta, eps, wq.w, L.b_qkv, rows, 3 * d, d, kProjBias, dtype,
+                                wq.layout)))
           break;
         if ((st = attention(i))) break;
-        if ((st = projection(partials, attn, L.w_o, nullptr, rows, d, d, so, kProjPartials, dtype))) break;
-        if ((st = projection_ln(mlp, xb, x, partials, so, L.b_o, L.ln2_gamma, L.ln2_beta, eps, L.w_fc, L.b_fc, rows,
-                                4 * d, d, kProjGelu, dtype)))
+        if ((st = projection(partials, attn, wo.w, nullptr, rows, d, d, so, kProjPartials, dtype, wo.layout))) break;
+        if ((st = projection_ln(mlp, xb, x, partials, so, L.b_o, L.ln2_gamma, L.ln2_beta, eps, wf.w, L.b_fc, rows,
+                                4 * d, d, kProjGelu, dtype, wf.layout)))
           break;
-        st = projection(partials, mlp, L.w_proj, nullptr, rows, d, 4 * d, sp, kProjPartials, dtype);
+        st = projection(partials, mlp, wp.w, nullptr, rows, d, 4 * d, sp, kProjPartials, dtype, wp.layout);
       }
       if (!st)
         st = residual_layernorm_partials(h, x, partials, sp, layers[n_layer - 1].b_proj, final_gamma, final_beta,
@@ -1374,38 +1525,102 @@ int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer,
       return st;
     }
   }
+  // More rows, up to decode_tiled_rows(): the QKV, fc and proj projections run
+  // on the projection kernel with fragment-tiled activations, which the
+  // LayerNorm kernels (ht) and the fc epilogue (mlp) write in that layout, and
+  // proj leaves split partial sums for the next residual LayerNorm. The
+  // out-projection reads attention's row-major output: split partial sums
+  // (split_o) or hipBLASLt.
+  if (own && ht && rows <= decode_tiled_rows()) {
+    const int so = projection_splits(rows, d, d), sp = projection_splits(rows, d, 4 * d);
+    // the out-projection's partial sums cost the LayerNorm a read each: own
+    // kernel while they are few (GPT-2-medium at 128 rows: 4 splits, 1.80
+    // against 1.81 ms with hipBLASLt; DistilGPT-2: 8 splits, 0.448 against
+    // 0.439 ms)
+    const bool split_o = rows <= kProjSplitRows || so <= 4;
+    bool ok = wave_rows(ht, x, nullptr, layers[0].ln1_gamma, layers[0].ln1_beta, d, dtype) &&
+              partials_ln_ok(h, x, partials, layers[n_layer - 1].b_proj, final_gamma, final_beta, d, dtype);
+    for (int i = 0; i < n_layer && ok; ++i) {
+      const mt_decoder_layer& L = layers[i];
+      const ProjWeight wq = qkv_weight(L), wo = out_weight(L), wf = fc_weight(L), wp = proj_weight(L);
+      const bool last = i + 1 == n_layer;
+      ok = projection_ok(qkv, ht, wq.w, L.b_qkv, rows, 3 * d, d, 1, kProjBias, dtype, kProjXTiled | wq.layout) &&
+           (split_o ? projection_ok(partials, attn, wo.w, nullptr, rows, d, d, so, kProjPartials, dtype, wo.layout) &&
+                          partials_ln_ok(ht, x, partials, L.b_o, L.ln2_gamma, L.ln2_beta, d, dtype)
+                    : wave_rows(ht, x, proj, L.ln2_gamma, L.ln2_beta, d, dtype)) &&
+           projection_ok(mlp, ht, wf.w, L.b_fc, rows, 4 * d, d, 1, kProjGelu, dtype,
+                         kProjXTiled | kProjOutTiled | wf.layout) &&
+           projection_ok(partials, mlp, wp.w, nullptr, rows, d, 4 * d, sp, kProjPartials, dtype,
+                         kProjXTiled | wp.layout) &&
+           (last || partials_ln_ok(ht, x, partials, L.b_proj, layers[i + 1].ln1_gamma, layers[i + 1].ln1_beta, d,
+                                   dtype));
+    }
+    if (ok) {
+      int st = layernorm(ht, x, layers[0].ln1_gamma, layers[0].ln1_beta, rows, d, eps, dtype, 1);
+      for (int i = 0; i < n_layer && !st; ++i) {
+        const mt_decoder_layer& L = layers[i];
+        const ProjWeight wq = qkv_weight(L), wo = out_weight(L), wf = fc_weight(L), wp = proj_weight(L);
+        if ((st = projection(qkv, ht, wq.w, L.b_qkv, rows, 3 * d, d, 1, kProjBias, dtype, kProjXTiled | wq.layout)))
+          break;
+        if ((st = attention(i))) break;
+        if (split_o) {
+          if ((st = projection(partials, attn, wo.w, nullptr, rows, d, d, so, kProjPartials, dtype, wo.layout)))
+            break;
+          st = residual_layernorm_partials(ht, x, partials, so, L.b_o, L.ln2_gamma, L.ln2_beta, rows, d, eps, dtype, 1);
+        } else {
+          if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 1, dtype, dtype, kEpiNone, true))) break;
+          st = residual_layernorm(ht, x, proj, L.ln2_gamma, L.ln2_beta, rows, d, eps, dtype, 1);
+        }
+        if (st) break;
+        if ((st = projection(mlp, ht, wf.w, L.b_fc, rows, 4 * d, d, 1, kProjGelu, dtype,
+                             kProjXTiled | kProjOutTiled | wf.layout)))
+          break;
+        if ((st = projection(partials, mlp, wp.w, nullptr, rows, d, 4 * d, sp, kProjPartials, dtype,
+                             kProjXTiled | wp.layout)))
+          break;
+        const bool last = i + 1 == n_layer;
+        st = residual_layernorm_partials(last ? h : ht, x, partials, sp, L.b_proj,
+                                         last ? final_gamma : layers[i + 1].ln1_gamma,
+                                         last ? final_beta : layers[i + 1].ln1_beta, rows, d, eps, dtype, last ? 0 : 1);
+      }
+      if (!st && logits)
+        st = gemm(blas, logits, h, head_weight, nullptr, rows, vocab, d, 1, dtype, dtype, kEpiNone, true);
+      return st;
+    }
+  }
   // out = epi(in @ wt^T + b): the decode projection kernel where it takes
   // the shape, else hipBLASLt.
-  auto project = [&](void* out, const void* in, const void* wt, const void* b, int n, int k, int epi) -> int {
-    if (own && rows <= kProjDirectRows && projection_ok(out, in, wt, b, rows, n, k, 1, epi, dtype))
-      return projection(out, in, wt, b, rows, n, k, 1, epi, dtype);
+  auto project = [&](void* out, const void* in, const void* wt, const void* b, int n, int k, int epi,
+                     ProjWeight pw) -> int {
+    if (own && rows <= kProjDirectRows && projection_ok(out, in, pw.w, b, rows, n, k, 1, epi, dtype, pw.layout))
+      return projection(out, in, pw.w, b, rows, n, k, 1, epi, dtype, pw.layout);
     if (epi == kProjGelu) return gemm_gelu(blas, out, in, wt, b, rows, n, k, dtype, fused_gelu != 0, true, 1);
     return gemm(blas, out, in, wt, b, rows, n, k, 1, dtype, dtype, kEpiNone, true);
   };
   // x += in @ wt^T + b, then h = LayerNorm(x): split-k partial sums that the
   // LayerNorm kernel adds up, or one projection and residual_layernorm.
   auto project_residual = [&](const void* in, const void* wt, const void* b, int k, const float* g,
-                              const float* be) -> int {
+                              const float* be, ProjWeight pw) -> int {
     const int s = projection_splits(rows, d, k);
     if (own && partials && rows <= kProjSplitRows &&
-        projection_ok(partials, in, wt, nullptr, rows, d, k, s, kProjPartials, dtype) &&
+        projection_ok(partials, in, pw.w, nullptr, rows, d, k, s, kProjPartials, dtype, pw.layout) &&
         partials_ln_ok(h, x, partials, b, g, be, d, dtype)) {
-      const int st = projection(partials, in, wt, nullptr, rows, d, k, s, kProjPartials, dtype);
+      const int st = projection(partials, in, pw.w, nullptr, rows, d, k, s, kProjPartials, dtype, pw.layout);
       return st ? st : residual_layernorm_partials(h, x, partials, s, b, g, be, rows, d, eps, dtype);
     }
-    const int st = project(proj, in, wt, b, d, k, kProjBias);
+    const int st = project(proj, in, wt, b, d, k, kProjBias, pw);
     return st ? st : residual_layernorm(h, x, proj, g, be, rows, d, eps, dtype);
   };
   int st = layernorm(h, x, layers[0].ln1_gamma, layers[0].ln1_beta, rows, d, eps, dtype);
   for (int i = 0; i < n_layer && !st; ++i) {
     const mt_decoder_layer& L = layers[i];
-    if ((st = project(qkv, h, L.w_qkv, L.b_qkv, 3 * d, d, kProjBias))) break;
+    if ((st = project(qkv, h, L.w_qkv, L.b_qkv, 3 * d, d, kProjBias, qkv_weight(L)))) break;
     if ((st = attention(i))) break;
-    if ((st = project_residual(attn, L.w_o, L.b_o, d, L.ln2_gamma, L.ln2_beta))) break;
-    if ((st = project(mlp, h, L.w_fc, L.b_fc, 4 * d, d, kProjGelu))) break;
+    if ((st = project_residual(attn, L.w_o, L.b_o, d, L.ln2_gamma, L.ln2_beta, out_weight(L)))) break;
+    if ((st = project(mlp, h, L.w_fc, L.b_fc, 4 * d, d, kProjGelu, fc_weight(L)))) break;
     const bool last = i + 1 == n_layer;
     st = project_residual(mlp, L.w_proj, L.b_proj, 4 * d, last ? final_gamma : layers[i + 1].ln1_gamma,
-                          last ? final_beta : layers[i + 1].ln1_beta);
+                          last ? final_beta : layers[i + 1].ln1_beta, proj_weight(L));
   }
   // Tied head: logits [rows, vocab] = h @ head_weight^T (head_weight [vocab, d]).
   if (!st && logits)

@@ -59,7 +59,8 @@ class _Blas:
 class DecoderLayerStruct(ct.Structure):
     """``mt_decoder_layer`` (include/mt_model.h)."""
     _fields_ = [(name, P) for name in ('ln1_gamma', 'ln1_beta', 'w_qkv', 'b_qkv', 'w_o', 'b_o',
-                                       'ln2_gamma', 'ln2_beta', 'w_fc', 'b_fc', 'w_proj', 'b_proj')]
+                                       'ln2_gamma', 'ln2_beta', 'w_fc', 'b_fc', 'w_proj', 'b_proj',
+                                       'w_qkv_tiled', 'w_o_tiled', 'w_fc_tiled', 'w_proj_tiled')]
 
 
 class PrefillAttentionStruct(ct.Structure):
@@ -105,6 +106,24 @@ def init_gpt2_state(*, n_vocab, n_embd, n_layer, n_positions, seed=0, std=0.02):
     return state
 
 
+def fragment_tiled(a):
+    """A [rows, width] matrix (width a multiple of 32) in the fragment-tiled
+    layout the decode projection kernel reads (include/mt_model.h,
+    mt_decode_projection), flat, rows padded with zeros to a multiple of 16:
+    the 16 x 32 block (R, K) at element (R * width / 32 + K) * 512, its
+    element (r, c) at ((c // 8) * 16 + r) * 8 + c % 8 -- the lane order of a
+    matrix-core operand fragment, so that one wave reads a fragment as 1 KB of
+    consecutive 16-byte loads."""
+    a = np.asarray(a)
+    rows, width = a.shape
+    if width % 32:
+        raise ValueError('fragment_tiled: width must be a multiple of 32')
+    mp = -(-rows // 16) * 16
+    p = np.zeros((mp, width), a.dtype)
+    p[:rows] = a
+    return np.ascontiguousarray(p.reshape(mp // 16, 16, width // 32, 4, 8).transpose(0, 2, 3, 1, 4)).reshape(-1)
+
+
 class _DeviceWeights:
     """Device copies of the weights for one compute type."""
 
@@ -135,11 +154,22 @@ class _DeviceWeights:
                 fc=(put(p + 'mlp.c_fc.weight', array=state[p + 'mlp.c_fc.weight'].T), put(p + 'mlp.c_fc.bias')),
                 proj=(put(p + 'mlp.c_proj.weight', array=state[p + 'mlp.c_proj.weight'].T),
                       put(p + 'mlp.c_proj.bias')))
+            if dtype != 'float32':
+                # the decode projection kernel's copies: coalesced weight fragments
+                for key, name in (('qkv', 'attn.c_attn'), ('o', 'attn.c_proj'), ('fc', 'mlp.c_fc'),
+                                  ('proj', 'mlp.c_proj')):
+                    layer[key + '_tiled'] = put(p + name + '.weight',
+                                                array=fragment_tiled(state[p + name + '.weight'].T))
             self.layers.append(layer)
+
+        def tiled_ptr(L, key):
+            return L[key + '_tiled'].ptr if key + '_tiled' in L else None
+
         self.layer_array = (DecoderLayerStruct * n_layer)(*[
             DecoderLayerStruct(L['ln_1'][0].ptr, L['ln_1'][1].ptr, L['qkv'][0].ptr, L['qkv'][1].ptr,
                                L['o'][0].ptr, L['o'][1].ptr, L['ln_2'][0].ptr, L['ln_2'][1].ptr,
-                               L['fc'][0].ptr, L['fc'][1].ptr, L['proj'][0].ptr, L['proj'][1].ptr)
+                               L['fc'][0].ptr, L['fc'][1].ptr, L['proj'][0].ptr, L['proj'][1].ptr,
+                               tiled_ptr(L, 'qkv'), tiled_ptr(L, 'o'), tiled_ptr(L, 'fc'), tiled_ptr(L, 'proj'))
             for L in self.layers])
 
 

@@ -313,34 +313,39 @@ def test_decode_projection_entries_reject_invalid_arguments():
     # stand-in pointers that are never dereferenced: every call is invalid).
     lib = library('model_kernels')
     pr = lib.mt_decode_projection
-    pr.argtypes, pr.restype = [P, P, P, P, I, I, I, I, I, I], I
+    pr.argtypes, pr.restype = [P, P, P, P, I, I, I, I, I, I, I], I
     A = 256
-    #          out x  w  bias  m    n     k    splits epi dtype
-    for args in [(A, A, A, 0, 0, 1024, 1024, 1, 0, 2),      # no rows
-                 (A, A, A, 0, 257, 1024, 1024, 1, 0, 2),    # more rows than the kernel takes
-                 (A, A, A, 0, 4, 40, 1024, 1, 0, 2),        # n not a multiple of 16
-                 (A, A, A, 0, 4, 1024, 100, 1, 0, 2),       # k not a multiple of 32
-                 (A, A, A, 0, 4, 1024, 1024, 3, 2, 2),      # splits not a power of two
-                 (A, A, A, 0, 4, 1024, 1024, 2, 0, 2),      # a split needs the partial-sum epilogue
-                 (A, A, A, 0, 4, 1024, 1024, 1, 0, 0),      # fp32
-                 (A, A + 2, A, 0, 4, 1024, 1024, 1, 0, 2),  # misaligned activations
-                 (None, A, A, 0, 4, 1024, 1024, 1, 0, 2)]:
+    #          out x  w  bias  m    n     k    splits epi dtype layout
+    for args in [(A, A, A, 0, 0, 1024, 1024, 1, 0, 2, 0),      # no rows
+                 (A, A, A, 0, 257, 1024, 1024, 1, 0, 2, 0),    # more rows than the kernel takes
+                 (A, A, A, 0, 4, 40, 1024, 1, 0, 2, 0),        # n not a multiple of 16
+                 (A, A, A, 0, 4, 1024, 100, 1, 0, 2, 0),       # k not a multiple of 32
+                 (A, A, A, 0, 4, 1024, 1024, 3, 2, 2, 0),      # splits not a power of two
+                 (A, A, A, 0, 4, 1024, 1024, 2, 0, 2, 0),      # a split needs the partial-sum epilogue
+                 (A, A, A, 0, 4, 1024, 1024, 1, 0, 0, 0),      # fp32
+                 (A, A + 2, A, 0, 4, 1024, 1024, 1, 0, 2, 0),  # misaligned activations
+                 (None, A, A, 0, 4, 1024, 1024, 1, 0, 2, 0),
+                 (A, A, A, 0, 4, 1024, 1024, 2, 2, 2, 2),      # split partials are written row-major
+                 (A, A, A, 0, 4, 48, 1024, 1, 0, 2, 2),        # a tiled output needs n a multiple of 32
+                 (A, A, A, 0, 4, 1024, 1024, 1, 0, 2, 8)]:     # no such layout bit
         assert pr(*args) == 1, args
     ln = lib.mt_decode_projection_ln
-    ln.argtypes, ln.restype = [P, P, P, P, I, P, P, P, ct.c_float, P, P, I, I, I, I, I], I
-    #          out x_in x_out part splits pbias gamma beta eps w bias m n k epi dtype
-    for args in [(A, A, A, A, 4, 0, A, A, 1e-5, A, 0, 4, 1024, 1024, 0, 2),          # x_out is x_in
-                 (A, A, 2 * A, A, 4, 0, A, A, 1e-5, A, 0, 4, 1024, 1280, 0, 2),      # k above 1024
-                 (A, A, 2 * A, A, 3, 0, A, A, 1e-5, A, 0, 4, 1024, 1024, 0, 2),      # 3 partial splits
-                 (A, A, 2 * A, 0, 4, 0, A, A, 1e-5, A, 0, 4, 1024, 1024, 0, 2),      # splits without partials
-                 (A, A, 2 * A, 0, 0, A, A, A, 1e-5, A, 0, 4, 1024, 1024, 0, 2),      # a bias without partials
-                 (A, A, 2 * A, A, 4, 0, A, A, 1e-5, A, 0, 17, 1024, 1024, 0, 2),     # more than 16 rows
-                 (A, A, 2 * A, A, 4, 0, A, A, 1e-5, A, 0, 4, 1024, 1024, 2, 2)]:     # partial-sum epilogue
+    ln.argtypes, ln.restype = [P, P, P, P, I, P, P, P, ct.c_float, P, P, I, I, I, I, I, I], I
+    #          out x_in x_out part splits pbias gamma beta eps w bias m n k epi dtype layout
+    for args in [(A, A, A, A, 4, 0, A, A, 1e-5, A, 0, 4, 1024, 1024, 0, 2, 0),          # x_out is x_in
+                 (A, A, 2 * A, A, 4, 0, A, A, 1e-5, A, 0, 4, 1024, 1280, 0, 2, 0),      # k above 1024
+                 (A, A, 2 * A, A, 3, 0, A, A, 1e-5, A, 0, 4, 1024, 1024, 0, 2, 0),      # 3 partial splits
+                 (A, A, 2 * A, 0, 4, 0, A, A, 1e-5, A, 0, 4, 1024, 1024, 0, 2, 0),      # splits without partials
+                 (A, A, 2 * A, 0, 0, A, A, A, 1e-5, A, 0, 4, 1024, 1024, 0, 2, 0),      # a bias without partials
+                 (A, A, 2 * A, A, 4, 0, A, A, 1e-5, A, 0, 17, 1024, 1024, 0, 2, 0),     # more than 16 rows
+                 (A, A, 2 * A, A, 4, 0, A, A, 1e-5, A, 0, 4, 1024, 1024, 2, 2, 0),      # partial-sum epilogue
+                 (A, A, 2 * A, A, 4, 0, A, A, 1e-5, A, 0, 4, 1024, 1024, 0, 2, 1)]:     # only the weights may be tiled
         assert ln(*args) == 1, args
     rp = lib.mt_residual_layernorm_partials
-    rp.argtypes, rp.restype = [P, P, P, I, P, P, P, I, I, ct.c_float, I], I
-    for args in [(A, A, A, 1, 0, A, A, 4, 1000, 1e-5, 2),   # width not a multiple of 256
-                 (A, A, A, 9, 0, A, A, 4, 1024, 1e-5, 2),   # more than 8 splits
-                 (A, A, A, 1, 0, A, A, 4, 1024, 1e-5, 0),   # fp32
-                 (A, A, A, 1, 0, A, A, 0, 1024, 1e-5, 2)]:  # no rows
+    rp.argtypes, rp.restype = [P, P, P, I, P, P, P, I, I, ct.c_float, I, I], I
+    for args in [(A, A, A, 1, 0, A, A, 4, 1000, 1e-5, 2, 0),   # width not a multiple of 256
+                 (A, A, A, 9, 0, A, A, 4, 1024, 1e-5, 2, 0),   # more than 8 splits
+                 (A, A, A, 1, 0, A, A, 4, 1024, 1e-5, 0, 0),   # fp32
+                 (A, A, A, 1, 0, A, A, 0, 1024, 1e-5, 2, 0),   # no rows
+                 (A, A, A, 1, 0, A, A, 4, 1024, 1e-5, 2, 1)]:  # layout 1 (a tiled input) is not taken
         assert rp(*args) == 1, args

@@ -19,8 +19,8 @@ from minitorch_amd.dtypes import dtype_code
 
 pytestmark = pytest.mark.gpu
 
-PROJ = [P, P, P, P, I, I, I, I, I, I]
-LN_PARTIALS = [P, P, P, I, P, P, P, I, I, F, I]
+PROJ = [P, P, P, P, I, I, I, I, I, I, I]
+LN_PARTIALS = [P, P, P, I, P, P, P, I, I, F, I, I]
 MANT = {'bfloat16': 7, 'float16': 10}
 
 
@@ -79,7 +79,7 @@ def test_decode_projection(dtype, m, n, k, splits, epilogue):
     if epilogue == 2:
         out = DeviceTensor((splits, m, n), 'float32')
         call(model_library(), 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, 0, m, n, k, splits, 2,
-             dtype_code(dtype))
+             dtype_code(dtype), 0)
         got = host(out)
         kc = k // splits
         for s in range(splits):
@@ -89,7 +89,7 @@ def test_decode_projection(dtype, m, n, k, splits, epilogue):
         return
     out = DeviceTensor((m, n), dtype)
     call(model_library(), 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, B.ptr, m, n, k, 1, epilogue,
-         dtype_code(dtype))
+         dtype_code(dtype), 0)
     pre = prod + br
     if epilogue == 1:
         ref = gelu64(pre)
@@ -109,7 +109,7 @@ def test_decode_projection_without_bias(dtype):
     X, xr = rounded(rng.standard_normal((m, k)), dtype)
     W, wr = rounded(rng.standard_normal((n, k)) * 0.05, dtype)
     out = DeviceTensor((m, n), dtype)
-    call(model_library(), 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, 0, m, n, k, 1, 0, dtype_code(dtype))
+    call(model_library(), 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, 0, m, n, k, 1, 0, dtype_code(dtype), 0)
     ref = xr @ wr.T
     err = 1e-5 * (np.abs(xr) @ np.abs(wr).T) + 1e-7
     assert np.all(np.abs(host(out) - ref) <= half_ulp(np.abs(ref) + err, dtype) + err)
@@ -135,9 +135,16 @@ def test_decode_projection_rejects_unsupported_shapes():
     ]
     for m, n, k, s, e, d in bad:
         with pytest.raises(RuntimeError):
-            call(lib, 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, 0, m, n, k, s, e, d)
+            call(lib, 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, 0, m, n, k, s, e, d, 0)
     with pytest.raises(RuntimeError):  # misaligned activations
-        call(lib, 'mt_decode_projection', PROJ, out.ptr, X.ptr + 2, W.ptr, 0, 4, 1024, 1024, 1, 0, bf)
+        call(lib, 'mt_decode_projection', PROJ, out.ptr, X.ptr + 2, W.ptr, 0, 4, 1024, 1024, 1, 0, bf, 0)
+    for m, n, k, s, e, layout in [(4, 1024, 1024, 2, 2, 2),   # split partials are written row-major
+                                  (4, 1024, 1024, 2, 2, 3),
+                                  (4, 48, 1024, 1, 0, 2),     # a tiled output needs n a multiple of 32
+                                  (4, 1024, 1024, 1, 0, 8),   # no such layout bit
+                                  (4, 1024, 1024, 1, 0, -1)]:
+        with pytest.raises(RuntimeError):
+            call(lib, 'mt_decode_projection', PROJ, out.ptr, X.ptr, W.ptr, 0, m, n, k, s, e, bf, layout)
 
 
 @pytest.mark.parametrize('dtype', ['bfloat16', 'float16'])
@@ -156,7 +163,7 @@ def test_residual_layernorm_partials(dtype, width, splits, bias):
     G, Bt = DeviceTensor.from_numpy(g, 'float32'), DeviceTensor.from_numpy(be, 'float32')
     out = DeviceTensor((rows, width), dtype)
     call(model_library(), 'mt_residual_layernorm_partials', LN_PARTIALS, out.ptr, X.ptr, Pt.ptr, splits,
-         Bv.ptr if bias else 0, G.ptr, Bt.ptr, rows, width, 1e-5, dtype_code(dtype))
+         Bv.ptr if bias else 0, G.ptr, Bt.ptr, rows, width, 1e-5, dtype_code(dtype), 0)
     xs = x.astype(np.float64) + part.astype(np.float64).sum(axis=0) + (bv if bias else 0.0)
     assert np.allclose(host(X), xs, rtol=1e-6, atol=1e-5)
     mean = xs.mean(axis=1, keepdims=True)
@@ -176,16 +183,31 @@ def test_residual_layernorm_partials_rejects():
                                    (4, 2304, 1, 2)]:
         with pytest.raises(RuntimeError):
             call(lib, 'mt_residual_layernorm_partials', LN_PARTIALS, out.ptr, X.ptr, Pt.ptr, splits, 0, G.ptr,
-                 G.ptr, rows, width, 1e-5, d)
+                 G.ptr, rows, width, 1e-5, d, 0)
+    with pytest.raises(RuntimeError):  # layout 1 (tiled input) means nothing here
+        call(lib, 'mt_residual_layernorm_partials', LN_PARTIALS, out.ptr, X.ptr, Pt.ptr, 1, 0, G.ptr,
+             G.ptr, 4, 768, 1e-5, 2, 1)
 
 
-PROJ_LN = [P, P, P, P, I, P, P, P, F, P, P, I, I, I, I, I]
+PROJ_LN = [P, P, P, P, I, P, P, P, F, P, P, I, I, I, I, I, I]
 
 
 @pytest.mark.parametrize('dtype', ['bfloat16', 'float16'])
 @pytest.mark.parametrize('m,n,k,splits,epilogue', [(1, 2304, 768, 0, 0), (2, 3072, 768, 4, 1), (8, 4096, 1024, 2, 1),
                                                     (5, 3072, 1024, 1, 0), (16, 256, 256, 4, 0)])
 def test_decode_projection_layernorm_prologue(dtype, m, n, k, splits, epilogue):
+    run_layernorm_prologue(dtype, m, n, k, splits, epilogue, 0)
+
+
+@pytest.mark.parametrize('dtype', ['bfloat16', 'float16'])
+@pytest.mark.parametrize('m,n,k,splits,epilogue', [(1, 2304, 768, 0, 0), (2, 4096, 1024, 4, 1), (8, 3072, 1024, 2, 0)])
+def test_decode_projection_layernorm_prologue_tiled_weights(dtype, m, n, k, splits, epilogue):
+    """layout 4 (tiled weights) gives bit for bit the row-major result."""
+    got = run_layernorm_prologue(dtype, m, n, k, splits, epilogue, 4)
+    assert np.array_equal(got, run_layernorm_prologue(dtype, m, n, k, splits, epilogue, 0))
+
+
+def run_layernorm_prologue(dtype, m, n, k, splits, epilogue, layout):
     rng = np.random.default_rng([m, n, k, splits, epilogue, 1])
     x = (rng.standard_normal((m, k)) * 2 + 0.5).astype(np.float32)
     part = rng.standard_normal((max(splits, 1), m, k)).astype(np.float32)
@@ -196,10 +218,13 @@ def test_decode_projection_layernorm_prologue(dtype, m, n, k, splits, epilogue):
     PB, pb = rounded(rng.standard_normal(k) * 0.5, dtype)
     G, Bt = DeviceTensor.from_numpy(g, 'float32'), DeviceTensor.from_numpy(be, 'float32')
     W, wr = rounded(rng.standard_normal((n, k)) * 0.05, dtype)
+    if layout & 4:
+        W = DeviceTensor.from_numpy(tiled(wr).astype(np.float32), dtype)
     B, br = rounded(rng.standard_normal(n) * 0.5, dtype)
     out = DeviceTensor((m, n), dtype)
     call(model_library(), 'mt_decode_projection_ln', PROJ_LN, out.ptr, X.ptr, Xo.ptr, Pt.ptr if splits else 0,
-         splits, PB.ptr if splits else 0, G.ptr, Bt.ptr, 1e-5, W.ptr, B.ptr, m, n, k, epilogue, dtype_code(dtype))
+         splits, PB.ptr if splits else 0, G.ptr, Bt.ptr, 1e-5, W.ptr, B.ptr, m, n, k, epilogue, dtype_code(dtype),
+         layout)
     v = x.astype(np.float64) + (part.astype(np.float64).sum(axis=0) + pb if splits else 0.0)
     assert np.allclose(host(Xo), v, rtol=1e-6, atol=1e-5)
     assert np.array_equal(X.to_numpy(), x)
@@ -219,6 +244,7 @@ def test_decode_projection_layernorm_prologue(dtype, m, n, k, splits, epilogue):
     got = host(out)
     tol = half_ulp(np.abs(ref) + err, dtype) + err
     assert np.all(np.abs(got - ref) <= tol), float(np.max(np.abs(got - ref) / tol))
+    return got
 
 
 def test_decode_projection_layernorm_prologue_rejects():
@@ -229,11 +255,129 @@ def test_decode_projection_layernorm_prologue_rejects():
     out = DeviceTensor((16, 1024), 'bfloat16')
     lib, bf = model_library(), dtype_code('bfloat16')
 
-    def run(x_out=Xo.ptr, part=Pt.ptr, splits=4, part_bias=0, m=4, n=1024, k=1024, epi=0, d=bf):
+    def run(x_out=Xo.ptr, part=Pt.ptr, splits=4, part_bias=0, m=4, n=1024, k=1024, epi=0, d=bf, layout=0):
         call(lib, 'mt_decode_projection_ln', PROJ_LN, out.ptr, X.ptr, x_out, part, splits, part_bias, G.ptr, G.ptr,
-             1e-5, W.ptr, 0, m, n, k, epi, d)
+             1e-5, W.ptr, 0, m, n, k, epi, d, layout)
     run()  # valid
     for kw in [dict(x_out=X.ptr), dict(k=1280), dict(k=640), dict(splits=3), dict(splits=0), dict(part=0),
-               dict(part=0, splits=0, part_bias=G.ptr), dict(m=17), dict(m=0), dict(n=40), dict(epi=2), dict(d=0)]:
+               dict(part=0, splits=0, part_bias=G.ptr), dict(m=17), dict(m=0), dict(n=40), dict(epi=2), dict(d=0),
+               dict(layout=1), dict(layout=2), dict(layout=5)]:
         with pytest.raises(RuntimeError):
             run(**kw)
+
+
+def tiled(a, fill=np.nan):
+    """[rows, width] -> the fragment-tiled layout of mt_decode_projection
+    (flat, ceil(rows / 16) * 16 rows, padding rows set to `fill`): block
+    (R, K) of 16 rows x 32 columns at (R * width / 32 + K) * 512, element
+    (r, c) of the block at ((c // 8) * 16 + r) * 8 + c % 8."""
+    rows, width = a.shape
+    mp = -(-rows // 16) * 16
+    p = np.full((mp, width), fill, np.float64)
+    p[:rows] = a
+    # [R, r, K, g, e] -> [R, K, g, r, e]
+    return p.reshape(mp // 16, 16, width // 32, 4, 8).transpose(0, 2, 3, 1, 4).reshape(-1)
+
+
+def untiled(flat, rows, width):
+    mp = -(-rows // 16) * 16
+    return np.asarray(flat, np.float64).reshape(mp // 16, width // 32, 4, 16, 8).transpose(
+        0, 3, 1, 2, 4).reshape(mp, width)[:rows]
+
+
+def test_tiled_layout_helpers_invert():
+    a = np.arange(37 * 64, dtype=np.float64).reshape(37, 64)
+    t = tiled(a)
+    assert t.size == 48 * 64
+    # element (r, c) sits where the layout's formula puts it
+    for r, c in [(0, 0), (5, 9), (16, 31), (17, 32), (36, 63)]:
+        assert t[((r // 16) * 2 + c // 32) * 512 + (((c // 8) % 4) * 16 + r % 16) * 8 + c % 8] == a[r, c]
+    assert np.array_equal(untiled(t, 37, 64), a)
+
+
+TILED_CASES = [
+    # m, n, k, splits, epilogue, layout
+    (1, 64, 128, 1, 0, 1),
+    (9, 2304, 768, 1, 0, 3),
+    (17, 768, 768, 2, 2, 1),
+    (37, 3072, 768, 1, 1, 3),
+    (128, 3072, 1024, 1, 0, 1),
+    (128, 4096, 1024, 1, 1, 3),
+    (128, 1024, 4096, 4, 2, 1),
+    (128, 1024, 4096, 8, 2, 1),
+    (150, 1024, 1024, 1, 1, 2),
+    (150, 4096, 1024, 1, 1, 3),
+    (150, 1024, 4096, 4, 2, 1),
+    (256, 768, 3072, 4, 2, 1),
+    # tiled weights (layout bit 2)
+    (1, 64, 128, 1, 0, 4),
+    (2, 2304, 768, 1, 1, 4),
+    (9, 2304, 768, 1, 0, 7),
+    (17, 768, 768, 2, 2, 5),
+    (16, 1024, 4096, 4, 2, 4),
+    (128, 3072, 1024, 1, 0, 5),
+    (128, 4096, 1024, 1, 1, 7),
+    (128, 1024, 4096, 4, 2, 5),
+    (150, 1024, 1024, 1, 1, 6),
+]
+
+
+@pytest.mark.parametrize('dtype', ['bfloat16', 'float16'])
+@pytest.mark.parametrize('m,n,k,splits,epilogue,layout', TILED_CASES)
+def test_decode_projection_tiled_layouts(dtype, m, n, k, splits, epilogue, layout):
+    """The tiled layouts give bit for bit the row-major results (the same
+    products summed in the same order), with NaN in the padding rows of a
+    tiled input, and match the float64 product."""
+    rng = np.random.default_rng([m, n, k, splits, epilogue, layout])
+    x = rng.standard_normal((m, k))
+    X, xr = rounded(x, dtype)
+    XT = DeviceTensor.from_numpy(tiled(xr).astype(np.float32), dtype) if layout & 1 else X
+    W, wr = rounded(rng.standard_normal((n, k)) * 0.05, dtype)
+    WT = DeviceTensor.from_numpy(tiled(wr).astype(np.float32), dtype) if layout & 4 else W
+    B, br = rounded(rng.standard_normal(n) * 0.5, dtype)
+    lib, code = model_library(), dtype_code(dtype)
+    if epilogue == 2:
+        ref_out, out = DeviceTensor((splits, m, n), 'float32'), DeviceTensor((splits, m, n), 'float32')
+        call(lib, 'mt_decode_projection', PROJ, ref_out.ptr, X.ptr, W.ptr, 0, m, n, k, splits, 2, code, 0)
+        call(lib, 'mt_decode_projection', PROJ, out.ptr, XT.ptr, WT.ptr, 0, m, n, k, splits, 2, code, layout)
+        got, want = host(out), host(ref_out)
+        assert np.array_equal(got, want)
+        bound = 1e-5 * (np.abs(xr) @ np.abs(wr).T) + 1e-7
+        assert np.all(np.abs(got.sum(axis=0) - xr @ wr.T) <= bound)
+        return
+    ref_out = DeviceTensor((m, n), dtype)
+    call(lib, 'mt_decode_projection', PROJ, ref_out.ptr, X.ptr, W.ptr, B.ptr, m, n, k, 1, epilogue, code, 0)
+    mp = -(-m // 16) * 16
+    out = DeviceTensor((mp * n,) if layout & 2 else (m, n), dtype)
+    call(lib, 'mt_decode_projection', PROJ, out.ptr, XT.ptr, WT.ptr, B.ptr, m, n, k, 1, epilogue, code, layout)
+    got = untiled(host(out), m, n) if layout & 2 else host(out)
+    want = host(ref_out)
+    assert np.array_equal(got, want)
+    pre = xr @ wr.T + br
+    ref = gelu64(pre) if epilogue == 1 else pre
+    err = (1e-5 * (np.abs(xr) @ np.abs(wr).T) + 1e-7) * (1.2 if epilogue == 1 else 1.0) + 1e-6 * epilogue
+    assert np.all(np.abs(got - ref) <= half_ulp(np.abs(ref) + err, dtype) + err)
+
+
+@pytest.mark.parametrize('dtype', ['bfloat16', 'float16'])
+@pytest.mark.parametrize('rows,width,splits', [(37, 1024, 4), (128, 768, 8), (5, 2048, 1)])
+def test_residual_layernorm_partials_tiled_output(dtype, rows, width, splits):
+    """layout 2 writes the same rounded values as layout 0, in the tiled
+    order; the residual stream is updated the same way."""
+    rng = np.random.default_rng([rows, width, splits, 2])
+    x = (rng.standard_normal((rows, width)) * 3 + 1).astype(np.float32)
+    part = rng.standard_normal((splits, rows, width)).astype(np.float32)
+    Pt = DeviceTensor.from_numpy(part, 'float32')
+    Bv, _ = rounded(rng.standard_normal(width), dtype)
+    G = DeviceTensor.from_numpy((1 + 0.1 * rng.standard_normal(width)).astype(np.float32), 'float32')
+    Bt = DeviceTensor.from_numpy((0.1 * rng.standard_normal(width)).astype(np.float32), 'float32')
+    lib, code = model_library(), dtype_code(dtype)
+    outs = []
+    for layout in (0, 2):
+        X = DeviceTensor.from_numpy(x, 'float32')
+        out = DeviceTensor((-(-rows // 16) * 16 * width,) if layout else (rows, width), dtype)
+        call(lib, 'mt_residual_layernorm_partials', LN_PARTIALS, out.ptr, X.ptr, Pt.ptr, splits, Bv.ptr, G.ptr,
+             Bt.ptr, rows, width, 1e-5, code, layout)
+        outs.append((host(X), untiled(host(out), rows, width) if layout else host(out)))
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])
