@@ -678,6 +678,11 @@ __global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
       xoff[t] = row * p.k + k0;
     }
   }
+  // the bias of the output tile this wave finishes first (q = wave), loaded
+  // with the operands instead of after the reduction
+  uint2 bias0 = uint2{0u, 0u};
+  if (EPI != kProjPartials && p.bias && wave < NQ)
+    bias0 = *reinterpret_cast<const uint2*>(static_cast<const T*>(p.bias) + f0 + 16 * (wave / MT) + 4 * grp);
   u32x4 buf[SMAX][NL];
   if constexpr (LN) {
     float* vbuf = reinterpret_cast<float*>(red + waves * 64);
@@ -738,7 +743,7 @@ __global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
       *reinterpret_cast<float4*>(o) = float4{v[0], v[1], v[2], v[3]};
     } else {
       if (p.bias) {
-        const uint2 b = *reinterpret_cast<const uint2*>(static_cast<const T*>(p.bias) + feat);
+        const uint2 b = q == wave ? bias0 : *reinterpret_cast<const uint2*>(static_cast<const T*>(p.bias) + feat);
         v[0] += to_f32<DT>(T(b.x & 0xffffu)); v[1] += to_f32<DT>(T(b.x >> 16));
         v[2] += to_f32<DT>(T(b.y & 0xffffu)); v[3] += to_f32<DT>(T(b.y >> 16));
       }
@@ -757,7 +762,9 @@ __global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
 // x[r, :] += bias + sum over the S splits of partials[s, r, :] (fp32);
 // out[r, :] = LayerNorm(x[r, :]) in T. One wave per row, as
 // residual_layernorm_wave_kernel; every load of a row (x, bias, the S
-// partials, which other XCDs wrote) is issued before the first add.
+// partials, which other XCDs wrote, gamma and beta) is issued before the
+// first add, so the kernel waits for one memory round trip (loading gamma and
+// beta after the reduction made GPT-2-medium decode steps 2-4 % slower).
 template <int DT, int NJ, int S>
 __global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* out, float* x, const float* part,
                                                                           const void* bias, const float* gamma,
@@ -771,7 +778,7 @@ __global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* 
   float* xr = x + int64_t(row) * width;
   const int64_t split_stride = int64_t(rows) * width;
   const float* pr = part + int64_t(row) * width;
-  float4 v[NJ], q[NJ][S];
+  float4 v[NJ], q[NJ][S], gm[NJ], bt[NJ];
   uint2 b[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
@@ -781,6 +788,8 @@ __global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* 
       b[j] = bias ? *reinterpret_cast<const uint2*>(static_cast<const T*>(bias) + c) : uint2{0u, 0u};
 #pragma unroll
       for (int s = 0; s < S; ++s) q[j][s] = *reinterpret_cast<const float4*>(pr + s * split_stride + c);
+      gm[j] = *reinterpret_cast<const float4*>(gamma + c);
+      bt[j] = *reinterpret_cast<const float4*>(beta + c);
     }
   }
   float sum = 0.f, sq = 0.f;
@@ -812,8 +821,7 @@ __global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* 
     if (j >= nj) break;
     const int c = 256 * j + 4 * lane;
     const int64_t at = out_tiled ? tiled_offset(row, c, width) : int64_t(row) * width + c;
-    const float4 g = *reinterpret_cast<const float4*>(gamma + c);
-    const float4 b = *reinterpret_cast<const float4*>(beta + c);
+    const float4 g = gm[j], b = bt[j];
     const float r0 = g.x * ((v[j].x - mean) * inv) + b.x;
     const float r1 = g.y * ((v[j].y - mean) * inv) + b.y;
     const float r2 = g.z * ((v[j].z - mean) * inv) + b.z;
