@@ -179,15 +179,21 @@ size_t mt_decoder_scratch_bytes(int rows, int d, int dtype);
  * in place; h [rows, d] in dtype receives the final LayerNorm output and,
  * when logits is not null, logits [rows, vocab] = h @ head_weight^T (the tied
  * head, head_weight [vocab, d]). For fp16/bf16 the layer projections run on
- * mt_decode_projection where it takes their shapes: the QKV and fc
- * projections for rows <= 16, the out- and proj-projections (as split-k
- * partial sums reduced by mt_residual_layernorm_partials, d a multiple of
- * 256) for rows <= 32; for rows <= 8 and d <= 1024 the residual add and
- * LayerNorm move into the QKV and fc projections (mt_decode_projection_ln,
- * the residual stream alternating between x and a scratch copy). Larger batches, fp32, other shapes and
- * MT_DECODE_PROJECTIONS=0 in the environment use hipBLASLt, which chooses its
- * algorithm by timing (cold caches) on the third call of a shape, as does the
- * tied head.
+ * mt_decode_projection (reading the layer's tiled weight copies where given):
+ * for rows <= 8 and d <= 1024 the residual add and LayerNorm move into the
+ * QKV and fc projections (mt_decode_projection_ln, the residual stream
+ * alternating between x and a scratch copy) and the out- and proj-projections
+ * leave split-k partial sums; for 9 <= rows <= 128 (d a multiple of 256) the
+ * LayerNorms (mt_residual_layernorm_partials after the split out- and
+ * proj-projections) and the fc epilogue write the activations of QKV, fc and
+ * proj in the fragment-tiled layout, and the out-projection runs split while
+ * rows <= 32 or it takes at most 4 splits. Otherwise (larger batches, fp32,
+ * other shapes, MT_DECODE_PROJECTIONS=0 in the environment) the QKV and fc
+ * projections take the kernel up to 16 rows and the out- and proj-projections
+ * up to 32, on row-major activations, and hipBLASLt the rest; hipBLASLt
+ * chooses its algorithm by timing (cold caches) on the third call of a shape,
+ * as does the tied head. MT_DECODE_TILED_ROWS=<rows> moves the tiled path's
+ * upper bound (0: off).
  * Replaces the reference's per-op layer loop of DecoderLM.decode_batch
  * (minitorch/modules_transformer.py:373-390,258-284). */
 int mt_decoder_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
