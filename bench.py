@@ -735,7 +735,7 @@ def main():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--split', type=int, default=0, help='split length in tokens (0 = automatic)')
     ap.add_argument('--unroll', type=int, default=0)
-    ap.add_argument('--waves', type=int, default=0, help='waves per decode workgroup (4 or 8; 0 = default)')
+    ap.add_argument('--waves', type=int, default=0, help='waves per decode workgroup (2, 4 or 8; 0 = default)')
     ap.add_argument('--natural-order', action='store_true',
                     help='no work list: schedule every (split, row) in batch order')
     ap.add_argument('--cpu-seconds', type=float, default=10.0)

@@ -97,8 +97,10 @@ int mt_paged_decode_split_tokens(int page_size, int columns, int requested, int*
 /* mt_paged_decode_batch with a caller-owned workspace and tuning knobs:
  * split_tokens (a multiple of 64, at most 2048; 0 = automatic), unroll (1, 2
  * or 4 row-blocks per register stage, capped by the row size; 0 = automatic:
- * 2), waves per workgroup (4 or 8; 0 = automatic: 8 when the whole grid is
- * resident at the 8-wave kernel's occupancy, else 4), qkv_stride (elements between consecutive rows of q, k and
+ * 2), waves per workgroup (2, 4 or 8; 0 = automatic: 8 when the whole grid is
+ * resident at the 8-wave kernel's occupancy, 2 when the 2-wave kernel's grid
+ * spans more than two residency rounds, else 4; 2 takes splits of at most
+ * 1024 tokens, 512 for pages below 8, and runs 4 beyond), qkv_stride (elements between consecutive rows of q, k and
  * v, so that they can be column blocks of one fused [b, 3*h*d] projection
  * output; 0 = h*d, contiguous; out is always contiguous), and an optional
  * work list built by the caller from the

@@ -1506,6 +1506,15 @@ int device_compute_units() {
   return cached[dev];
 }
 
+// A wave resolves the page of each of its steps into one lane, so a split
+// may give a wave at most 64 steps (32 when a step spans two pages): 2-wave
+// workgroups take splits of at most 1024 tokens (512 for pages below 8).
+bool two_wave_split_ok(const DecodeArgs& a) {
+  constexpr int RB = kWave / kDecodeGroup;  // tokens per wave step
+  const int steps = a.split_tokens / RB / 2;
+  return a.split_tokens % (2 * RB) == 0 && steps * (a.g.page_size < RB ? 2 : 1) <= kWave;
+}
+
 // Workgroups of decode_kernel<DT, D, VEC, U, kStages, WAVES, G> resident per
 // compute unit (0 if the query fails), looked up once per instantiation.
 template <int DT, int D, bool VEC, int U, int WAVES, int G>
@@ -1558,16 +1567,23 @@ hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
 // their occupancy (a (row, head) streamed by 8 waves finishes its longest
 // rows sooner; config 2: 21.0 us vs 21.9 us with 4), else 4 (more
 // workgroups per compute unit for grids of several residency rounds;
-// config 5: 256 us vs 267 us with 8).
+// config 5: 256 us vs 267 us with 8), and 2 when even 2-wave workgroups take
+// more than two residency rounds (finer-grained hand-out of the tail; config
+// 5: 261-263 us vs 267 us with 4; config 4's layer, 2048 workgroups that 2
+// waves would make resident at once, took 9 % longer per step with 2).
 template <int DT, int D, bool VEC>
 hipError_t launch_decode_t(const DecodeArgs& a, int64_t blocks, int unroll, int waves) {
   constexpr int G = kDecodeGroup;
+  constexpr int U8 = VEC && G == 8 ? 2 : 1;
   if (waves == 0) {
-    constexpr int U8 = VEC && G == 8 ? 2 : 1;
-    waves = blocks <= int64_t(decode_occupancy<DT, D, VEC, U8, 8, G>()) * device_compute_units() ? 8 : 4;
+    const int64_t cus = device_compute_units();
+    waves = blocks <= int64_t(decode_occupancy<DT, D, VEC, U8, 8, G>()) * cus ? 8 : 4;
+    if (waves == 4 && two_wave_split_ok(a) && blocks > 2 * int64_t(decode_occupancy<DT, D, VEC, U8, 2, G>()) * cus)
+      waves = 2;
   }
-  if (a.split_tokens % ((kWave / G) * waves) != 0) waves = 4;
+  if (a.split_tokens % ((kWave / G) * waves) != 0 || (waves == 2 && !two_wave_split_ok(a))) waves = 4;
   if (waves == 8) return launch_decode_w<DT, D, VEC, 8, G>(a, blocks, unroll);
+  if (waves == 2) return launch_decode_w<DT, D, VEC, 2, G>(a, blocks, unroll);
   return launch_decode_w<DT, D, VEC, 4, G>(a, blocks, unroll);
 }
 
@@ -1588,7 +1604,7 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   if (work && split_tokens <= 0) return hipErrorInvalidValue;
   const int S = choose_split(cap, split_tokens);
   if (S < 64 || S % 64 != 0 || S > kMaxSplitTokens) return hipErrorInvalidValue;
-  if (waves != 0 && waves != 4 && waves != 8) return hipErrorInvalidValue;
+  if (waves != 0 && waves != 2 && waves != 4 && waves != 8) return hipErrorInvalidValue;
   const int64_t nsplit_max = (cap + S - 1) / S;
   const int64_t bh = int64_t(b) * h;
   if (nsplit_max > INT_MAX) return hipErrorInvalidValue;
@@ -2180,7 +2196,7 @@ int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v
   if (!out || !q || !k || !v || !slabs || !table || !offsets ||
       !paged_shape(b, h, 1, 1, d, page_size, pages_per_slab, num_slabs, columns, layer, layers, 0) ||
       int64_t(columns) * page_size > INT32_MAX || split_tokens < 0 || unroll < 0 ||
-      (waves != 0 && waves != 4 && waves != 8) ||
+      (waves != 0 && waves != 2 && waves != 4 && waves != 8) ||
       (qkv_stride != 0 && int64_t(qkv_stride) < int64_t(h) * d) || qkv_stride < 0)
     return hipErrorInvalidValue;
   if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;

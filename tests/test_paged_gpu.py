@@ -136,12 +136,22 @@ def test_null_slab_reads_nan():
 
 @pytest.mark.parametrize('split_tokens', [64, 128, 256, 1024])
 @pytest.mark.parametrize('unroll', [1, 2, 4])
-@pytest.mark.parametrize('waves', [4, 8])
+@pytest.mark.parametrize('waves', [2, 4, 8])
 def test_split_entry_equals_oracle(split_tokens, unroll, waves):
     case = make_decode_case(7, batch=6, heads=3, dim=64, page_size=16,
                             lengths=[1, 64, 65, 500, 1024, 777], pool_pages=256, pages_per_slab=8,
                             dtype='float16')
     check_case(case, entry='split', split_tokens=split_tokens, unroll=unroll, waves=waves)
+
+
+@pytest.mark.parametrize('dtype,dim,split_tokens', [('bfloat16', 128, 1024), ('float16', 64, 2048),
+                                                     ('float32', 128, 512)])
+def test_two_wave_workgroups_equal_oracle(dtype, dim, split_tokens):
+    # 2-wave workgroups (a wave resolves the pages of up to 64 steps, so
+    # splits above 1024 tokens fall back to 4 waves: the 2048 case)
+    case = make_decode_case(15, batch=5, heads=4, dim=dim, page_size=16, lengths=[3, 1024, 1500, 700, 2048],
+                            pool_pages=640, pages_per_slab=16, dtype=dtype)
+    check_case(case, entry='split', split_tokens=split_tokens, waves=2)
 
 
 def run_work_list(dev, lengths, split_tokens, waves=0, compute_units=8, reverse=False):
@@ -165,7 +175,7 @@ def run_work_list(dev, lengths, split_tokens, waves=0, compute_units=8, reverse=
 
 
 @pytest.mark.parametrize('page_size', [8, 16, 32])
-@pytest.mark.parametrize('waves', [4, 8])
+@pytest.mark.parametrize('waves', [2, 4, 8])
 def test_work_list_equals_oracle_and_grid(page_size, waves):
     # rows of 0..3 splits visited longest first: same bits as the full grid
     lengths = [300, 5, 1024, 77, 16, 640, 1, 2100]
