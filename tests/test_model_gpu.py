@@ -449,15 +449,15 @@ def test_distilgpt2_shape_batched_prefill_fp16():
 
 
 @pytest.mark.parametrize('precision', ['fp16', 'bf16'])
-@pytest.mark.parametrize('batch,d,heads', [(3, 256, 4), (8, 256, 4), (20, 256, 4), (40, 256, 4), (5, 1024, 16),
-                                           (40, 1024, 16), (128, 768, 12)])
+@pytest.mark.parametrize('batch,d,heads', [(3, 256, 4), (8, 256, 4), (12, 256, 4), (20, 256, 4), (40, 256, 4),
+                                           (5, 1024, 16), (40, 1024, 16), (128, 768, 12)])
 def test_low_precision_batched_decode_near_oracle(precision, batch, d, heads):
     # fp16/bf16 decode steps of 3 and 8 rows (d = 256) run every layer
     # projection on the matrix-core projection kernel, with the residual add
     # and LayerNorm inside the QKV and fc projections and the out- and
     # proj-projections as split-k partial sums; d = 1024 (GPT-2-medium's
     # width) with 5 rows takes that fused loop at its largest LayerNorm-prologue
-    # tile. 20, 40 and 128 rows take the tiled path (fragment-tiled
+    # tile. 12, 20, 40 and 128 rows take the tiled path (fragment-tiled
     # activations written by the LayerNorm kernels and the fc epilogue): the
     # out-projection split at 20 rows and at 40 rows of width 1024 (4 splits),
     # on hipBLASLt at 40 rows of width 256 and at 128 rows of width 768 (8
