@@ -13,10 +13,14 @@ MI355X-first choices: projection weights are kept resident on the device in
 the compute type (the reference re-casts fp32 masters on every matmul,
 minitorch/tensor.py:226-231); Q, K and V come from one fused [d, 3d]
 projection (GPT-2's c_attn) whose output the paged decode reads as three
-column blocks (no split copies); every projection is one hipBLASLt call with
-the bias (and for the MLP's fc, the GELU) as its epilogue; the batched decode
-step runs its whole layer loop in one native call (mt_decoder_layers), with
-the residual adds fused into the following LayerNorms.
+column blocks (no split copies); the batched decode step runs its whole layer
+loop in one native call (mt_decoder_layers), with the residual adds fused into
+the following LayerNorms. In fp16/bf16 a decode step of up to 128 rows runs
+its projections on the matrix-core projection kernel, reading a second copy of
+each projection weight stored fragment-tiled (``fragment_tiled``: each operand
+fragment one contiguous 1 KB run); prefill, larger batches and fp32 use one
+hipBLASLt call per projection with the bias (and for the MLP's fc, the GELU)
+as its epilogue.
 """
 import ctypes as ct
 import numpy as np
