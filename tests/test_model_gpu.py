@@ -450,7 +450,7 @@ def test_distilgpt2_shape_batched_prefill_fp16():
 
 @pytest.mark.parametrize('precision', ['fp16', 'bf16'])
 @pytest.mark.parametrize('batch,d,heads', [(3, 256, 4), (8, 256, 4), (12, 256, 4), (20, 256, 4), (40, 256, 4),
-                                           (5, 1024, 16), (40, 1024, 16), (128, 768, 12)])
+                                           (5, 1024, 16), (40, 1024, 16), (128, 768, 12), (150, 256, 4)])
 def test_low_precision_batched_decode_near_oracle(precision, batch, d, heads):
     # fp16/bf16 decode steps of 3 and 8 rows (d = 256) run every layer
     # projection on the matrix-core projection kernel, with the residual add
@@ -461,8 +461,9 @@ def test_low_precision_batched_decode_near_oracle(precision, batch, d, heads):
     # activations written by the LayerNorm kernels and the fc epilogue): the
     # out-projection split at 20 rows and at 40 rows of width 1024 (4 splits),
     # on hipBLASLt at 40 rows of width 256 and at 128 rows of width 768 (8
-    # splits). Each row's logits against the fp64 numpy GPT-2 on its own
-    # sequence, within 2 % of the logits' range as above.
+    # splits); 150 rows run every projection on hipBLASLt. Each row's logits
+    # against the fp64 numpy GPT-2 on its own sequence, within 2 % of the
+    # logits' range as above.
     model = tiny(seed=19, d=d, heads=heads)
     rng = np.random.default_rng([19, batch])
     prompts = [rng.integers(0, model.n_vocab, int(rng.integers(5, 40))) for _ in range(batch)]
