@@ -24,6 +24,8 @@
 namespace {
 
 constexpr int kThreads = 1024;
+constexpr int kPrepareRows = 2048;  // rows of a decode step whose slot and page count stay in LDS
+constexpr int kTableUnroll = 8;     // block-table entries each thread loads before storing
 
 struct Header {           // must match include/mt_sched.h (mt_pool_header)
   int top;                // free pages on the stack
@@ -272,6 +274,9 @@ __global__ __launch_bounds__(kThreads) void decode_prepare_kernel(Pool p, const 
                                                                   int* cu_seqlens, int* new_page) {
   __shared__ int sh[33];
   __shared__ int s_red;
+  // Each row's slot and page count after this step, kept for the table pass
+  // (rows past kPrepareRows read them again from the pool state).
+  __shared__ int s_slot[kPrepareRows], s_npages[kPrepareRows];
   if (threadIdx.x == 0) s_red = 0;
   const int F = p.h->top, opened = p.h->slabs_opened, pps = p.pages_per_slab;
   // limit -1: the pages the budget has left, read from the pool header on
@@ -306,6 +311,10 @@ __global__ __launch_bounds__(kThreads) void decode_prepare_kernel(Pool p, const 
         last_rank = rank;
       }
       new_page[i] = page;
+      if (i < kPrepareRows) {
+        s_slot[i] = slot;
+        s_npages[i] = page >= 0 ? have + 1 : have;
+      }
     }
     need_base += total_need;
     seq_base += total_seq;
@@ -328,10 +337,28 @@ __global__ __launch_bounds__(kThreads) void decode_prepare_kernel(Pool p, const 
   (void)last_rank;
   open_slabs(p, opened, nslab);
   __syncthreads();
-  for (int64_t e = threadIdx.x; e < int64_t(b) * columns; e += blockDim.x) {
-    const int i = int(e / columns), c = int(e - int64_t(i) * columns);
-    const int slot = slots[i];
-    table[e] = c < p.slot_npages[slot] ? p.slot_pages[int64_t(slot) * p.max_cols + c] : -1;
+  // Table rows: kTableUnroll entries per thread are loaded before any is
+  // stored, so their page-list reads overlap instead of taking one round
+  // trip each.
+  const int64_t entries = int64_t(b) * columns;
+  for (int64_t e0 = threadIdx.x; e0 < entries; e0 += int64_t(blockDim.x) * kTableUnroll) {
+    int v[kTableUnroll];
+#pragma unroll
+    for (int u = 0; u < kTableUnroll; ++u) {
+      const int64_t e = e0 + int64_t(u) * blockDim.x;
+      v[u] = -1;
+      if (e < entries) {
+        const int i = int(e / columns), c = int(e - int64_t(i) * columns);
+        const int slot = i < kPrepareRows ? s_slot[i] : slots[i];
+        const int np = i < kPrepareRows ? s_npages[i] : p.slot_npages[slot];
+        if (c < np) v[u] = p.slot_pages[int64_t(slot) * p.max_cols + c];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kTableUnroll; ++u) {
+      const int64_t e = e0 + int64_t(u) * blockDim.x;
+      if (e < entries) table[e] = v[u];
+    }
   }
   if (threadIdx.x == 0) {
     p.h->top = top;

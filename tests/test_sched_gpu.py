@@ -230,6 +230,46 @@ def test_decode_batches_match_oracle_over_many_steps():
     assert_same_pool(pool, oracle)
 
 
+def test_decode_batch_of_2143_rows_matches_oracle():
+    # Past the rows whose slot and page count the metadata kernel keeps in
+    # LDS (2048), with a table of 2143 x 8 entries (several unrolled passes
+    # of 1024 threads x 8): pages, table and free list bit-exact.
+    rng = np.random.default_rng(7)
+    model = StubModel(layers=1, heads=1, dim=64, n_positions=128)
+    pool, oracle = pool_pair(model, page_size=16, max_bytes=24000 * 2 * 64 * 16 * 4, pages_per_slab=64)
+    pairs = []
+    for _ in range(2500):
+        n = int(rng.integers(1, 60))
+        c = PagedKVCache(model, 1, 128, page_size=16, page_pool=pool)
+        oc = CacheOracle(oracle, 1, 128)
+        c.prepare_append(n)
+        oc.prepare_append(n)
+        c._written_layers.update(range(len(c.layout)))
+        c.commit_append()
+        oc.commit_append()
+        pairs.append((c, oc))
+    # free every seventh request so the step pops reused pages and opens slabs
+    live = []
+    for i, (c, oc) in enumerate(pairs):
+        if i % 7 == 3:
+            c.close()
+            oc.close()
+        else:
+            live.append((c, oc))
+    assert len(live) == 2143
+    order = list(rng.permutation(len(live)))
+    live = [live[i] for i in order]
+    for _ in range(2):
+        _decode_round(model, pool, oracle, live, rng)
+        for c, oc in live:
+            assert c.pages() == oc.pages
+        assert_same_pool(pool, oracle)
+    for c, oc in live:
+        c.close()
+        oc.close()
+    assert_same_pool(pool, oracle)
+
+
 def test_decode_budget_exhaustion_aborts_like_reference():
     model = StubModel(layers=1, heads=1, dim=64, n_positions=128)
     page_bytes = 2 * 1 * 1 * 64 * 16 * 4
