@@ -607,7 +607,9 @@ def e2e_config4(args, loops=('sync', 'sync-free')):
     """Config 4 end to end: 128 concurrent GPT-2-medium (bf16) requests, 5 %
     replaced per step. Reports decode tokens/s and ms per decode step (whole
     24-layer model step with the tied head, tokens to the host) and the whole
-    loop's rate including the replacement prefills, per loop."""
+    loop's rate including the replacement prefills, per loop; the merged loop
+    (decode and replacement prefills of a step in one layer loop) reports the
+    whole loop's rate only."""
     from minitorch_amd import model as model_mod, e2e
     distil = args.model == 'distilgpt2'
     model = model_mod.distilgpt2(seed=args.seed) if distil else model_mod.gpt2_medium(seed=args.seed)
@@ -619,6 +621,9 @@ def e2e_config4(args, loops=('sync', 'sync-free')):
         r['sync_free'] = e2e.run_config4(model, **kw, token_feedback=True)
         # the sync-free loop with each decode step replayed from a HIP graph
         r['graph'] = e2e.run_config4(model, **kw, token_feedback=True, graph=True)
+        # the sync-free loop with each step's decode and replacement prefills
+        # in one layer loop
+        r['merged'] = e2e.run_config4(model, **kw, token_feedback=True, merge_prefill=True)
     if not args.no_cpu_baseline:
         r['cpu_baseline'] = e2e_cpu_baseline(
             model, e2e.config4_lengths(np.random.default_rng([args.seed, 4]), args.concurrent),
@@ -708,7 +713,7 @@ def e2e_summary(r3, r4):
             kv_pool_used_pages_after=r3.get('kv_pool_used_pages_after'),
             cpu_baseline=r3.get('cpu_baseline'))
     if r4 is not None:
-        sf, gr = r4.get('sync_free', {}), r4.get('graph', {})
+        sf, gr, mg = r4.get('sync_free', {}), r4.get('graph', {}), r4.get('merged', {})
         out['config4'] = dict(
             workload=r4['workload'],
             decode_tokens_per_sec=r4.get('decode_tokens_per_sec'), ms_per_decode_step=r4.get('ms_per_step'),
@@ -720,6 +725,9 @@ def e2e_summary(r3, r4):
                        decode_ms_per_step=gr.get('ms_per_step'),
                        loop_tokens_per_sec=gr.get('loop_tokens_per_sec'),
                        loop_ms_per_step=gr.get('loop_ms_per_step')) if gr else None,
+            merged=dict(loop_tokens_per_sec=mg.get('loop_tokens_per_sec'),
+                        loop_ms_per_step=mg.get('loop_ms_per_step'),
+                        replaced_requests=mg.get('replaced_requests')) if mg else None,
             steps=r4.get('steps'), mean_context_tokens=r4.get('mean_context_tokens'),
             replaced_requests=r4.get('replaced_requests'), page_reuses=r4.get('page_reuses'),
             cpu_baseline=r4.get('cpu_baseline'))

@@ -239,6 +239,30 @@ int mt_prefill_layers_ragged(void* handle, const mt_decoder_layer* layers, int n
                              const int* tokens, int d, int heads, float eps, int dtype, int fused_gelu,
                              void* scratch, size_t scratch_bytes, const mt_prefill_attention* att);
 
+/* One decode step and one ragged prefill in a single layer loop: rows
+ * [0, decode_rows) of x [decode_rows + sum tokens, d] fp32 (updated in place)
+ * are the decode batch (datt, as mt_decoder_layers takes it), the rest the
+ * prompts, tokens[r] rows for request r in request order (patt[r], as
+ * mt_prefill_layers_ragged takes them; all on the decode batch's pool). The
+ * projections (hipBLASLt, first heuristic choice), LayerNorms and GELU run
+ * once over every row; per layer the decode rows' append and attention run
+ * before the prompts' appends and attention, so that pages the prompts were
+ * given after a decode row's request ended (its pages released once the
+ * step's pages were taken) are written, layer by layer, only after that row
+ * has read them. When logits is not null, logits [decode_rows + requests,
+ * vocab] = final-LayerNorm(x)[decode rows, then each prompt's last row] @
+ * head_weight^T. decode_rows <= 65471. Scratch as
+ * mt_decoder_scratch_bytes(decode_rows + sum tokens). Results equal
+ * mt_decoder_layers followed by mt_prefill_layers_ragged up to the
+ * projections' algorithm choice for the row count. No reference counterpart
+ * (the reference runs a step's decode batch and its prefills as separate
+ * forward passes, minitorch/continuous_batching.py:140-176). */
+int mt_mixed_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
+                    const float* final_gamma, const float* final_beta, const void* head_weight, void* logits,
+                    int vocab, int decode_rows, int requests, const int* tokens, int d, int heads, float eps,
+                    int dtype, int fused_gelu, void* scratch, size_t scratch_bytes,
+                    const mt_decode_attention* datt, const mt_prefill_attention* patt);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1226,39 +1226,73 @@ int gemm_gelu(Blas* blas, void* out, const void* a, const void* b, const void* b
 }
 
 // Row gather with the source rows in the launch arguments: out[i, :] =
-// in[row[i], :] for i < count (at most kGatherRows per launch), width in
-// 16-bit or 32-bit elements moved as 32-bit words.
+// in[i, :] for the first `head` rows, then out[head + i, :] = in[row[i], :]
+// for i < count (at most kGatherRows per launch), width in 16-bit or 32-bit
+// elements moved as 32-bit words.
 constexpr int kGatherRows = 64;
+constexpr int kGatherMaxHead = 65535 - kGatherRows;  // the grid's y extent bounds head + count
 struct GatherRows {
-  int count;
+  int head, count;
   int row[kGatherRows];
 };
 
 __global__ __launch_bounds__(256) void gather_rows_kernel(uint32_t* out, const uint32_t* in, int64_t words,
                                                           GatherRows g) {
   const int i = blockIdx.y;
-  if (i >= g.count) return;
-  const uint32_t* src = in + int64_t(g.row[i]) * words;
+  if (i >= g.head + g.count) return;
+  const uint32_t* src = in + int64_t(i < g.head ? i : g.row[i - g.head]) * words;
   uint32_t* dst = out + int64_t(i) * words;
   for (int64_t w = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; w < words; w += int64_t(gridDim.x) * blockDim.x)
     dst[w] = src[w];
 }
 
-// out[i, :] = in[rows[i], :] for `count` rows of `row_bytes` (a multiple of 4).
-hipError_t gather_rows(void* out, const void* in, const int* rows, int count, size_t row_bytes) {
-  if (row_bytes % 4) return hipErrorInvalidValue;
+// out[i, :] = in[i, :] for i < head, then out[head + i, :] = in[rows[i], :]
+// for `count` rows, rows of `row_bytes` (a multiple of 4); out and in do not
+// overlap.
+hipError_t gather_rows(void* out, const void* in, const int* rows, int count, size_t row_bytes, int head = 0) {
+  if (row_bytes % 4 || head < 0 || head > kGatherMaxHead) return hipErrorInvalidValue;
   const int64_t words = int64_t(row_bytes / 4);
-  for (int c0 = 0; c0 < count; c0 += kGatherRows) {
+  for (int c0 = 0; c0 < count || (c0 == 0 && head > 0); c0 += kGatherRows) {
     GatherRows g{};
+    g.head = c0 == 0 ? head : 0;
     g.count = count - c0 < kGatherRows ? count - c0 : kGatherRows;
     for (int i = 0; i < g.count; ++i) g.row[i] = rows[c0 + i];
-    const dim3 grid(unsigned((words + 255) / 256), unsigned(g.count));
-    gather_rows_kernel<<<grid, 256>>>(static_cast<uint32_t*>(out) + int64_t(c0) * words,
+    const dim3 grid(unsigned((words + 255) / 256), unsigned(g.head + g.count));
+    gather_rows_kernel<<<grid, 256>>>(static_cast<uint32_t*>(out) + (c0 ? int64_t(head + c0) * words : 0),
                                       static_cast<const uint32_t*>(in), words, g);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+// The prompts of a ragged prefill: every request's table row and offset, the
+// row of its last token (after `first` rows that precede the prompts) and the
+// total token count. False when a count is not positive, the total exceeds
+// INT32_MAX or the requests do not describe one pool.
+struct RaggedPrompts {
+  std::vector<const int*> tables;
+  std::vector<int> offsets, last;
+  int64_t total = 0;
+};
+bool ragged_prompts(const mt_prefill_attention* att, const int* tokens, int requests, int first, RaggedPrompts& rp) {
+  rp.tables.resize(requests);
+  rp.offsets.resize(requests);
+  rp.last.resize(requests);
+  rp.total = 0;
+  for (int r = 0; r < requests; ++r) {
+    const mt_prefill_attention& A = att[r];
+    if (tokens[r] < 1 || A.slabs != att[0].slabs || A.page_size != att[0].page_size ||
+        A.pages_per_slab != att[0].pages_per_slab || A.num_slabs != att[0].num_slabs ||
+        A.columns != att[0].columns || A.layers != att[0].layers)
+      return false;
+    rp.tables[r] = A.table;
+    rp.offsets[r] = A.offset;
+    rp.total += tokens[r];
+    if (int64_t(first) + rp.total > INT32_MAX) return false;
+    rp.last[r] = int(first + rp.total - 1);
+  }
+  return true;
 }
 
 }  // namespace
@@ -1691,27 +1725,11 @@ int mt_prefill_layers_ragged(void* handle, const mt_decoder_layer* layers, int n
       (logits && (!head_weight || vocab < 1)) || requests < 1 || !tokens || d < 1 || heads < 1 ||
       d % heads || !dtype_ok(dtype) || !scratch || !att)
     return hipErrorInvalidValue;
-  int64_t total = 0;
-  for (int r = 0; r < requests; ++r) {
-    if (tokens[r] < 1) return hipErrorInvalidValue;
-    total += tokens[r];
-  }
-  if (total > INT32_MAX || total * 4 * d > INT32_MAX ||
-      scratch_bytes < mt_decoder_scratch_bytes(int(total), d, dtype))
+  RaggedPrompts rp;
+  if (!ragged_prompts(att, tokens, requests, 0, rp) || rp.total * 4 * d > INT32_MAX ||
+      scratch_bytes < mt_decoder_scratch_bytes(int(rp.total), d, dtype))
     return hipErrorInvalidValue;
-  // One pool: every request's attention metadata shares the pool geometry.
-  std::vector<const int*> tables(requests);
-  std::vector<int> offsets(requests);
-  for (int r = 0; r < requests; ++r) {
-    const mt_prefill_attention& A = att[r];
-    if (A.slabs != att[0].slabs || A.page_size != att[0].page_size ||
-        A.pages_per_slab != att[0].pages_per_slab || A.num_slabs != att[0].num_slabs ||
-        A.columns != att[0].columns || A.layers != att[0].layers)
-      return hipErrorInvalidValue;
-    tables[r] = A.table;
-    offsets[r] = A.offset;
-  }
-  const int rows = int(total);
+  const int rows = int(rp.total);
   Blas* blas = static_cast<Blas*>(handle);
   const size_t e = dtype == kF32 ? 4 : 2;
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
@@ -1726,7 +1744,7 @@ int mt_prefill_layers_ragged(void* handle, const mt_decoder_layer* layers, int n
     if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 1, dtype, dtype))) break;
     // Every request's append and causal attention over its own pages.
     if ((st = mt_paged_prefill_ragged(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, att[0].slabs,
-                                      tables.data(), tokens, offsets.data(), requests, heads, hd,
+                                      rp.tables.data(), tokens, rp.offsets.data(), requests, heads, hd,
                                       att[0].page_size, att[0].pages_per_slab, att[0].num_slabs,
                                       att[0].columns, i, att[0].layers, dtype, 3 * d, d)))
       break;
@@ -1741,12 +1759,69 @@ int mt_prefill_layers_ragged(void* handle, const mt_decoder_layer* layers, int n
   // Tied head over each request's last row, gathered into the (now free)
   // attention scratch.
   if (!st && logits) {
-    std::vector<int> last(requests);
-    int64_t end = 0;
-    for (int r = 0; r < requests; ++r) last[r] = int((end += tokens[r]) - 1);
-    st = gather_rows(attn, h, last.data(), requests, size_t(d) * e);
+    st = gather_rows(attn, h, rp.last.data(), requests, size_t(d) * e);
     if (!st) st = gemm(blas, logits, attn, head_weight, nullptr, requests, vocab, d, 1, dtype, dtype);
   }
+  return st;
+}
+
+int mt_mixed_layers(void* handle, const mt_decoder_layer* layers, int n_layer, float* x, void* h,
+                    const float* final_gamma, const float* final_beta, const void* head_weight, void* logits,
+                    int vocab, int decode_rows, int requests, const int* tokens, int d, int heads, float eps,
+                    int dtype, int fused_gelu, void* scratch, size_t scratch_bytes,
+                    const mt_decode_attention* datt, const mt_prefill_attention* patt) {
+  if (!handle || !layers || n_layer < 1 || !x || !h || !final_gamma || !final_beta ||
+      (logits && (!head_weight || vocab < 1)) || decode_rows < 1 || requests < 1 || !tokens || d < 1 ||
+      heads < 1 || d % heads || !dtype_ok(dtype) || !scratch || !datt || !patt)
+    return hipErrorInvalidValue;
+  RaggedPrompts rp;
+  if (decode_rows > kGatherMaxHead || !ragged_prompts(patt, tokens, requests, decode_rows, rp))
+    return hipErrorInvalidValue;
+  const int64_t rows64 = decode_rows + rp.total;
+  // the decode rows and the prompts share one pool
+  if (rows64 * 4 * d > INT32_MAX || scratch_bytes < mt_decoder_scratch_bytes(int(rows64), d, dtype) ||
+      patt[0].slabs != datt->slabs || patt[0].page_size != datt->page_size ||
+      patt[0].pages_per_slab != datt->pages_per_slab || patt[0].layers != datt->layers)
+    return hipErrorInvalidValue;
+  const int rows = int(rows64);
+  Blas* blas = static_cast<Blas*>(handle);
+  const size_t e = dtype == kF32 ? 4 : 2;
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+  char* qkv = static_cast<char*>(scratch);
+  char* attn = qkv + al(size_t(rows) * 3 * d * e);
+  char* proj = attn + al(size_t(rows) * d * e);
+  char* mlp = proj + al(size_t(rows) * d * e);
+  char* pqkv = qkv + size_t(decode_rows) * 3 * d * e;   // the prompts' QKV rows
+  char* pattn = attn + size_t(decode_rows) * d * e;     // and attention rows
+  const int hd = d / heads;
+  int st = layernorm(h, x, layers[0].ln1_gamma, layers[0].ln1_beta, rows, d, eps, dtype);
+  for (int i = 0; i < n_layer && !st; ++i) {
+    const mt_decoder_layer& L = layers[i];
+    if ((st = gemm(blas, qkv, h, L.w_qkv, L.b_qkv, rows, 3 * d, d, 1, dtype, dtype))) break;
+    if ((st = mt_paged_decode_split(attn, qkv, qkv + size_t(d) * e, qkv + size_t(2 * d) * e, datt->slabs,
+                                    datt->table, datt->offsets, decode_rows, heads, hd, datt->page_size,
+                                    datt->pages_per_slab, datt->num_slabs, datt->columns, i, datt->layers, dtype,
+                                    datt->split_tokens, 0, 0, 3 * d, datt->work, datt->work_items,
+                                    datt->merge_rows, datt->partials, datt->partial_bytes)))
+      break;
+    if ((st = mt_paged_prefill_ragged(pattn, pqkv, pqkv + size_t(d) * e, pqkv + size_t(2 * d) * e, patt[0].slabs,
+                                      rp.tables.data(), tokens, rp.offsets.data(), requests, heads, hd,
+                                      patt[0].page_size, patt[0].pages_per_slab, patt[0].num_slabs,
+                                      patt[0].columns, i, patt[0].layers, dtype, 3 * d, d)))
+      break;
+    if ((st = gemm(blas, proj, attn, L.w_o, L.b_o, rows, d, d, 1, dtype, dtype))) break;
+    if ((st = residual_layernorm(h, x, proj, L.ln2_gamma, L.ln2_beta, rows, d, eps, dtype))) break;
+    if ((st = gemm_gelu(blas, mlp, h, L.w_fc, L.b_fc, rows, 4 * d, d, dtype, fused_gelu != 0, false, 1))) break;
+    if ((st = gemm(blas, proj, mlp, L.w_proj, L.b_proj, rows, d, 4 * d, 1, dtype, dtype))) break;
+    const bool last = i + 1 == n_layer;
+    st = residual_layernorm(h, x, proj, last ? final_gamma : layers[i + 1].ln1_gamma,
+                            last ? final_beta : layers[i + 1].ln1_beta, rows, d, eps, dtype);
+  }
+  // Tied head over the decode rows and each prompt's last row, gathered in
+  // that order into the (now free) attention scratch.
+  if (!st && logits) st = gather_rows(attn, h, rp.last.data(), requests, size_t(d) * e, decode_rows);
+  if (!st && logits)
+    st = gemm(blas, logits, attn, head_weight, nullptr, decode_rows + requests, vocab, d, 1, dtype, dtype);
   return st;
 }
 

@@ -117,7 +117,7 @@ def config4_lengths(rng, n):
 
 def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_rate=0.05,
                 precision='bf16', page_size=16, kv_pages=None, token_feedback=False, batch_prefills=True,
-                graph=False):
+                graph=False, merge_prefill=False):
     """Steady-state decode throughput; returns a dict of measurements.
 
     ``decode_tokens_per_sec`` times each step's decode: in the synchronous
@@ -130,7 +130,13 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
     the next step's input and are never read). With ``batch_prefills`` the
     requests replaced in a step are prefilled together
     (``DecoderLM.prefill_batch``), else one ``prefill`` call each; the random
-    draws, and so the replacements and prompts, are the same either way."""
+    draws, and so the replacements and prompts, are the same either way.
+    With ``merge_prefill`` (sync-free only) a step that replaces requests runs
+    its decode and the replacements' prefill as one layer loop
+    (``DecoderLM.decode_prefill_greedy``; the replaced requests' caches are
+    closed inside it, after the step's pages are taken): same replacements,
+    prompts and page IDs; only the loop's rate is reported, since the decode
+    step is no longer timed on its own."""
     dtype = {'fp16': 'float16', 'bf16': 'bfloat16', 'fp32': 'float32'}[precision]
     rng = np.random.default_rng([seed, 4])
     rt = runtime()
@@ -172,11 +178,33 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
             last += first
         decode_seconds, tokens, replaced, context, step_events = 0.0, 0, 0, [], []
         loop0 = None
+        if merge_prefill and not token_feedback:
+            raise ValueError('merge_prefill needs the sync-free loop (token_feedback=True)')
         for step in range(warmup + steps):
             context.append(sum(c.length + 1 for c in caches))
             if step == warmup:
                 rt.synchronize()
                 loop0 = time.perf_counter()
+            if merge_prefill:
+                # the replacements are drawn as after the step (the condition
+                # on the length counts the step's token), then run with it
+                slots, prompts = [], []
+                for i in range(len(caches)):
+                    if rng.random() < replace_rate or caches[i].length + 2 >= caches[i].capacity:
+                        slots.append(i)
+                        prompts.append(draw())
+                if slots:
+                    new = [model.create_kv_cache(1, model.n_positions, page_size=page_size, page_pool=pool)
+                           for _ in prompts]
+                    model.decode_prefill_greedy(caches, prompts, new, finished=[caches[i] for i in slots])
+                    for i, c in zip(slots, new):
+                        caches[i] = c
+                    replaced += len(slots)
+                else:
+                    model.decode_greedy(caches, graph=graph)
+                if step >= warmup:
+                    tokens += len(caches)
+                continue
             if token_feedback:
                 if step >= warmup:
                     # events around the decode step: its time on the device,
@@ -221,6 +249,7 @@ def run_config4(model, *, seed=0, concurrent=128, steps=40, warmup=5, replace_ra
             c.close()
         pool.close()
     return dict(token_feedback=token_feedback, graph=graph, batch_prefills=batch_prefills,
+                merge_prefill=merge_prefill,
                 decode_tokens_per_sec=tokens / decode_seconds if decode_seconds else None,
                 decode_seconds=decode_seconds, loop_tokens_per_sec=tokens / loop_seconds,
                 loop_seconds=loop_seconds, steps=steps, concurrent=concurrent,

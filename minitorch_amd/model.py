@@ -277,23 +277,7 @@ class DecoderLM:
         cache by cache in the given order, as consecutive ``prefill`` calls
         would. No reference counterpart (the reference prefills one request per
         call, minitorch/continuous_batching.py:164-170)."""
-        from .paged_kv_cache import PagedKVCache
-        caches = tuple(caches)
-        prompts = [np.asarray(p) for p in prompts]
-        if not caches or len(prompts) != len(caches) or len({id(c) for c in caches}) != len(caches):
-            raise ValueError('prefill_batch needs one prompt per distinct cache')
-        pool = getattr(caches[0], 'pool', None)
-        for cache, prompt in zip(caches, prompts):
-            if not isinstance(cache, PagedKVCache) or cache.pool is not pool or cache.batch_size != 1:
-                raise ValueError('prefill_batch requires paged caches of batch size 1 on one pool')
-            if prompt.ndim != 1 or prompt.size < 1 or prompt.dtype.kind not in 'iuf':
-                raise ValueError('Each prompt must be a nonempty 1-D array of token IDs')
-            cache._validate_model(self)
-            if cache.length != 0:
-                raise ValueError('prefill requires an empty cache')
-            if prompt.size > cache.capacity:
-                raise ValueError('KV cache capacity exceeded or empty prompt')
-        tokens = [int(p.size) for p in prompts]
+        caches, prompts, pool, tokens = self._check_prefill(prompts, caches, 'prefill_batch')
         dtype, d = caches[0].dtype, self.n_embd
         w = self._weights(dtype)
         prepared = []
@@ -310,9 +294,7 @@ class DecoderLM:
             lib = model_library()
             scratch_bytes = _scratch_bytes(lib, total, d, dtype)
             scratch = DeviceTensor(((scratch_bytes + 3) // 4,), 'float32')
-            att = (PrefillAttentionStruct * len(caches))(*[
-                PrefillAttentionStruct(pool.slab_table.ptr, c.block_table.ptr, c.page_size, pool.pages_per_slab,
-                                       pool.num_slabs, pool.max_cols, len(c.layout), 0) for c in caches])
+            att = _prefill_attention(pool, caches)
             counts = (I * len(caches))(*tokens)
             logits = DeviceTensor((len(caches), 1, self.n_vocab), dtype)
             call(lib, 'mt_prefill_layers_ragged',
@@ -330,6 +312,28 @@ class DecoderLM:
                 if cache._pending_tokens is not None:
                     cache.abort_append()
             raise
+
+    def _check_prefill(self, prompts, caches, name):
+        """Validated (caches, prompts, pool, token counts) of a batched
+        prefill: one nonempty 1-D prompt per distinct empty paged cache of
+        batch size 1, all on one pool, each within its cache's capacity."""
+        from .paged_kv_cache import PagedKVCache
+        caches = tuple(caches)
+        prompts = [np.asarray(p) for p in prompts]
+        if not caches or len(prompts) != len(caches) or len({id(c) for c in caches}) != len(caches):
+            raise ValueError(f'{name} needs one prompt per distinct cache')
+        pool = getattr(caches[0], 'pool', None)
+        for cache, prompt in zip(caches, prompts):
+            if not isinstance(cache, PagedKVCache) or cache.pool is not pool or cache.batch_size != 1:
+                raise ValueError(f'{name} requires paged caches of batch size 1 on one pool')
+            if prompt.ndim != 1 or prompt.size < 1 or prompt.dtype.kind not in 'iuf':
+                raise ValueError('Each prompt must be a nonempty 1-D array of token IDs')
+            cache._validate_model(self)
+            if cache.length != 0:
+                raise ValueError('prefill requires an empty cache')
+            if prompt.size > cache.capacity:
+                raise ValueError('KV cache capacity exceeded or empty prompt')
+        return caches, prompts, pool, [int(p.size) for p in prompts]
 
     def _cached_forward(self, idx, cache, prefill):
         cache.validate(self, idx, prefill)
@@ -395,6 +399,86 @@ class DecoderLM:
         if graph and idx is None:
             return self._decode_greedy_graph(caches)
         return self._decode_batch(idx, caches, greedy=True)
+
+    def decode_prefill_greedy(self, caches, prompts, new_caches, *, finished=()):
+        """One sync-free greedy decode step of ``caches`` (as ``decode_greedy``
+        with ``idx`` None) and the prefill of ``prompts`` into the empty caches
+        ``new_caches`` (one each, as ``prefill_batch``), run as one native
+        layer loop (``mt_mixed_layers``): the projections cover both sets of
+        rows at once. ``finished`` names caches of ``caches`` whose requests end
+        with this step: they are closed once the step's pages are taken and its
+        lengths committed, and before ``new_caches`` take their pages, which is
+        the order of ``decode_greedy``, then closing them, then
+        ``prefill_batch`` -- page IDs, tables and the free list come out the
+        same. Returns the greedy token IDs [len(caches) + len(prompts), 1] fp32
+        on the device (the decode rows, then each prompt's first token), which
+        also become each cache's last token for the next step. Nothing waits
+        for the device. No reference counterpart (the reference runs a step's
+        decode batch and its prefills as separate forward passes,
+        minitorch/continuous_batching.py:140-176)."""
+        from .paged_decode import PagedDecodeBatch
+        new_caches, prompts, pool, tokens = self._check_prefill(prompts, new_caches, 'decode_prefill_greedy')
+        caches = tuple(caches)
+        ids_of = {id(c) for c in caches}
+        if any(id(c) not in ids_of for c in finished) or ids_of & {id(c) for c in new_caches}:
+            raise ValueError('finished caches must be decoded in the step and new caches must not')
+        if caches and caches[0].pool is not pool:
+            raise ValueError('decode_prefill_greedy requires the decode and new caches on one pool')
+        with PagedDecodeBatch(self, None, caches) as batch:
+            batch.prepare()
+            b, dtype, d = batch.batch_size, batch.dtype, self.n_embd
+            w = self._weights(dtype)
+            datt = batch.attention_metadata()
+            slots, positions = batch.device_slots, batch.position_ids
+            # the decode half's lengths are committed before any page changes
+            # hands; its kernels read the step's own table and offsets
+            batch.mark_layers_written()
+            batch.commit()
+        for cache in finished:
+            cache.close()
+        prepared = []
+        try:
+            for cache, n in zip(new_caches, tokens):
+                cache.prepare_append(n)
+                prepared.append(cache)
+            total, r = sum(tokens), len(new_caches)
+            x = DeviceTensor((b + total, d), 'float32')
+            paged_ops.embed_tokens(x.ptr, w.wte.ptr, w.wpe.ptr, None, positions.ptr, b, self.n_vocab,
+                                   self.n_positions, d, slot_tokens=pool.slot_tokens.ptr, slots=slots.ptr,
+                                   num_slots=pool.max_slots)
+            ids = DeviceTensor.from_numpy(np.concatenate(prompts).astype(np.float32), 'float32')
+            prompt_positions = DeviceTensor.from_numpy(
+                np.concatenate([np.arange(n, dtype=np.float32) for n in tokens]), 'float32')
+            paged_ops.embed_tokens(x.ptr + 4 * b * d, w.wte.ptr, w.wpe.ptr, ids.ptr, prompt_positions.ptr, total,
+                                   self.n_vocab, self.n_positions, d)
+            h = DeviceTensor((b + total, d), dtype)
+            lib = model_library()
+            scratch_bytes = _scratch_bytes(lib, b + total, d, dtype)
+            scratch = DeviceTensor(((scratch_bytes + 3) // 4,), 'float32')
+            logits = DeviceTensor((b + r, 1, self.n_vocab), dtype)
+            call(lib, 'mt_mixed_layers',
+                 [P, P, I, P, P, P, P, P, P, I, I, I, P, I, I, F, I, I, P, ct.c_size_t, P, P],
+                 self.blas().handle, w.layer_array, self.n_layer, x.ptr, h.ptr, w.ln_f[0].ptr, w.ln_f[1].ptr,
+                 w.head.ptr, logits.ptr, self.n_vocab, b, r, (I * r)(*tokens), d, self.n_head, self.ln_eps,
+                 dtype_code(dtype), 1 if FUSED_GELU else 0, scratch.ptr, scratch_bytes, ct.byref(datt),
+                 _prefill_attention(pool, new_caches))
+            out = DeviceTensor((b + r, 1), 'float32')
+            new_slots = DeviceTensor.from_numpy(np.array([c.slot for c in new_caches], np.int32), 'int32')
+            row_bytes = self.n_vocab * (logits.nbytes // logits.size)
+            paged_ops.row_argmax_feedback(out.ptr, pool.slot_tokens.ptr, slots.ptr, pool.max_slots, logits.ptr, b,
+                                          self.n_vocab, dtype)
+            paged_ops.row_argmax_feedback(out.ptr + 4 * b, pool.slot_tokens.ptr, new_slots.ptr, pool.max_slots,
+                                          logits.ptr + b * row_bytes, r, self.n_vocab, dtype)
+            for cache in new_caches:
+                cache._written_layers.update(range(len(cache.layout)))
+                cache.last_attention_path = 'paged_prefill'
+                cache.commit_append()
+            return out
+        except Exception:
+            for cache in prepared:
+                if cache._pending_tokens is not None:
+                    cache.abort_append()
+            raise
 
     def _decode_greedy_graph(self, caches):
         from .paged_decode import PagedDecodeBatch
@@ -529,6 +613,13 @@ class _StepBuffers:
         self.scratch = DeviceTensor(((self.scratch_bytes + 3) // 4,), 'float32')
         self.logits = DeviceTensor((b, 1, n_vocab), dtype)
         self.ids = DeviceTensor((b, 1), 'float32')
+
+
+def _prefill_attention(pool, caches):
+    """``mt_prefill_attention`` of each empty cache (offset 0), as a ctypes array."""
+    return (PrefillAttentionStruct * len(caches))(*[
+        PrefillAttentionStruct(pool.slab_table.ptr, c.block_table.ptr, c.page_size, pool.pages_per_slab,
+                               pool.num_slabs, pool.max_cols, len(c.layout), 0) for c in caches])
 
 
 def _scratch_bytes(lib, rows, d, dtype):
