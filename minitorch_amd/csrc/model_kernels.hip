@@ -19,6 +19,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 #include <vector>
 
 using namespace mt;
@@ -387,42 +388,50 @@ __host__ __device__ __forceinline__ int64_t tiled_offset(int row, int col, int w
 // every 256-column block j. All loads of a row (x, y, gamma, beta) are issued
 // at once and the row stays in registers, so the kernel makes one dependent
 // memory round trip and reduces within the wave (no LDS, no barrier).
-// XOR-butterfly sums leave every lane with the row total.
-template <int DT, int NJ>
-__global__ __launch_bounds__(256) void residual_layernorm_wave_kernel(void* out, float* x, const void* y,
-                                                                      const float* gamma,
-                                                                      const float* beta, int rows,
-                                                                      int width, float eps,
-                                                                      int has_residual, int out_tiled) {
+// XOR-butterfly sums leave every lane with the row total. Blocks past the
+// row's last (j >= width / 256) repeat the last one and add nothing to the
+// sums, so that the code has no branch on the width (a branch made the
+// compiler wait for the residual stores before the output stores).
+template <int DT, int NJ, bool RES>
+__global__ __launch_bounds__(256) void residual_layernorm_wave_kernel(void* __restrict__ out, float* __restrict__ x,
+                                                                      const void* __restrict__ y,
+                                                                      const float* __restrict__ gamma,
+                                                                      const float* __restrict__ beta, int rows,
+                                                                      int width, float eps, int out_tiled) {
   using T = typename Elem<DT>::T;
+  using R = typename std::conditional<DT == kF32, float4, uint2>::type;  // 4 elements of y
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
   if (row >= rows) return;
   const int nj = width >> 8;
   float* xr = x + int64_t(row) * width;
   const T* yr = static_cast<const T*>(y) + int64_t(row) * width;
+  int col[NJ];
   float4 v[NJ], g[NJ], b[NJ];
+  R r[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    col[j] = 256 * (j < nj ? j : nj - 1) + 4 * lane;
+    v[j] = *reinterpret_cast<const float4*>(xr + col[j]);
+    g[j] = *reinterpret_cast<const float4*>(gamma + col[j]);
+    b[j] = *reinterpret_cast<const float4*>(beta + col[j]);
+    if constexpr (RES) r[j] = *reinterpret_cast<const R*>(yr + col[j]);
+  }
   float sum = 0.f, sq = 0.f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    if (j >= nj) break;
-    const int c = 256 * j + 4 * lane;
-    v[j] = *reinterpret_cast<const float4*>(xr + c);
-    g[j] = *reinterpret_cast<const float4*>(gamma + c);
-    b[j] = *reinterpret_cast<const float4*>(beta + c);
-    if (has_residual) {
+    if constexpr (RES) {
       if constexpr (DT == kF32) {
-        const float4 r = *reinterpret_cast<const float4*>(yr + c);
-        v[j].x += r.x; v[j].y += r.y; v[j].z += r.z; v[j].w += r.w;
+        v[j].x += r[j].x; v[j].y += r[j].y; v[j].z += r[j].z; v[j].w += r[j].w;
       } else {
-        const uint2 r = *reinterpret_cast<const uint2*>(yr + c);
-        v[j].x += to_f32<DT>(T(r.x & 0xffffu)); v[j].y += to_f32<DT>(T(r.x >> 16));
-        v[j].z += to_f32<DT>(T(r.y & 0xffffu)); v[j].w += to_f32<DT>(T(r.y >> 16));
+        v[j].x += to_f32<DT>(T(r[j].x & 0xffffu)); v[j].y += to_f32<DT>(T(r[j].x >> 16));
+        v[j].z += to_f32<DT>(T(r[j].y & 0xffffu)); v[j].w += to_f32<DT>(T(r[j].y >> 16));
       }
-      *reinterpret_cast<float4*>(xr + c) = v[j];
+      *reinterpret_cast<float4*>(xr + col[j]) = v[j];  // a repeated block stores the same values again
     }
-    sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-    sq += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+    const float keep = j < nj ? 1.f : 0.f;
+    sum += keep * ((v[j].x + v[j].y) + (v[j].z + v[j].w));
+    sq += keep * ((v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w));
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
@@ -435,8 +444,7 @@ __global__ __launch_bounds__(256) void residual_layernorm_wave_kernel(void* out,
   T* o = static_cast<T*>(out);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    if (j >= nj) break;
-    const int c = 256 * j + 4 * lane;
+    const int c = col[j];
     const int64_t at = out_tiled ? tiled_offset(row, c, width) : int64_t(row) * width + c;
     const float r0 = g[j].x * ((v[j].x - mean) * inv) + b[j].x;
     const float r1 = g[j].y * ((v[j].y - mean) * inv) + b[j].y;
@@ -765,11 +773,16 @@ __global__ __launch_bounds__(1024) void projection_kernel(ProjArgs p) {
 // partials, which other XCDs wrote, gamma and beta) is issued before the
 // first add, so the kernel waits for one memory round trip (loading gamma and
 // beta after the reduction made GPT-2-medium decode steps 2-4 % slower).
+// Blocks past the row's last repeat it and add nothing to the sums, and a
+// missing bias is read from gamma and zeroed, so that no branch makes the
+// output stores wait for the residual stores.
 template <int DT, int NJ, int S>
-__global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* out, float* x, const float* part,
-                                                                          const void* bias, const float* gamma,
-                                                                          const float* beta, int rows, int width,
-                                                                          float eps, int out_tiled) {
+__global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* __restrict__ out, float* __restrict__ x,
+                                                                          const float* __restrict__ part,
+                                                                          const void* __restrict__ bias,
+                                                                          const float* __restrict__ gamma,
+                                                                          const float* __restrict__ beta, int rows,
+                                                                          int width, float eps, int out_tiled) {
   using T = typename Elem<DT>::T;
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
@@ -778,34 +791,36 @@ __global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* 
   float* xr = x + int64_t(row) * width;
   const int64_t split_stride = int64_t(rows) * width;
   const float* pr = part + int64_t(row) * width;
+  const bool has_bias = bias != nullptr;
+  const T* bp = has_bias ? static_cast<const T*>(bias) : reinterpret_cast<const T*>(gamma);
+  int col[NJ];
   float4 v[NJ], q[NJ][S], gm[NJ], bt[NJ];
   uint2 b[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    if (j < nj) {
-      const int c = 256 * j + 4 * lane;
-      v[j] = *reinterpret_cast<const float4*>(xr + c);
-      b[j] = bias ? *reinterpret_cast<const uint2*>(static_cast<const T*>(bias) + c) : uint2{0u, 0u};
+    col[j] = 256 * (j < nj ? j : nj - 1) + 4 * lane;
+    const int c = col[j];
+    v[j] = *reinterpret_cast<const float4*>(xr + c);
+    b[j] = *reinterpret_cast<const uint2*>(bp + c);
 #pragma unroll
-      for (int s = 0; s < S; ++s) q[j][s] = *reinterpret_cast<const float4*>(pr + s * split_stride + c);
-      gm[j] = *reinterpret_cast<const float4*>(gamma + c);
-      bt[j] = *reinterpret_cast<const float4*>(beta + c);
-    }
+    for (int s = 0; s < S; ++s) q[j][s] = *reinterpret_cast<const float4*>(pr + s * split_stride + c);
+    gm[j] = *reinterpret_cast<const float4*>(gamma + c);
+    bt[j] = *reinterpret_cast<const float4*>(beta + c);
   }
   float sum = 0.f, sq = 0.f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    if (j >= nj) break;
-    const int c = 256 * j + 4 * lane;
-    v[j].x += to_f32<DT>(T(b[j].x & 0xffffu)); v[j].y += to_f32<DT>(T(b[j].x >> 16));
-    v[j].z += to_f32<DT>(T(b[j].y & 0xffffu)); v[j].w += to_f32<DT>(T(b[j].y >> 16));
+    const uint2 bj = has_bias ? b[j] : uint2{0u, 0u};
+    v[j].x += to_f32<DT>(T(bj.x & 0xffffu)); v[j].y += to_f32<DT>(T(bj.x >> 16));
+    v[j].z += to_f32<DT>(T(bj.y & 0xffffu)); v[j].w += to_f32<DT>(T(bj.y >> 16));
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       v[j].x += q[j][s].x; v[j].y += q[j][s].y; v[j].z += q[j][s].z; v[j].w += q[j][s].w;
     }
-    *reinterpret_cast<float4*>(xr + c) = v[j];
-    sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-    sq += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+    *reinterpret_cast<float4*>(xr + col[j]) = v[j];  // a repeated block stores the same values again
+    const float keep = j < nj ? 1.f : 0.f;
+    sum += keep * ((v[j].x + v[j].y) + (v[j].z + v[j].w));
+    sq += keep * ((v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w));
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
@@ -818,14 +833,13 @@ __global__ __launch_bounds__(256) void residual_layernorm_partials_kernel(void* 
   T* o = static_cast<T*>(out);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    if (j >= nj) break;
-    const int c = 256 * j + 4 * lane;
+    const int c = col[j];
     const int64_t at = out_tiled ? tiled_offset(row, c, width) : int64_t(row) * width + c;
-    const float4 g = gm[j], b = bt[j];
-    const float r0 = g.x * ((v[j].x - mean) * inv) + b.x;
-    const float r1 = g.y * ((v[j].y - mean) * inv) + b.y;
-    const float r2 = g.z * ((v[j].z - mean) * inv) + b.z;
-    const float r3 = g.w * ((v[j].w - mean) * inv) + b.w;
+    const float4 g = gm[j], bb = bt[j];
+    const float r0 = g.x * ((v[j].x - mean) * inv) + bb.x;
+    const float r1 = g.y * ((v[j].y - mean) * inv) + bb.y;
+    const float r2 = g.z * ((v[j].z - mean) * inv) + bb.z;
+    const float r3 = g.w * ((v[j].w - mean) * inv) + bb.w;
     *reinterpret_cast<uint2*>(o + at) =
         uint2{uint32_t(from_f32<DT>(r0)) | (uint32_t(from_f32<DT>(r1)) << 16),
               uint32_t(from_f32<DT>(r2)) | (uint32_t(from_f32<DT>(r3)) << 16)};
@@ -1158,17 +1172,27 @@ bool wave_rows(const void* out, const float* x, const void* y, const float* gamm
          (dtype == kF32 ? a16(out) : (reinterpret_cast<uintptr_t>(out) & 7u) == 0);
 }
 
+// Blocks of 256 columns a lane carries: exactly the width's for 768 and 1024
+// (DistilGPT-2, GPT-2-medium), else 3 or 8 (repeated blocks past the width).
+template <int DT, bool RES>
+void launch_wave_rows_res(int blocks, int threads, void* out, float* x, const void* y, const float* gamma,
+                          const float* beta, int rows, int width, float eps, int tiled) {
+  const int nj = width >> 8;
+  if (nj <= 3)
+    residual_layernorm_wave_kernel<DT, 3, RES><<<blocks, threads>>>(out, x, y, gamma, beta, rows, width, eps, tiled);
+  else if (nj == 4)
+    residual_layernorm_wave_kernel<DT, 4, RES><<<blocks, threads>>>(out, x, y, gamma, beta, rows, width, eps, tiled);
+  else
+    residual_layernorm_wave_kernel<DT, 8, RES><<<blocks, threads>>>(out, x, y, gamma, beta, rows, width, eps, tiled);
+}
+
 template <int DT>
 void launch_wave_rows(void* out, float* x, const void* y, const float* gamma, const float* beta,
                       int rows, int width, float eps, int tiled) {
   constexpr int R = kLnRowsPerBlock;  // one wave per row
   const int blocks = (rows + R - 1) / R;
-  if (width <= 1024)
-    residual_layernorm_wave_kernel<DT, 4>
-        <<<blocks, 64 * R>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr, tiled);
-  else
-    residual_layernorm_wave_kernel<DT, 8>
-        <<<blocks, 64 * R>>>(out, x, y, gamma, beta, rows, width, eps, y != nullptr, tiled);
+  if (y) launch_wave_rows_res<DT, true>(blocks, 64 * R, out, x, y, gamma, beta, rows, width, eps, tiled);
+  else launch_wave_rows_res<DT, false>(blocks, 64 * R, out, x, y, gamma, beta, rows, width, eps, tiled);
 }
 
 // tiled: out in the fragment-tiled layout (fp16/bf16, rows that the
