@@ -65,6 +65,15 @@ int mt_pool_push(MT_POOL_ARGS, const int* pages, int count, int owner);
  * (minitorch/paged_kv_cache.py:171-186). */
 int mt_pool_acquire_rows(MT_POOL_ARGS, const int* slots, int rows, int per_row, int* scratch);
 
+/* prepare_append of n one-row caches in order: for i = 0..n-1, one pop of
+ * counts[i] (device int32 [n]; host-checked against the budget and the
+ * slot's columns) pages appended to slot slots[i]'s page list, the pops
+ * opening slabs exactly as n mt_pool_acquire_rows calls of one row would
+ * (scratch: device int32 [max counts[i]]). Replaces the page part of n
+ * consecutive reference PagedKVCache.prepare_append calls
+ * (minitorch/paged_kv_cache.py:171-186) with one launch. */
+int mt_pool_acquire_lists(MT_POOL_ARGS, const int* slots, const int* counts, int n, int* scratch);
+
 /* Release the pages [keep:] of each row slots[0..rows), row by row; with
  * reset_length the rows' lengths become 0. keep = 0 replaces reference
  * _release_cache / PagedKVCache.close (minitorch/paged_kv_cache.py:125-131);
@@ -85,6 +94,11 @@ int mt_sched_decode_prepare(MT_POOL_ARGS, const int* slots, int b, int columns, 
 /* lengths[slots[i]] += tokens. Replaces the length update of reference
  * CacheBase.commit_append (minitorch/kv_cache.py:142-147). */
 int mt_sched_add_length(MT_POOL_ARGS, const int* slots, int b, int tokens);
+
+/* lengths[slots[i]] += tokens[i] for i < n (device int32 arrays): the length
+ * update of n reference CacheBase.commit_append calls
+ * (minitorch/kv_cache.py:142-147) with one launch. */
+int mt_sched_add_lengths(MT_POOL_ARGS, const int* slots, const int* tokens, int n);
 
 /* Return the pages taken by mt_sched_decode_prepare (new_page >= 0), in row
  * order. Replaces reference PagedDecodeBatch.__exit__'s aborts

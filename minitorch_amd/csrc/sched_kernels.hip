@@ -227,6 +227,27 @@ __global__ __launch_bounds__(kThreads) void acquire_rows_kernel(Pool p, const in
   for (int row = threadIdx.x; row < rows; row += blockDim.x) p.slot_npages[slots[row]] += per_row;
 }
 
+// prepare_append of n one-row caches in order, as n acquire_rows_kernel
+// launches of one row would run: for i = 0..n-1 one bulk pop of counts[i]
+// pages (owner slots[i]) appended to slot i's page list.
+__global__ __launch_bounds__(kThreads) void acquire_lists_kernel(Pool p, const int* slots, const int* counts, int n,
+                                                                 int* scratch) {
+  __shared__ int s_red;
+  if (threadIdx.x == 0) s_red = 0;
+  __syncthreads();
+  for (int i = 0; i < n; ++i) {
+    const int slot = slots[i], count = counts[i];
+    if (count <= 0) continue;
+    bulk_pop(p, count, slot, scratch, &s_red);
+    const int have = p.slot_npages[slot];
+    for (int r = threadIdx.x; r < count; r += blockDim.x)
+      p.slot_pages[int64_t(slot) * p.max_cols + have + r] = scratch[r];
+    __syncthreads();  // every thread has read `have` and its scratch entries
+    if (threadIdx.x == 0) p.slot_npages[slot] = have + count;
+    __syncthreads();
+  }
+}
+
 // Release the pages [keep:] of each row slots[0..rows), row by row, in page
 // order (close: keep = 0; abort of an append: keep = the count before it).
 __global__ __launch_bounds__(kThreads) void release_rows_kernel(Pool p, const int* slots, int rows,
@@ -375,6 +396,12 @@ __global__ __launch_bounds__(kThreads) void add_length_kernel(Pool p, const int*
     p.slot_len[slots[i]] += tokens;
 }
 
+// Commit of n one-row caches: lengths[slots[i]] += tokens[i].
+__global__ __launch_bounds__(kThreads) void add_lengths_kernel(Pool p, const int* slots, const int* tokens, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    p.slot_len[slots[i]] += tokens[i];
+}
+
 // Abort of a decode step: push back the pages popped by decode_prepare_kernel,
 // in row order (the reference aborts every prepared cache in batch order).
 __global__ __launch_bounds__(kThreads) void decode_abort_kernel(Pool p, const int* slots, int b,
@@ -457,6 +484,20 @@ int mt_pool_acquire_rows(MT_POOL_ARGS, const int* slots, int rows, int per_row, 
       (per_row > 0 && !scratch))
     return hipErrorInvalidValue;
   if (per_row) acquire_rows_kernel<<<1, kThreads>>>(MT_POOL, slots, rows, per_row, scratch);
+  return hipGetLastError();
+}
+
+int mt_pool_acquire_lists(MT_POOL_ARGS, const int* slots, const int* counts, int n, int* scratch) {
+  MT_POOL_CHECK
+  if (!slots || !counts || n < 1 || !scratch) return hipErrorInvalidValue;
+  acquire_lists_kernel<<<1, kThreads>>>(MT_POOL, slots, counts, n, scratch);
+  return hipGetLastError();
+}
+
+int mt_sched_add_lengths(MT_POOL_ARGS, const int* slots, const int* tokens, int n) {
+  MT_POOL_CHECK
+  if (!slots || !tokens || n < 1) return hipErrorInvalidValue;
+  add_lengths_kernel<<<(n + kThreads - 1) / kThreads, kThreads>>>(MT_POOL, slots, tokens, n);
   return hipGetLastError();
 }
 

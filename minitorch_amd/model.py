@@ -434,22 +434,31 @@ class DecoderLM:
             # hands; its kernels read the step's own table and offsets
             batch.mark_layers_written()
             batch.commit()
-        for cache in finished:
-            cache.close()
+        pool.close_caches(finished)
+        total, r = sum(tokens), len(new_caches)
+        # one upload: the new caches' slots, page counts and tokens
+        # (append_lists), then the prompts' token IDs and positions (fp32)
+        lists = pool.append_lists(new_caches, tokens)
+        blob = DeviceTensor.from_numpy(np.concatenate([
+            np.array(lists, np.int32), np.concatenate(prompts).astype(np.float32).view(np.int32),
+            np.concatenate([np.arange(n, dtype=np.float32) for n in tokens]).view(np.int32)]), 'int32')
+        new_slots, prompt_ids, prompt_positions = blob.ptr, blob.ptr + 12 * r, blob.ptr + 12 * r + 4 * total
         prepared = []
         try:
-            for cache, n in zip(new_caches, tokens):
-                cache.prepare_append(n)
-                prepared.append(cache)
-            total, r = sum(tokens), len(new_caches)
+            try:
+                pool.prepare_appends(new_caches, tokens, blob.ptr)
+                prepared = list(new_caches)
+            except MemoryError:
+                # past the budget together: one by one, failing where the
+                # consecutive prefills would
+                for cache, n in zip(new_caches, tokens):
+                    cache.prepare_append(n)
+                    prepared.append(cache)
             x = DeviceTensor((b + total, d), 'float32')
             paged_ops.embed_tokens(x.ptr, w.wte.ptr, w.wpe.ptr, None, positions.ptr, b, self.n_vocab,
                                    self.n_positions, d, slot_tokens=pool.slot_tokens.ptr, slots=slots.ptr,
                                    num_slots=pool.max_slots)
-            ids = DeviceTensor.from_numpy(np.concatenate(prompts).astype(np.float32), 'float32')
-            prompt_positions = DeviceTensor.from_numpy(
-                np.concatenate([np.arange(n, dtype=np.float32) for n in tokens]), 'float32')
-            paged_ops.embed_tokens(x.ptr + 4 * b * d, w.wte.ptr, w.wpe.ptr, ids.ptr, prompt_positions.ptr, total,
+            paged_ops.embed_tokens(x.ptr + 4 * b * d, w.wte.ptr, w.wpe.ptr, prompt_ids, prompt_positions, total,
                                    self.n_vocab, self.n_positions, d)
             h = DeviceTensor((b + total, d), dtype)
             lib = model_library()
@@ -463,16 +472,15 @@ class DecoderLM:
                  dtype_code(dtype), 1 if FUSED_GELU else 0, scratch.ptr, scratch_bytes, ct.byref(datt),
                  _prefill_attention(pool, new_caches))
             out = DeviceTensor((b + r, 1), 'float32')
-            new_slots = DeviceTensor.from_numpy(np.array([c.slot for c in new_caches], np.int32), 'int32')
             row_bytes = self.n_vocab * (logits.nbytes // logits.size)
             paged_ops.row_argmax_feedback(out.ptr, pool.slot_tokens.ptr, slots.ptr, pool.max_slots, logits.ptr, b,
                                           self.n_vocab, dtype)
-            paged_ops.row_argmax_feedback(out.ptr + 4 * b, pool.slot_tokens.ptr, new_slots.ptr, pool.max_slots,
+            paged_ops.row_argmax_feedback(out.ptr + 4 * b, pool.slot_tokens.ptr, new_slots, pool.max_slots,
                                           logits.ptr + b * row_bytes, r, self.n_vocab, dtype)
             for cache in new_caches:
                 cache._written_layers.update(range(len(cache.layout)))
                 cache.last_attention_path = 'paged_prefill'
-                cache.commit_append()
+            pool.commit_appends(new_caches, blob.ptr)
             return out
         except Exception:
             for cache in prepared:

@@ -180,6 +180,78 @@ class KVPagePool:
     def used_pages(self):
         return self._leased_count
 
+    # ------------------------------------- several one-row caches at once ---
+    def close_caches(self, caches):
+        """``close()`` of one-row caches of this pool, in order, with one
+        release launch: pages are pushed cache by cache in page order, as
+        consecutive ``close()`` calls push them."""
+        caches = [c for c in caches if not c.closed]
+        if len(caches) < 2 or any(c.pool is not self or c.batch_size != 1 or c._owns_pool for c in caches):
+            for c in caches:
+                c.close()
+            return
+        for c in caches:
+            c.abort_append()
+        slots = DeviceTensor.from_numpy(np.array([c.slot for c in caches], np.int32), 'int32')
+        self._call('mt_pool_release_rows', [P, I, I, I], slots.ptr, len(caches), 0, 1)
+        for c in caches:
+            counts = self._row_counts.pop(c.slot, None) or []
+            self._mirror_release(sum(counts))
+            for i in range(len(counts)):
+                counts[i] = 0
+            self._free_slots(c.slot, 1)
+            c._release.detach()
+            c.closed, c.valid, c.length = True, False, 0
+
+    def append_lists(self, caches, tokens):
+        """Host int32 lists for ``prepare_appends`` and ``commit_appends`` of
+        one-row caches before their appends: the caches' slots, the pages each
+        append takes, the tokens."""
+        slots = [c.slot for c in caches]
+        counts = [(c.length + int(n) + c.page_size - 1) // c.page_size - c._counts[0] for c, n in zip(caches, tokens)]
+        return slots + counts + [int(n) for n in tokens]
+
+    def prepare_appends(self, caches, tokens, device_lists):
+        """``prepare_append(tokens[i])`` of one-row caches of this pool, in
+        order, with one launch (``mt_pool_acquire_lists``): the same pages as
+        consecutive calls. ``device_lists``: device address of
+        ``append_lists(caches, tokens)`` (int32), uploaded by the caller. When
+        the appends together exceed the page budget nothing is prepared and
+        MemoryError is raised (consecutive calls would have prepared the
+        caches before the one that fails)."""
+        lists = self.append_lists(caches, tokens)
+        n = len(caches)
+        counts = lists[n:2 * n]
+        if sum(counts) > self.max_pages - self._leased_count:
+            raise MemoryError('KV page budget exhausted')
+        prepared = []
+        try:
+            for c, t in zip(caches, tokens):
+                CacheBase.prepare_append(c, int(t))
+                prepared.append(c)
+                c._previous_counts = list(c._counts)
+        except Exception:
+            for c in prepared:
+                c.abort_append()
+            raise
+        if sum(counts):
+            self._call('mt_pool_acquire_lists', [P, P, I, P], device_lists, device_lists + 4 * n, n,
+                       self._scratch.ptr)
+        for c, k in zip(caches, counts):
+            if k:
+                self._mirror_bulk_pop(k)
+                c._counts[0] += k
+            c._new_count = k
+
+    def commit_appends(self, caches, device_lists):
+        """``commit_append()`` of prepared one-row caches with one length
+        launch (``mt_sched_add_lengths``); ``device_lists`` as
+        ``prepare_appends`` takes it, followed by the tokens."""
+        n = len(caches)
+        for c in caches:
+            c.commit_append(device=False)
+        self._call('mt_sched_add_lengths', [P, P, I], device_lists, device_lists + 8 * n, n)
+
     # ------------------------------------------------------------ slots ---
     def _alloc_slots(self, n):
         first = self._slot_used.find(b'\x00' * n)

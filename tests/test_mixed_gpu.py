@@ -140,3 +140,41 @@ def test_mixed_step_argument_checks():
     for c in other:
         c.close()
     w.close()
+
+
+def test_mixed_step_budget_exhaustion_like_separate_calls():
+    # the prompts together need more pages than the budget holds: both paths
+    # raise MemoryError with the decode step committed, the ending caches
+    # closed, no new cache left holding pages, and the same pool state
+    model = tiny(seed=5)
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, model.n_vocab, 40) for _ in range(3)]
+
+    def world():
+        w = World.__new__(World)
+        w.model = model
+        w.pool = KVPagePool(model, page_size=16, max_bytes=14 * 2 * model.n_layer * model.n_embd * 16 * 4,
+                            pages_per_slab=2)
+        w.caches = w.new_caches(len(prompts))
+        w.tokens = greedy_token(model.prefill_batch(prompts, w.caches), feedback=list(w.caches))
+        return w
+
+    a, b = world(), world()
+    big = [rng.integers(0, model.n_vocab, n) for n in (30, 60, 40)]   # 2 + 4 + 3 pages
+    ids = a.model.decode_greedy(a.caches)
+    a.caches[1].close()
+    new_a = a.new_caches(3)
+    with pytest.raises(MemoryError):
+        a.model.prefill_batch(big, new_a)
+    new_b = b.new_caches(3)
+    with pytest.raises(MemoryError):
+        b.model.decode_prefill_greedy(b.caches, big, new_b, finished=[b.caches[1]])
+    runtime().synchronize()
+    a._advance([1], [])
+    b._advance([1], [])
+    assert_same_pools(a, b)
+    assert [c.length for c in new_a] == [c.length for c in new_b] == [0, 0, 0]
+    for c in new_a + new_b:
+        c.close()
+    a.close()
+    b.close()
