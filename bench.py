@@ -592,6 +592,10 @@ def e2e_config3(args, loops=('sync', 'sync-free')):
         # and with each decode step replayed from a HIP graph (one per batch size)
         e2e.run_config3(model, warm, precision='fp16', token_feedback=True, graph=True, report_every=0)
         r['graph'] = e2e.run_config3(model, trace, precision='fp16', token_feedback=True, graph=True)
+        # graph replay of decode-only steps, and steps that admit run decode
+        # and prefill as one layer loop
+        r['merged'] = e2e.run_config3(model, trace, precision='fp16', token_feedback=True, graph=True,
+                                      merge_prefill=True)
     if not args.no_cpu_baseline:
         # the trace's mean decode batch, mid-generation contexts of its first requests
         batch = max(1, int(round((r.get('sync_free') or r).get('mean_decode_batch_size', 2))))
@@ -621,6 +625,7 @@ def e2e_config4(args, loops=('sync', 'sync-free')):
         r['sync_free'] = e2e.run_config4(model, **kw, token_feedback=True)
         # the sync-free loop with each decode step replayed from a HIP graph
         r['graph'] = e2e.run_config4(model, **kw, token_feedback=True, graph=True)
+    if 'sync-free' in loops or 'merged' in loops:
         # the sync-free loop with each step's decode and replacement prefills
         # in one layer loop
         r['merged'] = e2e.run_config4(model, **kw, token_feedback=True, merge_prefill=True)
@@ -676,13 +681,16 @@ def config1_times(args):
 
 def bench_e2e(args):
     if args.config == 3:
+        if args.loop == 'merged':
+            raise SystemExit('--loop merged applies to config 4')
         loops = ('sync', 'sync-free') if args.loop == 'both' else (args.loop,)
         r = e2e_config3(args, loops)
         value, dtype = (r.get('busy_decode_tokens_per_sec') or r.get('sync_free', {}).get('busy_step_tokens_per_sec')), 'f16'
     else:
         loops = ('sync', 'sync-free') if args.loop == 'both' else (args.loop,)
         r = e2e_config4(args, loops)
-        value = r.get('decode_tokens_per_sec') or r.get('sync_free', {}).get('loop_tokens_per_sec')
+        value = (r.get('decode_tokens_per_sec') or r.get('sync_free', {}).get('loop_tokens_per_sec') or
+                 r.get('merged', {}).get('loop_tokens_per_sec'))
         dtype = 'f16' if args.model == 'distilgpt2' else 'bf16'
     return {'metric': 'decode tokens/s (1 GPU), end to end', 'value': value, 'unit': 'tokens/s',
             'n_gpus': 1, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
@@ -695,7 +703,7 @@ def e2e_summary(r3, r4):
     """The end-to-end figures of configs 3 and 4 for the default line."""
     out = {}
     if r3 is not None:
-        sf, gr = r3.get('sync_free', {}), r3.get('graph', {})
+        sf, gr, mg = r3.get('sync_free', {}), r3.get('graph', {}), r3.get('merged', {})
         out['config3'] = dict(
             workload=r3['workload'],
             decode_tokens_per_sec_reference_formula=r3.get('output_tokens_per_sec'),
@@ -707,6 +715,10 @@ def e2e_summary(r3, r4):
             graph=dict(decode_tokens_per_sec_reference_formula=gr.get('output_tokens_per_sec'),
                        busy_step_decode_tokens_per_sec=gr.get('busy_step_tokens_per_sec'),
                        ttft_p50_ms=gr.get('ttft_p50_ms'), completed=gr.get('completed')) if gr else None,
+            merged=dict(decode_tokens_per_sec_reference_formula=mg.get('output_tokens_per_sec'),
+                        busy_step_decode_tokens_per_sec=mg.get('busy_step_tokens_per_sec'),
+                        ttft_p50_ms=mg.get('ttft_p50_ms'), completed=mg.get('completed'),
+                        kv_pool_used_pages_after=mg.get('kv_pool_used_pages_after')) if mg else None,
             elapsed_seconds=r3.get('elapsed_seconds'), generated_tokens=r3.get('generated_tokens'),
             completed=r3.get('completed'), mean_decode_batch_size=r3.get('mean_decode_batch_size'),
             ttft_p50_ms=r3.get('ttft_p50_ms'), ttft_p95_ms=r3.get('ttft_p95_ms'),
@@ -756,8 +768,10 @@ def main():
     ap.add_argument('--config', type=int, default=2, choices=(2, 3, 4, 5),
                     help='2: op-level decode (default, the headline line); 5: ragged op-level '
                          'decode, bf16, H=25, P=16 and 32; 3 / 4: end-to-end decode')
-    ap.add_argument('--loop', choices=('both', 'sync', 'sync-free'), default='both',
-                    help='configs 3/4: the synchronous loop, the sync-free one, or both')
+    ap.add_argument('--loop', choices=('both', 'sync', 'sync-free', 'merged'), default='both',
+                    help='configs 3/4: the synchronous loop, the sync-free one (for config 4 with its graph '
+                         'and merged variants), or both; config 4 merged: only the loop whose steps run '
+                         'decode and replacement prefills in one layer loop')
     ap.add_argument('--prefill-each', action='store_true',
                     help='config 4: one prefill call per replaced request instead of one batched call per step')
     ap.add_argument('--replace-rate', type=float, default=0.05,

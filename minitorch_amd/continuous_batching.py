@@ -19,7 +19,12 @@ first tokens are not delayed). Scheduling decisions, pages and tokens are the sa
 the synchronous mode; a step whose batch has a request with an EOS token
 waits for its tokens, since finishing then depends on their values. With
 ``graph=True`` as well, each decode step's device work is replayed from a HIP
-graph captured per batch size (``DecoderLM.decode_greedy(graph=True)``).
+graph captured per batch size (``DecoderLM.decode_greedy(graph=True)``). With
+``merge_prefill=True`` (sync-free) a step whose batch has no EOS token decides
+its admissions before its decode runs -- the requests that end with the step's
+token leave the batch first, as their count already decides -- and runs the
+decode and the admissions' prefill as one layer loop
+(``DecoderLM.decode_prefill_greedy``): same decisions, pages and tokens.
 """
 from collections import deque
 from contextlib import nullcontext
@@ -67,7 +72,8 @@ class ContinuousBatcher:
 
     def __init__(self, model, *, max_batch_size=4, page_size=16, kv_budget_bytes=256 * 1024 ** 2,
                  pages_per_slab=4, precision='fp32', max_prefills_per_step=1,
-                 prefill_token_budget=512, clock=time.perf_counter, token_feedback=False, graph=False):
+                 prefill_token_budget=512, clock=time.perf_counter, token_feedback=False, graph=False,
+                 merge_prefill=False):
         for value in (max_batch_size, max_prefills_per_step, prefill_token_budget):
             if type(value) is not int or value < 1:
                 raise ValueError('Positive integer batch size and prefill limits required')
@@ -89,10 +95,11 @@ class ContinuousBatcher:
         self.iteration = 0
         self.last_step = None
         self.closed = False
-        if graph and not token_feedback:
-            raise ValueError('graph replay needs the sync-free loop (token_feedback=True)')
+        if (graph or merge_prefill) and not token_feedback:
+            raise ValueError('graph replay and merged prefills need the sync-free loop (token_feedback=True)')
         self.token_feedback = bool(token_feedback)
         self.graph = bool(graph)
+        self.merge_prefill = bool(merge_prefill)
         self._readback = TokenReadback(max_prefills_per_step + 4) if self.token_feedback else None
         self._inflight = deque()  # (readback ticket, requests) in issue order
 
@@ -170,7 +177,7 @@ class ContinuousBatcher:
         self._inflight.append((self._readback.push(ids), list(requests)))
         for request in requests:
             request.generated += 1
-            if request.eos_token_id is None and request.generated >= request.max_new_tokens:
+            if request.eos_token_id is None and request.generated >= request.max_new_tokens and not request.done:
                 self._finish(request, 'completed', 'length')
 
     @staticmethod
@@ -209,7 +216,20 @@ class ContinuousBatcher:
             first_ticket = self._readback.issued
         prefill_tokens = 0
         with self._precision_context():
-            if decode_ids and self.token_feedback:
+            merged = None
+            if decode_ids and self.merge_prefill and all(self.active[rid].eos_token_id is None for rid in decode_ids):
+                # the step's decode runs with its admissions' prefills (below):
+                # the requests that end with this step's token leave the batch
+                # now, as their token's count already decides
+                batch = [self.active[rid] for rid in decode_ids]
+                ending = [r for r in batch if r.generated + 1 >= r.max_new_tokens]
+                needs = sum(1 for r in batch if r.cache.length % self.pool.page_size == 0)
+                merged = (batch, ending, self.pool.used_pages + needs)
+                for request in ending:
+                    del self.active[request.request_id]
+                    self.reserved_pages -= request.reserved_pages
+                    request.state, request.finish_reason, request.finished_at = 'completed', 'length', self.clock()
+            elif decode_ids and self.token_feedback:
                 batch = [self.active[rid] for rid in decode_ids]
                 try:
                     ids = self.model.decode_greedy([r.cache for r in batch], graph=self.graph)
@@ -257,7 +277,9 @@ class ContinuousBatcher:
                 admitted.append(request)
                 prefill_ids.append(request.request_id)
                 prefill_tokens += len(request.prompt_ids)
-            if admitted:
+            if merged is not None:
+                events.extend(self._merged_step(*merged, admitted))
+            elif admitted:
                 events.extend(self._prefill(admitted))
         if self.token_feedback:
             # Only the read-backs issued in this step stay in flight: the
@@ -280,6 +302,35 @@ class ContinuousBatcher:
                               **self.pool.memory_stats())
         self.iteration += 1
         return events
+
+    def _merged_step(self, batch, ending, used_after_decode, admitted):
+        """The decode of ``batch`` and the prefill of ``admitted`` as one
+        layer loop (``DecoderLM.decode_prefill_greedy``), the caches of the
+        ``ending`` requests closed inside it once the step's pages are taken
+        (without admissions: ``decode_greedy``, then those caches closed).
+        Issues the read-back of every token of the step."""
+        try:
+            if admitted:
+                ids = self.model.decode_prefill_greedy(
+                    [r.cache for r in batch], [np.array(r.prompt_ids) for r in admitted],
+                    [r.cache for r in admitted], finished=[r.cache for r in ending])
+            else:
+                ids = self.model.decode_greedy([r.cache for r in batch], graph=self.graph)
+                self.pool.close_caches([r.cache for r in ending])
+        except Exception:
+            ended = {id(r) for r in ending}
+            for request in batch:
+                if id(request) in ended or not request.done:
+                    self._finish(request, 'failed', 'decode_error')
+            for request in admitted:
+                if not request.done:
+                    self._finish(request, 'failed', 'prefill_error')
+            raise
+        for request in ending:
+            request.cache = None
+        self.peak_used_pages = max(self.peak_used_pages, used_after_decode, self.pool.used_pages)
+        self._issue(batch + admitted, ids)
+        return []
 
     def _prefill(self, admitted):
         """Prefill the requests admitted in this step and emit (or, sync-free,

@@ -56,8 +56,9 @@ def _progress(message):
 
 def run_config3(model, trace, *, precision='fp16', max_batch_size=256, page_size=16, kv_pages=16384,
                 max_prefills_per_step=1, prefill_token_budget=512, clock=time.perf_counter,
-                report_every=200, token_feedback=False, graph=False):
-    """Replay a config-3 trace through the batcher. ``busy_step_tokens_per_sec``
+                report_every=200, token_feedback=False, graph=False, merge_prefill=False):
+    """Replay a config-3 trace through the batcher (``merge_prefill``: steps
+    that admit requests run their decode and the prefills as one layer loop). ``busy_step_tokens_per_sec``
     is decode tokens over the wall time of the steps (decode, prefill and
     scheduling, idle gaps between arrivals excluded), comparable between the
     synchronous and the sync-free (``token_feedback``) loop;
@@ -69,7 +70,7 @@ def run_config3(model, trace, *, precision='fp16', max_batch_size=256, page_size
                                 kv_budget_bytes=kv_pages * page_bytes, precision=precision,
                                 max_prefills_per_step=max_prefills_per_step,
                                 prefill_token_budget=prefill_token_budget, clock=clock,
-                                token_feedback=token_feedback, graph=graph)
+                                token_feedback=token_feedback, graph=graph, merge_prefill=merge_prefill)
     pending = list(trace)
     steps = []
     start = clock()

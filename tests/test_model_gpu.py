@@ -83,7 +83,7 @@ def test_decode_batch_equals_independent_decode_fp32():
 
 
 def run_trace(model, trace, precision='fp32', max_batch_size=4, budget_pages=None, page_size=16,
-              token_feedback=False, eos=None, max_prefills_per_step=1):
+              token_feedback=False, eos=None, max_prefills_per_step=1, merge_prefill=False):
     """Replay (arrival_step, id, prompt, new_tokens) on a step-indexed clock;
     ``eos`` maps request IDs to EOS token IDs. Returns the batcher, the
     per-step statistics and the events each step returned."""
@@ -91,7 +91,7 @@ def run_trace(model, trace, precision='fp32', max_batch_size=4, budget_pages=Non
     budget = (budget_pages or 4096) * page_bytes
     batcher = ContinuousBatcher(model, max_batch_size=max_batch_size, page_size=page_size,
                                 kv_budget_bytes=budget, precision=precision, token_feedback=token_feedback,
-                                max_prefills_per_step=max_prefills_per_step)
+                                max_prefills_per_step=max_prefills_per_step, merge_prefill=merge_prefill)
     steps, pending, events = [], sorted(trace), []
     while pending or batcher.has_work:
         while pending and pending[0][0] <= batcher.iteration:
@@ -206,15 +206,19 @@ def assert_same_run(sync, sync_steps, fb, fb_steps, fb_events, trace):
     assert sum(map(len, delivered.values())) == sum(len(fb.requests[t[1]].output_ids) for t in trace)
 
 
-@pytest.mark.parametrize('precision,max_prefills', [('fp32', 1), ('bf16', 1), ('fp32', 3)])
-def test_sync_free_loop_matches_synchronous_loop(precision, max_prefills):
+@pytest.mark.parametrize('precision,max_prefills,merge', [('fp32', 1, False), ('bf16', 1, False),
+                                                         ('fp32', 3, False), ('fp32', 1, True),
+                                                         ('fp32', 3, True)])
+def test_sync_free_loop_matches_synchronous_loop(precision, max_prefills, merge):
+    # merge: each step's decode and its admissions' prefill in one layer loop
     model = tiny(seed=14)
     rng = np.random.default_rng(14)
     trace = make_trace(model, rng, 12)
     sync, sync_steps = run_trace(model, trace, precision=precision, max_batch_size=3, budget_pages=30,
                                  max_prefills_per_step=max_prefills)
     fb, fb_steps, fb_events = run_trace(model, trace, precision=precision, max_batch_size=3, budget_pages=30,
-                                        token_feedback=True, max_prefills_per_step=max_prefills)
+                                        token_feedback=True, max_prefills_per_step=max_prefills,
+                                        merge_prefill=merge)
     assert_same_run(sync, sync_steps, fb, fb_steps, fb_events, trace)
     if precision == 'fp32':
         for _, rid, prompt, new in trace:
@@ -240,8 +244,13 @@ def test_sync_free_loop_with_eos_waits_for_tokens():
     fb, fb_steps, fb_events = run_trace(model, trace, max_batch_size=3, budget_pages=30, token_feedback=True,
                                         eos=eos)
     assert_same_run(sync, sync_steps, fb, fb_steps, fb_events, trace)
+    # merged steps wherever a batch has no EOS token, separate passes elsewhere
+    mg, mg_steps, mg_events = run_trace(model, trace, max_batch_size=3, budget_pages=30, token_feedback=True,
+                                        eos=eos, merge_prefill=True)
+    assert_same_run(sync, sync_steps, mg, mg_steps, mg_events, trace)
     sync.close()
     fb.close()
+    mg.close()
 
 
 def test_decode_greedy_reads_and_writes_slot_tokens():
