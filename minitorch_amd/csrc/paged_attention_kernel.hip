@@ -1007,6 +1007,9 @@ struct UniformItems {
 // rows [first_row[r], first_row[r] + n[r]) of q/k/v/out, with its own table
 // row and key offset), passed by value: every (prompt, tile) pair in the
 // order of pair_prompt / pair_tile (heaviest first), times the heads.
+#ifndef MT_RAGGED_SHARE
+#define MT_RAGGED_SHARE 2  // workgroups per compute unit that a ragged launch's key blocks are shared over
+#endif
 #ifndef MT_RAGGED_KEY_SPLIT
 #define MT_RAGGED_KEY_SPLIT 1
 #endif
@@ -2019,7 +2022,8 @@ int mt_paged_prefill_ragged(void* out, const void* q, const void* k, const void*
       max_blocks = std::max(max_blocks, blocks_of(z));
     }
     const int cus = device_compute_units();
-    int B = std::max<int>(2, int((total_blocks * h + 2 * cus - 1) / (2 * std::max(cus, 1))));
+    const int share = MT_RAGGED_SHARE * std::max(cus, 1);
+    int B = std::max<int>(2, int((total_blocks * h + share - 1) / share));
     auto pieces = [&](int B) {
       int64_t c = 0;
       for (const auto& z : order) c += (blocks_of(z) + B - 1) / B;
