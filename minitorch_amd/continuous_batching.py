@@ -308,7 +308,10 @@ class ContinuousBatcher:
         layer loop (``DecoderLM.decode_prefill_greedy``), the caches of the
         ``ending`` requests closed inside it once the step's pages are taken
         (without admissions: ``decode_greedy``, then those caches closed).
-        Issues the read-back of every token of the step."""
+        Issues the read-back of every token of the step. The logical
+        reservation of every active request's whole demand keeps both the
+        decode's and the prompts' pages within the budget, as it does for
+        separate passes."""
         try:
             if admitted:
                 ids = self.model.decode_prefill_greedy(
