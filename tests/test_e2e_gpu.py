@@ -72,6 +72,7 @@ def replay_config3(model, trace, precision):
                        max_prefills_per_step=1, prefill_token_budget=512, n_positions=model.n_positions)
     pending = list(trace)
     worked = 0
+    schedule = []
     while pending or batcher.has_work:
         while pending and pending[0][0] <= batcher.iteration:
             _, rid, prompt, new = pending.pop(0)
@@ -80,6 +81,7 @@ def replay_config3(model, trace, precision):
         batcher.step()
         ob.step()
         s, o = batcher.last_step, ob.steps[-1]
+        schedule.append({key: s[key] for key in SCHEDULE_KEYS})
         if not (s['decode_batch_size'] or s['prefill_request_ids']):
             assert not (o['decode_request_ids'] or o['prefill_request_ids'])
             continue
@@ -98,12 +100,18 @@ def replay_config3(model, trace, precision):
     stats = batcher.pool.memory_stats()
     assert stats['kv_pool_used_pages'] == 0 and batcher.reserved_pages == 0
     assert batcher.pool.header()['leased'] == 0 and not pool_o.leased
-    outputs = {rid: list(batcher.requests[rid].output_ids) for _, rid, _, _ in trace}
+    outputs = Run({rid: list(batcher.requests[rid].output_ids) for _, rid, _, _ in trace})
+    outputs.schedule = schedule
     print(f'config 3 {precision}: {worked} working steps, peak {batcher.peak_used_pages} pages, '
           f'{stats["kv_pool_page_reuses"]} reuses, max decode batch '
           f'{max(len(x["decode_request_ids"]) for x in ob.steps)}', flush=True)
     batcher.close()
     return outputs
+
+
+class Run(dict):
+    """A replay's tokens by request ID, with ``schedule``: every step's
+    decisions and pool counters (SCHEDULE_KEYS)."""
 
 
 @pytest.fixture(scope='module')
@@ -155,6 +163,36 @@ def test_config3_fp32_prefix_equals_gpt2_oracle(distil, config3_fp32, trace3):
             k = next(j for j in range(n) if got[j] != ref[j])
             pytest.fail(f'{rid}: token {k} is {got[k]}, oracle {ref[k]} (margin {m[k]:.3g}, '
                         f'smallest margin before it {min(m[:k + 1]):.3g})')
+
+
+def test_config3_fp32_merged_sync_free_loop_equals_synchronous(distil, config3_fp32, trace3):
+    # the same trace through the sync-free loop whose admitting steps run the
+    # decode and the prefill as one layer loop (merge_prefill): every step's
+    # decisions and pool counters, and every request's tokens, equal the
+    # synchronous replay (itself checked against the scheduling oracle)
+    page_bytes = 2 * distil.n_layer * distil.n_embd * PAGE_SIZE * 4
+    batcher = ContinuousBatcher(distil, max_batch_size=256, page_size=PAGE_SIZE,
+                                kv_budget_bytes=CONFIG3_PAGES * page_bytes, precision='fp32',
+                                max_prefills_per_step=1, prefill_token_budget=512, token_feedback=True,
+                                merge_prefill=True)
+    pending = list(trace3)
+    schedule = []
+    while pending or batcher.has_work:
+        while pending and pending[0][0] <= batcher.iteration:
+            _, rid, prompt, new = pending.pop(0)
+            batcher.submit(rid, prompt, max_new_tokens=new)
+        batcher.step()
+        schedule.append({key: batcher.last_step[key] for key in SCHEDULE_KEYS})
+    sync = config3_fp32.schedule
+    assert len(schedule) >= len(sync)
+    for i, (a, b) in enumerate(zip(sync, schedule)):
+        assert a == b, (i, a, b)
+    for extra in schedule[len(sync):]:  # trailing steps only deliver tokens
+        assert not extra['decode_request_ids'] and not extra['prefill_request_ids']
+    mismatched = [rid for _, rid, _, _ in trace3 if batcher.requests[rid].output_ids != config3_fp32[rid]]
+    assert not mismatched, mismatched[:5]
+    assert batcher.pool.memory_stats()['kv_pool_used_pages'] == 0
+    batcher.close()
 
 
 def test_config3_fp16_trace_completes_with_oracle_schedule(distil, trace3):
