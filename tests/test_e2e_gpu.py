@@ -58,6 +58,11 @@ def trace3():
     return config3_step_trace(0)
 
 
+class Run(dict):
+    """A replay's tokens by request ID, with ``schedule``: every step's
+    decisions and pool counters (SCHEDULE_KEYS)."""
+
+
 def replay_config3(model, trace, precision):
     """Replay the step trace through ContinuousBatcher and, in lockstep, the
     scheduling restatement fed with the GPU's tokens; compare after every step
@@ -108,10 +113,6 @@ def replay_config3(model, trace, precision):
     batcher.close()
     return outputs
 
-
-class Run(dict):
-    """A replay's tokens by request ID, with ``schedule``: every step's
-    decisions and pool counters (SCHEDULE_KEYS)."""
 
 
 @pytest.fixture(scope='module')
