@@ -229,8 +229,10 @@ def test_token_feedback_entries_reject_invalid_arguments():
 
 
 class _Layer(ct.Structure):
+    # mt_decoder_layer (include/mt_model.h), the tiled weight copies last
     _fields_ = [(n, P) for n in ('ln1_gamma', 'ln1_beta', 'w_qkv', 'b_qkv', 'w_o', 'b_o',
-                                 'ln2_gamma', 'ln2_beta', 'w_fc', 'b_fc', 'w_proj', 'b_proj')]
+                                 'ln2_gamma', 'ln2_beta', 'w_fc', 'b_fc', 'w_proj', 'b_proj',
+                                 'w_qkv_tiled', 'w_o_tiled', 'w_fc_tiled', 'w_proj_tiled')]
 
 
 class _Prefill(ct.Structure):
@@ -349,3 +351,51 @@ def test_decode_projection_entries_reject_invalid_arguments():
                  (A, A, A, 1, 0, A, A, 0, 1024, 1e-5, 2, 0),   # no rows
                  (A, A, A, 1, 0, A, A, 4, 1024, 1e-5, 2, 1)]:  # layout 1 (a tiled input) is not taken
         assert rp(*args) == 1, args
+
+
+class _DecodeAtt(ct.Structure):
+    _fields_ = [('slabs', P), ('table', P), ('offsets', P), ('page_size', I), ('pages_per_slab', I),
+                ('num_slabs', I), ('columns', I), ('layers', I), ('split_tokens', I), ('work', P),
+                ('work_items', I), ('merge_rows', I), ('partials', P), ('partial_bytes', Z)]
+
+
+def test_mixed_layers_and_batched_pool_entries_reject_invalid_arguments():
+    # validation only: every call below returns before any device work
+    lib = library('model_kernels')
+    g = lib.mt_mixed_layers
+    g.argtypes = [P, P, I, P, P, P, P, P, P, I, I, I, P, I, I, ct.c_float, I, I, P, Z, P, P]
+    g.restype = I
+    layer = _Layer(*([8] * 12))
+    need = lib.mt_decoder_scratch_bytes
+    need.argtypes, need.restype = [I, I, I], Z
+    scratch = need(3 + 12, 64, 1)
+    datt = _DecodeAtt(8, 8, 8, 16, 4, 4, 8, 1, 1024, 8, 3, 0, 8, 1024)
+    atts = (_Prefill * 2)(_Prefill(8, 8, 16, 4, 4, 8, 1, 0), _Prefill(8, 8, 16, 4, 4, 8, 1, 0))
+
+    def call(decode_rows=3, tokens=(5, 7), requests=2, scratch_bytes=scratch, heads=2, d_att=datt, att=atts):
+        return g(8, ct.byref(layer), 1, 8, 8, 8, 8, 8, 8, 10, decode_rows, requests, (I * 2)(*tokens), 64, heads,
+                 1e-5, 1, 1, 8, scratch_bytes, None if d_att is None else ct.byref(d_att), att)
+    assert call(decode_rows=0) == 1
+    assert call(decode_rows=65535) == 1             # more decode rows than the head gather takes
+    assert call(tokens=(5, 0)) == 1                 # an empty prompt
+    assert call(requests=0) == 1
+    assert call(scratch_bytes=scratch - 1) == 1
+    assert call(heads=3) == 1                       # d % heads
+    assert call(d_att=None) == 1
+    assert call(att=None) == 1
+    other = _DecodeAtt(8, 8, 8, 32, 4, 4, 8, 1, 1024, 8, 3, 0, 8, 1024)
+    assert call(d_att=other) == 1                   # decode rows and prompts on different pools
+
+    sched = library('sched_kernels')
+    geometry = [P, I, I, I, I, I, ct.c_ulonglong, ct.c_ulonglong]
+    acquire = sched.mt_pool_acquire_lists
+    acquire.argtypes, acquire.restype = geometry + [P, P, I, P], I
+    lengths = sched.mt_sched_add_lengths
+    lengths.argtypes, lengths.restype = geometry + [P, P, I], I
+    pool = (8, 16, 4, 16, 4, 4, 8, 1 << 20)
+    assert acquire(*pool, 8, 8, 0, 8) == 1           # no cache
+    assert acquire(*pool, None, 8, 2, 8) == 1
+    assert acquire(*pool, 8, 8, 2, None) == 1        # no scratch
+    assert acquire(8, 16, 4, 16, 4, 5, 8, 1 << 20, 8, 8, 2, 8) == 1   # slabs * pages_per_slab != pages
+    assert lengths(*pool, 8, 8, 0) == 1
+    assert lengths(*pool, 8, None, 2) == 1
