@@ -41,7 +41,9 @@ int mt_device_count(int* n);
 /* Compute units of the current device (256 on MI355X); sizes the row
  * visiting order of the decode. No reference counterpart. */
 int mt_compute_units(int* n);
-/* Measuring kernel: reads `count` chunks of chunk_bytes (multiple of 1 KiB,
+/* BENCH-ONLY measuring kernel, not part of the runtime the reference binds
+ * (its CudaRuntime table, minitorch/cuda_storage.py:29-45, never names it) and
+ * not called by any product path: reads `count` chunks of chunk_bytes (multiple of 1 KiB,
  * addresses listed in the device array `chunks`, 16-byte aligned) with
  * `blocks` workgroups of 4 waves, each wave taking every (waves)-th chunk.
  * Used by bench.py --ceiling to time a decode step's exact K/V access pattern

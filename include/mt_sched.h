@@ -30,7 +30,8 @@ typedef struct mt_pool_header {
   int top;          /* free pages on the stack */
   int slabs_opened; /* slabs whose pages have entered the free list */
   int leased;       /* pages owned by caches or API owners */
-  int error;        /* nonzero after a release of pages the owner does not hold */
+  int error;        /* bit 0: a release of pages the owner does not hold; bit 1: an
+                       mt_pool_acquire_lists entry beyond its slot's columns or the budget */
   long long acquires, releases, reuses;
 } mt_pool_header;
 
@@ -67,7 +68,10 @@ int mt_pool_acquire_rows(MT_POOL_ARGS, const int* slots, int rows, int per_row, 
 
 /* prepare_append of n one-row caches in order: for i = 0..n-1, one pop of
  * counts[i] (device int32 [n]; host-checked against the budget and the
- * slot's columns) pages appended to slot slots[i]'s page list, the pops
+ * slot's columns, and checked again by the kernel: an entry with an invalid
+ * slot, more pages than its slot's free columns or than the free budget is
+ * skipped and sets bit 1 of header.error) pages appended to slot slots[i]'s
+ * page list, the pops
  * opening slabs exactly as n mt_pool_acquire_rows calls of one row would
  * (scratch: device int32 [max counts[i]]). Replaces the page part of n
  * consecutive reference PagedKVCache.prepare_append calls

@@ -1059,11 +1059,11 @@ hipError_t projection(void* out, const void* x, const void* w, const void* bias,
   return hipGetLastError();
 }
 
-// Whether residual_layernorm_partials takes the row shape (width a multiple of
-// 256, at most 2048, 16-byte aligned rows).
+// Whether residual_layernorm_partials takes the row shape (width a positive
+// multiple of 256, at most 2048, 16-byte aligned rows).
 bool partials_ln_ok(const void* out, const float* x, const float* part, const void* bias, const float* gamma,
                     const float* beta, int width, int dtype) {
-  return (dtype == kF16 || dtype == kBF16) && width % 256 == 0 && width <= 2048 && aligned(x, 16) &&
+  return (dtype == kF16 || dtype == kBF16) && width >= 256 && width % 256 == 0 && width <= 2048 && aligned(x, 16) &&
          aligned(part, 16) && aligned(gamma, 16) && aligned(beta, 16) && aligned(out, 8) && (!bias || aligned(bias, 8));
 }
 

@@ -238,6 +238,15 @@ __global__ __launch_bounds__(kThreads) void acquire_lists_kernel(Pool p, const i
   for (int i = 0; i < n; ++i) {
     const int slot = slots[i], count = counts[i];
     if (count <= 0) continue;
+    // The counts come from device memory: an entry that names no slot, would
+    // write past its slot's columns or pop beyond the budget is skipped and
+    // flagged (every thread reads the same header and page count after the
+    // previous entry's barrier, so all skip together).
+    if (slot < 0 || slot >= p.max_slots || count > p.max_cols - p.slot_npages[slot] ||
+        count > p.max_pages - p.h->leased) {
+      if (threadIdx.x == 0) atomicOr(&p.h->error, 2);
+      continue;
+    }
     bulk_pop(p, count, slot, scratch, &s_red);
     const int have = p.slot_npages[slot];
     for (int r = threadIdx.x; r < count; r += blockDim.x)

@@ -400,7 +400,7 @@ class DecoderLM:
             return self._decode_greedy_graph(caches)
         return self._decode_batch(idx, caches, greedy=True)
 
-    def decode_prefill_greedy(self, caches, prompts, new_caches, *, finished=()):
+    def decode_prefill_greedy(self, caches, prompts, new_caches, *, finished=(), return_logits=False):
         """One sync-free greedy decode step of ``caches`` (as ``decode_greedy``
         with ``idx`` None) and the prefill of ``prompts`` into the empty caches
         ``new_caches`` (one each, as ``prefill_batch``), run as one native
@@ -413,8 +413,18 @@ class DecoderLM:
         same. Returns the greedy token IDs [len(caches) + len(prompts), 1] fp32
         on the device (the decode rows, then each prompt's first token), which
         also become each cache's last token for the next step. Nothing waits
-        for the device. No reference counterpart (the reference runs a step's
-        decode batch and its prefills as separate forward passes,
+        for the device. With ``return_logits`` the result is (ids, logits
+        [len(caches) + len(prompts), 1, V]) in the compute type.
+
+        The step's whole page demand (the decode rows' new pages, less what
+        the ending requests return, plus the prompts' pages) is checked on the
+        host before anything changes: a step that does not fit raises
+        MemoryError with every cache, page and length as it was, and the
+        caller may run the separate calls instead. If the native layer loop
+        fails after the decode rows' lengths were committed, those caches are
+        marked invalid (their K/V for the step was not written). No reference
+        counterpart (the reference runs a step's decode batch and its
+        prefills as separate forward passes,
         minitorch/continuous_batching.py:140-176)."""
         from .paged_decode import PagedDecodeBatch
         new_caches, prompts, pool, tokens = self._check_prefill(prompts, new_caches, 'decode_prefill_greedy')
@@ -425,6 +435,14 @@ class DecoderLM:
         if caches and caches[0].pool is not pool:
             raise ValueError('decode_prefill_greedy requires the decode and new caches on one pool')
         with PagedDecodeBatch(self, None, caches) as batch:
+            ps = pool.page_size
+            grows = {id(c): int(c.length % ps == 0) for c in caches}
+            free = pool.max_pages - pool.used_pages
+            decode_pages = sum(grows.values())
+            returned = sum(c._counts[0] + grows[id(c)] for c in finished)
+            prompt_pages = sum(-(-n // ps) for n in tokens)
+            if decode_pages > free or decode_pages - returned + prompt_pages > free:
+                raise MemoryError('KV page budget exhausted')
             batch.prepare()
             b, dtype, d = batch.batch_size, batch.dtype, self.n_embd
             w = self._weights(dtype)
@@ -445,15 +463,8 @@ class DecoderLM:
         new_slots, prompt_ids, prompt_positions = blob.ptr, blob.ptr + 12 * r, blob.ptr + 12 * r + 4 * total
         prepared = []
         try:
-            try:
-                pool.prepare_appends(new_caches, tokens, blob.ptr)
-                prepared = list(new_caches)
-            except MemoryError:
-                # past the budget together: one by one, failing where the
-                # consecutive prefills would
-                for cache, n in zip(new_caches, tokens):
-                    cache.prepare_append(n)
-                    prepared.append(cache)
+            pool.prepare_appends(new_caches, tokens, blob.ptr)
+            prepared = list(new_caches)
             x = DeviceTensor((b + total, d), 'float32')
             paged_ops.embed_tokens(x.ptr, w.wte.ptr, w.wpe.ptr, None, positions.ptr, b, self.n_vocab,
                                    self.n_positions, d, slot_tokens=pool.slot_tokens.ptr, slots=slots.ptr,
@@ -481,11 +492,14 @@ class DecoderLM:
                 cache._written_layers.update(range(len(cache.layout)))
                 cache.last_attention_path = 'paged_prefill'
             pool.commit_appends(new_caches, blob.ptr)
-            return out
+            return (out, logits) if return_logits else out
         except Exception:
             for cache in prepared:
                 if cache._pending_tokens is not None:
                     cache.abort_append()
+            for cache in caches:
+                if not cache.closed:
+                    cache.valid = False
             raise
 
     def _decode_greedy_graph(self, caches):

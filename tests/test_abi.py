@@ -349,6 +349,9 @@ def test_decode_projection_entries_reject_invalid_arguments():
                  (A, A, A, 9, 0, A, A, 4, 1024, 1e-5, 2, 0),   # more than 8 splits
                  (A, A, A, 1, 0, A, A, 4, 1024, 1e-5, 0, 0),   # fp32
                  (A, A, A, 1, 0, A, A, 0, 1024, 1e-5, 2, 0),   # no rows
+                 (A, A, A, 1, 0, A, A, 4, 0, 1e-5, 2, 0),      # zero width
+                 (A, A, A, 1, 0, A, A, 4, -256, 1e-5, 2, 0),   # negative width (a multiple of 256)
+                 (A, A, A, 1, 0, A, A, 4, -2048, 1e-5, 2, 0),
                  (A, A, A, 1, 0, A, A, 4, 1024, 1e-5, 2, 1)]:  # layout 1 (a tiled input) is not taken
         assert rp(*args) == 1, args
 

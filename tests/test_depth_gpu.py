@@ -1,0 +1,255 @@
+"""Low-precision output at full model depth.
+
+The reference's logits gate (project/benchmark_inference.py:62-89,
+``validate_logits``) compares, at the run's own precision, the cached prefill
+with the full forward, and one decode step with the full forward of the
+extended sequence, at rtol = atol = fp32 .003 / fp16 .03 / bf16 .15 (:78).
+Here it runs on the two end-to-end architectures at their full depth --
+DistilGPT-2 in fp16 (6 layers, d 768) and GPT-2-medium in bf16 (24 layers,
+d 1024) -- at 1, 8, 40 and 128 decode rows, so that every projection path of
+the decode step runs through every layer: the LayerNorm-prologue projections
+(<= 8 rows), the fragment-tiled path with split out-projections (40 rows) and
+with hipBLASLt out-projections (128 rows). The "full forward" of this build is
+a prefill of the whole sequence into fresh caches. Every check is also made
+against the fp64 numpy GPT-2 (oracle/gpt2_oracle.py, pinned to transformers'
+GPT2LMHeadModel) on sampled rows, with the gate's tolerance and a normwise
+bound.
+
+The weights are the configs' N(0, 0.02) matrices with every bias and
+LayerNorm gain/shift drawn at random per layer (the configs' zero biases and
+unit gains would hide a bias or LayerNorm parameter taken from the wrong
+layer). GPT-2-medium in fp32 checks greedy tokens against the fp64 oracle,
+and each layer's device weight copies (row-major and fragment-tiled) are
+compared with that layer's host weights bit for bit.
+"""
+import numpy as np
+import pytest
+
+from minitorch_amd.amp import autocast
+from minitorch_amd.dtypes import encode_host
+from minitorch_amd.kv_cache import greedy_token
+from minitorch_amd.model import DecoderLM, init_gpt2_state, fragment_tiled
+from minitorch_amd.paged_kv_cache import KVPagePool
+from minitorch_amd.runtime import DeviceTensor
+from oracle import gpt2_oracle as go
+
+pytestmark = pytest.mark.gpu
+
+# project/benchmark_inference.py:78
+GATE = {'float32': .003, 'float16': .03, 'bfloat16': .15}
+# normwise ||got - fp64|| / ||fp64|| of one row's logits; a layer or row
+# mix-up moves a row's logits by about their own norm
+NORMWISE = {'float16': 0.02, 'bfloat16': 0.08}
+
+ARCH = {
+    'distilgpt2': dict(n_vocab=50257, n_embd=768, n_head=12, n_layer=6, n_positions=1024),
+    'gpt2-medium': dict(n_vocab=50257, n_embd=1024, n_head=16, n_layer=24, n_positions=1024),
+}
+PRECISION = {'distilgpt2': 'float16', 'gpt2-medium': 'bfloat16'}
+
+
+def varied_state(arch, seed):
+    """The architecture's seeded N(0, 0.02) weights, with biases ~ N(0, 0.02),
+    LayerNorm gains ~ 1 + N(0, 0.1) and shifts ~ N(0, 0.05), drawn per layer."""
+    state = init_gpt2_state(seed=seed, **{k: v for k, v in ARCH[arch].items() if k != 'n_head'})
+    rng = np.random.default_rng([seed, 1])
+    for key, value in state.items():
+        if key.endswith('.bias'):
+            scale = 0.05 if '.ln_' in key or key.startswith('transformer.ln_f') else 0.02
+            state[key] = (rng.standard_normal(value.shape) * scale).astype(np.float32)
+        elif '.ln_' in key or key.startswith('transformer.ln_f'):
+            state[key] = (1 + 0.1 * rng.standard_normal(value.shape)).astype(np.float32)
+    return state
+
+
+_MODELS = {}
+
+
+def model_for(arch):
+    if arch not in _MODELS:
+        state = varied_state(arch, seed=3)
+        model = DecoderLM(seed=3, state=state, **ARCH[arch])
+        state64 = {k: v.astype(np.float64) for k, v in state.items()}
+        _MODELS[arch] = (model, state64)
+    return _MODELS[arch]
+
+
+def oracle_logits(model, state64, prompt, extra):
+    """fp64 last-position logits of ``prompt``, then of ``prompt`` extended by
+    each token of ``extra`` in turn (KV-cached, each equal to the full forward)."""
+    cache, last = go.prefill_cache(state64, prompt, n_head=model.n_head, n_layer=model.n_layer,
+                                   capacity=len(prompt) + len(extra), dtype=np.float64)
+    out = [last]
+    for t in extra:
+        out.append(go.decode_step(state64, [cache], [t], n_head=model.n_head, n_layer=model.n_layer,
+                                  dtype=np.float64)[0])
+    return out
+
+
+def check(got, ref, tol, label):
+    """The gate's elementwise tolerance (as numpy.testing.assert_allclose with
+    rtol = atol = tol); returns the largest |got - ref| / (tol + tol |ref|)."""
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    ratio = np.abs(got - ref) / (tol + tol * np.abs(ref))
+    worst = float(ratio.max())
+    assert worst <= 1, f'{label}: {worst:.3f} of the tolerance (max |err| {np.abs(got - ref).max():.4g})'
+    return worst
+
+
+def normwise(got, ref):
+    return float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+
+
+def make_pool(model, rows, pages_per_row):
+    page_bytes = 2 * model.n_layer * model.n_embd * 16 * 2
+    return KVPagePool(model, page_size=16, max_bytes=(2 * rows * pages_per_row + 16) * page_bytes,
+                      pages_per_slab=16)
+
+
+def prefill_fresh(model, pool, seqs):
+    """Last-position logits [R, V] of a prefill of each sequence into a fresh
+    cache (the gate's full forward)."""
+    caches = [model.create_kv_cache(1, len(s), page_size=16, page_pool=pool) for s in seqs]
+    logits = model.prefill_batch([np.asarray(s) for s in seqs], caches).to_numpy()[:, 0].astype(np.float64)
+    for c in caches:
+        c.close()
+    return logits
+
+
+@pytest.mark.parametrize('rows', [1, 8, 40, 128])
+@pytest.mark.parametrize('arch', ['distilgpt2', 'gpt2-medium'])
+def test_decode_logits_gate_at_depth(arch, rows):
+    model, state64 = model_for(arch)
+    dtype = PRECISION[arch]
+    tol = GATE[dtype]
+    rng = np.random.default_rng([7, rows])
+    prompts = [rng.integers(0, model.n_vocab, int(n)).tolist() for n in rng.integers(4, 97, rows)]
+    with autocast(dtype):
+        pool = make_pool(model, rows, 7)
+        caches = [model.create_kv_cache(1, len(p) + 2, page_size=16, page_pool=pool) for p in prompts]
+        prefill = model.prefill_batch([np.asarray(p) for p in prompts], caches)
+        seqs = [list(p) for p in prompts]
+        got = [prefill.to_numpy()[:, 0].astype(np.float64)]
+        tokens = greedy_token(prefill).to_numpy()[:, 0].astype(int)
+        for _ in range(2):
+            for s, t in zip(seqs, tokens):
+                s.append(int(t))
+            logits = model.decode_batch(DeviceTensor.from_numpy(tokens[:, None].astype(np.float32)), caches)
+            got.append(logits.to_numpy()[:, 0].astype(np.float64))
+            tokens = greedy_token(logits).to_numpy()[:, 0].astype(int)
+        for c in caches:
+            c.close()
+        # the gate: each decode step against the full forward of its sequence
+        worst_gate = 0.0
+        for k in (1, 2):
+            full = prefill_fresh(model, pool, [s[:len(p) + k] for s, p in zip(seqs, prompts)])
+            for r in range(rows):
+                worst_gate = max(worst_gate, check(got[k][r], full[r], tol, f'step {k} row {r} vs full forward'))
+        assert pool.used_pages == 0
+        pool.close()
+    # the fp64 oracle on sampled rows: the prefill and both decode steps
+    worst_oracle, worst_norm = 0.0, 0.0
+    for r in sorted({0, rows // 2, rows - 1}):
+        refs = oracle_logits(model, state64, prompts[r], seqs[r][len(prompts[r]):])
+        for k, ref in enumerate(refs):
+            worst_oracle = max(worst_oracle, check(got[k][r], ref, tol, f'step {k} row {r} vs fp64 oracle'))
+            nw = normwise(got[k][r], ref)
+            worst_norm = max(worst_norm, nw)
+            assert nw <= NORMWISE[dtype], f'step {k} row {r}: normwise error {nw:.4f}'
+    print(f'{arch} {dtype} rows={rows}: gate {worst_gate:.3f}, oracle {worst_oracle:.3f} of the tolerance; '
+          f'normwise vs fp64 {worst_norm:.4f}')
+
+
+@pytest.mark.parametrize('arch', ['distilgpt2', 'gpt2-medium'])
+def test_merged_step_logits_at_depth(arch):
+    # DecoderLM.decode_prefill_greedy (mt_mixed_layers): 24 decode rows and
+    # three new prompts through one layer loop, every layer; decode rows
+    # against the full forward of their sequences and prompts against their
+    # own prefill, both with the gate's tolerance; sampled rows against fp64.
+    model, state64 = model_for(arch)
+    dtype = PRECISION[arch]
+    tol = GATE[dtype]
+    rng = np.random.default_rng(11)
+    prompts = [rng.integers(0, model.n_vocab, int(n)).tolist() for n in rng.integers(4, 97, 24)]
+    new_prompts = [rng.integers(0, model.n_vocab, int(n)).tolist() for n in (5, 77, 300)]
+    with autocast(dtype):
+        pool = make_pool(model, 30, 20)
+        caches = [model.create_kv_cache(1, len(p) + 1, page_size=16, page_pool=pool) for p in prompts]
+        first = greedy_token(model.prefill_batch([np.asarray(p) for p in prompts], caches), feedback=caches)
+        seqs = [list(p) + [int(t)] for p, t in zip(prompts, first.to_numpy()[:, 0])]
+        new = [model.create_kv_cache(1, len(p), page_size=16, page_pool=pool) for p in new_prompts]
+        ids, logits = model.decode_prefill_greedy(caches, [np.asarray(p) for p in new_prompts], new,
+                                                  return_logits=True)
+        got = logits.to_numpy()[:, 0].astype(np.float64)
+        assert np.array_equal(ids.to_numpy()[:, 0].astype(int), got.argmax(axis=1))
+        for c in caches + new:
+            c.close()
+        full = prefill_fresh(model, pool, seqs + new_prompts)
+        for r in range(len(full)):
+            check(got[r], full[r], tol, f'merged row {r} vs full forward')
+        pool.close()
+    for r in (0, 23):
+        ref = oracle_logits(model, state64, seqs[r], [])[0]
+        check(got[r], ref, tol, f'decode row {r} vs fp64 oracle')
+        assert normwise(got[r], ref) <= NORMWISE[dtype]
+    for j, p in enumerate(new_prompts):
+        ref = oracle_logits(model, state64, p, [])[0]
+        check(got[24 + j], ref, tol, f'prompt {j} vs fp64 oracle')
+        assert normwise(got[24 + j], ref) <= NORMWISE[dtype]
+
+
+def test_gpt2_medium_fp32_greedy_tokens_match_oracle():
+    # 4 requests x 8 greedy tokens on GPT-2-medium (24 layers) in fp32: batched
+    # prefill, then batched decode steps, against the fp64 oracle's greedy
+    # tokens (the north star's exact-token bar); the fp64 top-2 margins are
+    # reported on a mismatch.
+    model, state64 = model_for('gpt2-medium')
+    rng = np.random.default_rng(23)
+    prompts = [rng.integers(0, model.n_vocab, n).tolist() for n in (7, 30, 64, 120)]
+    pool = KVPagePool(model, page_size=16, max_bytes=64 * 2 * 24 * 1024 * 16 * 4, pages_per_slab=8)
+    caches = [model.create_kv_cache(1, len(p) + 8, page_size=16, page_pool=pool) for p in prompts]
+    tokens = greedy_token(model.prefill_batch([np.asarray(p) for p in prompts], caches)).to_numpy()[:, 0]
+    out = [[int(t)] for t in tokens]
+    for _ in range(7):
+        logits = model.decode_batch(DeviceTensor.from_numpy(tokens[:, None].astype(np.float32)), caches)
+        tokens = greedy_token(logits).to_numpy()[:, 0]
+        for o, t in zip(out, tokens):
+            o.append(int(t))
+    for c in caches:
+        c.close()
+    pool.close()
+    ref, margins = go.greedy_cached(state64, prompts, [8] * 4, n_head=model.n_head, n_layer=model.n_layer)
+    assert out == ref, f'margins {margins}'
+
+
+@pytest.mark.parametrize('arch', ['distilgpt2', 'gpt2-medium'])
+def test_layer_weight_copies_match_their_layer(arch):
+    # every layer's device weights -- the row-major [out, in] copy hipBLASLt
+    # reads and the fragment-tiled copy of the decode projection kernel --
+    # equal that layer's host weights bit for bit, and the native layer table
+    # points at that layer's copies
+    from minitorch_amd.model import DecoderLayerStruct
+    model, _ = model_for(arch)
+    dtype = PRECISION[arch]
+    w = model._weights(dtype)
+    state = model.state
+    names = {'qkv': 'attn.c_attn', 'o': 'attn.c_proj', 'fc': 'mlp.c_fc', 'proj': 'mlp.c_proj'}
+    assert len(w.layers) == model.n_layer
+    for i, L in enumerate(w.layers):
+        p = f'transformer.h.{i}.'
+        for key, name in names.items():
+            weight = state[p + name + '.weight'].T
+            assert np.array_equal(L[key][0].raw_numpy().reshape(-1), encode_host(weight, dtype)), (i, key)
+            assert np.array_equal(L[key][1].raw_numpy().reshape(-1), encode_host(state[p + name + '.bias'], dtype))
+            assert np.array_equal(L[key + '_tiled'].raw_numpy().reshape(-1),
+                                  encode_host(fragment_tiled(weight), dtype)), (i, key, 'tiled')
+        for key in ('ln_1', 'ln_2'):
+            assert np.array_equal(L[key][0].to_numpy(), state[p + key + '.weight'])
+            assert np.array_equal(L[key][1].to_numpy(), state[p + key + '.bias'])
+        s = w.layer_array[i]
+        fields = [f for f, _ in DecoderLayerStruct._fields_]
+        expect = [L['ln_1'][0].ptr, L['ln_1'][1].ptr, L['qkv'][0].ptr, L['qkv'][1].ptr, L['o'][0].ptr,
+                  L['o'][1].ptr, L['ln_2'][0].ptr, L['ln_2'][1].ptr, L['fc'][0].ptr, L['fc'][1].ptr,
+                  L['proj'][0].ptr, L['proj'][1].ptr, L['qkv_tiled'].ptr, L['o_tiled'].ptr, L['fc_tiled'].ptr,
+                  L['proj_tiled'].ptr]
+        assert [getattr(s, f) for f in fields] == expect, i

@@ -142,10 +142,12 @@ def test_mixed_step_argument_checks():
     w.close()
 
 
-def test_mixed_step_budget_exhaustion_like_separate_calls():
-    # the prompts together need more pages than the budget holds: both paths
-    # raise MemoryError with the decode step committed, the ending caches
-    # closed, no new cache left holding pages, and the same pool state
+def test_mixed_step_budget_exhaustion_changes_nothing():
+    # the prompts together need more pages than the budget holds: the merged
+    # step raises MemoryError before any change (no decode committed, the
+    # ending cache still open, no new cache holding pages); the caller then
+    # runs the separate calls, which fail at the same prompt, and both worlds
+    # decode the next step to the same tokens and pool state
     model = tiny(seed=5)
     rng = np.random.default_rng(5)
     prompts = [rng.integers(0, model.n_vocab, 40) for _ in range(3)]
@@ -161,20 +163,60 @@ def test_mixed_step_budget_exhaustion_like_separate_calls():
 
     a, b = world(), world()
     big = [rng.integers(0, model.n_vocab, n) for n in (30, 60, 40)]   # 2 + 4 + 3 pages
-    ids = a.model.decode_greedy(a.caches)
-    a.caches[1].close()
-    new_a = a.new_caches(3)
-    with pytest.raises(MemoryError):
-        a.model.prefill_batch(big, new_a)
     new_b = b.new_caches(3)
+    before = (b.pool.free_stack(), b.pool.header(), b.pool.memory_stats(), [c.pages() for c in b.caches])
     with pytest.raises(MemoryError):
         b.model.decode_prefill_greedy(b.caches, big, new_b, finished=[b.caches[1]])
     runtime().synchronize()
-    a._advance([1], [])
-    b._advance([1], [])
-    assert_same_pools(a, b)
-    assert [c.length for c in new_a] == [c.length for c in new_b] == [0, 0, 0]
-    for c in new_a + new_b:
+    assert (b.pool.free_stack(), b.pool.header(), b.pool.memory_stats(), [c.pages() for c in b.caches]) == before
+    assert [c.length for c in b.caches] == [40, 40, 40] and all(c.valid and not c.closed for c in b.caches)
+    assert [c.length for c in new_b] == [0, 0, 0] and b.pool.used_pages == 9
+    for c in new_b:
         c.close()
+    for w in (a, b):
+        # the separate calls, as the caller's fallback
+        w.model.decode_greedy(w.caches)
+        w.caches[1].close()
+        new = w.new_caches(3)
+        with pytest.raises(MemoryError):
+            w.model.prefill_batch(big, new)
+        for c in new:
+            assert c.length == 0
+            c.close()
+        w._advance([1], [])
+    runtime().synchronize()
+    assert_same_pools(a, b)
+    ta = a.model.decode_greedy(a.caches).to_numpy()[:, 0].tolist()
+    tb = b.model.decode_greedy(b.caches).to_numpy()[:, 0].tolist()
+    assert ta == tb
+    assert_same_pools(a, b)
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+def test_mixed_step_logits_near_oracle(dtype):
+    # The merged step's logits in fp16/bf16 (4 layers, d 256): every decode
+    # row and every new prompt's last row against the fp64 numpy GPT-2 on its
+    # own sequence, within 2 % of the logits' range (the bound of the other
+    # low-precision model tests; a wrong row, layer or position misses it by
+    # far), and the returned tokens are the first maxima of those logits.
+    from oracle import gpt2_oracle as go
+    model = tiny(seed=41, layers=4, d=256, heads=4)
+    rng = np.random.default_rng(41)
+    with autocast(dtype):
+        prompts = [rng.integers(0, model.n_vocab, int(n)) for n in rng.integers(5, 120, 12)]
+        w = World(model, prompts, 16)
+        seqs = [list(p) + [t] for p, t in zip(prompts, w.tokens)]
+        new_prompts = [rng.integers(0, model.n_vocab, int(n)) for n in (3, 50, 97)]
+        new = w.new_caches(len(new_prompts))
+        ids, logits = model.decode_prefill_greedy(w.caches, new_prompts, new, finished=[w.caches[4]],
+                                                  return_logits=True)
+        got = logits.to_numpy()[:, 0].astype(np.float64)
+        assert np.array_equal(ids.to_numpy()[:, 0].astype(int), got.argmax(axis=1))
+        w._advance([4], new)
+        w.close()
+    for i, seq in enumerate(seqs + [list(p) for p in new_prompts]):
+        ref = go.forward(model.state, seq, n_head=model.n_head, n_layer=model.n_layer)[-1]
+        err = np.abs(got[i] - ref).max()
+        assert err <= 0.02 * (ref.max() - ref.min()), (i, err, ref.max() - ref.min())

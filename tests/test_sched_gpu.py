@@ -7,7 +7,7 @@ import pytest
 from minitorch_amd.amp import autocast
 from minitorch_amd.paged_kv_cache import KVPagePool, PagedKVCache
 from minitorch_amd.paged_decode import PagedDecodeBatch
-from minitorch_amd.runtime import DeviceTensor, runtime
+from minitorch_amd.runtime import DeviceTensor, runtime, P, I
 from oracle.pool_oracle import PoolOracle, CacheOracle, decode_batch_metadata
 
 pytestmark = pytest.mark.gpu
@@ -321,4 +321,43 @@ def test_low_precision_pool_dtype_and_bytes():
     assert pool.dtype == 'bfloat16'
     assert pool.page_bytes == 2 * 3 * 4 * 64 * 32 * 2
     assert pool.memory_stats()['kv_pool_reserved_bytes'] == 0
+    pool.close()
+
+
+def test_acquire_lists_skips_entries_beyond_columns_or_budget():
+    # mt_pool_acquire_lists reads its page counts from device memory, so the
+    # kernel checks them itself: an entry that would write past its slot's
+    # columns, or pop beyond the free budget, is skipped and sets bit 1 of the
+    # header's error word; valid entries around it still run. (Each bad count
+    # exceeds its limit by one, so that even an unguarded pop stays inside the
+    # pool state.)
+    model = StubModel(n_positions=128)           # 8 columns of 16 tokens
+    pool = KVPagePool(model, page_size=16, max_bytes=64 * 16384, pages_per_slab=4)   # 64 pages
+    caches = [PagedKVCache(model, 1, 128, page_size=16, page_pool=pool) for _ in range(3)]
+    slots = [c.slot for c in caches]
+    before = pool.header()
+
+    def run(counts):
+        lists = DeviceTensor.from_numpy(np.array(slots + counts, np.int32), 'int32')
+        pool._call('mt_pool_acquire_lists', [P, P, I, P], lists.ptr, lists.ptr + 4 * len(slots), len(slots),
+                   pool._scratch.ptr)
+        runtime().synchronize()
+        return pool.header()
+
+    h = run([0, pool.max_cols + 1, 0])          # one more than a slot's columns
+    assert h['error'] == 2 and (h['top'], h['leased'], h['acquires']) == (before['top'], 0, 0)
+    assert pool.slot_pages.download(np.int32).tolist() == [-1] * (pool.max_slots * pool.max_cols)
+    h = run([2, pool.max_pages - 1, 3])         # the middle entry exceeds what the first leaves free
+    assert h['error'] == 2 and h['leased'] == 5 and h['acquires'] == 5
+    table = pool.slot_pages.download(np.int32).reshape(pool.max_slots, pool.max_cols)
+    assert table[slots[0], :2].tolist() == [0, 1] and table[slots[1]].tolist() == [-1] * pool.max_cols
+    # the third pop finds 2 free pages (slab 0's 3, 2), opens slab 1 on top
+    assert table[slots[2], :3].tolist() == [4, 5, 6]
+    # leave the pool consistent for close(): the host mirrors never saw these pops
+    pool._call('mt_pool_release_rows', [P, I, I, I], pool.slots_ptr(slots[0]), 1, 0, 1)
+    pool._call('mt_pool_release_rows', [P, I, I, I], pool.slots_ptr(slots[2]), 1, 0, 1)
+    runtime().synchronize()
+    assert pool.header()['leased'] == 0
+    for c in caches:
+        c.close()
     pool.close()
