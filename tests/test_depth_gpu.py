@@ -37,9 +37,11 @@ pytestmark = pytest.mark.gpu
 
 # project/benchmark_inference.py:78
 GATE = {'float32': .003, 'float16': .03, 'bfloat16': .15}
-# normwise ||got - fp64|| / ||fp64|| of one row's logits; a layer or row
-# mix-up moves a row's logits by about their own norm
-NORMWISE = {'float16': 0.02, 'bfloat16': 0.08}
+# normwise ||got - fp64|| / ||fp64|| of one row's logits: measured on MI355X
+# at most 0.0009 (fp16, 6 layers) and 0.0090 (bf16, 24 layers) over every
+# row count here; a layer or row mix-up moves a row's logits by about their
+# own norm
+NORMWISE = {'float16': 0.005, 'bfloat16': 0.03}
 
 ARCH = {
     'distilgpt2': dict(n_vocab=50257, n_embd=768, n_head=12, n_layer=6, n_positions=1024),
@@ -188,14 +190,13 @@ def test_merged_step_logits_at_depth(arch):
         for r in range(len(full)):
             check(got[r], full[r], tol, f'merged row {r} vs full forward')
         pool.close()
-    for r in (0, 23):
-        ref = oracle_logits(model, state64, seqs[r], [])[0]
-        check(got[r], ref, tol, f'decode row {r} vs fp64 oracle')
-        assert normwise(got[r], ref) <= NORMWISE[dtype]
-    for j, p in enumerate(new_prompts):
-        ref = oracle_logits(model, state64, p, [])[0]
-        check(got[24 + j], ref, tol, f'prompt {j} vs fp64 oracle')
-        assert normwise(got[24 + j], ref) <= NORMWISE[dtype]
+    worst = 0.0
+    for r, seq in [(0, seqs[0]), (23, seqs[23])] + [(24 + j, p) for j, p in enumerate(new_prompts)]:
+        ref = oracle_logits(model, state64, seq, [])[0]
+        check(got[r], ref, tol, f'row {r} vs fp64 oracle')
+        worst = max(worst, normwise(got[r], ref))
+        assert normwise(got[r], ref) <= NORMWISE[dtype], r
+    print(f'{arch} {dtype} merged step: normwise vs fp64 {worst:.4f}')
 
 
 def test_gpt2_medium_fp32_greedy_tokens_match_oracle():
