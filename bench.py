@@ -214,6 +214,71 @@ def time_launches(fn, calls, steps, warmup):
     return end.seconds_since(start) / steps
 
 
+def dropin_config2(case, devs, steps, warmup):
+    """Config 2 through ``mt_paged_decode_batch``, the entry the reference's
+    decode binds (minitorch/paged_decode.py:65-69): the same rotated pools,
+    no host work list, the kernel's own visiting order. Returns the launch
+    time and its roofline."""
+    from minitorch_amd.dtypes import dtype_code
+    fn = paged_ops.paged_library().mt_paged_decode_batch
+    fn.argtypes, fn.restype = [P] * 7 + [I] * 10, I
+    kw = devs[0].kwargs()
+    calls = [(d.out.ptr, d.q.ptr, d.k.ptr, d.v.ptr, d.slab_table.ptr, d.block_table.ptr, d.offsets.ptr,
+              kw['b'], kw['h'], kw['d'], kw['page_size'], kw['pages_per_slab'], kw['num_slabs'],
+              kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype'])) for d in devs]
+    per = time_launches(fn, calls, steps, warmup)
+    nbytes = algorithmic_bytes(case)
+    achieved = nbytes / per / 1e9
+    return dict(entry='mt_paged_decode_batch (reference ABI, include/mt_paged.h)',
+                ms_per_step=per * 1e3, tokens_per_sec=case.batch / per,
+                roofline={'bound': 'hbm', 'achieved': achieved, 'peak': PEAK_HBM_GBS, 'unit': 'GB/s',
+                          'frac': achieved / PEAK_HBM_GBS, 'traffic': None,
+                          'algorithmic_bytes_per_launch': nbytes})
+
+
+def bench_entries(args):
+    """The decode entries side by side on config 2 and on a prologue-bound
+    case of the same shape (every context 16 tokens, one page): the split
+    entry with a host work list (longest first), the split entry in batch
+    order, and the reference-ABI mt_paged_decode_batch (its own order);
+    mean launch time from HIP events over rotated pools."""
+    from minitorch_amd.workloads import make_decode_case
+    from minitorch_amd.runtime import RawDeviceBuffer
+    from minitorch_amd.dtypes import dtype_code
+    rt = runtime()
+    split_fn = paged_ops.paged_library().mt_paged_decode_split
+    split_fn.argtypes, split_fn.restype = paged_ops.SPLIT_ARGTYPES, I
+    batch_fn = paged_ops.paged_library().mt_paged_decode_batch
+    batch_fn.argtypes, batch_fn.restype = [P] * 7 + [I] * 10, I
+    cases = {'config2': config2_case(args.seed),
+             'one_page_rows': make_decode_case(args.seed, batch=64, heads=12, dim=64, page_size=16,
+                                               lengths=[16] * 64, pool_pages=8192, pages_per_slab=64,
+                                               dtype='float16', columns=64)}
+    out = {}
+    for name, case in cases.items():
+        devs = [DevicePagedCase(case) for _ in range(args.pools)]
+        kw = devs[0].kwargs()
+        split = paged_ops.split_tokens_for(page_size=case.page_size, columns=case.columns)
+        work, items, merges = paged_ops.decode_work_list(case.lengths, case.heads, split, rt.compute_units())
+        order = RawDeviceBuffer(4 * len(work))
+        order.upload(work)
+        base = [(d.out.ptr, d.q.ptr, d.k.ptr, d.v.ptr, d.slab_table.ptr, d.block_table.ptr, d.offsets.ptr,
+                 kw['b'], kw['h'], kw['d'], kw['page_size'], kw['pages_per_slab'], kw['num_slabs'],
+                 kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype'])) for d in devs]
+        tail = (split, args.unroll, args.waves, 0)
+        times = {
+            'split_work_list': time_launches(split_fn, [c + tail + (order.ptr, items, merges, None, 0)
+                                                        for c in base], args.steps, args.warmup),
+            'split_batch_order': time_launches(split_fn, [c + tail + (None, 0, 0, None, 0) for c in base],
+                                               args.steps, args.warmup),
+            'decode_batch': time_launches(batch_fn, base, args.steps, args.warmup),
+        }
+        nbytes = algorithmic_bytes(case)
+        out[name] = {k: dict(us_per_launch=t * 1e6, frac=nbytes / t / 1e9 / PEAK_HBM_GBS) for k, t in times.items()}
+        del devs, order
+    return {'entries': out, 'pools_rotated': args.pools, 'steps': args.steps}
+
+
 def bench_config5(args):
     """Config 5: B=512, H=25, D=64, bf16, contexts lognormal(ln 256, 1.2)
     clipped to [1, 8192], page 16 and 32; contexts over 1024 tokens take the
@@ -244,6 +309,11 @@ def bench_config5(args):
                 kw['pages_per_slab'], kw['num_slabs'], kw['columns'], kw['layer'], kw['layers'],
                 dtype_code(kw["dtype"]), split, args.unroll, args.waves, 0, *work_args, ws.ptr, ws_bytes)
         per = time_launches(fn, [call], min(args.steps, 50), min(args.warmup, 5))
+        # the reference-ABI entry on the same case: no work list, its own
+        # workspace and visiting order
+        batch_fn = paged_ops.paged_library().mt_paged_decode_batch
+        batch_fn.argtypes, batch_fn.restype = [P] * 7 + [I] * 10, I
+        per_batch = time_launches(batch_fn, [call[:17]], min(args.steps, 50), min(args.warmup, 5))
         s = 2
         L = case.lengths
         nbytes = (512 * 25 * 64 * 2 * (s + s) + int((2 * L * 25 * 64 * s).sum()) + 512 * 25 * 64 * (s + s)
@@ -251,7 +321,10 @@ def bench_config5(args):
         lines[page_size] = dict(ms_per_step=per * 1e3, tokens_per_sec=512 / per,
                                 achieved_gbs=nbytes / per / 1e9, frac=nbytes / per / 1e9 / PEAK_HBM_GBS,
                                 algorithmic_bytes=nbytes, columns=case.columns,
-                                rows_over_1024=int((L > 1024).sum()), max_context=int(L.max()))
+                                rows_over_1024=int((L > 1024).sum()), max_context=int(L.max()),
+                                dropin=dict(entry='mt_paged_decode_batch', ms_per_step=per_batch * 1e3,
+                                            achieved_gbs=nbytes / per_batch / 1e9,
+                                            frac=nbytes / per_batch / 1e9 / PEAK_HBM_GBS))
         if page_size == 16 and not args.no_cpu_baseline:
             lines['cpu_baseline'] = ragged_cpu_baseline(case, args.cpu_seconds)
         del case, ws, order
@@ -783,6 +856,11 @@ def main():
     ap.add_argument('--concurrent', type=int, default=128, help='config 4: requests decoded every step')
     ap.add_argument('--projections', action='store_true',
                     help='time the decode projections (projection kernel vs hipBLASLt) at several batch sizes')
+    ap.add_argument('--entries', action='store_true',
+                    help='time the decode entries (work list, batch order, mt_paged_decode_batch) on config 2 '
+                         'and on one-page rows of the same shape')
+    ap.add_argument('--no-config5', action='store_true',
+                    help='default line: skip config 5 (ragged bf16 decode at page sizes 16 and 32)')
     ap.add_argument('--no-e2e', action='store_true',
                     help='default line: skip the end-to-end configs 3 and 4 and config 1')
     args = ap.parse_args()
@@ -804,6 +882,9 @@ def main():
         return
     if args.config == 5:
         print(json.dumps(bench_config5(args)), flush=True)
+        return
+    if args.entries:
+        print(json.dumps(bench_entries(args)), flush=True)
         return
     if args.prefill:
         print(json.dumps(bench_prefill(args)), flush=True)
@@ -900,7 +981,13 @@ def main():
         result['pattern_ceiling'] = pattern_ceiling(case, devs, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         result['cpu_baseline'] = cpu_baseline(case, args.cpu_seconds)
+    result['dropin'] = dropin_config2(case, devs, args.steps, args.warmup)
     del devs, calls, ws, order
+    if not args.no_config5:
+        print('config 5 (page sizes 16 and 32)', file=sys.stderr, flush=True)
+        c5 = bench_config5(args)
+        result['config5'] = {k: c5[k] for k in ('config', 'ms_per_step', 'value', 'unit', 'roofline',
+                                                'page_size_16', 'page_size_32', 'cpu_baseline')}
     if not args.no_e2e:
         print('config 1, then end-to-end configs 3 and 4', file=sys.stderr, flush=True)
         result['config1'] = config1_times(args)

@@ -40,11 +40,17 @@ int mt_paged_attention(void* out, const void* q, const uint64_t* slabs, const in
 /* Ragged batched decode: q/k/v/out [b, h, 1, d]; offsets[b] (device) are the
  * committed lengths. Appends k/v at position offsets[i] of request i, then
  * attends its offsets[i] + 1 keys. One fused append + attention launch, plus
- * a split-reduction launch when the table is longer than one context split;
- * the split partials live in a library-owned device workspace, one per
- * device, kept until the process ends and grown stream-ordered on the null
- * stream (hipMallocAsync / hipFreeAsync, no device synchronization) when a
- * table needs more; status 2 if it cannot grow.
+ * a split-reduction launch when the table is longer than one context split
+ * (1024 tokens). When no row can split and b <= 256, every workgroup ranks
+ * the rows by offsets[] on the device and visits them longest first (the
+ * order mt_paged_decode_split takes from a host work list); otherwise rows
+ * are visited in batch order. The split partials live in a library-owned
+ * device workspace, one per (host thread, device) -- so calls from several
+ * host threads, each on its own default stream, never share one -- kept
+ * until the thread exits and grown stream-ordered on the calling thread's
+ * default stream (hipMallocAsync / hipFreeAsync, no device synchronization)
+ * when a table needs more; status 2 if it cannot grow. Tables of at most 1024
+ * tokens allocate nothing.
  * Replaces reference mt_paged_decode_batch (src/paged_attention_kernel.cu:121-137). */
 int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v,
                           const uint64_t* slabs, const int* table, const int* offsets, int b,

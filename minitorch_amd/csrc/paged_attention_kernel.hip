@@ -438,7 +438,18 @@ struct DecodeArgs {
   int work_items;
   int merge_rows;
   int64_t qkv_stride;  // elements between the rows of q, k and v (h * d when contiguous)
+  // Without a work list and with one split per row: when rank_rows is set,
+  // every workgroup ranks the batch's rows by context length from `offsets`
+  // (longest first, ties by row) into dynamic LDS and visits them in the
+  // order a host work list would give -- passes of rank_per rows, every
+  // other pass reversed. Needs 2 * (batch rounded up to 4) ints of dynamic LDS.
+  int rank_rows;
+  int rank_per;
 };
+
+// Rows a decode workgroup ranks on its own (the ranking costs each thread
+// batch / threads * batch LDS reads).
+constexpr int kRankRows = 256;
 
 // Stream one wave's share of a split: row-blocks j = wave + waves * i
 // (16 tokens each) of tokens [t0, t0 + ntok). Lane s of the wave holds in
@@ -519,8 +530,15 @@ __device__ __forceinline__ void stream_wave(Softmax<D / G, G>& st, const Query<D
 // Fused KV append + decode attention over (request, head, split) items.
 // Items come from the work list when one is given (visiting order chosen by
 // the caller, e.g. longest first), else from the full (split, row, head) grid.
+// 8-wave fp16/bf16 workgroups at D = 64 (config 2's shape) are meant to be
+// resident three per compute unit, i.e. six waves per SIMD and at most 80
+// VGPRs: one VGPR more drops a whole workgroup per compute unit (and the
+// launcher then picks 4-wave workgroups), so the bound is stated. Other
+// shapes need more registers and keep the compiler's choice.
 template <int DT, int D, bool VEC, int U, int STAGES, int WAVES, int G>
-__global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(WAVES * kWave)
+__attribute__((amdgpu_waves_per_eu(WAVES == 8 && D == 64 && VEC && DT != kF32 && U <= 2 ? 6 : 1)))
+void decode_kernel(DecodeArgs a) {
   using T = typename Elem<DT>::T;
   constexpr int DL = D / G;
   constexpr int RB = kWave / G;
@@ -558,7 +576,48 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
     }
     slabs_loaded = true;
   };
-  if (lds_slabs && (a.work || blockIdx.x < bh_count)) load_slabs();
+  if (lds_slabs && (a.work || a.rank_rows || blockIdx.x < bh_count)) load_slabs();
+  // In-kernel longest-first order (see DecodeArgs::rank_rows): s_len holds
+  // the offsets, s_order[k] the row of rank k; (length desc, row asc) is a
+  // strict order, so the ranks are a permutation whatever the offsets hold.
+  // s_len is padded to a multiple of 4 rows with INT_MIN, which no row
+  // ranks behind, and read 4 rows per LDS load. Each row's rank is counted
+  // by tpr consecutive lanes (the largest power of two up to 64 with
+  // tpr * batch <= threads), each over its own slice of the candidates, and
+  // summed with lane shuffles: the count runs on every wave, not one.
+  extern __shared__ __align__(16) int s_rank[];
+  const int len4 = (a.batch + 3) & ~3;
+  int* const s_len = s_rank;
+  int* const s_order = s_rank + len4;
+  if (a.rank_rows) {
+    for (int r = tid; r < len4; r += NT) s_len[r] = r < a.batch ? a.offsets[r] : INT_MIN;
+    __syncthreads();
+    const int4* len_v = reinterpret_cast<const int4*>(s_len);
+    int tpr = 1;
+    while (tpr < kWave && 2 * tpr * a.batch <= NT) tpr *= 2;
+    const int n4 = len4 / 4;
+    const int per_part = (n4 + tpr - 1) / tpr;  // int4 candidates per lane
+    for (int t0 = 0; t0 < a.batch * tpr; t0 += NT) {
+      const int t = t0 + tid;
+      const int r = t / tpr, part = t - r * tpr;
+      int rank = 0;
+      if (r < a.batch) {
+        const int lr = s_len[r];
+        const int c1 = min(n4, (part + 1) * per_part);
+        for (int q4 = part * per_part; q4 < c1; ++q4) {
+          const int4 l = len_v[q4];
+          const int q = 4 * q4;
+          rank += (l.x > lr) | ((l.x == lr) & (q < r));
+          rank += (l.y > lr) | ((l.y == lr) & (q + 1 < r));
+          rank += (l.z > lr) | ((l.z == lr) & (q + 2 < r));
+          rank += (l.w > lr) | ((l.w == lr) & (q + 3 < r));
+        }
+      }
+      for (int o = 1; o < tpr; o <<= 1) rank += __shfl_xor(rank, o);
+      if (r < a.batch && part == 0) s_order[rank] = r;
+    }
+    __syncthreads();
+  }
   const int wave = tid >> 6;
   const int lane = tid & (kWave - 1);
   const int col0 = (lane % G) * DL;
@@ -581,6 +640,14 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
       b = int(uint32_t(e));
       split = int(uint32_t(e >> 32));
       if (!((unsigned(b) < unsigned(a.batch)) & (unsigned(split) < unsigned(a.nsplit_max)))) continue;
+    } else if (a.rank_rows) {
+      // item = (visiting position, head); one split per row
+      const int pos = int(item / g.heads);
+      head = int(item - int64_t(pos) * g.heads);
+      const int pass = pos / a.rank_per, within = pos - pass * a.rank_per;
+      const int width = min(a.rank_per, a.batch - pass * a.rank_per);
+      b = s_order[pass * a.rank_per + ((pass & 1) ? width - 1 - within : within)];
+      split = 0;
     } else {
       split = int(item / bh_count);
       const int64_t bhi = item - int64_t(split) * bh_count;
@@ -605,7 +672,7 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeArgs a) {
     qv.load(qp + qrow, col0, dim, a.qscale);
     T new_k{}, new_v{};
     if (tid < dim) { new_k = kin[qrow + tid]; new_v = vin[qrow + tid]; }
-    const int offset = a.offsets[b];
+    const int offset = a.rank_rows ? s_len[b] : a.offsets[b];
 
     const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
     T* orow = out + bh * dim;
@@ -1551,14 +1618,15 @@ hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
   }
   // Requests between the supported values round down (3 -> 2, 5+ -> 4).
   unroll = unroll >= 4 ? 4 : unroll >= 2 ? 2 : 1;
+  const size_t rank_lds = a.rank_rows ? size_t(2) * ((a.batch + 3) & ~3) * sizeof(int) : 0;
   if (unroll > kMaxUnroll) unroll = kMaxUnroll;
   if constexpr (kMaxUnroll >= 4) {
-    if (unroll == 4) decode_kernel<DT, D, VEC, 4, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
+    if (unroll == 4) decode_kernel<DT, D, VEC, 4, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
   }
   if constexpr (kMaxUnroll >= 2) {
-    if (unroll == 2) decode_kernel<DT, D, VEC, 2, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
+    if (unroll == 2) decode_kernel<DT, D, VEC, 2, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
   }
-  if (unroll == 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G><<<grid_for(blocks), NT>>>(a);
+  if (unroll == 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
   hipError_t e = hipGetLastError();
   const int64_t merge_rows = a.work ? a.merge_rows : a.batch;
   if (e != hipSuccess || a.nsplit_max == 1 || merge_rows == 0) return e;
@@ -1601,7 +1669,8 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
                   const int* table, const int* offsets, int b, int h, int d, int page_size,
                   int pps, int num_slabs, int columns, int layer, int layers, int dtype,
                   int split_tokens, int unroll, int waves, int qkv_stride, const int* work,
-                  int work_items, int merge_rows, void* workspace, size_t workspace_bytes) {
+                  int work_items, int merge_rows, void* workspace, size_t workspace_bytes,
+                  bool rank_order = false) {
   const int64_t cap = int64_t(columns) * page_size;
   // A work list is built for one split length, so it must be given.
   if (work && split_tokens <= 0) return hipErrorInvalidValue;
@@ -1630,6 +1699,12 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   a.work = work;
   a.work_items = work ? work_items : 0;
   a.merge_rows = work ? merge_rows : 0;
+  // Entries without a work list visit rows longest first when every row has
+  // one split and the batch is small enough to rank in each workgroup.
+  if (rank_order && !work && nsplit_max == 1 && b <= kRankRows) {
+    a.rank_rows = 1;
+    a.rank_per = std::max(1, device_compute_units() / h);
+  }
   if (dtype == kF32) return launch_decode_dt<kF32>(a, a.items, vec, d, unroll, waves);
   if (dtype == kF16) return launch_decode_dt<kF16>(a, a.items, vec, d, unroll, waves);
   if (dtype == kBF16) return launch_decode_dt<kBF16>(a, a.items, vec, d, unroll, waves);
@@ -1639,23 +1714,37 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
 // Library-owned split workspace of the reference entry points, which have no
 // workspace argument (mt_paged_decode_batch for tables longer than one split,
 // the key-split prefill of mt_paged_attention / mt_paged_prefill). One buffer
-// per device, kept until the process ends. It grows stream-ordered on the
-// calling thread's default stream, where every launch of this library runs
-// (the libraries are built with per-thread default streams): hipMallocAsync for
-// the larger buffer and hipFreeAsync for the old one, which is released only
-// after the work queued before it, so growing neither synchronizes the device
-// nor blocks the host. Callers that cannot allocate use mt_paged_decode_split
-// with their own workspace.
-std::mutex g_ws_mutex;
-std::vector<std::pair<void*, size_t>> g_ws;
+// per (host thread, device): every launch of these libraries goes to the
+// calling thread's default stream (they are built with per-thread default
+// streams), so a buffer private to the thread is private to the stream its
+// kernels run on, and calls from several host threads never share one. It
+// grows stream-ordered on that stream: hipMallocAsync for the larger buffer
+// and hipFreeAsync for the old one, which is released only after the work
+// queued before it, so growing neither synchronizes the device nor blocks the
+// host. A thread's buffers are released (stream-ordered) when it exits.
+// Callers that cannot allocate use mt_paged_decode_split with their own
+// workspace, or mt_paged_decode_batch_noalloc.
+struct ThreadWorkspaces {
+  std::vector<std::pair<void*, size_t>> per_device;
+  ~ThreadWorkspaces() {
+    int current = 0;
+    if (hipGetDevice(&current) != hipSuccess) return;
+    for (size_t dev = 0; dev < per_device.size(); ++dev) {
+      if (!per_device[dev].first || hipSetDevice(int(dev)) != hipSuccess) continue;
+      (void)hipFreeAsync(per_device[dev].first, hipStreamPerThread);
+    }
+    (void)hipSetDevice(current);
+  }
+};
+thread_local ThreadWorkspaces t_workspaces;
 
 int library_workspace(size_t bytes, void** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
-  std::lock_guard<std::mutex> lock(g_ws_mutex);
-  if (g_ws.size() <= size_t(dev)) g_ws.resize(dev + 1, {nullptr, 0});
-  auto& slot = g_ws[dev];
+  auto& ws = t_workspaces.per_device;
+  if (ws.size() <= size_t(dev)) ws.resize(dev + 1, {nullptr, 0});
+  auto& slot = ws[dev];
   if (slot.second < bytes) {
     void* p = nullptr;
     e = hipMallocAsync(&p, bytes, hipStreamPerThread);
@@ -2132,7 +2221,7 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
   }
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, S, 0, 0, 0,
-                       nullptr, 0, 0, ws, ws_bytes);
+                       nullptr, 0, 0, ws, ws_bytes, true);
 }
 
 int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const void* v,
@@ -2158,7 +2247,7 @@ int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const
   }
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, S, 0, 0, 0,
-                       nullptr, 0, 0, ws, nsplit_max > 1 ? kNoAllocScratchBytes : 0);
+                       nullptr, 0, 0, ws, nsplit_max > 1 ? kNoAllocScratchBytes : 0, true);
 }
 
 int mt_paged_prefill_key_splits(long long* launches) {

@@ -351,3 +351,27 @@ def test_multi_token_append_and_causal_attention(dtype):
     ref = po.image_paged_attention(image, CODES[dtype], case.table, case.columns, q, 0, offset,
                                    offset + n)
     assert_attention_close(out.to_numpy(), ref, dtype)
+
+
+@pytest.mark.parametrize('batch', [4, 200, 256, 257])
+def test_decode_batch_device_ranked_order(batch):
+    # Without a host work list mt_paged_decode_batch ranks the rows by their
+    # offsets inside every workgroup (b <= 256, one split per row) and visits
+    # them longest first in passes of compute_units / heads rows, every other
+    # pass reversed; 257 rows take batch order. Many equal lengths (ties go
+    # by row), an empty row (offset -1: zero output, no append) and a row past
+    # its table (NaN output, no append) keep the ranking a permutation: every
+    # (row, head) is written once, equal to the oracle, and the pool image
+    # matches bit for bit.
+    import dataclasses
+    rng = np.random.default_rng([17, batch])
+    lengths = rng.choice([1, 16, 17, 64, 200, 1024], size=batch)
+    case = make_decode_case(17, batch=batch, heads=3, dim=64, page_size=16, lengths=lengths,
+                            pool_pages=int(((lengths + 15) // 16).sum()) // 8 * 8 + 8, pages_per_slab=8,
+                            dtype='float16', columns=64)
+    lengths = case.lengths.copy()
+    lengths[1] = 0                     # offset -1
+    lengths[batch - 2] = 64 * 16 + 5   # beyond the 64-column table
+    case = dataclasses.replace(case, lengths=lengths)
+    dev, out = check_case(case)
+    assert np.all(out[1] == 0) and np.all(np.isnan(out[batch - 2]))
