@@ -772,6 +772,43 @@ def bench_e2e(args):
             'measurements': r}
 
 
+# The reference's published DistilGPT-2 figures (pretrained weights, fp32, one
+# RTX 4060 Laptop GPU; README.md:267-281, docs/images/01_inference_modes.png,
+# docs/images/02_continuous_batching.png): context beside this build's
+# numbers, not a target.
+REFERENCE_PUBLISHED = {
+    'hardware': 'RTX 4060 Laptop GPU 8 GB, fp32, pretrained DistilGPT-2',
+    'trace': {'serial': {'output_tokens_per_sec': 87.60, 'ttft_p50_ms': 289.16, 'ttft_p95_ms': 483.22,
+                         'kv_reserved_peak_mib': 20.25},
+              'continuous': {'output_tokens_per_sec': 184.92, 'ttft_p50_ms': 40.47, 'ttft_p95_ms': 89.31,
+                             'max_decode_batch_size': 4, 'mean_decode_batch_size': 2.84,
+                             'kv_reserved_peak_mib': 36.00},
+              'continuous_vs_serial': 2.11},
+    'inference_modes_paged': {'32': {'decode_tokens_per_sec': 84.77, 'output_tokens_per_sec': 83.87,
+                                     'median_ttft_ms': 13.47},
+                              '128': {'decode_tokens_per_sec': 86.41, 'output_tokens_per_sec': 84.66,
+                                      'median_ttft_ms': 15.76},
+                              '256': {'decode_tokens_per_sec': 87.62, 'output_tokens_per_sec': 84.46,
+                                      'median_ttft_ms': 18.13},
+                              '512': {'decode_tokens_per_sec': 92.30, 'output_tokens_per_sec': 78.86,
+                                      'median_ttft_ms': 40.40}},
+}
+
+
+def reference_scenarios(args):
+    """The reference's two published scenarios on random-init DistilGPT-2 in
+    fp32 (minitorch_amd.e2e.run_reference_scenarios): the serial vs
+    continuous trace and batch-1 paged inference at 32-512-token prompts, 1
+    warmup and 3 measured runs each, beside the reference's own figures."""
+    from minitorch_amd import e2e, model as model_mod
+    model = model_mod.distilgpt2(seed=args.seed)
+    r = e2e.run_reference_scenarios(model, seed=args.seed)
+    r['workload'] = ('DistilGPT-2 architecture, random-init weights, synthetic prompt IDs of the reference '
+                     'lengths, fp32, KV budget 256 MiB, pages of 16 tokens, 4 pages per slab')
+    r['reference_published'] = REFERENCE_PUBLISHED
+    return r
+
+
 def e2e_summary(r3, r4):
     """The end-to-end figures of configs 3 and 4 for the default line."""
     out = {}
@@ -859,6 +896,9 @@ def main():
     ap.add_argument('--entries', action='store_true',
                     help='time the decode entries (work list, batch order, mt_paged_decode_batch) on config 2 '
                          'and on one-page rows of the same shape')
+    ap.add_argument('--reference-scenarios', action='store_true',
+                    help="the reference's published DistilGPT-2 scenarios (serial vs continuous trace, "
+                         'batch-1 paged inference at 32-512-token prompts) and its figures beside them')
     ap.add_argument('--no-config5', action='store_true',
                     help='default line: skip config 5 (ragged bf16 decode at page sizes 16 and 32)')
     ap.add_argument('--no-e2e', action='store_true',
@@ -885,6 +925,9 @@ def main():
         return
     if args.entries:
         print(json.dumps(bench_entries(args)), flush=True)
+        return
+    if args.reference_scenarios:
+        print(json.dumps(reference_scenarios(args)), flush=True)
         return
     if args.prefill:
         print(json.dumps(bench_prefill(args)), flush=True)
@@ -992,6 +1035,8 @@ def main():
         print('config 1, then end-to-end configs 3 and 4', file=sys.stderr, flush=True)
         result['config1'] = config1_times(args)
         result['e2e'] = e2e_summary(e2e_config3(args), e2e_config4(args))
+        print('reference scenarios', file=sys.stderr, flush=True)
+        result['reference_scenarios'] = reference_scenarios(args)
     print(json.dumps(result), flush=True)
 
 

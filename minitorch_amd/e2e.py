@@ -266,3 +266,190 @@ class _null:
 
     def __exit__(self, *a):
         return False
+
+
+# The reference's published serial-vs-continuous trace
+# (project/benchmark_continuous_batching.py:26-33): request id, arrival (ms
+# after the start), prompt tokens, new tokens.
+REFERENCE_TRACE = (('A', 0, 32, 12), ('B', 0, 128, 8), ('C', 30, 256, 16), ('D', 60, 512, 8),
+                   ('E', 100, 32, 12), ('F', 180, 128, 4))
+REFERENCE_PROMPT_LENGTHS = (32, 128, 256, 512)   # project/benchmark_inference.py:26
+
+
+def reference_prompts(seed, vocab, lengths=REFERENCE_PROMPT_LENGTHS):
+    """One prompt of random token IDs per length. The reference tokenizes a
+    fixed prose text to these lengths (project/benchmark_inference.py:36-52);
+    its tokenizer files are not available here, so the IDs are synthetic."""
+    rng = np.random.default_rng([seed, 9])
+    return {n: rng.integers(0, vocab, n).tolist() for n in lengths}
+
+
+def independent_tokens(model, prompt, new_tokens, precision='fp32'):
+    """Greedy tokens of one request by prefill then decode_step on its own
+    paged cache (the reference's untimed validation generation,
+    project/benchmark_continuous_batching.py:50-66)."""
+    from .amp import autocast as _autocast
+    ctx = _autocast('float16' if precision == 'fp16' else 'bfloat16') if precision != 'fp32' else None
+    if ctx:
+        ctx.__enter__()
+    try:
+        cache = model.create_kv_cache(1, len(prompt) + new_tokens - 1)
+        logits, _ = model.prefill(DeviceTensor.from_numpy(np.array([prompt], np.float32)), cache)
+        out = []
+        for step in range(new_tokens):
+            if step:
+                logits = model.decode_step(token, cache)
+            token = greedy_token(logits)
+            out.append(int(token.to_numpy()[0, 0]))
+        cache.close()
+        return out
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+
+
+def run_reference_trace(model, prompts, *, mode, precision='fp32', max_batch_size=4, page_size=16,
+                        budget_bytes=256 * 1024 ** 2, pages_per_slab=4, max_prefills_per_step=1,
+                        prefill_token_budget=512, trace=REFERENCE_TRACE, clock=time.perf_counter):
+    """One run of the reference's trace (project/benchmark_continuous_batching.py:69-138):
+    ``serial`` is the batcher at max_batch_size 1, ``continuous`` at
+    ``max_batch_size``; requests are submitted when their arrival time has
+    passed on the wall clock, the batcher steps while it has work, TTFT is
+    counted from each request's scheduled arrival, throughput is generated
+    tokens / (end - start) with the idle arrival gaps included."""
+    if mode not in ('serial', 'continuous'):
+        raise ValueError('Unknown benchmark mode')
+    batcher = ContinuousBatcher(model, precision=precision, max_batch_size=1 if mode == 'serial' else max_batch_size,
+                                page_size=page_size, kv_budget_bytes=budget_bytes, pages_per_slab=pages_per_slab,
+                                max_prefills_per_step=max_prefills_per_step,
+                                prefill_token_budget=prefill_token_budget, clock=clock)
+    pending = sorted(trace, key=lambda r: r[1])
+    steps = []
+    runtime().synchronize()
+    start = clock()
+    index = 0
+    while index < len(pending) or batcher.has_work:
+        elapsed_ms = (clock() - start) * 1e3
+        while index < len(pending) and pending[index][1] <= elapsed_ms:
+            rid, _, n, new = pending[index]
+            batcher.submit(rid, np.array(prompts[n]), max_new_tokens=new)
+            index += 1
+        if not batcher.has_work:
+            if index < len(pending):
+                time.sleep(min(1e-3, max(0.0, pending[index][1] / 1e3 - (clock() - start))))
+            continue
+        batcher.step()
+        steps.append(dict(batcher.last_step))
+    end = clock()
+    rows = {}
+    for rid, arrival_ms, n, new in trace:
+        r = batcher.requests[rid]
+        scheduled = start + arrival_ms / 1e3
+        rows[rid] = dict(state=r.state, tokens=list(r.output_ids),
+                         ttft_ms=(r.token_times[0] - scheduled) * 1e3 if r.token_times else None)
+    stats = batcher.pool.memory_stats()
+    counts = [s['decode_batch_size'] for s in steps if s['decode_batch_size']]
+    ttft = [v['ttft_ms'] for v in rows.values() if v['ttft_ms'] is not None]
+    generated = sum(len(v['tokens']) for v in rows.values())
+    summary = dict(mode=mode, elapsed_seconds=end - start, generated_tokens=generated,
+                   output_tokens_per_sec=generated / (end - start),
+                   completed_requests=sum(v['state'] == 'completed' for v in rows.values()),
+                   ttft_ms=ttft, max_decode_batch_size=max(counts, default=0),
+                   mean_decode_batch_size=float(np.mean(counts)) if counts else 0.0,
+                   peak_used_pages=batcher.peak_used_pages,
+                   kv_pool_reserved_bytes=stats['kv_pool_reserved_bytes'],
+                   kv_pool_physical_bytes=stats['kv_pool_physical_bytes'],
+                   kv_pool_used_pages_after=stats['kv_pool_used_pages'],
+                   reserved_pages_after=batcher.reserved_pages)
+    batcher.close()
+    return summary, rows
+
+
+def run_reference_scenarios(model, *, seed=0, precision='fp32', warmup=1, repeats=3, max_batch_size=4,
+                            new_tokens=16):
+    """The reference's two published DistilGPT-2 scenarios on this build:
+
+    * the serial (max batch 1) vs continuous (max batch 4) trace, 1 warmup and
+      ``repeats`` measured runs with the mode order alternating per run
+      (project/benchmark_continuous_batching.py:171-178,193-211): tok/s over
+      the measured runs, TTFT p50/p95 over their requests, max and mean
+      non-empty decode batch, KV reserved peak (logical, the reference's
+      figure, and physical), pages left after the run, and every completed
+      request's tokens against independent generation;
+    * batch-1 paged inference at prompts of 32/128/256/512 tokens with
+      ``new_tokens`` new tokens (project/benchmark_inference.py:92-175):
+      TTFT from before the cache is created to the first token on the host,
+      end-to-end tok/s = new tokens / request time, decode tok/s = (new
+      tokens - 1) / time from the first to the last token, medians and sums
+      over the measured runs, and the tokens against independent generation."""
+    prompts = reference_prompts(seed, model.n_vocab)
+    gold = {rid: independent_tokens(model, prompts[n], new, precision) for rid, _, n, new in REFERENCE_TRACE}
+    runs = {'serial': [], 'continuous': []}
+    parity = True
+    for repeat in range(warmup + repeats):
+        order = ('serial', 'continuous') if repeat % 2 == 0 else ('continuous', 'serial')
+        for mode in order:
+            summary, rows = run_reference_trace(model, prompts, mode=mode, precision=precision,
+                                                max_batch_size=max_batch_size)
+            parity &= all(v['tokens'] == gold[rid] for rid, v in rows.items() if v['state'] == 'completed')
+            if repeat >= warmup:
+                runs[mode].append(summary)
+    trace = {}
+    for mode, measured in runs.items():
+        seconds = sum(s['elapsed_seconds'] for s in measured)
+        ttft = [t for s in measured for t in s['ttft_ms']]
+        trace[mode] = dict(
+            output_tokens_per_sec=sum(s['generated_tokens'] for s in measured) / seconds,
+            completed_requests=sum(s['completed_requests'] for s in measured),
+            ttft_p50_ms=float(np.median(ttft)), ttft_p95_ms=float(np.percentile(ttft, 95)),
+            max_decode_batch_size=max(s['max_decode_batch_size'] for s in measured),
+            mean_decode_batch_size=float(np.mean([s['mean_decode_batch_size'] for s in measured])),
+            kv_reserved_peak_mib=max(s['kv_pool_reserved_bytes'] for s in measured) / 2 ** 20,
+            kv_physical_mib=max(s['kv_pool_physical_bytes'] for s in measured) / 2 ** 20,
+            unreturned_pages=max(s['kv_pool_used_pages_after'] for s in measured),
+            unreturned_reservations=max(s['reserved_pages_after'] for s in measured))
+    trace['continuous_vs_serial'] = trace['continuous']['output_tokens_per_sec'] / trace['serial']['output_tokens_per_sec']
+    trace['token_parity_vs_independent_generation'] = bool(parity)
+
+    modes = {}
+    for n, prompt in prompts.items():
+        gold_n = independent_tokens(model, prompt, new_tokens, precision)
+        measured, match = [], True
+        for repeat in range(warmup + repeats):
+            r = _paged_request(model, prompt, new_tokens)
+            match &= r.pop('tokens') == gold_n
+            if repeat >= warmup:
+                measured.append(r)
+        seconds = sum(r['request_seconds'] for r in measured)
+        decode = sum(r['decode_seconds'] for r in measured)
+        modes[n] = dict(median_ttft_ms=float(np.median([r['ttft_seconds'] for r in measured])) * 1e3,
+                        output_tokens_per_sec=new_tokens * len(measured) / seconds,
+                        decode_tokens_per_sec=(new_tokens - 1) * len(measured) / decode,
+                        kv_reserved_bytes=measured[-1]['kv_reserved_bytes'],
+                        tokens_match_independent_generation=bool(match))
+    return dict(precision=precision, warmup=warmup, repeats=repeats, trace=trace, inference_modes=modes)
+
+
+def _paged_request(model, prompt, new_tokens, clock=time.perf_counter):
+    """One batch-1 paged request timed as the reference's run_request
+    (project/benchmark_inference.py:92-160): the cache is created inside the
+    timed region, each step's token is read on the host."""
+    runtime().synchronize()
+    start = clock()
+    cache = model.create_kv_cache(1, len(prompt) + new_tokens - 1, page_size=16,
+                                  kv_budget_bytes=256 * 1024 ** 2, pages_per_slab=4)
+    tokens, first, ids = [], None, None
+    for step in range(new_tokens):
+        if step == 0:
+            logits, _ = model.prefill(DeviceTensor.from_numpy(np.array([prompt], np.float32)), cache)
+        else:
+            logits = model.decode_step(ids, cache)
+        ids = greedy_token(logits)
+        tokens.append(int(ids.to_numpy()[0, 0]))
+        arrival = clock()
+        if first is None:
+            first = arrival
+    reserved = cache.memory_stats()['kv_pool_reserved_bytes']
+    cache.close()
+    return dict(ttft_seconds=first - start, request_seconds=arrival - start, decode_seconds=arrival - first,
+                kv_reserved_bytes=reserved, tokens=tokens)

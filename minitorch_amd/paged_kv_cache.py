@@ -311,9 +311,15 @@ class KVPagePool:
         self._mirror_release(len(pages))
 
     def memory_stats(self):
+        """The reference's keys (minitorch/paged_kv_cache.py:105-117):
+        ``kv_pool_reserved_bytes`` counts the slabs opened so far, as the
+        reference's lazily allocated slabs would hold them. This pool holds
+        its whole budget in one device allocation from construction, which
+        ``kv_pool_physical_bytes`` reports (0 once closed)."""
         reserved = len(self._slabs) * self.slab_bytes
         assigned = self._leased_count * self.page_bytes
         return dict(kv_pool_reserved_bytes=reserved, kv_pool_assigned_bytes=assigned,
+                    kv_pool_physical_bytes=0 if self.closed else self.kv.nbytes,
                     kv_pool_free_bytes=reserved - assigned,
                     kv_pool_metadata_bytes=0 if self.closed else self.state.nbytes,
                     kv_pool_used_pages=self._leased_count, kv_pool_free_pages=len(self._free_issued),

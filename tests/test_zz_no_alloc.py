@@ -77,11 +77,31 @@ def test_noalloc_matches_decode_batch_on_consecutive_calls():
 
 
 def test_noalloc_rejects_partials_beyond_its_array():
-    f = _entry('mt_paged_decode_batch_noalloc')
     # b*h = 32768 rows, 2 splits of d' = 128 partials: 34 MB > 32 MiB, refused
-    # on the host before any launch (the pointers are never dereferenced)
-    b, h, d, psize, columns = 1024, 32, 128, 16, 128
+    # on the host before any launch. The arguments are real device buffers of
+    # the call's shapes, laid out so that even a launch would stay in bounds:
+    # every offset is 0 (one key, no row needs a split, so no partial is
+    # written), every table entry is -1 and every slab null (nothing is read
+    # from or appended to a page).
+    from minitorch_amd.runtime import RawDeviceBuffer
+    f = _entry('mt_paged_decode_batch_noalloc')
+    b, h, d, psize, columns, slabs = 1024, 32, 128, 16, 128, 64
     assert b * h * 2 * (128 + 2) * 4 > SCRATCH_BYTES
-    assert f(8, 8, 8, 8, 8, 8, 8, b, h, d, psize, 16, 64, columns, 0, 1, 1) == 1
-    # half the rows fit
+    rows = [RawDeviceBuffer(b * h * d * 2) for _ in range(4)]        # out, q, k, v: fp16 [b, h, 1, d]
+    for t in rows:
+        t.fill_words(0)
+    slab_table = RawDeviceBuffer(8 * slabs)
+    slab_table.fill_words(0)
+    table = RawDeviceBuffer(4 * b * columns)
+    table.fill_words(0xFFFFFFFF)
+    offsets = RawDeviceBuffer(4 * b)
+    offsets.fill_words(0)
+    args = [t.ptr for t in rows] + [slab_table.ptr, table.ptr, offsets.ptr]
+    assert f(*args, b, h, d, psize, 16, slabs, columns, 0, 1, 1) == 1
+    # half the rows fit: the same buffers are accepted
     assert (b // 2) * h * 2 * (128 + 2) * 4 <= SCRATCH_BYTES
+    assert f(*args, b // 2, h, d, psize, 16, slabs, columns, 0, 1, 1) == 0
+    runtime().synchronize()
+    # each row's one key is the new token, whose page is missing: a NaN row
+    out = rows[0].download(np.float16, (b // 2) * h * d)
+    assert np.all(np.isnan(out))
