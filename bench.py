@@ -250,13 +250,26 @@ def bench_entries(args):
     split_fn.argtypes, split_fn.restype = paged_ops.SPLIT_ARGTYPES, I
     batch_fn = paged_ops.paged_library().mt_paged_decode_batch
     batch_fn.argtypes, batch_fn.restype = [P] * 7 + [I] * 10, I
-    cases = {'config2': config2_case(args.seed),
-             'one_page_rows': make_decode_case(args.seed, batch=64, heads=12, dim=64, page_size=16,
-                                               lengths=[16] * 64, pool_pages=8192, pages_per_slab=64,
-                                               dtype='float16', columns=64)}
+    from minitorch_amd.e2e import config4_lengths
+    from minitorch_amd.workloads import config5_lengths, DeviceRaggedCase
+    l4 = config4_lengths(np.random.default_rng([args.seed, 4]), 128)
+    l5 = config5_lengths(args.seed, 512)
+    one_page = make_decode_case(args.seed, batch=64, heads=12, dim=64, page_size=16, lengths=[16] * 64,
+                                pool_pages=8192, pages_per_slab=64, dtype='float16', columns=64)
+    # device case lists: host-built pools for configs 2 and the one-page rows,
+    # device-filled ones (DeviceRaggedCase) for config 4's layer and config 5
+    cases = {
+        'config2': lambda: [DevicePagedCase(config2_case(args.seed)) for _ in range(args.pools)],
+        'one_page_rows': lambda: [DevicePagedCase(one_page) for _ in range(args.pools)],
+        'config4_layer': lambda: [DeviceRaggedCase(args.seed + i, batch=128, heads=16, dim=64, page_size=16,
+                                                   lengths=l4, dtype='bfloat16') for i in range(4)],
+        'config5_p16': lambda: [DeviceRaggedCase(args.seed, batch=512, heads=25, dim=64, page_size=16,
+                                                 lengths=l5, dtype='bfloat16')],
+    }
     out = {}
-    for name, case in cases.items():
-        devs = [DevicePagedCase(case) for _ in range(args.pools)]
+    for name, make in cases.items():
+        devs = make()
+        case = getattr(devs[0], 'case', devs[0])
         kw = devs[0].kwargs()
         split = paged_ops.split_tokens_for(page_size=case.page_size, columns=case.columns)
         work, items, merges = paged_ops.decode_work_list(case.lengths, case.heads, split, rt.compute_units())
@@ -265,17 +278,23 @@ def bench_entries(args):
         base = [(d.out.ptr, d.q.ptr, d.k.ptr, d.v.ptr, d.slab_table.ptr, d.block_table.ptr, d.offsets.ptr,
                  kw['b'], kw['h'], kw['d'], kw['page_size'], kw['pages_per_slab'], kw['num_slabs'],
                  kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype'])) for d in devs]
+        ws_bytes = paged_ops.decode_workspace_bytes(b=case.batch, h=case.heads, page_size=case.page_size,
+                                                    columns=case.columns, split_tokens=split)
+        ws = RawDeviceBuffer(max(ws_bytes, 4))
         tail = (split, args.unroll, args.waves, 0)
-        times = {
-            'split_work_list': time_launches(split_fn, [c + tail + (order.ptr, items, merges, None, 0)
-                                                        for c in base], args.steps, args.warmup),
-            'split_batch_order': time_launches(split_fn, [c + tail + (None, 0, 0, None, 0) for c in base],
-                                               args.steps, args.warmup),
-            'decode_batch': time_launches(batch_fn, base, args.steps, args.warmup),
-        }
+        steps = args.steps if case.batch < 512 else min(args.steps, 50)
+        times = {}
+        for schedule, label in ((1, 'items'), (2, 'persistent'), (3, 'persistent_static')):
+            paged_ops.decode_schedule(schedule)
+            times[f'split_work_list_{label}'] = time_launches(
+                split_fn, [c + tail + (order.ptr, items, merges, ws.ptr, ws_bytes) for c in base], steps, args.warmup)
+            times[f'split_batch_order_{label}'] = time_launches(
+                split_fn, [c + tail + (None, 0, 0, ws.ptr, ws_bytes) for c in base], steps, args.warmup)
+            times[f'decode_batch_{label}'] = time_launches(batch_fn, base, steps, args.warmup)
+        paged_ops.decode_schedule(0)
         nbytes = algorithmic_bytes(case)
         out[name] = {k: dict(us_per_launch=t * 1e6, frac=nbytes / t / 1e9 / PEAK_HBM_GBS) for k, t in times.items()}
-        del devs, order
+        del devs, order, ws
     return {'entries': out, 'pools_rotated': args.pools, 'steps': args.steps}
 
 
