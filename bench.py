@@ -237,11 +237,12 @@ def dropin_config2(case, devs, steps, warmup):
 
 
 def bench_entries(args):
-    """The decode entries side by side on config 2 and on a prologue-bound
-    case of the same shape (every context 16 tokens, one page): the split
-    entry with a host work list (longest first), the split entry in batch
-    order, and the reference-ABI mt_paged_decode_batch (its own order);
-    mean launch time from HIP events over rotated pools."""
+    """The decode entries side by side on config 2, a prologue-bound case of
+    its shape (every context 16 tokens, one page), config 4's layer shape and
+    config 5 (P = 16): the split entry with a host work list (longest first),
+    the split entry in batch order, and the reference-ABI
+    mt_paged_decode_batch (its own order); mean launch time from HIP events
+    over rotated pools (one pool for config 5, beyond the caches anyway)."""
     from minitorch_amd.workloads import make_decode_case
     from minitorch_amd.runtime import RawDeviceBuffer
     from minitorch_amd.dtypes import dtype_code
@@ -283,15 +284,13 @@ def bench_entries(args):
         ws = RawDeviceBuffer(max(ws_bytes, 4))
         tail = (split, args.unroll, args.waves, 0)
         steps = args.steps if case.batch < 512 else min(args.steps, 50)
-        times = {}
-        for schedule, label in ((1, 'items'), (2, 'persistent'), (3, 'persistent_static')):
-            paged_ops.decode_schedule(schedule)
-            times[f'split_work_list_{label}'] = time_launches(
-                split_fn, [c + tail + (order.ptr, items, merges, ws.ptr, ws_bytes) for c in base], steps, args.warmup)
-            times[f'split_batch_order_{label}'] = time_launches(
-                split_fn, [c + tail + (None, 0, 0, ws.ptr, ws_bytes) for c in base], steps, args.warmup)
-            times[f'decode_batch_{label}'] = time_launches(batch_fn, base, steps, args.warmup)
-        paged_ops.decode_schedule(0)
+        times = {
+            'split_work_list': time_launches(split_fn, [c + tail + (order.ptr, items, merges, ws.ptr, ws_bytes)
+                                                        for c in base], steps, args.warmup),
+            'split_batch_order': time_launches(split_fn, [c + tail + (None, 0, 0, ws.ptr, ws_bytes) for c in base],
+                                               steps, args.warmup),
+            'decode_batch': time_launches(batch_fn, base, steps, args.warmup),
+        }
         nbytes = algorithmic_bytes(case)
         out[name] = {k: dict(us_per_launch=t * 1e6, frac=nbytes / t / 1e9 / PEAK_HBM_GBS) for k, t in times.items()}
         del devs, order, ws

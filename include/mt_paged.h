@@ -82,22 +82,6 @@ int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const
                                   int b, int h, int d, int page_size, int pages_per_slab,
                                   int num_slabs, int columns, int layer, int layers, int dtype);
 
-/* The decode kernels' schedule for the calling process: 0 = automatic
- * (a workgroup per item while the grid fits one residency round; beyond it,
- * one round of persistent workgroups that claim items from a counter, the
- * next item's loads issued while the current one streams), 1 = always a
- * workgroup per item, 2 = persistent whenever the row layout allows (16-byte
- * rows, a work list of at most 2048 entries). Results are identical under
- * every schedule. mode -1 only reads it; *previous (if not NULL) receives the
- * previous mode. The persistent schedule keeps one counter pair per host
- * thread in a fixed device array (1024 threads; beyond, a workgroup per
- * item), reset by the last workgroup of each launch: launches from one
- * thread are stream-ordered and never share a pair with another thread's; a
- * captured launch replays the capturing thread's pair, so it must not be
- * replayed from another thread while that thread decodes.
- * No reference counterpart (a tuning and measurement knob). */
-int mt_paged_decode_schedule(int mode, int* previous);
-
 /* Number of launches since the library was loaded in which
  * mt_paged_attention / mt_paged_prefill split one long prompt's keys over
  * workgroups (query tiles x heads <= compute units, >= 6 key blocks in the

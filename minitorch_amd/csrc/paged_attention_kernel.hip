@@ -445,16 +445,7 @@ struct DecodeArgs {
   // other pass reversed. Needs 2 * (batch rounded up to 4) ints of dynamic LDS.
   int rank_rows;
   int rank_per;
-  // Persistent schedule (decode_kernel<..., PERSIST = true>): the claim
-  // counter pair (next ticket, finished workgroups), zero at launch, and
-  // whether the work list is staged in LDS (work_items entries of dynamic LDS).
-  unsigned* claim;
-  int work_lds;
 };
-
-// Work-list entries a persistent decode workgroup stages in LDS (8 bytes
-// each); longer lists run one workgroup per item.
-constexpr int kLdsWorkItems = 2048;
 
 // Rows a decode workgroup ranks on its own (the ranking costs each thread
 // batch / threads * batch LDS reads).
@@ -538,31 +529,15 @@ __device__ __forceinline__ void stream_wave(Softmax<D / G, G>& st, const Query<D
 
 // Fused KV append + decode attention over (request, head, split) items.
 // Items come from the work list when one is given (visiting order chosen by
-// the caller, e.g. longest first), else from the full (split, row, head) grid
-// or the in-kernel ranking (DecodeArgs::rank_rows).
-//
-// Two schedules. PERSIST = false: a workgroup per item (grid-stride when the
-// grid is capped); a workgroup's prologue -- work entry, table row, query,
-// offset, page resolve -- is a chain of dependent round trips before its
-// stream starts. PERSIST = true: one residency round of workgroups, each
-// taking its first item by block index and every later one from a claim
-// counter (a.claim[0], one atomic add by one lane, issued an item ahead), so
-// that items go to whichever workgroup frees first, on whichever XCD; the
-// next item's table entries, query, new K/V and offset are loaded before the
-// current item streams, so its prologue is hidden. The work list (or the
-// ranking) is staged in LDS, so finding an item needs no global round trip.
-// The last workgroup to finish resets the counter to zero for the next
-// launch (a.claim[1] counts finished workgroups), so launches need no memset
-// and a captured launch replays as it was recorded.
-//
+// the caller, e.g. longest first), else from the full (split, row, head) grid.
 // 8-wave fp16/bf16 workgroups at D = 64 (config 2's shape) are meant to be
 // resident three per compute unit, i.e. six waves per SIMD and at most 80
 // VGPRs: one VGPR more drops a whole workgroup per compute unit (and the
 // launcher then picks 4-wave workgroups), so the bound is stated. Other
 // shapes need more registers and keep the compiler's choice.
-template <int DT, int D, bool VEC, int U, int STAGES, int WAVES, int G, bool PERSIST>
+template <int DT, int D, bool VEC, int U, int STAGES, int WAVES, int G>
 __global__ __launch_bounds__(WAVES * kWave)
-__attribute__((amdgpu_waves_per_eu(WAVES == 8 && D == 64 && VEC && DT != kF32 && U <= 2 && !PERSIST ? 6 : 1)))
+__attribute__((amdgpu_waves_per_eu(WAVES == 8 && D == 64 && VEC && DT != kF32 && U <= 2 ? 6 : 1)))
 void decode_kernel(DecodeArgs a) {
   using T = typename Elem<DT>::T;
   constexpr int DL = D / G;
@@ -580,7 +555,6 @@ void decode_kernel(DecodeArgs a) {
   __shared__ float s2_acc[GROUPS][D];
   __shared__ uint64_t s_slabs[kLdsSlabs];
   __shared__ __align__(16) T s_new[2][D];  // the new token's K and V rows
-  __shared__ int64_t s_next[2];             // persistent: the workgroup's item after next
 
   const Geometry& g = a.g;
   const int dim = VEC ? D : g.dim;
@@ -603,19 +577,6 @@ void decode_kernel(DecodeArgs a) {
     slabs_loaded = true;
   };
   if (lds_slabs && (a.work || a.rank_rows || blockIdx.x < bh_count)) load_slabs();
-  // Dynamic LDS: the ranking's offsets and order (2 * len4 ints, when
-  // rank_rows), then the staged work list (work_items entries, when work_lds).
-  extern __shared__ __align__(16) int s_rank[];
-  const int len4 = a.rank_rows ? (a.batch + 3) & ~3 : 0;
-  int* const s_len = s_rank;
-  int* const s_order = s_rank + len4;
-  uint64_t* const s_work = reinterpret_cast<uint64_t*>(s_rank + 2 * len4);
-  if constexpr (PERSIST) {
-    if (a.work_lds) {
-      for (int i = tid; i < a.work_items; i += NT) s_work[i] = reinterpret_cast<const uint64_t*>(a.work)[i];
-      if (!a.rank_rows) __syncthreads();
-    }
-  }
   // In-kernel longest-first order (see DecodeArgs::rank_rows): s_len holds
   // the offsets, s_order[k] the row of rank k; (length desc, row asc) is a
   // strict order, so the ranks are a permutation whatever the offsets hold.
@@ -624,6 +585,10 @@ void decode_kernel(DecodeArgs a) {
   // by tpr consecutive lanes (the largest power of two up to 64 with
   // tpr * batch <= threads), each over its own slice of the candidates, and
   // summed with lane shuffles: the count runs on every wave, not one.
+  extern __shared__ __align__(16) int s_rank[];
+  const int len4 = (a.batch + 3) & ~3;
+  int* const s_len = s_rank;
+  int* const s_order = s_rank + len4;
   if (a.rank_rows) {
     for (int r = tid; r < len4; r += NT) s_len[r] = r < a.batch ? a.offsets[r] : INT_MIN;
     __syncthreads();
@@ -664,81 +629,62 @@ void decode_kernel(DecodeArgs a) {
   const T* vin = static_cast<const T*>(a.v);
   T* out = static_cast<T*>(a.out);
 
-  // What an item needs from memory before it streams.
-  struct ItemIn {
-    int b, head, split, physical, offset;
-    bool ok;
-    T new_k, new_v;
-    Query<DT, D, VEC, G> qv;
-  };
-  // (row, head, split) of an item; false for a work-list entry to skip.
-  auto locate = [&](int64_t item, ItemIn& in) -> bool {
+  for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
+    int split, b, head;
     if (a.work) {
-      // (row, split) as one 8-byte entry: from LDS when staged, else the
-      // workgroup's first dependent round trip
+      // (row, split) read as one 8-byte load: the workgroup's first dependent
+      // round trip.
       const int64_t w = item / g.heads;
-      in.head = int(item - w * g.heads);
-      uint64_t e;
-      if constexpr (PERSIST) e = a.work_lds ? s_work[w] : reinterpret_cast<const uint64_t*>(a.work)[w];
-      else e = reinterpret_cast<const uint64_t*>(a.work)[w];
-      in.b = int(uint32_t(e));
-      in.split = int(uint32_t(e >> 32));
-      return (unsigned(in.b) < unsigned(a.batch)) & (unsigned(in.split) < unsigned(a.nsplit_max));
-    }
-    if (a.rank_rows) {
+      head = int(item - w * g.heads);
+      const uint64_t e = reinterpret_cast<const uint64_t*>(a.work)[w];
+      b = int(uint32_t(e));
+      split = int(uint32_t(e >> 32));
+      if (!((unsigned(b) < unsigned(a.batch)) & (unsigned(split) < unsigned(a.nsplit_max)))) continue;
+    } else if (a.rank_rows) {
       // item = (visiting position, head); one split per row
       const int pos = int(item / g.heads);
-      in.head = int(item - int64_t(pos) * g.heads);
+      head = int(item - int64_t(pos) * g.heads);
       const int pass = pos / a.rank_per, within = pos - pass * a.rank_per;
       const int width = min(a.rank_per, a.batch - pass * a.rank_per);
-      in.b = s_order[pass * a.rank_per + ((pass & 1) ? width - 1 - within : within)];
-      in.split = 0;
-      return true;
+      b = s_order[pass * a.rank_per + ((pass & 1) ? width - 1 - within : within)];
+      split = 0;
+    } else {
+      split = int(item / bh_count);
+      const int64_t bhi = item - int64_t(split) * bh_count;
+      b = int(bhi / g.heads);
+      head = int(bhi - int64_t(b) * g.heads);
     }
-    in.split = int(item / bh_count);
-    const int64_t bhi = item - int64_t(in.split) * bh_count;
-    in.b = int(bhi / g.heads);
-    in.head = int(bhi - int64_t(in.b) * g.heads);
-    return true;
-  };
-  // Issue the loads that do not depend on the context length, all in one
-  // round trip: the table entry of each of this wave's page slots (the next
-  // link of the chain to the K/V loads), the query, the new token's K/V and
-  // the offset.
-  auto fetch = [&](int64_t item, ItemIn& in) {
-    in.ok = locate(item, in);
-    if (!in.ok) return;
-    const int* table_row = a.table + int64_t(in.b) * g.columns;
-    const int slot_i = lane >> sub_shift;
-    const int slot_tok0 = (wave + WAVES * slot_i) * RB + ((lane & sub_shift) << 3);
-    const int64_t slot_logical = (int64_t(in.split) * a.split_tokens + slot_tok0) >> g.log2_page;
-    in.physical = -1;
-    if (slot_i < rb_per_wave && slot_logical < g.columns) in.physical = table_row[slot_logical];
-    const int64_t qrow = int64_t(in.b) * a.qkv_stride + int64_t(in.head) * dim;  // q, k, v row
-    in.qv.load(qp + qrow, col0, dim, a.qscale);
-    in.new_k = T{};
-    in.new_v = T{};
-    if (tid < dim) { in.new_k = kin[qrow + tid]; in.new_v = vin[qrow + tid]; }
-    in.offset = a.rank_rows ? s_len[in.b] : a.offsets[in.b];
-  };
-  // Stream, score the new token, merge and write one item.
-  auto run = [&](const ItemIn& in) {
-    const int b = in.b, head = in.head, split = in.split;
     const int64_t bh = int64_t(b) * g.heads + head;
+
+    // Loads that do not depend on the context length are issued first, all
+    // in one round trip: the table entry of each of this wave's page slots
+    // (the next link of the chain to the K/V loads), the query, the new
+    // token's K/V (wave 0) and the offset.
     const int* table_row = a.table + int64_t(b) * g.columns;
-    const int64_t qrow = int64_t(b) * a.qkv_stride + int64_t(head) * dim;
-    const Query<DT, D, VEC, G>& qv = in.qv;
-    const int64_t L = in.offset < 0 ? 0 : int64_t(in.offset) + 1;
+    const int t0i = split * a.split_tokens;
+    const int slot_i = lane >> sub_shift;
+    const int slot_tok = (wave + WAVES * slot_i) * RB + ((lane & sub_shift) << 3);
+    const int64_t slot_logical = (int64_t(t0i) + slot_tok) >> g.log2_page;
+    int physical = -1;
+    if (slot_i < rb_per_wave && slot_logical < g.columns) physical = table_row[slot_logical];
+    Query<DT, D, VEC, G> qv;
+    const int64_t qrow = int64_t(b) * a.qkv_stride + int64_t(head) * dim;  // q, k, v row
+    qv.load(qp + qrow, col0, dim, a.qscale);
+    T new_k{}, new_v{};
+    if (tid < dim) { new_k = kin[qrow + tid]; new_v = vin[qrow + tid]; }
+    const int offset = a.rank_rows ? s_len[b] : a.offsets[b];
+
+    const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
     T* orow = out + bh * dim;
     if (L > cap) {
       // A token beyond the table's columns reads as a missing page: NaN row.
       if (split == 0)
         for (int t = tid; t < dim; t += NT) orow[t] = from_f32<DT>(NAN);
-      return;
+      continue;
     }
     const int nsplit = L == 0 ? 1 : int((L + a.split_tokens - 1) / a.split_tokens);
-    if (split >= nsplit) return;
-    const int64_t t0 = int64_t(split) * a.split_tokens;
+    if (split >= nsplit) continue;
+    const int64_t t0 = t0i;
     const int64_t t1 = L < t0 + a.split_tokens ? L : t0 + a.split_tokens;
     const bool owns_new = L > 0 && split == nsplit - 1;
     const int ntok_paged = int((owns_new ? t1 - 1 : t1) - t0);  // tokens read from pages
@@ -751,7 +697,7 @@ void decode_kernel(DecodeArgs a) {
       for (int j = 0; j < SLABS_PER_THREAD; ++j)
         if (tid + j * NT < kLdsSlabs) s_slabs[tid + j * NT] = slab_reg[j];
     }
-    if (tid < dim) { s_new[0][tid] = in.new_k; s_new[1][tid] = in.new_v; }
+    if (tid < dim) { s_new[0][tid] = new_k; s_new[1][tid] = new_v; }
     __syncthreads();
     slabs_staged = true;
     auto slab_of = [&](int physical) -> uint64_t {
@@ -762,9 +708,7 @@ void decode_kernel(DecodeArgs a) {
                                            : nullptr;
     };
 
-    const int slot_i = lane >> sub_shift;
-    const int slot_tok0 = (wave + WAVES * slot_i) * RB + ((lane & sub_shift) << 3);
-    const T* my_page = (slot_i < rb_per_wave && t0 + slot_tok0 < t1) ? resolve(in.physical) : nullptr;
+    const T* my_page = (slot_i < rb_per_wave && t0 + slot_tok < t1) ? resolve(physical) : nullptr;
     // The new token's page (wave 0, scalar loads; needed only after the stream).
     const T* new_page = nullptr;
     if (owns_new && wave == 0) {
@@ -864,235 +808,6 @@ void decode_kernel(DecodeArgs a) {
       }
     }
     __syncthreads();  // LDS is reused by the next item
-  };
-
-  if constexpr (!PERSIST) {
-    for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
-      int split, b, head;
-      if (a.work) {
-        // (row, split) read as one 8-byte load: the workgroup's first dependent
-        // round trip.
-        const int64_t w = item / g.heads;
-        head = int(item - w * g.heads);
-        const uint64_t e = reinterpret_cast<const uint64_t*>(a.work)[w];
-        b = int(uint32_t(e));
-        split = int(uint32_t(e >> 32));
-        if (!((unsigned(b) < unsigned(a.batch)) & (unsigned(split) < unsigned(a.nsplit_max)))) continue;
-      } else if (a.rank_rows) {
-        // item = (visiting position, head); one split per row
-        const int pos = int(item / g.heads);
-        head = int(item - int64_t(pos) * g.heads);
-        const int pass = pos / a.rank_per, within = pos - pass * a.rank_per;
-        const int width = min(a.rank_per, a.batch - pass * a.rank_per);
-        b = s_order[pass * a.rank_per + ((pass & 1) ? width - 1 - within : within)];
-        split = 0;
-      } else {
-        split = int(item / bh_count);
-        const int64_t bhi = item - int64_t(split) * bh_count;
-        b = int(bhi / g.heads);
-        head = int(bhi - int64_t(b) * g.heads);
-      }
-      const int64_t bh = int64_t(b) * g.heads + head;
-
-      // Loads that do not depend on the context length are issued first, all
-      // in one round trip: the table entry of each of this wave's page slots
-      // (the next link of the chain to the K/V loads), the query, the new
-      // token's K/V (wave 0) and the offset.
-      const int* table_row = a.table + int64_t(b) * g.columns;
-      const int t0i = split * a.split_tokens;
-      const int slot_i = lane >> sub_shift;
-      const int slot_tok = (wave + WAVES * slot_i) * RB + ((lane & sub_shift) << 3);
-      const int64_t slot_logical = (int64_t(t0i) + slot_tok) >> g.log2_page;
-      int physical = -1;
-      if (slot_i < rb_per_wave && slot_logical < g.columns) physical = table_row[slot_logical];
-      Query<DT, D, VEC, G> qv;
-      const int64_t qrow = int64_t(b) * a.qkv_stride + int64_t(head) * dim;  // q, k, v row
-      qv.load(qp + qrow, col0, dim, a.qscale);
-      T new_k{}, new_v{};
-      if (tid < dim) { new_k = kin[qrow + tid]; new_v = vin[qrow + tid]; }
-      const int offset = a.rank_rows ? s_len[b] : a.offsets[b];
-
-      const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
-      T* orow = out + bh * dim;
-      if (L > cap) {
-        // A token beyond the table's columns reads as a missing page: NaN row.
-        if (split == 0)
-          for (int t = tid; t < dim; t += NT) orow[t] = from_f32<DT>(NAN);
-        continue;
-      }
-      const int nsplit = L == 0 ? 1 : int((L + a.split_tokens - 1) / a.split_tokens);
-      if (split >= nsplit) continue;
-      const int64_t t0 = t0i;
-      const int64_t t1 = L < t0 + a.split_tokens ? L : t0 + a.split_tokens;
-      const bool owns_new = L > 0 && split == nsplit - 1;
-      const int ntok_paged = int((owns_new ? t1 - 1 : t1) - t0);  // tokens read from pages
-      // Staged in LDS once the loads above are in flight: the slab table (first
-      // item only) and the new token's K/V row, which is needed only after the
-      // stream and so holds no registers during it.
-      if (!slabs_staged) {
-        if (!slabs_loaded) load_slabs();
-  #pragma unroll
-        for (int j = 0; j < SLABS_PER_THREAD; ++j)
-          if (tid + j * NT < kLdsSlabs) s_slabs[tid + j * NT] = slab_reg[j];
-      }
-      if (tid < dim) { s_new[0][tid] = new_k; s_new[1][tid] = new_v; }
-      __syncthreads();
-      slabs_staged = true;
-      auto slab_of = [&](int physical) -> uint64_t {
-        return lds_slabs ? s_slabs[physical / g.pps] : a.slabs[physical / g.pps];
-      };
-      auto resolve = [&](int physical) -> const T* {
-        return physical_in_pool(physical, g) ? page_in_slab<T>(slab_of(physical), physical, g, head)
-                                             : nullptr;
-      };
-
-      const T* my_page = (slot_i < rb_per_wave && t0 + slot_tok < t1) ? resolve(physical) : nullptr;
-      // The new token's page (wave 0, scalar loads; needed only after the stream).
-      const T* new_page = nullptr;
-      if (owns_new && wave == 0) {
-        const int64_t logical = (L - 1) >> g.log2_page;
-        new_page = logical < g.columns ? resolve(table_row[logical]) : nullptr;
-      }
-
-      Softmax<DL, G> st;
-      st.init();
-      stream_wave<DT, D, VEC, U, STAGES, G>(st, qv, reinterpret_cast<uint64_t>(my_page), ntok_paged,
-                                             wave, WAVES, g, dim);
-
-      if (owns_new && wave == 0) {
-        // The new token: read from the K/V inputs, scored by group 0 of wave 0,
-        // and written into its page when the page exists (reference append,
-        // src/paged_attention_kernel.cu:23-33). A missing page reads as NaN.
-        const int64_t pos = L - 1;
-        Chunk<DT, DL, VEC> kn, vn;
-        kn.load_lds(&s_new[0][col0], col0, dim);
-        vn.load_lds(&s_new[1][col0], col0, dim);
-        if (lane < G && new_page) {
-          T* kp = const_cast<T*>(new_page) + (pos & (g.page_size - 1)) * dim + col0;
-          T* vp = kp + g.kind_stride;
-          if constexpr (VEC) {
-  #pragma unroll
-            for (int i = 0; i < Chunk<DT, DL, VEC>::NV; ++i) {
-              global_view(reinterpret_cast<u32x4*>(kp))[i] = kn.raw[i];
-              global_view(reinterpret_cast<u32x4*>(vp))[i] = vn.raw[i];
-            }
-          } else {
-            for (int i = 0; i < DL && col0 + i < dim; ++i) {
-              kp[i] = kin[qrow + col0 + i];
-              vp[i] = vin[qrow + col0 + i];
-            }
-          }
-        }
-        if (!new_page) { kn.nan_fill(); vn.nan_fill(); }
-        const float sc = qv.score(kn);
-        if (lane < G) {
-          float vf[DL];
-          vn.to_float(vf);
-          st.add(sc, vf);
-        }
-      }
-
-      // Row merges by DPP, then the WAVES * 4 row states meet in LDS.
-      st.row_merge();
-      const int row = lane >> 4;
-      if ((lane & 15) < G) {
-        const int si = wave * 4 + row;
-  #pragma unroll
-        for (int i = 0; i < DL; ++i) s_acc[si][col0 + i] = st.acc[i];
-        if ((lane & 15) == 0) { s_m[si] = st.m; s_l[si] = st.l; }
-      }
-      __syncthreads();
-
-      // Two-level merge with every thread busy: group q of D threads merges
-      // row states [q*PER, (q+1)*PER) per dim, then D threads merge the groups.
-      {
-        const int d = tid % D, q = tid / D;
-        float M = -INFINITY;
-  #pragma unroll
-        for (int j = 0; j < PER; ++j) M = fmaxf(M, s_m[q * PER + j]);
-        float lq = 0.f, aq = 0.f;
-  #pragma unroll
-        for (int j = 0; j < PER; ++j) {
-          const int w = q * PER + j;
-          const float mw = s_m[w];
-          const float sc = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
-          lq = fmaf(s_l[w], sc, lq);
-          aq = fmaf(s_acc[w][d], sc, aq);
-        }
-        s2_acc[q][d] = aq;
-        if (d == 0) { s2_m[q] = M; s2_l[q] = lq; }
-      }
-      __syncthreads();
-
-      const int t = tid;
-      if (t < dim) {
-        float M = -INFINITY;
-  #pragma unroll
-        for (int q = 0; q < GROUPS; ++q) M = fmaxf(M, s2_m[q]);
-        float lsum = 0.f, asum = 0.f;
-  #pragma unroll
-        for (int q = 0; q < GROUPS; ++q) {
-          const float mq = s2_m[q];
-          const float sc = (mq == -INFINITY) ? 0.f : fast_exp2(mq - M);
-          lsum = fmaf(s2_l[q], sc, lsum);
-          asum = fmaf(s2_acc[q][t], sc, asum);
-        }
-        if (nsplit == 1) {
-          orow[t] = from_f32<DT>(finalize(asum, lsum));
-        } else {
-          float* part = a.partials + (bh * a.nsplit_max + split) * PSTRIDE;
-          part[2 + t] = asum;
-          if (t == 0) { part[0] = M; part[1] = lsum; }
-        }
-      }
-      __syncthreads();  // LDS is reused by the next item
-    }
-  } else {
-    // With a claim counter (schedule 2), items after the first are claimed
-    // one ahead by lane 0 and published through s_next; without one
-    // (schedule 3) a workgroup takes every grid-th item. Either way the
-    // loads of the next item are issued before the current item runs. Every
-    // claiming workgroup draws tickets until one falls past the last item,
-    // so exactly a.items tickets are drawn and the last workgroup out
-    // resets the counter.
-    const int64_t grid = gridDim.x;
-    const bool claiming = a.claim != nullptr;
-    unsigned ticket = 0;
-    if (claiming && tid == 0) ticket = atomicAdd(a.claim, 1u);
-    int64_t item = blockIdx.x;
-    ItemIn cur;
-    fetch(item, cur);
-    int64_t next = item + grid;
-    if (claiming) {
-      if (tid == 0) s_next[0] = grid + ticket;
-      __syncthreads();
-      next = s_next[0];
-    }
-    int turn = 0;
-    while (item < a.items) {
-      ItemIn nxt;
-      nxt.ok = false;
-      const bool more = next < a.items;
-      if (more) {
-        fetch(next, nxt);
-        if (claiming && tid == 0) ticket = atomicAdd(a.claim, 1u);
-      }
-      if (cur.ok) run(cur);
-      int64_t after = next + grid;
-      if (claiming) {
-        turn ^= 1;
-        if (tid == 0) s_next[turn] = more ? grid + ticket : a.items;
-        __syncthreads();
-        after = s_next[turn];
-      }
-      item = next;
-      cur = nxt;
-      next = after;
-    }
-    if (claiming && tid == 0 && atomicAdd(a.claim + 1, 1u) == unsigned(grid) - 1u) {
-      atomicExch(a.claim, 0u);
-      atomicExch(a.claim + 1, 0u);
-    }
   }
 }
 
@@ -1848,15 +1563,6 @@ size_t partial_bytes(int64_t bh, int64_t nsplit_max, bool vec, int d) {
   return size_t(bh) * size_t(nsplit_max) * size_t(dt + 2) * sizeof(float);
 }
 
-// Decode schedule knob (mt_paged_decode_schedule): automatic, one
-// workgroup per item, or persistent workgroups claiming items.
-constexpr int kScheduleAuto = 0, kScheduleItems = 1, kSchedulePersistent = 2, kScheduleStatic = 3;
-std::atomic<int> g_decode_schedule{kScheduleAuto};
-
-// The calling thread's claim counter pair on the current device (defined
-// with the device arrays below).
-int claim_counter(unsigned** out);
-
 // Compute units of the current device (cached per device).
 int device_compute_units() {
   static int cached[64] = {};
@@ -1881,37 +1587,14 @@ bool two_wave_split_ok(const DecodeArgs& a) {
 
 // Workgroups of decode_kernel<DT, D, VEC, U, kStages, WAVES, G> resident per
 // compute unit (0 if the query fails), looked up once per instantiation.
-template <int DT, int D, bool VEC, int U, int WAVES, int G, bool PERSIST = false>
+template <int DT, int D, bool VEC, int U, int WAVES, int G>
 int decode_occupancy() {
   static const int per_cu = [] {
     int n = 0;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<DT, D, VEC, U, kStages, WAVES, G, PERSIST>,
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<DT, D, VEC, U, kStages, WAVES, G>,
                                                         WAVES * kWave, 0) == hipSuccess ? n : 0;
   }();
   return per_cu;
-}
-
-// Workgroups of an instantiation resident per compute unit with `dyn` bytes
-// of dynamic LDS: its register/wave bound (dyn = 0) capped by the LDS per
-// compute unit over its static plus dynamic LDS.
-template <int DT, int D, bool VEC, int U, int WAVES, int G, bool PERSIST>
-int decode_occupancy_lds(size_t dyn) {
-  static const size_t static_lds = [] {
-    hipFuncAttributes attr{};
-    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(
-                                           decode_kernel<DT, D, VEC, U, kStages, WAVES, G, PERSIST>)) == hipSuccess
-               ? size_t(attr.sharedSizeBytes) : size_t(0);
-  }();
-  static const size_t lds_per_cu = [] {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess)
-      return size_t(0);
-    return size_t(n);
-  }();
-  const int regs = decode_occupancy<DT, D, VEC, U, WAVES, G, PERSIST>();
-  if (!lds_per_cu || !static_lds) return regs;
-  return int(std::min<int64_t>(regs, int64_t(lds_per_cu / (static_lds + dyn))));
 }
 
 template <int DT, int D, bool VEC, int WAVES, int G>
@@ -1928,7 +1611,7 @@ hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
       // The deepest unroll when the whole grid is resident at its
       // occupancy (more loads in flight per wave), else unroll 1, whose
       // lower register count keeps the most workgroups per compute unit.
-      unroll = blocks <= int64_t(decode_occupancy<DT, D, VEC, 4, WAVES, G, false>()) * device_compute_units() ? 4 : 1;
+      unroll = blocks <= int64_t(decode_occupancy<DT, D, VEC, 4, WAVES, G>()) * device_compute_units() ? 4 : 1;
     } else {
       unroll = 1;
     }
@@ -1937,51 +1620,13 @@ hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
   unroll = unroll >= 4 ? 4 : unroll >= 2 ? 2 : 1;
   const size_t rank_lds = a.rank_rows ? size_t(2) * ((a.batch + 3) & ~3) * sizeof(int) : 0;
   if (unroll > kMaxUnroll) unroll = kMaxUnroll;
-  // Persistent schedule: one residency round of workgroups claiming items
-  // (decode_kernel<..., true>), automatically when the grid spans more than
-  // one residency round, or as the schedule knob says; 16-byte rows only,
-  // and a work list must fit its LDS stage.
-  const int mode = g_decode_schedule.load(std::memory_order_relaxed);
-  size_t persist_lds = rank_lds;
-  int64_t persist_grid = 0;
-  bool persist = false;
-  if constexpr (VEC) {
-    if (mode != kScheduleItems && (!a.work || a.work_items <= kLdsWorkItems)) {
-      persist_lds += a.work ? size_t(a.work_items) * sizeof(uint64_t) : 0;
-      int occ = 0;
-      if (unroll == 4) occ = decode_occupancy_lds<DT, D, VEC, (kMaxUnroll >= 4 ? 4 : 1), WAVES, G, true>(persist_lds);
-      else if (unroll == 2) occ = decode_occupancy_lds<DT, D, VEC, (kMaxUnroll >= 2 ? 2 : 1), WAVES, G, true>(persist_lds);
-      else occ = decode_occupancy_lds<DT, D, VEC, 1, WAVES, G, true>(persist_lds);
-      persist_grid = int64_t(occ) * device_compute_units();
-      persist = persist_grid > 0 && (mode == kSchedulePersistent || mode == kScheduleStatic || blocks > persist_grid);
-    }
+  if constexpr (kMaxUnroll >= 4) {
+    if (unroll == 4) decode_kernel<DT, D, VEC, 4, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
   }
-  unsigned* claim = nullptr;
-  if (persist && mode != kScheduleStatic && claim_counter(&claim) != hipSuccess) {
-    (void)hipGetLastError();
-    claim = nullptr;
+  if constexpr (kMaxUnroll >= 2) {
+    if (unroll == 2) decode_kernel<DT, D, VEC, 2, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
   }
-  if (persist && (claim || mode == kScheduleStatic)) {
-    DecodeArgs p = a;
-    p.claim = claim;
-    p.work_lds = a.work ? 1 : 0;
-    const int grid = int(std::min<int64_t>(blocks, persist_grid));
-    if constexpr (kMaxUnroll >= 4) {
-      if (unroll == 4) decode_kernel<DT, D, VEC, 4, kStages, WAVES, G, true><<<grid, NT, persist_lds>>>(p);
-    }
-    if constexpr (kMaxUnroll >= 2) {
-      if (unroll == 2) decode_kernel<DT, D, VEC, 2, kStages, WAVES, G, true><<<grid, NT, persist_lds>>>(p);
-    }
-    if (unroll == 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G, true><<<grid, NT, persist_lds>>>(p);
-  } else {
-    if constexpr (kMaxUnroll >= 4) {
-      if (unroll == 4) decode_kernel<DT, D, VEC, 4, kStages, WAVES, G, false><<<grid_for(blocks), NT, rank_lds>>>(a);
-    }
-    if constexpr (kMaxUnroll >= 2) {
-      if (unroll == 2) decode_kernel<DT, D, VEC, 2, kStages, WAVES, G, false><<<grid_for(blocks), NT, rank_lds>>>(a);
-    }
-    if (unroll == 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G, false><<<grid_for(blocks), NT, rank_lds>>>(a);
-  }
+  if (unroll == 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
   hipError_t e = hipGetLastError();
   const int64_t merge_rows = a.work ? a.merge_rows : a.batch;
   if (e != hipSuccess || a.nsplit_max == 1 || merge_rows == 0) return e;
@@ -2126,13 +1771,6 @@ int library_workspace(size_t bytes, void** out) {
 
 static __device__ __align__(256) float scratch[MT_PAGED_NOALLOC_SCRATCH_BYTES / sizeof(float)];
 
-// Claim counters of the persistent decode schedule: one (next ticket,
-// finished workgroups) pair per host thread, zero from module load and reset
-// to zero by the last workgroup of every launch. A host thread launches on
-// its own default stream, so launches sharing a pair are stream-ordered.
-constexpr int kClaimSlots = 1024;
-static __device__ __align__(256) unsigned claims[2 * kClaimSlots];
-
 namespace {
 
 constexpr size_t kNoAllocScratchBytes = MT_PAGED_NOALLOC_SCRATCH_BYTES;
@@ -2155,33 +1793,6 @@ int scratch_address(void** out) {
     addresses[dev] = p;
   }
   *out = addresses[dev];
-  return hipSuccess;
-}
-
-// The calling thread's pair of `claims` on the current device: the array's
-// device address is looked up once per device (the host-side name is not a
-// device address), the slot once per thread; threads beyond kClaimSlots get
-// none (their decodes run one workgroup per item).
-int claim_counter(unsigned** out) {
-  static std::mutex mutex;
-  static std::vector<unsigned*> bases;
-  static std::atomic<int> next_slot{0};
-  thread_local int slot = -1;
-  if (slot < 0) slot = next_slot.fetch_add(1, std::memory_order_relaxed);
-  *out = nullptr;
-  if (slot >= kClaimSlots) return hipSuccess;
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  std::lock_guard<std::mutex> lock(mutex);
-  if (bases.size() <= size_t(dev)) bases.resize(dev + 1, nullptr);
-  if (!bases[dev]) {
-    void* p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(claims));
-    if (e != hipSuccess) return e;
-    bases[dev] = static_cast<unsigned*>(p);
-  }
-  *out = bases[dev] + 2 * slot;
   return hipSuccess;
 }
 
@@ -2637,13 +2248,6 @@ int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, S, 0, 0, 0,
                        nullptr, 0, 0, ws, nsplit_max > 1 ? kNoAllocScratchBytes : 0, true);
-}
-
-int mt_paged_decode_schedule(int mode, int* previous) {
-  if (mode < -1 || mode > kScheduleStatic) return hipErrorInvalidValue;
-  const int was = mode < 0 ? g_decode_schedule.load() : g_decode_schedule.exchange(mode);
-  if (previous) *previous = was;
-  return hipSuccess;
 }
 
 int mt_paged_prefill_key_splits(long long* launches) {

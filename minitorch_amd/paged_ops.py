@@ -106,16 +106,6 @@ def paged_decode_split(out, q, k, v, slab_table, block_table, offsets, *, b, h, 
          qkv_stride, work, work_items, merge_rows, workspace, workspace_bytes)
 
 
-def decode_schedule(mode=-1):
-    """``mt_paged_decode_schedule``: set the decode kernels' schedule (0
-    automatic, 1 a workgroup per item, 2 persistent workgroups claiming
-    items; -1 leaves it) and return the previous one. Results do not depend
-    on it."""
-    prev = ct.c_int()
-    call(paged_library(), 'mt_paged_decode_schedule', [I, ct.POINTER(ct.c_int)], mode, ct.byref(prev))
-    return prev.value
-
-
 def decode_work_list(lengths, heads, split_tokens, compute_units):
     """Work list for ``mt_paged_decode_split``: returns (int32 array,
     work_items, merge_rows).

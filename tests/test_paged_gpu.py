@@ -377,80 +377,10 @@ def test_decode_batch_device_ranked_order(batch):
     assert np.all(out[1] == 0) and np.all(np.isnan(out[batch - 2]))
 
 
-@pytest.fixture
-def persistent_schedule():
-    # mt_paged_decode_schedule(2): every launch whose rows allow it runs one
-    # residency round of persistent workgroups that claim items from the
-    # calling thread's counter
-    previous = paged_ops.decode_schedule(2)
-    yield
-    paged_ops.decode_schedule(previous)
-
-
-PERSISTENT_CASES = {
-    'config1': lambda: config1_case(0),
-    'config2': lambda: config2_case(0),
-    'boundaries_p8_bf16': lambda: make_decode_case(2, batch=9, heads=3, dim=64, page_size=8,
-                                                   lengths=[1, 8, 9, 255, 256, 257, 512, 513, 1000],
-                                                   pool_pages=512, pages_per_slab=8, dtype='bfloat16'),
-    'd128_fp32': lambda: make_decode_case(3, batch=5, heads=2, dim=128, page_size=16,
-                                          lengths=[1, 17, 100, 300, 700], pool_pages=96, pages_per_slab=4,
-                                          dtype='float32'),
-    'global_slab_table': lambda: make_decode_case(13, batch=5, heads=3, dim=64, page_size=16,
-                                                  lengths=[1, 17, 200, 513, 90], pool_pages=700,
-                                                  pages_per_slab=1, dtype='float16'),
-    'splits_fp16': lambda: make_decode_case(7, batch=6, heads=3, dim=64, page_size=16,
-                                            lengths=[1, 64, 65, 500, 1024, 3000], pool_pages=512,
-                                            pages_per_slab=8, dtype='float16'),
-}
-
-
-@pytest.mark.parametrize('name', list(PERSISTENT_CASES))
-@pytest.mark.parametrize('entry', ['batch', 'split'])
-def test_persistent_schedule_equals_oracle(persistent_schedule, name, entry):
-    case = PERSISTENT_CASES[name]()
-    check_case(case, entry=entry)
-
-
-def test_persistent_schedule_missing_pages_and_ranked_rows(persistent_schedule):
-    # missing and out-of-pool pages (NaN rows), then 200 ranked rows with an
-    # empty row and a row past its table, under the persistent schedule
-    case = make_decode_case(5, batch=4, heads=2, dim=64, page_size=16, lengths=[40, 40, 300, 20],
-                            pool_pages=64, pages_per_slab=4, dtype='float32')
-    case.table[0, 1] = -1
-    case.table[1, 2] = -1
-    case.table[2, 5] = 10 ** 6
-    check_case(case)
-    test_decode_batch_device_ranked_order(200)
-
-
-@pytest.mark.parametrize('waves', [2, 4, 8])
-def test_persistent_schedule_work_lists(persistent_schedule, waves):
-    # work lists with rows of 0..3 splits, in LPT and reversed order: the
-    # same bits as one workgroup per item
-    lengths = [300, 5, 1024, 77, 16, 640, 1, 2100]
-    case = make_decode_case(12, batch=8, heads=2, dim=64, page_size=16, lengths=lengths,
-                            pool_pages=1024, pages_per_slab=16, dtype='bfloat16')
-    dev = DevicePagedCase(case)
-    listed = run_work_list(dev, lengths, 1024, waves)
-    ref, image = oracle_decode(case)
-    assert_attention_close(listed, ref, 'bfloat16')
-    assert np.array_equal(dev.pool_image().view(np.uint8), image.view(np.uint8)), 'append differs'
-    again = run_work_list(DevicePagedCase(case), lengths, 1024, waves, reverse=True)
-    paged_ops.decode_schedule(1)
-    try:
-        items = run_work_list(DevicePagedCase(case), lengths, 1024, waves)
-    finally:
-        paged_ops.decode_schedule(2)
-    assert np.array_equal(listed.view(np.uint16), again.view(np.uint16))
-    assert np.array_equal(listed.view(np.uint16), items.view(np.uint16))
-
-
-def test_persistent_schedule_many_rounds_back_to_back(persistent_schedule):
+def test_many_residency_rounds_back_to_back():
     # config 5's shape class at a size the oracle checks quickly: far more
-    # items than one residency round, so most items are claimed; eight
-    # launches in a row (the claim counter must come back to zero after each)
-    # give the same bits each time
+    # items than one residency round, rows split over up to three context
+    # splits; eight launches in a row give the same bits each time
     rng = np.random.default_rng(31)
     lengths = np.clip(np.round(np.exp(rng.normal(np.log(256.0), 1.2, size=160))), 1, 3000).astype(np.int64)
     case = make_decode_case(31, batch=160, heads=25, dim=64, page_size=16, lengths=lengths,
