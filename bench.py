@@ -1038,11 +1038,13 @@ def main():
             'kernel': 'decode_kernel<kF16,64,true,U> (mt_paged_decode_split)',
         },
     }
+    # the reference entry on the same pools, right after the headline timing
+    # (the GPU still busy and clocked up)
+    result['dropin'] = dropin_config2(case, devs, args.steps, args.warmup)
     if not args.no_ceiling:
         result['pattern_ceiling'] = pattern_ceiling(case, devs, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         result['cpu_baseline'] = cpu_baseline(case, args.cpu_seconds)
-    result['dropin'] = dropin_config2(case, devs, args.steps, args.warmup)
     del devs, calls, ws, order
     if not args.no_config5:
         print('config 5 (page sizes 16 and 32)', file=sys.stderr, flush=True)
