@@ -41,16 +41,19 @@ int mt_paged_attention(void* out, const void* q, const uint64_t* slabs, const in
  * committed lengths. Appends k/v at position offsets[i] of request i, then
  * attends its offsets[i] + 1 keys. One fused append + attention launch, plus
  * a split-reduction launch when the table is longer than one context split
- * (1024 tokens). When no row can split and b <= 256, every workgroup ranks
- * the rows by offsets[] on the device and visits them longest first (the
- * order mt_paged_decode_split takes from a host work list); otherwise rows
- * are visited in batch order. The split partials live in a library-owned
+ * (1024 tokens). Rows are visited longest first, in the order
+ * mt_paged_decode_split takes from a host work list, ranked on the device:
+ * when no row can split and b <= 256 every workgroup ranks the rows by
+ * offsets[] itself; otherwise, up to 2048 rows, a one-workgroup launch
+ * (mt_paged_decode_order) writes the work list first and one residency
+ * round of workgroups strides over it. Larger batches are visited in batch
+ * order. The split partials and that list live in a library-owned
  * device workspace, one per (host thread, device) -- so calls from several
  * host threads, each on its own default stream, never share one -- kept
  * until the thread exits and grown stream-ordered on the calling thread's
  * default stream (hipMallocAsync / hipFreeAsync, no device synchronization)
- * when a table needs more; status 2 if it cannot grow. Tables of at most 1024
- * tokens allocate nothing.
+ * when a table needs more; status 2 if it cannot grow. Batches of at most
+ * 256 rows with tables of at most 1024 tokens allocate nothing.
  * Replaces reference mt_paged_decode_batch (src/paged_attention_kernel.cu:121-137). */
 int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v,
                           const uint64_t* slabs, const int* table, const int* offsets, int b,
@@ -65,12 +68,13 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
 /* mt_paged_decode_batch that allocates nothing: same arguments, kernels and
  * results, but the split partials of tables longer than one split (1024
  * tokens) live in the library's fixed device array of
- * MT_PAGED_NOALLOC_SCRATCH_BYTES instead of a workspace that may grow. It
- * returns 1 (invalid value) before any launch when the partials,
- * b * h * ceil(columns * page_size / split) * (d' + 2) * 4 bytes (d' = 64 for
- * 16-byte-aligned operands at d = 64, else 128), exceed that size; tables of
- * at most 1024 tokens need none (mt_paged_decode_workspace_bytes with
- * split_tokens 0 gives an upper bound). Calls on one device share the array: calls
+ * MT_PAGED_NOALLOC_SCRATCH_BYTES instead of a workspace that may grow, and so
+ * does the device-built visiting order. It returns 1 (invalid value) before
+ * any launch when the partials, b * h * n * (d' + 2) * 4 bytes rounded up to
+ * 256 (n = ceil(columns * page_size / split), d' = 64 for 16-byte-aligned
+ * operands at d = 64, else 128; none when n = 1), plus the order,
+ * (2 + (2 n + 1) b) * 4 bytes (none when n = 1 and b <= 256), exceed that
+ * size. Calls on one device share the array: calls
  * that overlap (different streams) race; calls in stream order do not. The
  * first call on a device looks the array's device address up
  * (hipGetSymbolAddress) and keeps it; no call allocates or frees.
@@ -99,6 +103,22 @@ int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, in
  * automatic choice: 1024 tokens, longer when a table of `columns` pages would
  * need more than 8 splits). No reference counterpart. */
 int mt_paged_decode_split_tokens(int page_size, int columns, int requested, int* split_tokens);
+
+/* The visiting order of a decode, built on the device from offsets[b]
+ * (device, committed lengths as in mt_paged_decode_batch; 1 <= b <= 2048):
+ * the work list mt_paged_decode_split takes, equal to the one a host caller
+ * builds from the same lengths -- every (row, split) pair once, by tokens
+ * descending, then row, then split, in passes of compute_units / h pairs
+ * with every other pass reversed -- followed by the rows with more than one
+ * split, ascending. A row past its table gets one pair (split 0). Writes
+ * count[0] = pairs, count[1] = merge rows (device int[2]) and `list` (device,
+ * 2 * b * n + b ints for n = ceil(columns * page_size / split)). split_tokens
+ * and compute_units 0 = automatic (as mt_paged_decode_split; the device's
+ * compute units). One launch of one workgroup on the calling thread's
+ * default stream. No reference counterpart: mt_paged_decode_batch uses it to
+ * order its rows. */
+int mt_paged_decode_order(const int* offsets, int b, int h, int page_size, int columns,
+                          int split_tokens, int compute_units, int* list, int* count);
 
 /* mt_paged_decode_batch with a caller-owned workspace and tuning knobs:
  * split_tokens (a multiple of 64, at most 2048; 0 = automatic), unroll (1, 2

@@ -445,11 +445,20 @@ struct DecodeArgs {
   // other pass reversed. Needs 2 * (batch rounded up to 4) ints of dynamic LDS.
   int rank_rows;
   int rank_per;
+  // Work list built on the device (order_kernel) for a batch whose rows may
+  // split: work_count[0] (row, split) pairs at `work`, then work_count[1]
+  // merge rows. `items` is then only the capacity (batch * nsplit_max *
+  // heads) and the grid one residency round that strides over the list.
+  const int* work_count;
 };
 
 // Rows a decode workgroup ranks on its own (the ranking costs each thread
 // batch / threads * batch LDS reads).
 constexpr int kRankRows = 256;
+// Rows order_kernel orders in its one workgroup; larger batches are visited
+// in batch order.
+constexpr int kOrderRows = 2048;
+constexpr int kOrderThreads = 1024;
 
 // Stream one wave's share of a split: row-blocks j = wave + waves * i
 // (16 tokens each) of tokens [t0, t0 + ntok). Lane s of the wave holds in
@@ -628,15 +637,26 @@ void decode_kernel(DecodeArgs a) {
   const T* kin = static_cast<const T*>(a.k);
   const T* vin = static_cast<const T*>(a.v);
   T* out = static_cast<T*>(a.out);
+  const uint64_t* work64 = reinterpret_cast<const uint64_t*>(a.work);
 
-  for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
+  // A device-built list's length is read together with the workgroup's first
+  // entry (within the list's capacity, which bounds the grid), so the count
+  // adds no round trip before the first item.
+  int64_t items = a.items;
+  uint64_t first_entry = 0;
+  if (a.work_count) {
+    first_entry = work64[blockIdx.x / g.heads];
+    items = std::min(int64_t(a.work_count[0]) * g.heads, a.items);  // never past the list
+  }
+
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
     int split, b, head;
     if (a.work) {
       // (row, split) read as one 8-byte load: the workgroup's first dependent
       // round trip.
       const int64_t w = item / g.heads;
       head = int(item - w * g.heads);
-      const uint64_t e = reinterpret_cast<const uint64_t*>(a.work)[w];
+      const uint64_t e = (a.work_count && item == blockIdx.x) ? first_entry : work64[w];
       b = int(uint32_t(e));
       split = int(uint32_t(e >> 32));
       if (!((unsigned(b) < unsigned(a.batch)) & (unsigned(split) < unsigned(a.nsplit_max)))) continue;
@@ -822,14 +842,16 @@ __global__ __launch_bounds__(128) void merge_kernel(DecodeArgs a) {
   constexpr int PSTRIDE = D + 2;
   const Geometry& g = a.g;
   const int dim = g.dim;
-  const int64_t rows = a.work ? a.merge_rows : a.batch;
+  // a device-built list's counts, bounded by its capacity
+  const int64_t work_items = a.work_count ? std::min(int64_t(a.work_count[0]), a.items / g.heads) : a.work_items;
+  const int64_t rows = a.work_count ? std::min(a.work_count[1], a.batch) : a.work ? a.merge_rows : a.batch;
   const int64_t count = rows * g.heads;
   const int64_t cap = int64_t(g.columns) * g.page_size;
   T* out = static_cast<T*>(a.out);
   for (int64_t i = blockIdx.x; i < count; i += gridDim.x) {
     const int64_t m = i / g.heads;
     const int head = int(i - m * g.heads);
-    const int b = a.work ? a.work[2 * int64_t(a.work_items) + m] : int(m);
+    const int b = a.work ? a.work[2 * work_items + m] : int(m);
     if (b < 0 || b >= a.batch) continue;
     const int64_t bh = int64_t(b) * g.heads + head;
     const float* base = a.partials + bh * a.nsplit_max * PSTRIDE;
@@ -876,6 +898,216 @@ __global__ __launch_bounds__(128) void merge_kernel(DecodeArgs a) {
     }
     if (t < dim) out[bh * dim + t] = from_f32<DT>(finalize(asum, lsum));
   }
+}
+
+// Work list of a decode launch built on the device from offsets[], for the
+// reference entry, which has no work-list argument: the list a host caller
+// builds from the lengths it knows (paged_ops.decode_work_list), bit for bit.
+// Row r attends L = offsets[r] + 1 keys (0 for a negative offset) in
+// n = max(1, ceil(L / S)) splits: splits 0 .. n-2 of S tokens and a last one
+// of t = L - (n-1) S (a row past its table: one entry, t = 0, which the
+// decode turns into a NaN row). Entries are ordered by tokens descending,
+// then row, then split; position p of that order goes to slot f(p) of
+// passes of `per` entries with every other pass reversed. The S-token
+// entries form the first run, in (row, split) order, so entry (r, s) of it
+// sits at the count of S-token entries of rows before r, plus s (a prefix
+// sum). The last splits of fewer than S tokens follow, sorted by (tokens
+// descending, row): a stable LDS radix sort of the rows on S - 1 - t, rows
+// whose last split is full keyed past every other. The rows with more than
+// one split follow the list, ascending: list[2W + m]. count = (W, M).
+struct OrderArgs {
+  const int* offsets;
+  int* list;   // 2 * capacity + batch ints
+  int* count;  // [2]
+  int batch, split_tokens, per;
+  int capacity;  // (row, split) pairs the list holds: batch * nsplit_max
+  int64_t cap;   // tokens a table holds
+};
+
+constexpr int kOrderWaves = kOrderThreads / 64;
+constexpr int kRadixBits = 6;
+constexpr int kRadixDigits = 1 << kRadixBits;  // one digit per lane
+constexpr int kOrderBlocks = kOrderRows / kOrderThreads;  // rows per thread (striped)
+constexpr int kRadixCounts = kRadixDigits * kOrderBlocks * kOrderWaves;
+static_assert(kRadixDigits == 64 && kRadixCounts % kOrderThreads == 0, "order_kernel layout");
+
+// Inclusive prefix sum over a wave: Hillis-Steele shifts of 1, 2, 4 and 8
+// lanes inside each row of 16 (lanes shifted in from outside the row add 0),
+// then rows 1 and 3 add lane 15 of the row before and rows 2 and 3 add lane 31.
+__device__ __forceinline__ int wave_inclusive_add(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
+  return x;
+}
+
+// Exclusive prefix sums of V per-thread values over a workgroup of
+// kOrderThreads, in thread order; totals in tot[].
+template <int V>
+__device__ __forceinline__ void order_scan(int (&v)[V], int (&tot)[V], int (*s_wave)[kOrderWaves]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) inc[j] = wave_inclusive_add(v[j]);
+  if (lane == 63) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) s_wave[j][wave] = inc[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kOrderWaves; ++w) {
+      const int x = s_wave[j][w];
+      before += w < wave ? x : 0;
+      all += x;
+    }
+    v[j] = before + inc[j] - v[j];
+    tot[j] = all;
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kOrderThreads) void order_kernel(OrderArgs o) {
+  __shared__ int s_full[kOrderRows];   // S-token entries of the rows before
+  __shared__ int s_merge[kOrderRows];  // merge rows before
+  __shared__ int s_key[2][kOrderRows];  // radix sort: keys, ping-pong
+  __shared__ short s_row[2][kOrderRows];
+  // per (digit, block, wave) counts of one radix pass, scanned in that order
+  __shared__ int s_cnt[kRadixCounts];
+  __shared__ int s_wave[2 * kOrderBlocks + kOrderBlocks][kOrderWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = o.batch;
+  const uint32_t S = uint32_t(o.split_tokens);
+  const int blocks = (b + kOrderThreads - 1) / kOrderThreads;
+  // Striped rows: thread tid holds rows tid + j * kOrderThreads.
+  int n[kOrderBlocks], t[kOrderBlocks];
+#pragma unroll
+  for (int j = 0; j < kOrderBlocks; ++j) {
+    const int r = tid + j * kOrderThreads;
+    n[j] = 0; t[j] = 0;
+    if (r < b) {
+      const int off = o.offsets[r];
+      const uint32_t L = off < 0 ? 0u : uint32_t(off) + 1u;
+      if (int64_t(L) > o.cap) {
+        n[j] = 1;
+      } else {
+        const uint32_t nn = L == 0 ? 1u : (L + S - 1) / S;
+        n[j] = int(nn);
+        t[j] = int(L - (nn - 1) * S);
+      }
+    }
+    // sort key: S - 1 - t ascending is tokens descending; a full last split
+    // (not sorted here) and padding rows go behind every other
+    s_key[0][r] = (r < b && t[j] < int(S)) ? int(S) - 1 - t[j] : 4095;
+    s_row[0][r] = short(r);
+  }
+  // Prefix sums in row order of the S-token entries, the last splits below
+  // S and the merge rows: block j's sums follow block j - 1's.
+  int v[3 * kOrderBlocks], tot[3 * kOrderBlocks];
+#pragma unroll
+  for (int j = 0; j < kOrderBlocks; ++j) {
+    const bool in = tid + j * kOrderThreads < b;
+    v[3 * j] = in ? n[j] - 1 + (t[j] == int(S)) : 0;
+    v[3 * j + 1] = in ? int(t[j] < int(S)) : 0;
+    v[3 * j + 2] = in ? int(n[j] > 1) : 0;
+  }
+  order_scan<3 * kOrderBlocks>(v, tot, s_wave);
+  int full_total = 0, last_count = 0, M = 0;
+#pragma unroll
+  for (int j = 0; j < kOrderBlocks; ++j) {
+    const int r = tid + j * kOrderThreads;
+    if (r < b) { s_full[r] = full_total + v[3 * j]; s_merge[r] = M + v[3 * j + 2]; }
+    full_total += tot[3 * j];
+    last_count += tot[3 * j + 1];
+    M += tot[3 * j + 2];
+  }
+  const int W = full_total + last_count;
+  // Stable LSD radix sort of (key, row) over 12 bits, 6 per pass. Six
+  // ballots give every lane the lanes of its wave with the same digit, and
+  // lane d the count of digit d in its wave; a position is the scanned count
+  // of (digit, block, wave) plus the same-digit lanes below it.
+  const uint64_t lt = (uint64_t(1) << lane) - 1;
+  int src = 0;
+  for (int shift = 0; shift < 12; shift += kRadixBits, src ^= 1) {
+    int digit[kOrderBlocks], within[kOrderBlocks];
+#pragma unroll
+    for (int j = 0; j < kOrderBlocks; ++j) {
+      digit[j] = 0; within[j] = 0;
+      int count = 0;
+      if (j < blocks) {
+        const int d = (s_key[src][tid + j * kOrderThreads] >> shift) & (kRadixDigits - 1);
+        uint64_t peers = ~uint64_t(0), mine = ~uint64_t(0);
+#pragma unroll
+        for (int bit = 0; bit < kRadixBits; ++bit) {
+          const uint64_t m = __ballot((d >> bit) & 1);
+          peers &= ((d >> bit) & 1) ? m : ~m;
+          mine &= ((lane >> bit) & 1) ? m : ~m;
+        }
+        digit[j] = d;
+        within[j] = __popcll(peers & lt);
+        count = __popcll(mine);
+      }
+      s_cnt[(lane * kOrderBlocks + j) * kOrderWaves + wave] = count;
+    }
+    __syncthreads();
+    {
+      constexpr int PER = kRadixCounts / kOrderThreads;
+      int c[PER], sv[1] = {0}, st[1];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) { c[i] = s_cnt[tid * PER + i]; sv[0] += c[i]; }
+      order_scan<1>(sv, st, s_wave);
+      int run = sv[0];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) { s_cnt[tid * PER + i] = run; run += c[i]; }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kOrderBlocks; ++j) {
+      if (j < blocks) {
+        const int i = tid + j * kOrderThreads;
+        const int pos = s_cnt[(digit[j] * kOrderBlocks + j) * kOrderWaves + wave] + within[j];
+        if (unsigned(pos) < unsigned(kOrderRows)) {
+          s_key[src ^ 1][pos] = s_key[src][i];
+          s_row[src ^ 1][pos] = s_row[src][i];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const int per = o.per;
+  auto place = [&](int p, int r, int s) {
+    const int pass = p / per, within = p - pass * per;
+    const int width = min(per, W - pass * per);
+    const int f = pass * per + ((pass & 1) ? width - 1 - within : within);
+    if (unsigned(f) < unsigned(min(W, o.capacity))) {
+      o.list[2 * f] = r;
+      o.list[2 * f + 1] = s;
+    }
+  };
+  // The sorted last splits below S.
+  for (int p = tid; p < last_count; p += kOrderThreads) {
+    const int r = s_row[src][p];
+    if (unsigned(r) >= unsigned(b)) continue;
+    const int full = (r + 1 < b ? s_full[r + 1] : full_total) - s_full[r];
+    place(full_total + p, r, full);
+  }
+  // Each row's S-token splits and its merge entry.
+#pragma unroll
+  for (int j = 0; j < kOrderBlocks; ++j) {
+    const int r = tid + j * kOrderThreads;
+    if (r < b) {
+      const int full = n[j] - 1 + (t[j] == int(S));
+      for (int s = 0; s < full; ++s) place(s_full[r] + s, r, s);
+      const int m = s_merge[r];
+      if (n[j] > 1 && W <= o.capacity && unsigned(m) < unsigned(b)) o.list[2 * W + m] = r;
+    }
+  }
+  if (tid == 0) { o.count[0] = W; o.count[1] = M; }
 }
 
 struct QueryArgs {
@@ -1620,6 +1852,16 @@ hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
   unroll = unroll >= 4 ? 4 : unroll >= 2 ? 2 : 1;
   const size_t rank_lds = a.rank_rows ? size_t(2) * ((a.batch + 3) & ~3) * sizeof(int) : 0;
   if (unroll > kMaxUnroll) unroll = kMaxUnroll;
+  if (a.work_count) {
+    // A device-built list of unknown length: one residency round of
+    // workgroups strides over it.
+    int occ = 0;
+    if (unroll == 4) occ = decode_occupancy<DT, D, VEC, (kMaxUnroll >= 4 ? 4 : 1), WAVES, G>();
+    else if (unroll == 2) occ = decode_occupancy<DT, D, VEC, (kMaxUnroll >= 2 ? 2 : 1), WAVES, G>();
+    else occ = decode_occupancy<DT, D, VEC, 1, WAVES, G>();
+    const int64_t resident = int64_t(occ > 0 ? occ : 1) * std::max(1, device_compute_units());
+    blocks = std::min(blocks, resident);
+  }
   if constexpr (kMaxUnroll >= 4) {
     if (unroll == 4) decode_kernel<DT, D, VEC, 4, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
   }
@@ -1628,9 +1870,13 @@ hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
   }
   if (unroll == 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
   hipError_t e = hipGetLastError();
-  const int64_t merge_rows = a.work ? a.merge_rows : a.batch;
+  const int64_t merge_rows = a.work && !a.work_count ? a.merge_rows : a.batch;
   if (e != hipSuccess || a.nsplit_max == 1 || merge_rows == 0) return e;
-  merge_kernel<DT, (D > 64 ? 128 : 64)><<<grid_for(merge_rows * a.g.heads), 128>>>(a);
+  int64_t merge_blocks = merge_rows * a.g.heads;
+  // Device-built list: the merge rows' count is on the device; a grid of
+  // four workgroups per compute unit strides over them.
+  if (a.work_count) merge_blocks = std::min(merge_blocks, 4 * int64_t(std::max(1, device_compute_units())));
+  merge_kernel<DT, (D > 64 ? 128 : 64)><<<grid_for(merge_blocks), 128>>>(a);
   return hipGetLastError();
 }
 
@@ -1670,7 +1916,7 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
                   int pps, int num_slabs, int columns, int layer, int layers, int dtype,
                   int split_tokens, int unroll, int waves, int qkv_stride, const int* work,
                   int work_items, int merge_rows, void* workspace, size_t workspace_bytes,
-                  bool rank_order = false) {
+                  bool rank_order = false, int* order = nullptr) {
   const int64_t cap = int64_t(columns) * page_size;
   // A work list is built for one split length, so it must be given.
   if (work && split_tokens <= 0) return hipErrorInvalidValue;
@@ -1704,12 +1950,41 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   if (rank_order && !work && nsplit_max == 1 && b <= kRankRows) {
     a.rank_rows = 1;
     a.rank_per = std::max(1, device_compute_units() / h);
+  } else if (rank_order && !work && order) {
+    // Larger batches, and rows that may split: order_kernel writes the work
+    // list a host caller would build (count, then the list) into `order`.
+    OrderArgs oa{};
+    oa.offsets = offsets; oa.count = order; oa.list = order + 2;
+    oa.batch = b; oa.split_tokens = S; oa.cap = cap; oa.capacity = int(int64_t(b) * nsplit_max);
+    oa.per = std::max(1, device_compute_units() / h);
+    order_kernel<<<1, kOrderThreads>>>(oa);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    a.work = order + 2;
+    if (nsplit_max > 1) {
+      a.work_count = order;  // a.items stays the capacity, bh * nsplit_max
+    } else {
+      a.work_items = b;      // one entry per row
+      a.items = bh;
+    }
   }
   if (dtype == kF32) return launch_decode_dt<kF32>(a, a.items, vec, d, unroll, waves);
   if (dtype == kF16) return launch_decode_dt<kF16>(a, a.items, vec, d, unroll, waves);
   if (dtype == kBF16) return launch_decode_dt<kBF16>(a, a.items, vec, d, unroll, waves);
   return hipErrorInvalidValue;
 }
+
+// Whether the reference entries have order_kernel build their visiting
+// order (batches past the in-workgroup ranking, or rows that may split, up to
+// kOrderRows rows), and the bytes it writes: the count pair, the (row, split)
+// list and the merge rows.
+bool device_order(int b, int64_t nsplit_max) {
+  return b <= kOrderRows && (nsplit_max > 1 || b > kRankRows) && int64_t(b) * nsplit_max <= INT32_MAX / 2;
+}
+size_t order_bytes(int b, int64_t nsplit_max) {
+  return size_t(2 + 2 * int64_t(b) * nsplit_max + b) * sizeof(int);
+}
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 // Library-owned split workspace of the reference entry points, which have no
 // workspace argument (mt_paged_decode_batch for tables longer than one split,
@@ -2212,16 +2487,19 @@ int mt_paged_decode_batch(void* out, const void* q, const void* k, const void* v
   const int64_t cap = int64_t(columns) * page_size;
   const int S = choose_split(cap, 0);
   const int64_t nsplit_max = (cap + S - 1) / S;
+  const bool ordered = device_order(b, nsplit_max);
+  // Workspace: split partials, then the device-built visiting order.
+  const size_t part = nsplit_max > 1 ? align256(workspace_bytes_for(int64_t(b) * h, int(nsplit_max))) : 0;
+  const size_t ws_bytes = part + (ordered ? order_bytes(b, nsplit_max) : 0);
   void* ws = nullptr;
-  size_t ws_bytes = 0;
-  if (nsplit_max > 1) {
-    ws_bytes = workspace_bytes_for(int64_t(b) * h, int(nsplit_max));
+  if (ws_bytes) {
     const int e = library_workspace(ws_bytes, &ws);
     if (e != hipSuccess) return e;
   }
+  int* order = ordered ? reinterpret_cast<int*>(static_cast<char*>(ws) + part) : nullptr;
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, S, 0, 0, 0,
-                       nullptr, 0, 0, ws, ws_bytes, true);
+                       nullptr, 0, 0, part ? ws : nullptr, part, true, order);
 }
 
 int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const void* v,
@@ -2236,18 +2514,22 @@ int mt_paged_decode_batch_noalloc(void* out, const void* q, const void* k, const
   const int64_t cap = int64_t(columns) * page_size;
   const int S = choose_split(cap, 0);
   const int64_t nsplit_max = (cap + S - 1) / S;
+  const bool ordered = device_order(b, nsplit_max);
+  // The fixed array holds the split partials, then the device-built visiting
+  // order; a shape that needs more is refused before any launch.
+  const bool vec = decode_vec(d, dtype, out, q, k, v, int64_t(h) * d);
+  const size_t part = nsplit_max > 1 ? align256(partial_bytes(int64_t(b) * h, nsplit_max, vec, d)) : 0;
+  const size_t need = part + (ordered ? order_bytes(b, nsplit_max) : 0);
+  if (need > kNoAllocScratchBytes) return hipErrorInvalidValue;
   void* ws = nullptr;
-  if (nsplit_max > 1) {
-    // Split partials beyond the fixed array are refused, before any launch.
-    const bool vec = decode_vec(d, dtype, out, q, k, v, int64_t(h) * d);
-    if (partial_bytes(int64_t(b) * h, nsplit_max, vec, d) > kNoAllocScratchBytes)
-      return hipErrorInvalidValue;
+  if (need) {
     const int e = scratch_address(&ws);
     if (e != hipSuccess) return e;
   }
+  int* order = ordered ? reinterpret_cast<int*>(static_cast<char*>(ws) + part) : nullptr;
   return decode_common(out, q, k, v, slabs, table, offsets, b, h, d, page_size, pages_per_slab,
                        num_slabs, columns, layer, layers, dtype, S, 0, 0, 0,
-                       nullptr, 0, 0, ws, nsplit_max > 1 ? kNoAllocScratchBytes : 0, true);
+                       nullptr, 0, 0, part ? ws : nullptr, part, true, order);
 }
 
 int mt_paged_prefill_key_splits(long long* launches) {
@@ -2277,6 +2559,26 @@ int mt_paged_decode_split_tokens(int page_size, int columns, int requested, int*
   if (S < 64 || S % 64 != 0 || S > kMaxSplitTokens) return hipErrorInvalidValue;
   *split_tokens = S;
   return hipSuccess;
+}
+
+int mt_paged_decode_order(const int* offsets, int b, int h, int page_size, int columns,
+                          int split_tokens, int compute_units, int* list, int* count) {
+  if (!offsets || !list || !count || b < 1 || b > kOrderRows || h < 1 || columns < 1 ||
+      split_tokens < 0 || compute_units < 0 || !(page_size == 8 || page_size == 16 || page_size == 32) ||
+      int64_t(columns) * page_size > INT32_MAX)
+    return hipErrorInvalidValue;
+  const int64_t cap = int64_t(columns) * page_size;
+  const int S = choose_split(cap, split_tokens);
+  if (S < 64 || S % 64 != 0 || S > kMaxSplitTokens) return hipErrorInvalidValue;
+  OrderArgs oa{};
+  oa.offsets = offsets; oa.count = count; oa.list = list;
+  oa.batch = b; oa.split_tokens = S; oa.cap = cap;
+  const int64_t nsplit_max = (cap + S - 1) / S;
+  if (int64_t(b) * nsplit_max > INT32_MAX / 2) return hipErrorInvalidValue;
+  oa.capacity = int(int64_t(b) * nsplit_max);
+  oa.per = std::max(1, (compute_units ? compute_units : device_compute_units()) / h);
+  order_kernel<<<1, kOrderThreads>>>(oa);
+  return hipGetLastError();
 }
 
 int mt_paged_decode_split(void* out, const void* q, const void* k, const void* v,

@@ -88,6 +88,15 @@ def split_tokens_for(*, page_size, columns, requested=0):
     return out.value
 
 
+def paged_decode_order(offsets, *, b, h, page_size, columns, list_out, count_out, split_tokens=0,
+                       compute_units=0):
+    """``mt_paged_decode_order``: the work list of :func:`decode_work_list`
+    built on the device from the device ``offsets`` (what
+    ``mt_paged_decode_batch`` does for batches it does not rank in-kernel)."""
+    call(paged_library(), 'mt_paged_decode_order', [P, I, I, I, I, I, I, P, P],
+         offsets, b, h, page_size, columns, split_tokens, compute_units, list_out, count_out)
+
+
 SPLIT_ARGTYPES = [P] * 7 + [I] * 14 + [P, I, I, P, Z]
 
 

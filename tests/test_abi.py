@@ -125,6 +125,20 @@ def test_split_entry_validation_and_workspace_size():
     assert split(*common, 64, 0, 1, 0, 1024, 0, 0, 0, 8, 0, 0, None, 0) == 0
 
 
+def test_order_entry_rejects_invalid_arguments():
+    # mt_paged_decode_order refuses before any launch: batch outside
+    # 1..2048, no heads, page size, split length, negative compute units,
+    # null pointers
+    f = library('paged_attention_kernel').mt_paged_decode_order
+    f.argtypes, f.restype = [P, I, I, I, I, I, I, P, P], I
+    ok = (8, 4, 12, 16, 64, 0, 0, 8, 8)
+    for i, bad in [(1, 0), (1, 2049), (2, 0), (3, 12), (4, 0), (5, 96), (5, 4096), (6, -1),
+                   (0, None), (7, None), (8, None)]:
+        args = list(ok)
+        args[i] = bad
+        assert f(*args) == 1, (i, bad)
+
+
 def test_inference_entries_reject_invalid_shapes():
     lib = library('inference_kernels')
     g = lib.mt_embedding_gather

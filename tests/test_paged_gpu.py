@@ -353,28 +353,82 @@ def test_multi_token_append_and_causal_attention(dtype):
     assert_attention_close(out.to_numpy(), ref, dtype)
 
 
-@pytest.mark.parametrize('batch', [4, 200, 256, 257])
-def test_decode_batch_device_ranked_order(batch):
-    # Without a host work list mt_paged_decode_batch ranks the rows by their
-    # offsets inside every workgroup (b <= 256, one split per row) and visits
-    # them longest first in passes of compute_units / heads rows, every other
-    # pass reversed; 257 rows take batch order. Many equal lengths (ties go
-    # by row), an empty row (offset -1: zero output, no append) and a row past
-    # its table (NaN output, no append) keep the ranking a permutation: every
-    # (row, head) is written once, equal to the oracle, and the pool image
-    # matches bit for bit.
+@pytest.mark.parametrize('batch,columns', [(4, 64), (200, 64), (256, 64), (257, 64), (700, 64),
+                                           (2100, 64), (5, 160), (300, 160)])
+def test_decode_batch_device_ranked_order(batch, columns):
+    # Without a host work list mt_paged_decode_batch visits the rows longest
+    # first: b <= 256 rows of one split are ranked inside every workgroup;
+    # larger batches and tables that may split (160 columns: 2560 tokens, up
+    # to three splits) get a work list from order_kernel and a grid that
+    # strides over it; 2100 rows take batch order. Many equal lengths (ties
+    # go by row), an empty row (offset -1: zero output, no append) and a row
+    # past its table (NaN output, no append) keep every order a permutation:
+    # every (row, head) is written once, equal to the oracle, and the pool
+    # image matches bit for bit.
     import dataclasses
-    rng = np.random.default_rng([17, batch])
-    lengths = rng.choice([1, 16, 17, 64, 200, 1024], size=batch)
+    rng = np.random.default_rng([17, batch, columns])
+    choices = [1, 16, 17, 64, 200, 1024] + ([1025, 2048, 2049, 2560] if columns > 64 else [])
+    lengths = rng.choice(choices, size=batch)
     case = make_decode_case(17, batch=batch, heads=3, dim=64, page_size=16, lengths=lengths,
                             pool_pages=int(((lengths + 15) // 16).sum()) // 8 * 8 + 8, pages_per_slab=8,
-                            dtype='float16', columns=64)
+                            dtype='float16', columns=columns)
     lengths = case.lengths.copy()
-    lengths[1] = 0                     # offset -1
-    lengths[batch - 2] = 64 * 16 + 5   # beyond the 64-column table
+    lengths[1] = 0                          # offset -1
+    lengths[batch - 2] = columns * 16 + 5   # beyond the table
     case = dataclasses.replace(case, lengths=lengths)
     dev, out = check_case(case)
     assert np.all(out[1] == 0) and np.all(np.isnan(out[batch - 2]))
+
+
+def _device_order(lengths, *, heads, page_size, columns, split_tokens=0, compute_units=0):
+    b = len(lengths)
+    S = paged_ops.split_tokens_for(page_size=page_size, columns=columns, requested=split_tokens)
+    nsplit = -(-columns * page_size // S)
+    offsets = RawDeviceBuffer(4 * b)
+    offsets.upload(np.asarray(lengths, np.int64).astype(np.int32) - 1)
+    cap = 2 * b * nsplit + b
+    lst = RawDeviceBuffer(4 * cap)
+    lst.fill_words(0x7EEEEEEE)
+    cnt = RawDeviceBuffer(8)
+    paged_ops.paged_decode_order(offsets.ptr, b=b, h=heads, page_size=page_size, columns=columns,
+                                 list_out=lst.ptr, count_out=cnt.ptr, split_tokens=split_tokens,
+                                 compute_units=compute_units)
+    runtime().synchronize()
+    w, m = (int(x) for x in cnt.download(np.int32, 2))
+    return lst.download(np.int32, cap), w, m, S
+
+
+@pytest.mark.parametrize('batch,heads,page_size,columns,split,cus', [
+    (1, 12, 16, 64, 0, 256), (64, 12, 16, 64, 0, 256), (300, 12, 16, 64, 0, 256),
+    (512, 25, 16, 512, 0, 256), (512, 25, 32, 256, 0, 256), (160, 25, 16, 200, 256, 100),
+    (2048, 7, 8, 300, 0, 256), (999, 16, 16, 64, 512, 37), (33, 300, 16, 128, 64, 256)])
+def test_device_order_equals_host_work_list(batch, heads, page_size, columns, split, cus):
+    # order_kernel's list equals paged_ops.decode_work_list (the numpy/Python
+    # restatement of the scheduling order) element for element: ties of equal
+    # lengths, lengths on split boundaries, one-token rows, full tables, more
+    # heads than compute units (passes of one entry)
+    rng = np.random.default_rng([5, batch, columns])
+    cap_tokens = columns * page_size
+    S = paged_ops.split_tokens_for(page_size=page_size, columns=columns, requested=split)
+    pool = np.unique(np.clip([1, 2, S - 1, S, S + 1, 2 * S, cap_tokens, cap_tokens - 1, 100, 257], 1, cap_tokens))
+    lengths = np.where(rng.random(batch) < 0.5, rng.choice(pool, batch), rng.integers(1, cap_tokens + 1, batch))
+    got, w, m, S2 = _device_order(lengths, heads=heads, page_size=page_size, columns=columns,
+                                  split_tokens=split, compute_units=cus)
+    assert S2 == S
+    ref, items, merges = paged_ops.decode_work_list(lengths.tolist(), heads, S, cus)
+    assert (w, m) == (items, merges)
+    assert np.array_equal(got[:2 * w + m], ref)
+
+
+def test_device_order_empty_and_past_table_rows():
+    # offset -1 (no key) and a row past its table each get one pair, split 0;
+    # every (row, split) of the others appears exactly once
+    lengths = np.array([0, 3000, 5, 1024 * 4 + 1, 2049, 1])  # columns 256 x 16 = 4096 tokens
+    got, w, m, S = _device_order(lengths, heads=4, page_size=16, columns=256)
+    pairs = got[:2 * w].reshape(-1, 2)
+    want = {(0, 0), (3, 0), (2, 0), (5, 0)} | {(1, s) for s in range(3)} | {(4, s) for s in range(3)}
+    assert sorted(map(tuple, pairs.tolist())) == sorted(want)
+    assert list(got[2 * w:2 * w + m]) == [1, 4]
 
 
 def test_many_residency_rounds_back_to_back():
