@@ -105,18 +105,24 @@ __device__ __forceinline__ bool better(const Cand& b, const Cand& a) {
   return b.k > a.k || (b.k == a.k && b.i < a.i);
 }
 
-constexpr int kArgmaxThreads = 512;
+constexpr int kArgmaxThreads = 1024;
+// 16-byte vectors each thread loads before comparing any: 128 KiB of a row per
+// round trip, so a 16-bit row of up to 64 Ki elements (GPT-2's 50257-wide
+// logits) is read in one.
+constexpr int kArgmaxBatch = 8;
 
-// One workgroup of 8 waves per row. The aligned interior of the row is read
-// with 16-byte loads; the unaligned head and tail element by element.
+// One workgroup of 16 waves per row. The aligned interior of the row is read
+// with 16-byte loads; the unaligned head and tail element by element, issued
+// with the first batch of vectors.
 template <int DT>
 __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, const void* src,
                                                                     int width, float* slot_tokens,
                                                                     const int* slots, int num_slots) {
   using T = typename Elem<DT>::T;
   constexpr int E = per16<DT>();
-  __shared__ int s_k[kArgmaxThreads / 64];
-  __shared__ int s_i[kArgmaxThreads / 64];
+  constexpr int NW = kArgmaxThreads / 64;
+  __shared__ int s_k[NW];
+  __shared__ int s_i[NW];
   const int row = blockIdx.x;
   const T* p = static_cast<const T*>(src) + int64_t(row) * width;
   const int tid = threadIdx.x;
@@ -130,25 +136,31 @@ __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, 
     else return uint32_t(x);
   };
   const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
-  int head = int(((16 - (addr & 15)) & 15) / sizeof(T));
+  // A row not aligned to its element size takes the element-by-element
+  // (tail) loop for all of it.
+  const bool aligned = (addr & (sizeof(T) - 1)) == 0;
+  int head = aligned ? int(((16 - (addr & 15)) & 15) / sizeof(T)) : 0;
   if (head > width) head = width;
-  if ((addr & (sizeof(T) - 1)) != 0) head = width;  // misaligned element type: scalar path
-  const int nvec = (width - head) / E;
+  const int nvec = aligned ? (width - head) / E : 0;
   const int tail = head + nvec * E;
-  if (tid < head) consider(raw(p[tid]), tid);
   const auto* vp = global_view(reinterpret_cast<const u32x4*>(p + head));
-  // kBatch vectors per thread are loaded before any is compared, so one row
-  // is read in a few round trips instead of one per 8 KiB.
-  constexpr int kBatch = 8;
-  for (int j0 = tid; j0 < nvec; j0 += kArgmaxThreads * kBatch) {
-    u32x4 x[kBatch];
+  // The head (< E elements) and the tail (< E elements, or the whole row on
+  // the scalar path) ride with the first batch; a thread's elements are
+  // compared in increasing index order (head, vectors, tail), so a strictly
+  // greater key keeps its first maximum.
+  uint32_t hb = 0;
+  const bool has_head = tid < head;
+  if (has_head) hb = raw(p[tid]);
+  for (int j0 = tid; j0 < nvec; j0 += kArgmaxThreads * kArgmaxBatch) {
+    u32x4 x[kArgmaxBatch];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
+    for (int u = 0; u < kArgmaxBatch; ++u) {
       const int j = j0 + u * kArgmaxThreads;
       if (j < nvec) x[u] = vp[j];
     }
+    if (j0 == tid && has_head) consider(hb, tid);
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
+    for (int u = 0; u < kArgmaxBatch; ++u) {
       const int j = j0 + u * kArgmaxThreads;
       if (j < nvec) {
         const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
@@ -166,6 +178,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, 
       }
     }
   }
+  if (tid >= nvec && has_head) consider(hb, tid);  // threads without vectors
   for (int j = tail + tid; j < width; j += kArgmaxThreads) consider(raw(p[j]), j);
   Cand c{bk, bi};
 #pragma unroll
@@ -176,18 +189,21 @@ __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, 
   const int wave = tid >> 6;
   if ((tid & 63) == 0) { s_k[wave] = c.k; s_i[wave] = c.i; }
   __syncthreads();
-  if (tid == 0) {
-    Cand best{s_k[0], s_i[0]};
-    for (int w = 1; w < kArgmaxThreads / 64; ++w) {
-      const Cand o{s_k[w], s_i[w]};
+  if (tid < 64) {
+    Cand best{tid < NW ? s_k[tid] : INT_MIN, tid < NW ? s_i[tid] : INT_MAX};
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const Cand o{__shfl_xor(best.k, off), __shfl_xor(best.i, off)};
       if (better(o, best)) best = o;
     }
-    dst[row] = float(best.i);
-    // Token feedback: the row's cache slot keeps the chosen token for the
-    // next decode step (a slot outside the table is skipped).
-    if (slot_tokens) {
-      const int s = slots[row];
-      if (s >= 0 && s < num_slots) slot_tokens[s] = float(best.i);
+    if (tid == 0) {
+      dst[row] = float(best.i);
+      // Token feedback: the row's cache slot keeps the chosen token for the
+      // next decode step (a slot outside the table is skipped).
+      if (slot_tokens) {
+        const int s = slots[row];
+        if (s >= 0 && s < num_slots) slot_tokens[s] = float(best.i);
+      }
     }
   }
 }

@@ -62,6 +62,51 @@ def test_row_argmax_unaligned_rows():
     assert greedy_token(t).to_numpy()[:, 0].tolist() == np.argmax(x[:, 0].astype(np.float32), -1).tolist()
 
 
+@pytest.mark.parametrize('rows', [1, 2, 3, 64, 128, 200, 256])
+def test_row_argmax_row_counts_and_element_positions(rows):
+    # GPT-2's 50257-wide bf16 logits at 1..256 rows (odd width: every row
+    # starts at another 16-byte phase, so head, vectors and tail all occur);
+    # each row's maximum sits in its head, a vector or its tail, sometimes
+    # tied with an earlier or later equal value (first index wins) or beaten
+    # by a NaN
+    rng = np.random.default_rng([9, rows])
+    width = 50257
+    x = rng.standard_normal((rows, 1, width)).astype(np.float32)
+    spots = [0, 1, 6, 7, 8, 15, 100, width // 2, width - 9, width - 2, width - 1]
+    for r in range(rows):
+        j = spots[r % len(spots)]
+        x[r, 0, j] = 60.0
+        if r % 3 == 1:
+            x[r, 0, (j + 12345) % width] = 60.0   # a tie
+        if r % 7 == 5:
+            x[r, 0, (j * 7 + 3) % width] = np.nan
+    stored = po.encode(x, 2)
+    t = DeviceTensor(x.shape, 'bfloat16')
+    runtime().h2d(t.ptr, stored)
+    got = greedy_token(t).to_numpy()[:, 0]
+    ref = po.row_argmax(po.decode(stored, 2))[:, 0]
+    assert got.tolist() == ref.tolist()
+
+
+@pytest.mark.parametrize('dtype,width', [('float16', 200003), ('float32', 50257), ('float32', 70001)])
+def test_row_argmax_rows_longer_than_one_round_trip(dtype, width):
+    # rows longer than the 128 KiB one workgroup loads per round trip: the
+    # maximum in the first, a middle and the last round, with a tie across rounds
+    rng = np.random.default_rng(width)
+    x = rng.standard_normal((5, 1, width)).astype(np.float32)
+    per_round = 131072 // (4 if dtype == 'float32' else 2)   # elements per round trip
+    for r, j in enumerate([3, width // 2, width - 1, per_round + 1, per_round - 1]):
+        x[r, 0, j] = 70.0
+    x[4, 0, width - 5] = 70.0
+    code = {'float32': 0, 'float16': 1}[dtype]
+    stored = po.encode(x, code)
+    t = DeviceTensor(x.shape, dtype)
+    runtime().h2d(t.ptr, stored)
+    got = greedy_token(t).to_numpy()[:, 0]
+    ref = po.row_argmax(po.decode(stored, code))[:, 0]
+    assert got.tolist() == ref.tolist()
+
+
 @pytest.mark.parametrize('dtype', ['float32', 'bfloat16'])
 def test_last_position(dtype):
     rng = np.random.default_rng(1)
