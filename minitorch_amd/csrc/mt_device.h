@@ -119,4 +119,38 @@ struct Mfma<kBF16> {
   }
 };
 
+// Inclusive prefix sum over a wave: Hillis-Steele shifts of 1, 2, 4 and 8
+// lanes inside each row of 16 (lanes shifted in from outside the row add 0),
+// then rows 1 and 3 add lane 15 of the row before and rows 2 and 3 add lane 31.
+__device__ __forceinline__ int wave_inclusive_add(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
+  return x;
+}
+
+// Keeps a kernel argument in scalar registers from here on: the empty asm
+// reads and writes it, so the compiler loads it at this point (together with
+// the other arguments pinned next to it, one round trip for all of their
+// kernarg cache lines) and cannot load it again later from the kernarg
+// segment, where a first touch of a line mid-kernel costs a memory round trip.
+template <class T>
+__device__ __forceinline__ T pin_arg(T x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+// pin_arg for a pointer to global memory, returned in the global address
+// space: the asm hides where the pointer came from, and a generic pointer
+// would make every access a flat instruction, which the LDS counter also
+// counts (an LDS wait would then wait for those stores to be acknowledged).
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* pin_global(T* p) {
+  auto g = global_view(p);
+  asm volatile("" : "+s"(g));
+  return g;
+}
+
 }  // namespace mt

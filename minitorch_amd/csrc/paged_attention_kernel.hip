@@ -931,19 +931,6 @@ constexpr int kOrderBlocks = kOrderRows / kOrderThreads;  // rows per thread (st
 constexpr int kRadixCounts = kRadixDigits * kOrderBlocks * kOrderWaves;
 static_assert(kRadixDigits == 64 && kRadixCounts % kOrderThreads == 0, "order_kernel layout");
 
-// Inclusive prefix sum over a wave: Hillis-Steele shifts of 1, 2, 4 and 8
-// lanes inside each row of 16 (lanes shifted in from outside the row add 0),
-// then rows 1 and 3 add lane 15 of the row before and rows 2 and 3 add lane 31.
-__device__ __forceinline__ int wave_inclusive_add(int x) {
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
-  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
-  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
-  return x;
-}
-
 // Exclusive prefix sums of V per-thread values over a workgroup of
 // kOrderThreads, in thread order; totals in tot[].
 template <int V>

@@ -26,6 +26,9 @@ namespace {
 constexpr int kThreads = 1024;
 constexpr int kPrepareRows = 2048;  // rows of a decode step whose slot and page count stay in LDS
 constexpr int kTableUnroll = 8;     // block-table entries each thread loads before storing
+// Block-table entries each thread of decode_prepare_kernel holds in registers
+// when the whole table of a step fits (b * columns <= kThreads * kEarlyTable).
+constexpr int kEarlyTable = 16;
 
 struct Header {           // must match include/mt_sched.h (mt_pool_header)
   int top;                // free pages on the stack
@@ -95,31 +98,45 @@ __device__ __forceinline__ int mark_issued(const Pool& p, int page, int owner) {
 }
 
 __device__ __forceinline__ void open_slabs(const Pool& p, int first, int count) {
-  for (int s = threadIdx.x; s < count; s += blockDim.x)
+  for (int s = threadIdx.x; s < count; s += kThreads)
     p.slab_table[first + s] = p.pool_base + (unsigned long long)(first + s) * p.slab_bytes;
 }
 
-// Block-wide exclusive scan of one int per thread (blockDim.x <= 1024).
-__device__ int block_exclusive_scan(int x, int* total, int* sh) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = (blockDim.x + 63) >> 6;
-  int incl = x;
+// Workgroup-wide exclusive prefix sums of N ints per thread, in thread order
+// (workgroups of kThreads threads, all of them calling): DPP wave scans, then
+// every thread adds the totals of the waves before its own. sh: N * 16 ints.
+template <int N>
+__device__ __forceinline__ void block_scan(int (&x)[N], int (&total)[N], int* sh) {
+  constexpr int W = kThreads / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl[N];
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(incl, off);
-    if (lane >= off) incl += y;
-  }
-  if (lane == 63 || tid == int(blockDim.x) - 1) sh[wave] = incl;
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int w = 0; w < nw; ++w) { const int v = sh[w]; sh[w] = run; run += v; }
-    sh[32] = run;
+  for (int j = 0; j < N; ++j) incl[j] = mt::wave_inclusive_add(x[j]);
+  if (lane == 63) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) sh[j * W + wave] = incl[j];
   }
   __syncthreads();
-  const int excl = sh[wave] + incl - x;
-  *total = sh[32];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const int v = sh[j * W + w];
+      before += w < wave ? v : 0;
+      all += v;
+    }
+    x[j] = before + incl[j] - x[j];
+    total[j] = all;
+  }
   __syncthreads();
-  return excl;
+}
+
+__device__ __forceinline__ int block_exclusive_scan(int x, int* total, int* sh) {
+  int v[1] = {x}, t[1];
+  block_scan<1>(v, t, sh);
+  *total = t[0];
+  return v[0];
 }
 
 // Bulk pop of `count` pages (one reference acquire(count)): opens slabs first
@@ -302,56 +319,157 @@ __global__ __launch_bounds__(kThreads) void decode_prepare_kernel(Pool p, const 
                                                                   int limit, int* table,
                                                                   int* offsets, float* positions,
                                                                   int* cu_seqlens, int* new_page) {
-  __shared__ int sh[33];
+  constexpr int TOPS = kPrepareRows / kThreads;  // stack-top candidates per thread
+  // Every argument is loaded at entry and kept in scalar registers; global
+  // memory is reached through global-address-space pointers only.
+  const auto h = mt::pin_global(p.h);
+  const auto stack = mt::pin_global(p.stack);
+  const auto issued = mt::pin_global(p.issued);
+  const auto owner = mt::pin_global(p.owner);
+  const auto slab_table = mt::pin_global(p.slab_table);
+  const auto slot_len = mt::pin_global(p.slot_len);
+  const auto slot_npages = mt::pin_global(p.slot_npages);
+  const auto slot_pages = mt::pin_global(p.slot_pages);
+  const auto g_slots = mt::pin_global(slots);
+  const auto g_table = mt::pin_global(table);
+  const auto g_offsets = mt::pin_global(offsets);
+  const auto g_positions = mt::pin_global(positions);
+  const auto g_cu = mt::pin_global(cu_seqlens);
+  const auto g_new = mt::pin_global(new_page);
+  const int max_pages = mt::pin_arg(p.max_pages), max_cols = mt::pin_arg(p.max_cols);
+  const unsigned long long pool_base = mt::pin_arg(p.pool_base), slab_bytes = mt::pin_arg(p.slab_bytes);
+  b = mt::pin_arg(b); columns = mt::pin_arg(columns);
+  page_size = mt::pin_arg(page_size); limit = mt::pin_arg(limit);
+  __shared__ int sh[2 * (kThreads / 64)];
   __shared__ int s_red;
-  // Each row's slot and page count after this step, kept for the table pass
-  // (rows past kPrepareRows read them again from the pool state).
-  __shared__ int s_slot[kPrepareRows], s_npages[kPrepareRows];
-  if (threadIdx.x == 0) s_red = 0;
-  const int F = p.h->top, opened = p.h->slabs_opened, pps = p.pages_per_slab;
+  // Each row's slot, page count before this step and popped page (-1: none),
+  // kept for the table (rows past kPrepareRows read them from the pool
+  // state); s_top[k]: the k-th page from the top of the free stack, and
+  // s_topbit[k] its issued bit (a pop of it is a reuse).
+  __shared__ int s_slot[kPrepareRows], s_have[kPrepareRows], s_new[kPrepareRows], s_top[kPrepareRows];
+  __shared__ unsigned char s_topbit[kPrepareRows];
+  const int tid = threadIdx.x;
+  if (tid == 0) s_red = 0;
+  const int F = h->top, opened = h->slabs_opened, pps = mt::pin_arg(p.pages_per_slab);
   // limit -1: the pages the budget has left, read from the pool header on
   // the device (so that a captured step needs no host-computed budget).
-  if (limit < 0) limit = p.max_pages - p.h->leased;
+  if (limit < 0) limit = max_pages - h->leased;
+  // Every load is issued from straight-line code at clamped (always valid)
+  // addresses, so the compiler counts them exactly and a wait covers only
+  // the loads it needs, and every load is consumed before the first global
+  // store (gfx9 counts stores and loads together, so a load consumed after
+  // stores would wait for their acknowledgements). The chain:
+  //   1. the slots of this thread's row and of its table entries;
+  //   2. the row's length and page count, every table entry's current
+  //      page-list value (when the whole table fits the threads' registers;
+  //      this step changes only the entry at each popping row's old page
+  //      count) and the top of the free stack;
+  //   3. the issued bits of those stack pages (a page from a slab opened now
+  //      was never issued), in flight while the ranks are scanned.
+  const int64_t entries = int64_t(b) * columns;
+  const bool early = entries <= int64_t(kThreads) * kEarlyTable && b <= kPrepareRows;
+  const float inv_columns = 1.0f / float(columns);
+  auto entry_row = [&](int e) {  // e / columns for e < 2^24 (one correction step)
+    int i = int(float(e) * inv_columns);
+    i -= i * columns > e;
+    i += (i + 1) * columns <= e;
+    return i;
+  };
+  const int last_entry = int(min(entries, int64_t(kThreads) * kEarlyTable)) - 1;
+  const int slot0 = g_slots[min(tid, b - 1)];
+  int tslot[kEarlyTable], tcol[kEarlyTable], tv[kEarlyTable];
+  if (early) {
+#pragma unroll
+    for (int u = 0; u < kEarlyTable; ++u) {
+      const int e = min(tid + u * kThreads, last_entry);
+      const int i = entry_row(e);
+      tcol[u] = e - i * columns;
+      tslot[u] = g_slots[i];
+    }
+  }
+  const int len0 = slot_len[slot0];
+  const int have0 = slot_npages[slot0];
+  if (early) {
+#pragma unroll
+    for (int u = 0; u < kEarlyTable; ++u) tv[u] = slot_pages[int64_t(tslot[u]) * max_cols + tcol[u]];
+  }
+  const int top_n = min(min(b, F), kPrepareRows);
+  int sv[TOPS];
+#pragma unroll
+  for (int j = 0; j < TOPS; ++j) {
+    const int k = min(j * kThreads + tid, max(top_n - 1, 0));
+    sv[j] = stack[top_n > 0 ? F - 1 - k : 0];
+  }
+  unsigned bw[TOPS];
+#pragma unroll
+  for (int j = 0; j < TOPS; ++j) {
+    sv[j] = min(max(sv[j], 0), max_pages - 1);  // in the pool whatever the stack holds
+    bw[j] = issued[sv[j] >> 5];
+    if (j * kThreads + tid < top_n) s_top[j * kThreads + tid] = sv[j];
+  }
   __syncthreads();
-  int need_base = 0, seq_base = 0, reused = 0, last_rank = -1;
-  for (int base = 0; base < b; base += blockDim.x) {
-    const int i = base + threadIdx.x;
-    const int slot = i < b ? slots[i] : 0;
-    const int len = i < b ? p.slot_len[slot] : 0;
-    const int have = i < b ? p.slot_npages[slot] : 0;
-    const int need = (i < b && (len + 1 + page_size - 1) / page_size > have) ? 1 : 0;
-    int total_need, total_seq;
-    const int rank = need_base + block_exclusive_scan(need, &total_need, sh);
-    const int seq = seq_base + block_exclusive_scan(i < b ? len + 1 : 0, &total_seq, sh);
-    if (i < b) {
-      offsets[i] = len;
-      positions[i] = float(len);
-      cu_seqlens[i] = seq;
-      int page = -1;
-      if (need && rank < limit) {
-        if (rank < F) {
-          page = p.stack[F - 1 - rank];
-        } else {
-          const int k = rank - F;
-          page = (opened + k / pps) * pps + k % pps;
+  int need_base = 0, seq_base = 0, reused = 0;
+  int rank0 = 0, seq0 = 0, need0 = 0;
+  auto scan_pass = [&](int base, int len, int have, int& rank, int& seq, int& need) {
+    const bool in = base + tid < b;
+    need = (in && (len + page_size) / page_size > have) ? 1 : 0;
+    int x[2] = {need, in ? len + 1 : 0}, tot[2];
+    block_scan<2>(x, tot, sh);
+    rank = need_base + x[0];
+    seq = seq_base + x[1];
+    need_base += tot[0];
+    seq_base += tot[1];
+  };
+  // Pops of one pass of kThreads rows (every load already consumed).
+  auto pop_pass = [&](int base, int slot, int len, int have, int rank, int seq, int need) {
+    const int i = base + tid;
+    const bool in = i < b;
+    const bool pop = need && rank < limit;
+    int page = -1;
+    if (pop) {
+      if (rank < F) {
+        if (rank < top_n) {
+          page = s_top[rank];
+          reused += s_topbit[rank];
+        } else {  // past the candidates kept in LDS (batches above kPrepareRows rows)
+          page = stack[F - 1 - rank];
+          reused += (issued[page >> 5] >> (page & 31)) & 1;
         }
-        reused += mark_issued(p, page, slot);
-        p.slot_pages[int64_t(slot) * p.max_cols + have] = page;
-        p.slot_npages[slot] = have + 1;
-        last_rank = rank;
+      } else {
+        const int k = rank - F;
+        page = (opened + k / pps) * pps + k % pps;
       }
-      new_page[i] = page;
+      owner[page] = slot;
+      __hip_atomic_fetch_or(&issued[page >> 5], 1u << (page & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      slot_pages[int64_t(slot) * max_cols + have] = page;
+      slot_npages[slot] = have + 1;
+    }
+    if (in) {
+      g_offsets[i] = len;
+      g_positions[i] = float(len);
+      g_cu[i] = seq;
+      g_new[i] = page;
       if (i < kPrepareRows) {
         s_slot[i] = slot;
-        s_npages[i] = page >= 0 ? have + 1 : have;
+        s_have[i] = have;
+        s_new[i] = page;
       }
     }
-    need_base += total_need;
-    seq_base += total_seq;
-  }
-  if (threadIdx.x == 0) cu_seqlens[b] = seq_base;
-  atomicAdd(&s_red, reused);
+  };
+  scan_pass(0, len0, have0, rank0, seq0, need0);
+#pragma unroll
+  for (int j = 0; j < TOPS; ++j)
+    if (j * kThreads + tid < top_n) s_topbit[j * kThreads + tid] = (bw[j] >> (sv[j] & 31)) & 1;
   __syncthreads();
+  pop_pass(0, slot0, len0, have0, rank0, seq0, need0);
+  for (int base = kThreads; base < b; base += kThreads) {
+    const int slot = g_slots[min(base + tid, b - 1)];
+    const int len = slot_len[slot], have = slot_npages[slot];
+    int rank, seq, need;
+    scan_pass(base, len, have, rank, seq, need);
+    pop_pass(base, slot, len, have, rank, seq, need);
+  }
+  if (tid == 0) g_cu[b] = seq_base;
   const int pops = need_base < limit ? need_base : limit;
   // Leftover pages of the last slab opened by the sequential pops stay on the
   // stack, reversed (its unused IDs with the smallest unused on top).
@@ -362,40 +480,54 @@ __global__ __launch_bounds__(kThreads) void decode_prepare_kernel(Pool p, const 
     const int used_last = m - (nslab - 1) * pps;
     const int last = opened + nslab - 1;
     top = pps - used_last;
-    for (int j = threadIdx.x; j < top; j += blockDim.x) p.stack[j] = last * pps + pps - 1 - j;
+    for (int j = tid; j < top; j += kThreads) stack[j] = last * pps + pps - 1 - j;
   }
-  (void)last_rank;
-  open_slabs(p, opened, nslab);
+  for (int s = tid; s < nslab; s += kThreads)
+    slab_table[opened + s] = pool_base + (unsigned long long)(opened + s) * slab_bytes;
+  atomicAdd(&s_red, reused);
   __syncthreads();
-  // Table rows: kTableUnroll entries per thread are loaded before any is
-  // stored, so their page-list reads overlap instead of taking one round
-  // trip each.
-  const int64_t entries = int64_t(b) * columns;
-  for (int64_t e0 = threadIdx.x; e0 < entries; e0 += int64_t(blockDim.x) * kTableUnroll) {
-    int v[kTableUnroll];
+  if (early) {
+    // entry (i, c): the old page list below the row's old count, the popped
+    // page at it, -1 beyond
 #pragma unroll
-    for (int u = 0; u < kTableUnroll; ++u) {
-      const int64_t e = e0 + int64_t(u) * blockDim.x;
-      v[u] = -1;
+    for (int u = 0; u < kEarlyTable; ++u) {
+      const int e = tid + u * kThreads;
       if (e < entries) {
-        const int i = int(e / columns), c = int(e - int64_t(i) * columns);
-        const int slot = i < kPrepareRows ? s_slot[i] : slots[i];
-        const int np = i < kPrepareRows ? s_npages[i] : p.slot_npages[slot];
-        if (c < np) v[u] = p.slot_pages[int64_t(slot) * p.max_cols + c];
+        const int i = entry_row(e), c = tcol[u];
+        const int have = s_have[i];
+        g_table[e] = c < have ? tv[u] : (c == have ? s_new[i] : -1);
       }
     }
+  } else {
+    // Table rows: kTableUnroll entries per thread are loaded before any is
+    // stored, so their page-list reads overlap instead of taking one round
+    // trip each.
+    for (int64_t e0 = tid; e0 < entries; e0 += int64_t(kThreads) * kTableUnroll) {
+      int v[kTableUnroll];
 #pragma unroll
-    for (int u = 0; u < kTableUnroll; ++u) {
-      const int64_t e = e0 + int64_t(u) * blockDim.x;
-      if (e < entries) table[e] = v[u];
+      for (int u = 0; u < kTableUnroll; ++u) {
+        const int64_t e = e0 + int64_t(u) * kThreads;
+        v[u] = -1;
+        if (e < entries) {
+          const int i = int(e / columns), c = int(e - int64_t(i) * columns);
+          const int slot = i < kPrepareRows ? s_slot[i] : g_slots[i];
+          const int np = i < kPrepareRows ? s_have[i] + (s_new[i] >= 0) : slot_npages[slot];
+          if (c < np) v[u] = slot_pages[int64_t(slot) * max_cols + c];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kTableUnroll; ++u) {
+        const int64_t e = e0 + int64_t(u) * kThreads;
+        if (e < entries) g_table[e] = v[u];
+      }
     }
   }
-  if (threadIdx.x == 0) {
-    p.h->top = top;
-    p.h->slabs_opened = opened + nslab;
-    p.h->leased += pops;
-    p.h->acquires += pops;
-    p.h->reuses += s_red;
+  if (tid == 0) {
+    h->top = top;
+    h->slabs_opened = opened + nslab;
+    h->leased += pops;
+    h->acquires += pops;
+    h->reuses += s_red;
   }
 }
 

@@ -270,6 +270,49 @@ def test_decode_batch_of_2143_rows_matches_oracle():
     assert_same_pool(pool, oracle)
 
 
+@pytest.mark.parametrize('rows,capacity', [(700, 256), (1500, 128), (300, 1024), (1024, 256)])
+def test_decode_batch_table_paths_match_oracle(rows, capacity):
+    # The metadata kernel holds the whole table in registers when rows x
+    # columns <= 16384 (700 x 16, 1500 x 8 over two 1024-row passes, 1024 x 16)
+    # and re-reads the page lists otherwise (300 x 64): pages, table and free
+    # list bit-exact over two steps that pop reused pages and open slabs.
+    rng = np.random.default_rng([11, rows])
+    model = StubModel(layers=1, heads=1, dim=64, n_positions=capacity)
+    pool, oracle = pool_pair(model, page_size=16, max_bytes=(rows * capacity // 16 + 64) * 2 * 64 * 16 * 4,
+                             pages_per_slab=32)
+    pairs = []
+    for _ in range(rows + rows // 5 + 8):
+        n = int(rng.integers(1, capacity - 4))
+        c = PagedKVCache(model, 1, capacity, page_size=16, page_pool=pool)
+        oc = CacheOracle(oracle, 1, capacity)
+        c.prepare_append(n)
+        oc.prepare_append(n)
+        c._written_layers.update(range(len(c.layout)))
+        c.commit_append()
+        oc.commit_append()
+        pairs.append((c, oc))
+    # close every seventh request, then all past the first `rows` left
+    live = []
+    for i, (c, oc) in enumerate(pairs):
+        if i % 7 == 3 or len(live) == rows:
+            c.close()
+            oc.close()
+        else:
+            live.append((c, oc))
+    assert len(live) == rows
+    order = list(rng.permutation(len(live)))
+    live = [live[i] for i in order]
+    for _ in range(2):
+        _decode_round(model, pool, oracle, live, rng)
+        for c, oc in live:
+            assert c.pages() == oc.pages
+        assert_same_pool(pool, oracle)
+    for c, oc in live:
+        c.close()
+        oc.close()
+    assert_same_pool(pool, oracle)
+
+
 def test_decode_budget_exhaustion_aborts_like_reference():
     model = StubModel(layers=1, heads=1, dim=64, n_positions=128)
     page_bytes = 2 * 1 * 1 * 64 * 16 * 4
