@@ -86,7 +86,17 @@ constexpr int kLdsSlabs = 512;
 struct Geometry {
   int heads, dim, page_size, log2_page, pps, num_slabs, columns, layer;
   int64_t kind_stride;  // elements between the K and V planes of one layer
+  // p / pps for 0 <= p < 2^31 as (p * pps_magic) >> pps_shift, so that page
+  // resolution needs no division: pps_magic = ceil(2^(31+s) / pps) with
+  // s = ceil(log2 pps), pps_shift = 31 + s (the error n * e / 2^(31+s),
+  // e < 1, stays below 1 / pps for n < 2^31 since pps <= 2^s).
+  uint64_t pps_magic;
+  int pps_shift;
 };
+
+__device__ __forceinline__ int slab_index(int physical, const Geometry& g) {
+  return int((uint64_t(uint32_t(physical)) * g.pps_magic) >> g.pps_shift);
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -100,9 +110,10 @@ __device__ __forceinline__ const T* page_base(const uint64_t* slabs, const int* 
   if (logical < 0 || logical >= g.columns) return nullptr;
   const int physical = table_row[logical];
   if (physical < 0 || int64_t(physical) >= int64_t(g.num_slabs) * g.pps) return nullptr;
-  const uint64_t address = slabs[physical / g.pps];
+  const int slab = slab_index(physical, g);
+  const uint64_t address = slabs[slab];
   if (!address) return nullptr;
-  const int slot = physical % g.pps;
+  const int slot = physical - slab * g.pps;
   const int64_t i = ((int64_t(g.layer) * 2 * g.pps + slot) * g.heads + head) *
                     int64_t(g.page_size) * g.dim;
   return reinterpret_cast<const T*>(address) + i;
@@ -114,9 +125,10 @@ template <class T>
 __device__ __forceinline__ const T* resolve_page(const uint64_t* slabs, int physical,
                                                  const Geometry& g, int head) {
   if (physical < 0 || int64_t(physical) >= int64_t(g.num_slabs) * g.pps) return nullptr;
-  const uint64_t address = slabs[physical / g.pps];
+  const int slab = slab_index(physical, g);
+  const uint64_t address = slabs[slab];
   if (!address) return nullptr;
-  const int slot = physical % g.pps;
+  const int slot = physical - slab * g.pps;
   const int64_t i = ((int64_t(g.layer) * 2 * g.pps + slot) * g.heads + head) *
                     int64_t(g.page_size) * g.dim;
   return reinterpret_cast<const T*>(address) + i;
@@ -128,7 +140,7 @@ template <class T>
 __device__ __forceinline__ const T* page_in_slab(uint64_t address, int physical, const Geometry& g,
                                                  int head) {
   if (!address) return nullptr;
-  const int slot = physical % g.pps;
+  const int slot = physical - slab_index(physical, g) * g.pps;
   const int64_t i = ((int64_t(g.layer) * 2 * g.pps + slot) * g.heads + head) *
                     int64_t(g.page_size) * g.dim;
   return reinterpret_cast<const T*>(address) + i;
@@ -452,6 +464,13 @@ struct DecodeArgs {
   const int* work_count;
 };
 
+// How decode_kernel finds its items, a template parameter so that each
+// instantiation carries only its own prologue (the kernel's start is
+// latency-bound, and measured slower when unused prologue code grew):
+// from a work list (host- or device-built), by ranking the rows in every
+// workgroup, or as the plain (split, row, head) grid.
+constexpr int kVisitList = 0, kVisitRank = 1, kVisitGrid = 2;
+
 // Rows a decode workgroup ranks on its own (the ranking costs each thread
 // batch / threads * batch LDS reads).
 constexpr int kRankRows = 256;
@@ -544,7 +563,7 @@ __device__ __forceinline__ void stream_wave(Softmax<D / G, G>& st, const Query<D
 // VGPRs: one VGPR more drops a whole workgroup per compute unit (and the
 // launcher then picks 4-wave workgroups), so the bound is stated. Other
 // shapes need more registers and keep the compiler's choice.
-template <int DT, int D, bool VEC, int U, int STAGES, int WAVES, int G>
+template <int DT, int D, bool VEC, int U, int STAGES, int WAVES, int G, int MODE>
 __global__ __launch_bounds__(WAVES * kWave)
 __attribute__((amdgpu_waves_per_eu(WAVES == 8 && D == 64 && VEC && DT != kF32 && U <= 2 ? 6 : 1)))
 void decode_kernel(DecodeArgs a) {
@@ -585,7 +604,7 @@ void decode_kernel(DecodeArgs a) {
     }
     slabs_loaded = true;
   };
-  if (lds_slabs && (a.work || a.rank_rows || blockIdx.x < bh_count)) load_slabs();
+  if (lds_slabs && (MODE != kVisitGrid || blockIdx.x < bh_count)) load_slabs();
   // In-kernel longest-first order (see DecodeArgs::rank_rows): s_len holds
   // the offsets, s_order[k] the row of rank k; (length desc, row asc) is a
   // strict order, so the ranks are a permutation whatever the offsets hold.
@@ -598,7 +617,7 @@ void decode_kernel(DecodeArgs a) {
   const int len4 = (a.batch + 3) & ~3;
   int* const s_len = s_rank;
   int* const s_order = s_rank + len4;
-  if (a.rank_rows) {
+  if constexpr (MODE == kVisitRank) {
     for (int r = tid; r < len4; r += NT) s_len[r] = r < a.batch ? a.offsets[r] : INT_MIN;
     __syncthreads();
     const int4* len_v = reinterpret_cast<const int4*>(s_len);
@@ -644,35 +663,35 @@ void decode_kernel(DecodeArgs a) {
   // adds no round trip before the first item.
   int64_t items = a.items;
   uint64_t first_entry = 0;
-  if (a.work_count) {
-    first_entry = work64[blockIdx.x / g.heads];
+  if (MODE == kVisitList && a.work_count) {
+    first_entry = work64[blockIdx.x / unsigned(g.heads)];
     items = std::min(int64_t(a.work_count[0]) * g.heads, a.items);  // never past the list
   }
 
   for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
     int split, b, head;
-    if (a.work) {
+    if constexpr (MODE == kVisitList) {
       // (row, split) read as one 8-byte load: the workgroup's first dependent
       // round trip.
-      const int64_t w = item / g.heads;
-      head = int(item - w * g.heads);
+      const int w = int(unsigned(item) / unsigned(g.heads));
+      head = int(item) - w * g.heads;
       const uint64_t e = (a.work_count && item == blockIdx.x) ? first_entry : work64[w];
       b = int(uint32_t(e));
       split = int(uint32_t(e >> 32));
       if (!((unsigned(b) < unsigned(a.batch)) & (unsigned(split) < unsigned(a.nsplit_max)))) continue;
-    } else if (a.rank_rows) {
+    } else if constexpr (MODE == kVisitRank) {
       // item = (visiting position, head); one split per row
-      const int pos = int(item / g.heads);
-      head = int(item - int64_t(pos) * g.heads);
+      const int pos = int(unsigned(item) / unsigned(g.heads));
+      head = int(item) - pos * g.heads;
       const int pass = pos / a.rank_per, within = pos - pass * a.rank_per;
       const int width = min(a.rank_per, a.batch - pass * a.rank_per);
       b = s_order[pass * a.rank_per + ((pass & 1) ? width - 1 - within : within)];
       split = 0;
     } else {
-      split = int(item / bh_count);
-      const int64_t bhi = item - int64_t(split) * bh_count;
-      b = int(bhi / g.heads);
-      head = int(bhi - int64_t(b) * g.heads);
+      split = int(unsigned(item) / unsigned(bh_count));
+      const int bhi = int(item) - split * int(bh_count);
+      b = int(unsigned(bhi) / unsigned(g.heads));
+      head = bhi - b * g.heads;
     }
     const int64_t bh = int64_t(b) * g.heads + head;
 
@@ -692,7 +711,7 @@ void decode_kernel(DecodeArgs a) {
     qv.load(qp + qrow, col0, dim, a.qscale);
     T new_k{}, new_v{};
     if (tid < dim) { new_k = kin[qrow + tid]; new_v = vin[qrow + tid]; }
-    const int offset = a.rank_rows ? s_len[b] : a.offsets[b];
+    const int offset = MODE == kVisitRank ? s_len[b] : a.offsets[b];
 
     const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
     T* orow = out + bh * dim;
@@ -702,7 +721,7 @@ void decode_kernel(DecodeArgs a) {
         for (int t = tid; t < dim; t += NT) orow[t] = from_f32<DT>(NAN);
       continue;
     }
-    const int nsplit = L == 0 ? 1 : int((L + a.split_tokens - 1) / a.split_tokens);
+    const int nsplit = L == 0 ? 1 : int((uint32_t(L) + uint32_t(a.split_tokens) - 1) / uint32_t(a.split_tokens));
     if (split >= nsplit) continue;
     const int64_t t0 = t0i;
     const int64_t t1 = L < t0 + a.split_tokens ? L : t0 + a.split_tokens;
@@ -721,7 +740,7 @@ void decode_kernel(DecodeArgs a) {
     __syncthreads();
     slabs_staged = true;
     auto slab_of = [&](int physical) -> uint64_t {
-      return lds_slabs ? s_slabs[physical / g.pps] : a.slabs[physical / g.pps];
+      return lds_slabs ? s_slabs[slab_index(physical, g)] : a.slabs[slab_index(physical, g)];
     };
     auto resolve = [&](int physical) -> const T* {
       return physical_in_pool(physical, g) ? page_in_slab<T>(slab_of(physical), physical, g, head)
@@ -1738,6 +1757,10 @@ Geometry make_geometry(int h, int d, int page_size, int pps, int num_slabs, int 
   g.heads = h; g.dim = d; g.page_size = page_size;
   g.log2_page = page_size == 8 ? 3 : page_size == 16 ? 4 : 5;
   g.pps = pps; g.num_slabs = num_slabs; g.columns = columns; g.layer = layer;
+  int sh = 0;
+  while ((int64_t(1) << sh) < pps) ++sh;
+  g.pps_shift = 31 + sh;
+  g.pps_magic = ((uint64_t(1) << (31 + sh)) + uint64_t(pps) - 1) / uint64_t(pps);
   g.kind_stride = int64_t(pps) * h * page_size * d;
   return g;
 }
@@ -1810,10 +1833,19 @@ template <int DT, int D, bool VEC, int U, int WAVES, int G>
 int decode_occupancy() {
   static const int per_cu = [] {
     int n = 0;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<DT, D, VEC, U, kStages, WAVES, G>,
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<DT, D, VEC, U, kStages, WAVES, G, kVisitList>,
                                                         WAVES * kWave, 0) == hipSuccess ? n : 0;
   }();
   return per_cu;
+}
+
+// The instantiation of the launch's visiting mode.
+template <int DT, int D, bool VEC, int U, int WAVES, int G>
+void launch_decode_mode(const DecodeArgs& a, int64_t blocks, size_t lds) {
+  constexpr int NT = WAVES * kWave;
+  if (a.work) decode_kernel<DT, D, VEC, U, kStages, WAVES, G, kVisitList><<<grid_for(blocks), NT, lds>>>(a);
+  else if (a.rank_rows) decode_kernel<DT, D, VEC, U, kStages, WAVES, G, kVisitRank><<<grid_for(blocks), NT, lds>>>(a);
+  else decode_kernel<DT, D, VEC, U, kStages, WAVES, G, kVisitGrid><<<grid_for(blocks), NT, lds>>>(a);
 }
 
 template <int DT, int D, bool VEC, int WAVES, int G>
@@ -1850,12 +1882,12 @@ hipError_t launch_decode_w(const DecodeArgs& a, int64_t blocks, int unroll) {
     blocks = std::min(blocks, resident);
   }
   if constexpr (kMaxUnroll >= 4) {
-    if (unroll == 4) decode_kernel<DT, D, VEC, 4, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
+    if (unroll == 4) launch_decode_mode<DT, D, VEC, 4, WAVES, G>(a, blocks, rank_lds);
   }
   if constexpr (kMaxUnroll >= 2) {
-    if (unroll == 2) decode_kernel<DT, D, VEC, 2, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
+    if (unroll == 2) launch_decode_mode<DT, D, VEC, 2, WAVES, G>(a, blocks, rank_lds);
   }
-  if (unroll == 1) decode_kernel<DT, D, VEC, 1, kStages, WAVES, G><<<grid_for(blocks), NT, rank_lds>>>(a);
+  if (unroll == 1) launch_decode_mode<DT, D, VEC, 1, WAVES, G>(a, blocks, rank_lds);
   hipError_t e = hipGetLastError();
   const int64_t merge_rows = a.work && !a.work_count ? a.merge_rows : a.batch;
   if (e != hipSuccess || a.nsplit_max == 1 || merge_rows == 0) return e;
@@ -1926,6 +1958,8 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   a.batch = b; a.split_tokens = S; a.nsplit_max = int(nsplit_max);
   a.qscale = (1.0f / std::sqrt(float(d))) * kLog2e;
   a.items = work ? int64_t(work_items) * h : bh * nsplit_max;
+  // The kernels index items with 32-bit arithmetic.
+  if (a.items > INT32_MAX) return hipErrorInvalidValue;
   a.g = make_geometry(h, d, page_size, pps, num_slabs, columns, layer);
   a.partials = static_cast<float*>(workspace);
   a.qkv_stride = stride;
