@@ -34,6 +34,15 @@ int mt_row_argmax_feedback(float* dst, float* slot_tokens, const int* slots, int
                            const void* src, int rows, int width, int dtype);
 int mt_gather_slot_tokens(float* ids, const float* slot_tokens, const int* slots, int num_slots,
                           int rows);
+/* mt_row_argmax_feedback that also commits the decode step of each row whose
+ * slot is in the table: slot_len[slots[r]] += tokens, where slot_len is the
+ * page pool's per-slot committed lengths (device, mt_pool_layout offset 5).
+ * The same launch thus replaces mt_row_argmax_feedback followed by
+ * mt_sched_add_length. slot_len NULL commits nothing; a non-null slot_len
+ * needs slot_tokens. No reference counterpart (the reference commits each
+ * cache on the host, minitorch/paged_decode.py:80-86). */
+int mt_row_argmax_commit(float* dst, float* slot_tokens, const int* slots, int num_slots, int* slot_len,
+                         int tokens, const void* src, int rows, int width, int dtype);
 
 /* x[t, :] = wte[id_t, :] + wpe[positions[t], :] (fp32) in one launch, with
  * id_t = ids[t], or slot_tokens[slots[t]] when slot_tokens is not null (token

@@ -95,6 +95,21 @@ int mt_sched_decode_prepare(MT_POOL_ARGS, const int* slots, int b, int columns, 
                             int limit, int* table, int* offsets, float* positions,
                             int* cu_seqlens, int* new_page);
 
+/* mt_sched_decode_prepare and the step's token embeddings in one launch:
+ * also x[i, :] = wte[id_i, :] + wpe[pos_i, :] (fp32, [b, dim]) with id_i =
+ * slot_tokens[slots[i]] (the slot's last token, num_slots entries) and
+ * pos_i = its committed length, as mt_embed_tokens computes them from the
+ * positions this call writes (same NaN rule: an id or position that is
+ * non-finite, negative, too large or not integral, or a slot outside the
+ * table, gives a NaN row). dim % 4 == 0, x/wte/wpe 16-byte aligned. One
+ * workgroup builds the metadata while the others embed. No reference
+ * counterpart (it saves the embedding's launch in a decode step). */
+int mt_sched_decode_prepare_embed(MT_POOL_ARGS, const int* slots, int b, int columns, int page_size,
+                                  int limit, int* table, int* offsets, float* positions,
+                                  int* cu_seqlens, int* new_page, float* x, const float* wte,
+                                  const float* wpe, const float* slot_tokens, int num_slots, int vocab,
+                                  int n_positions, int dim);
+
 /* lengths[slots[i]] += tokens. Replaces the length update of reference
  * CacheBase.commit_append (minitorch/kv_cache.py:142-147). */
 int mt_sched_add_length(MT_POOL_ARGS, const int* slots, int b, int tokens);

@@ -117,7 +117,8 @@ constexpr int kArgmaxBatch = 8;
 template <int DT>
 __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, const void* src,
                                                                     int width, float* slot_tokens,
-                                                                    const int* slots, int num_slots) {
+                                                                    const int* slots, int num_slots,
+                                                                    int* slot_len, int tokens) {
   using T = typename Elem<DT>::T;
   constexpr int E = per16<DT>();
   constexpr int NW = kArgmaxThreads / 64;
@@ -202,7 +203,11 @@ __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, 
       // next decode step (a slot outside the table is skipped).
       if (slot_tokens) {
         const int s = slots[row];
-        if (s >= 0 && s < num_slots) slot_tokens[s] = float(best.i);
+        if (s >= 0 && s < num_slots) {
+          slot_tokens[s] = float(best.i);
+          // the decode step's commit: the row's committed length grows
+          if (slot_len) slot_len[s] += tokens;
+        }
       }
     }
   }
@@ -256,13 +261,14 @@ int mt_embedding_gather(float* dst, const float* weights, const float* ids, int 
   return hipGetLastError();
 }
 
-int mt_row_argmax_feedback(float* dst, float* slot_tokens, const int* slots, int num_slots,
-                           const void* src, int rows, int width, int dtype) {
+int mt_row_argmax_commit(float* dst, float* slot_tokens, const int* slots, int num_slots, int* slot_len,
+                         int tokens, const void* src, int rows, int width, int dtype) {
   if (rows < 1 || width < 1 || width > 16777216 || int64_t(rows) * width > INT32_MAX)
     return hipErrorInvalidValue;
-  if (!dst || !src || (slot_tokens && (!slots || num_slots < 1))) return hipErrorInvalidValue;
+  if (!dst || !src || (slot_tokens && (!slots || num_slots < 1)) || (slot_len && !slot_tokens))
+    return hipErrorInvalidValue;
 #define MT_ARGMAX(DT) \
-  row_argmax_kernel<DT><<<rows, kArgmaxThreads>>>(dst, src, width, slot_tokens, slots, num_slots)
+  row_argmax_kernel<DT><<<rows, kArgmaxThreads>>>(dst, src, width, slot_tokens, slots, num_slots, slot_len, tokens)
   if (dtype == kF32) MT_ARGMAX(kF32);
   else if (dtype == kF16) MT_ARGMAX(kF16);
   else if (dtype == kBF16) MT_ARGMAX(kBF16);
@@ -271,8 +277,13 @@ int mt_row_argmax_feedback(float* dst, float* slot_tokens, const int* slots, int
   return hipGetLastError();
 }
 
+int mt_row_argmax_feedback(float* dst, float* slot_tokens, const int* slots, int num_slots,
+                           const void* src, int rows, int width, int dtype) {
+  return mt_row_argmax_commit(dst, slot_tokens, slots, num_slots, nullptr, 0, src, rows, width, dtype);
+}
+
 int mt_row_argmax(float* dst, const void* src, int rows, int width, int dtype) {
-  return mt_row_argmax_feedback(dst, nullptr, nullptr, 0, src, rows, width, dtype);
+  return mt_row_argmax_commit(dst, nullptr, nullptr, 0, nullptr, 0, src, rows, width, dtype);
 }
 
 int mt_embed_tokens(float* x, const float* wte, const float* wpe, const float* ids,

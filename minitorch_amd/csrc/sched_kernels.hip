@@ -314,11 +314,9 @@ __global__ __launch_bounds__(kThreads) void release_rows_kernel(Pool p, const in
 //   rows whose next token starts a new page pop one page each, row by row
 //   (sequential pops, limited to `limit` pops), new_page[i] = popped page or -1,
 //   table[i, :columns] = the row's pages, -1 beyond them.
-__global__ __launch_bounds__(kThreads) void decode_prepare_kernel(Pool p, const int* slots, int b,
-                                                                  int columns, int page_size,
-                                                                  int limit, int* table,
-                                                                  int* offsets, float* positions,
-                                                                  int* cu_seqlens, int* new_page) {
+__device__ __forceinline__ void decode_prepare_body(Pool p, const int* slots, int b, int columns,
+                                                    int page_size, int limit, int* table, int* offsets,
+                                                    float* positions, int* cu_seqlens, int* new_page) {
   constexpr int TOPS = kPrepareRows / kThreads;  // stack-top candidates per thread
   // Every argument is loaded at entry and kept in scalar registers; global
   // memory is reached through global-address-space pointers only.
@@ -531,6 +529,66 @@ __global__ __launch_bounds__(kThreads) void decode_prepare_kernel(Pool p, const 
   }
 }
 
+__global__ __launch_bounds__(kThreads) void decode_prepare_kernel(Pool p, const int* slots, int b,
+                                                                  int columns, int page_size,
+                                                                  int limit, int* table,
+                                                                  int* offsets, float* positions,
+                                                                  int* cu_seqlens, int* new_page) {
+  decode_prepare_body(p, slots, b, columns, page_size, limit, table, offsets, positions, cu_seqlens,
+                      new_page);
+}
+
+// The embeddings of a decode step's tokens, x[i, :] = wte[id_i, :] +
+// wpe[pos_i, :] (fp32), with id_i the slot's last token and pos_i its
+// committed length: the rule of the inference library's embed_tokens_kernel
+// (an id or position that is non-finite, negative, too large or not integral,
+// or a slot outside the table, gives a NaN row).
+struct EmbedArgs {
+  float* x;
+  const float* wte;
+  const float* wpe;
+  const float* slot_tokens;
+  int num_slots, vocab, n_positions, dim;
+};
+
+__device__ __forceinline__ bool bad_index(float raw, int limit) {
+  return !isfinite(raw) || raw < 0.f || raw >= float(limit) || raw != floorf(raw);
+}
+
+// decode_prepare_kernel and the step's embeddings in one launch: workgroup 0
+// builds the metadata; the others embed the rows. The embedding reads each
+// slot's committed length itself (the position prepare writes), so the two
+// parts do not wait for each other.
+__global__ __launch_bounds__(kThreads) void decode_prepare_embed_kernel(Pool p, const int* slots, int b,
+                                                                        int columns, int page_size,
+                                                                        int limit, int* table,
+                                                                        int* offsets, float* positions,
+                                                                        int* cu_seqlens, int* new_page,
+                                                                        EmbedArgs e) {
+  if (blockIdx.x == 0) {
+    decode_prepare_body(p, slots, b, columns, page_size, limit, table, offsets, positions, cu_seqlens,
+                        new_page);
+    return;
+  }
+  const int per_row = e.dim / 4;
+  const int total = b * per_row;
+  for (int i = (blockIdx.x - 1) * kThreads + threadIdx.x; i < total; i += (gridDim.x - 1) * kThreads) {
+    const int t = i / per_row;
+    const int col = (i - t * per_row) * 4;
+    const int s = slots[t];
+    const bool in = s >= 0 && s < e.num_slots;
+    const float id = in ? e.slot_tokens[s] : NAN;
+    const float pos = in ? float(p.slot_len[s]) : NAN;
+    float4 v = make_float4(NAN, NAN, NAN, NAN);
+    if (!bad_index(id, e.vocab) && !bad_index(pos, e.n_positions)) {
+      const float4 a = *reinterpret_cast<const float4*>(e.wte + int64_t(id) * e.dim + col);
+      const float4 w = *reinterpret_cast<const float4*>(e.wpe + int64_t(pos) * e.dim + col);
+      v = make_float4(a.x + w.x, a.y + w.y, a.z + w.z, a.w + w.w);
+    }
+    *reinterpret_cast<float4*>(e.x + int64_t(t) * e.dim + col) = v;
+  }
+}
+
 // Commit: lengths += tokens for every row.
 __global__ __launch_bounds__(kThreads) void add_length_kernel(Pool p, const int* slots, int b, int tokens) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < b; i += gridDim.x * blockDim.x)
@@ -659,6 +717,31 @@ int mt_sched_decode_prepare(MT_POOL_ARGS, const int* slots, int b, int columns, 
     return hipErrorInvalidValue;
   decode_prepare_kernel<<<1, kThreads>>>(MT_POOL, slots, b, columns, page_size, limit, table,
                                          offsets, positions, cu_seqlens, new_page);
+  return hipGetLastError();
+}
+
+int mt_sched_decode_prepare_embed(MT_POOL_ARGS, const int* slots, int b, int columns, int page_size,
+                                  int limit, int* table, int* offsets, float* positions,
+                                  int* cu_seqlens, int* new_page, float* x, const float* wte,
+                                  const float* wpe, const float* slot_tokens, int num_slots, int vocab,
+                                  int n_positions, int dim) {
+  MT_POOL_CHECK
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+  if (!slots || b < 1 || columns < 1 || columns > max_cols || limit < -1 || !table || !offsets ||
+      !positions || !cu_seqlens || !new_page || !(page_size == 8 || page_size == 16 || page_size == 32) ||
+      int64_t(b) * columns > INT32_MAX || !x || !wte || !wpe || !slot_tokens || num_slots < 1 ||
+      vocab < 1 || n_positions < 1 || dim < 4 || dim % 4 || !a16(x) || !a16(wte) || !a16(wpe) ||
+      int64_t(b) * dim > INT32_MAX || int64_t(vocab) * dim > INT32_MAX || int64_t(n_positions) * dim > INT32_MAX)
+    return hipErrorInvalidValue;
+  EmbedArgs e{};
+  e.x = x; e.wte = wte; e.wpe = wpe; e.slot_tokens = slot_tokens;
+  e.num_slots = num_slots; e.vocab = vocab; e.n_positions = n_positions; e.dim = dim;
+  const int64_t vecs = int64_t(b) * (dim / 4);
+  const int64_t need = (vecs + kThreads - 1) / kThreads;
+  const int embed_blocks = int(need < 64 ? need : 64);
+  decode_prepare_embed_kernel<<<1 + embed_blocks, kThreads>>>(MT_POOL, slots, b, columns, page_size, limit,
+                                                              table, offsets, positions, cu_seqlens,
+                                                              new_page, e);
   return hipGetLastError();
 }
 

@@ -525,11 +525,10 @@ class DecoderLM:
                     ws.uncapturable.add(b)
             if step is None:
                 ws.eager_steps[b] = ws.eager_steps.get(b, 0) + 1
-                batch.prepare_device()
                 ids = self._issue_decode(batch, w, att, _StepBuffers(model_library(), b, self.n_embd,
                                                                      self.n_vocab, dtype))
                 batch.mark_layers_written()
-                batch.commit()
+                batch.commit(device=False)  # the greedy selection committed on the device
                 return ids
             rt.check(rt.lib.mt_graph_launch(step.exec))
             batch._device_prepared = True
@@ -545,9 +544,7 @@ class DecoderLM:
         exec_ptr = P()
         rt.check(rt.lib.mt_graph_begin())
         try:
-            batch.prepare_device()
             self._issue_decode(batch, w, att, buffers)
-            batch.commit_device()
         except Exception:
             rt.lib.mt_graph_end(ct.byref(exec_ptr))     # ends and discards the capture
             if exec_ptr.value:
@@ -559,20 +556,21 @@ class DecoderLM:
         return _CapturedStep(exec_ptr.value, buffers, deps)
 
     def _issue_decode(self, batch, w, att, buffers):
-        """The device work of a sync-free decode step after its metadata:
-        embeddings of each slot's last token, the native layer loop with the
-        tied head, and the greedy selection with token feedback, into
-        ``buffers``; returns the IDs."""
+        """The device work of a sync-free decode step: its metadata and the
+        embeddings of each slot's last token in one launch
+        (``mt_sched_decode_prepare_embed``), the native layer loop with the
+        tied head, and the greedy selection with token feedback and the step's
+        commit (each row's committed length + 1, ``mt_row_argmax_commit``),
+        into ``buffers``; returns the IDs."""
         b, d, dtype, pool = batch.batch_size, self.n_embd, batch.dtype, batch.pool
-        paged_ops.embed_tokens(buffers.x.ptr, w.wte.ptr, w.wpe.ptr, None, batch.position_ids.ptr, b,
-                               self.n_vocab, self.n_positions, d, slot_tokens=pool.slot_tokens.ptr,
-                               slots=batch.device_slots.ptr, num_slots=pool.max_slots)
+        batch.prepare_device(embed=(buffers.x.ptr, w.wte.ptr, w.wpe.ptr, self.n_vocab, self.n_positions, d))
         call(model_library(), 'mt_decoder_layers', [P, P, I, P, P, P, P, P, P, I, I, I, I, F, I, I, P, ct.c_size_t, P],
              self.blas().handle, w.layer_array, self.n_layer, buffers.x.ptr, buffers.h.ptr, w.ln_f[0].ptr,
              w.ln_f[1].ptr, w.head.ptr, buffers.logits.ptr, self.n_vocab, b, d, self.n_head, self.ln_eps,
              dtype_code(dtype), 1 if FUSED_GELU else 0, buffers.scratch.ptr, buffers.scratch_bytes, ct.byref(att))
-        paged_ops.row_argmax_feedback(buffers.ids.ptr, pool.slot_tokens.ptr, batch.device_slots.ptr,
-                                      pool.max_slots, buffers.logits.ptr, b, self.n_vocab, dtype)
+        paged_ops.row_argmax_commit(buffers.ids.ptr, pool.slot_tokens.ptr, batch.device_slots.ptr,
+                                    pool.max_slots, pool.slot_len_ptr, 1, buffers.logits.ptr, b, self.n_vocab,
+                                    dtype)
         return buffers.ids
 
     def _decode_batch(self, idx, caches, greedy):

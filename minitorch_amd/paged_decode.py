@@ -67,6 +67,17 @@ class _DecodeWorkspace:
         # step's upload is still queued
         self.stagings = [PinnedHostBuffer(int(self.offsets[2])) for _ in range(2)]
         self.turn = 0
+        self.uploaded = None  # the slots and work list the device buffer holds
+
+    def upload(self, payload):
+        """Upload the slots and work list, unless the buffer already holds
+        exactly these (a steady batch: every row grows by one token, so the
+        longest-first order changes only when a row joins, leaves or reaches
+        another split). Only this method writes that part of the buffer."""
+        if self.uploaded is not None and np.array_equal(self.uploaded, payload):
+            return
+        self.staging.upload_async(self.ptr(0), payload)
+        self.uploaded = payload.copy()
 
     @property
     def staging(self):
@@ -166,7 +177,7 @@ class PagedDecodeBatch:
         upload[:b] = slots
         w0 = int(ws.offsets[1]) // 4
         upload[w0:w0 + len(work)] = work
-        ws.staging.upload_async(ws.ptr(0), upload[:w0 + len(work)])
+        ws.upload(upload[:w0 + len(work)])
         self._ws = ws
         self._limit = -1 if graph else avail
         if not graph:
@@ -191,13 +202,21 @@ class PagedDecodeBatch:
                 pool._mirror_sequential_pops(1)
                 pops += 1
 
-    def prepare_device(self):
+    def prepare_device(self, embed=None):
         """``mt_sched_decode_prepare``: each row's new page from the device
-        free list, and the table, offsets, positions and cu_seqlens."""
+        free list, and the table, offsets, positions and cu_seqlens. With
+        ``embed`` = (x, wte, wpe, vocab, n_positions, dim) the same launch also
+        writes the rows' token embeddings into ``x`` from the pool's per-slot
+        last tokens (``mt_sched_decode_prepare_embed``)."""
         ws, pool = self._ws, self.pool
-        pool._call('mt_sched_decode_prepare', [P, I, I, I, I, P, P, P, P, P],
-                   ws.ptr(0), self.batch_size, self.columns, pool.page_size, self._limit, ws.ptr(6), ws.ptr(2),
-                   ws.ptr(3), ws.ptr(4), ws.ptr(5))
+        args = (ws.ptr(0), self.batch_size, self.columns, pool.page_size, self._limit, ws.ptr(6), ws.ptr(2),
+                ws.ptr(3), ws.ptr(4), ws.ptr(5))
+        if embed is None:
+            pool._call('mt_sched_decode_prepare', [P, I, I, I, I, P, P, P, P, P], *args)
+        else:
+            x, wte, wpe, vocab, n_positions, dim = embed
+            pool._call('mt_sched_decode_prepare_embed', [P, I, I, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I],
+                       *args, x, wte, wpe, pool.slot_tokens.ptr, pool.max_slots, vocab, n_positions, dim)
         self._device_prepared = True
 
     def decode_attention(self, layer, q, k, v):

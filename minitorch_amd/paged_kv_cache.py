@@ -123,6 +123,11 @@ class KVPagePool:
     def _call(self, name, types, *args):
         call(sched_library(), name, self._GEOMETRY_TYPES + types, *self._geometry(), *args)
 
+    @property
+    def slot_len_ptr(self):
+        """Device address of the per-slot committed lengths (int32[max_slots])."""
+        return self.state.ptr + self._offsets[5]
+
     def slots_ptr(self, first):
         return self.slot_ids.ptr + 4 * first
 

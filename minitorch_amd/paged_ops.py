@@ -186,6 +186,14 @@ def row_argmax_feedback(dst, slot_tokens, slots, num_slots, src, rows, width, dt
          slots, num_slots, src, rows, width, dtype_code(dtype))
 
 
+def row_argmax_commit(dst, slot_tokens, slots, num_slots, slot_len, tokens, src, rows, width, dtype):
+    """``mt_row_argmax_commit``: ``row_argmax_feedback`` that also adds
+    ``tokens`` to each row's committed length ``slot_len[slots[r]]`` (the
+    decode step's commit in the same launch)."""
+    call(inference_library(), 'mt_row_argmax_commit', [P, P, P, I, P, I, P, I, I, I], dst, slot_tokens,
+         slots, num_slots, slot_len, tokens, src, rows, width, dtype_code(dtype))
+
+
 def gather_slot_tokens(ids, slot_tokens, slots, num_slots, rows):
     """``mt_gather_slot_tokens``: ``ids[r] = slot_tokens[slots[r]]`` (NaN for a
     slot outside the table)."""

@@ -240,6 +240,32 @@ def test_token_feedback_entries_reject_invalid_arguments():
     assert g(8, 8, 8, 4, 0) == 1
     assert g(8, 8, 8, 0, 1) == 1
     assert g(None, 8, 8, 4, 1) == 1
+    c = lib.mt_row_argmax_commit
+    c.argtypes, c.restype = [P, P, P, I, P, I, P, I, I, I], I
+    assert c(8, None, None, 0, 8, 1, 8, 1, 10, 0) == 1  # a commit needs the slot table
+    assert c(8, 8, None, 4, 8, 1, 8, 1, 10, 0) == 1     # slot table without slots
+    assert c(8, 8, 8, 4, 8, 1, 8, 0, 10, 0) == 1        # no rows
+    assert c(8, 8, 8, 4, 8, 1, 8, 1, 10, 5) == 1        # dtype
+
+
+def test_fused_prepare_embed_rejects_invalid_arguments():
+    # mt_sched_decode_prepare_embed refuses before any launch: pool geometry,
+    # metadata arguments and the embedding's (null, unaligned, width not a
+    # multiple of 4, no slot table)
+    f = library('sched_kernels').mt_sched_decode_prepare_embed
+    f.argtypes, f.restype = [P, I, I, I, I, I, ct.c_uint64, ct.c_uint64] + [P, I, I, I, I, P, P, P, P, P,
+                                                                        P, P, P, P, I, I, I, I], I
+    # state at 256 (16-byte aligned); 16 slabs of 16 pages, 1024 slots of 16 columns
+    pool = (256, 256, 16, 1024, 16, 16, 256, 4096)
+    ok = [256, 2, 4, 16, -1, 256, 256, 256, 256, 256, 256, 256, 256, 256, 8, 100, 64, 64]
+    # the valid shape passes validation (without a GPU the launch itself fails with another status)
+    assert f(*pool, *ok) != 1
+    for i, bad in [(1, 0), (2, 0), (2, 2000), (3, 12), (4, -2), (5, None), (10, None), (11, 8), (13, None),
+                   (14, 0), (15, 0), (16, 0), (17, 6), (17, 0)]:
+        args = list(ok)
+        args[i] = bad
+        assert f(*pool, *args) == 1, (i, bad)
+    assert f(None, *pool[1:], *ok) == 1
 
 
 class _Layer(ct.Structure):

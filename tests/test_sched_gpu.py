@@ -7,7 +7,7 @@ import pytest
 from minitorch_amd.amp import autocast
 from minitorch_amd.paged_kv_cache import KVPagePool, PagedKVCache
 from minitorch_amd.paged_decode import PagedDecodeBatch
-from minitorch_amd.runtime import DeviceTensor, runtime, P, I
+from minitorch_amd.runtime import DeviceTensor, RawDeviceBuffer, runtime, P, I
 from oracle.pool_oracle import PoolOracle, CacheOracle, decode_batch_metadata
 
 pytestmark = pytest.mark.gpu
@@ -404,3 +404,96 @@ def test_acquire_lists_skips_entries_beyond_columns_or_budget():
     for c in caches:
         c.close()
     pool.close()
+
+
+def _pool_with_rows(seed, rows, n_positions=512):
+    model = StubModel(layers=1, heads=2, dim=64, n_positions=n_positions)
+    pool = KVPagePool(model, page_size=16, max_bytes=(rows * n_positions // 16 + 64) * 2 * 2 * 64 * 16 * 4,
+                      pages_per_slab=8)
+    rng = np.random.default_rng(seed)
+    caches = []
+    for _ in range(rows):
+        c = PagedKVCache(model, 1, n_positions, page_size=16, page_pool=pool)
+        c.prepare_append(int(rng.integers(1, n_positions - 40)))
+        c._written_layers.update(range(len(c.layout)))
+        c.commit_append()
+        caches.append(c)
+    return model, pool, caches
+
+
+@pytest.mark.parametrize('rows', [1, 2, 37, 128])
+def test_fused_prepare_embed_equals_prepare_then_embed(rows):
+    # mt_sched_decode_prepare_embed against mt_sched_decode_prepare followed by
+    # mt_embed_tokens on two identically built pools: the step's metadata,
+    # the pool state and the embeddings bit for bit, including a NaN token and
+    # an id past the vocabulary (NaN rows)
+    from minitorch_amd import paged_ops
+    vocab, dim = 300, 64
+    rng = np.random.default_rng([3, rows])
+    wte = DeviceTensor.from_numpy(rng.standard_normal((vocab, dim)).astype(np.float32))
+    wpe = DeviceTensor.from_numpy(rng.standard_normal((512, dim)).astype(np.float32))
+    tokens = rng.integers(0, vocab, 4096).astype(np.float32)
+    tokens[[0, 5]] = [np.nan, vocab + 3]
+    worlds = []
+    for fused in (True, False):
+        model, pool, caches = _pool_with_rows(rows, rows)
+        pool.slot_tokens.upload(np.resize(tokens, pool.max_slots))
+        x = DeviceTensor((rows, dim), 'float32')
+        batch = PagedDecodeBatch(model, None, caches)
+        batch.prepare(graph=True)
+        if fused:
+            batch.prepare_device(embed=(x.ptr, wte.ptr, wpe.ptr, vocab, 512, dim))
+        else:
+            batch.prepare_device()
+            paged_ops.embed_tokens(x.ptr, wte.ptr, wpe.ptr, None, batch.position_ids.ptr, rows, vocab, 512, dim,
+                                   slot_tokens=pool.slot_tokens.ptr, slots=batch.device_slots.ptr,
+                                   num_slots=pool.max_slots)
+        runtime().synchronize()
+        worlds.append(dict(
+            x=x.to_numpy().view(np.uint32),
+            table=batch.table.download(np.int32, rows * batch.columns),
+            offsets=batch.device_offsets.download(np.int32, rows),
+            cu=batch.cu_seqlens.download(np.int32, rows + 1),
+            pos=batch.position_ids.to_numpy().view(np.uint32),
+            free=pool.free_stack(), header=pool.header()))
+    a, b = worlds
+    for key in a:
+        if isinstance(a[key], np.ndarray):
+            assert np.array_equal(a[key], b[key]), key
+        else:
+            assert a[key] == b[key], key
+
+
+@pytest.mark.parametrize('rows', [1, 3, 64])
+def test_argmax_commit_equals_feedback_then_add_length(rows):
+    # mt_row_argmax_commit against mt_row_argmax_feedback followed by
+    # mt_sched_add_length: the ids, the slot tokens and every slot's committed
+    # length (rows in a shuffled slot order)
+    from minitorch_amd import paged_ops
+    rng = np.random.default_rng([4, rows])
+    width = 50257
+    logits = DeviceTensor.from_numpy(rng.standard_normal((rows, 1, width)).astype(np.float32))
+    results = []
+    for fused in (True, False):
+        model, pool, caches = _pool_with_rows(rows + 11, rows)
+        order = rng.permutation(rows) if fused else order_used
+        order_used = order
+        slots = RawDeviceBuffer(4 * rows)
+        slots.upload(np.array([caches[i].slot for i in order], np.int32))
+        ids = DeviceTensor((rows, 1), 'float32')
+        if fused:
+            paged_ops.row_argmax_commit(ids.ptr, pool.slot_tokens.ptr, slots.ptr, pool.max_slots, pool.slot_len_ptr,
+                                        1, logits.ptr, rows, width, 'float32')
+        else:
+            paged_ops.row_argmax_feedback(ids.ptr, pool.slot_tokens.ptr, slots.ptr, pool.max_slots, logits.ptr,
+                                          rows, width, 'float32')
+            pool._call('mt_sched_add_length', [P, I, I], slots.ptr, rows, 1)
+        runtime().synchronize()
+        results.append((ids.to_numpy().ravel(), pool.slot_tokens.download(np.float32, pool.max_slots),
+                        pool.state.download(np.int32, pool.max_slots, pool._offsets[5])))
+    (i1, t1, l1), (i2, t2, l2) = results
+    assert np.array_equal(i1, i2)
+    assert np.array_equal(t1.view(np.uint32), t2.view(np.uint32))
+    assert np.array_equal(l1, l2)
+    ref = np.argmax(logits.to_numpy()[:, 0], axis=1)
+    assert np.array_equal(i1.astype(int), ref)
