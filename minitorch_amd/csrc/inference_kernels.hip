@@ -213,6 +213,164 @@ __global__ __launch_bounds__(kArgmaxThreads) void row_argmax_kernel(float* dst, 
   }
 }
 
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+// 16-bit order keys of the two halves of w (fp16 or bf16 bits), packed: a
+// half's bits as a signed 16-bit integer, with the magnitude bits flipped for
+// a negative value. Larger numbers get larger keys, +0 gets 0 and -0 gets -1,
+// a positive NaN lies above +inf and a negative NaN below -inf.
+__device__ __forceinline__ s16x2 key16x2(uint32_t w) {
+  const s16x2 v = __builtin_bit_cast(s16x2, w);
+  const s16x2 s = v >> (s16x2){15, 15};  // all ones for a negative half
+  return v ^ (s & (s16x2){0x7fff, 0x7fff});
+}
+
+__device__ __forceinline__ int key16(uint32_t h) {
+  const int v = int(short(h));
+  return v < 0 ? v ^ 0x7fff : v;
+}
+
+// Wave-wide max / min over lanes.
+__device__ __forceinline__ int wave_max(int x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = max(x, __shfl_xor(x, off));
+  return x;
+}
+__device__ __forceinline__ int wave_min(int x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = min(x, __shfl_xor(x, off));
+  return x;
+}
+
+// row_argmax_kernel for 16-bit rows read in one round trip (at most
+// kArgmaxThreads * kArgmaxBatch vectors) with element-aligned addresses, in
+// two passes over the registers instead of one (key, index) update per
+// element:
+// 1. each thread takes the packed max and min of its elements' 16-bit keys
+//    (five VALU operations per two elements); its summary is INT_MAX if it
+//    holds a NaN (max above +inf's key or min below -inf's), else its max
+//    key. The workgroup's max summary T is the row's winning key.
+// 2. the threads whose summary is T (or -1 when T is 0: -0 equals +0) scan
+//    their elements in index order for the first one that matches T (any NaN
+//    when T is INT_MAX); the lowest such index wins.
+// This is the rule of row_argmax_kernel: the first NaN, else the first
+// element of the largest value, -0 and +0 equal.
+template <int DT>
+__global__ __launch_bounds__(kArgmaxThreads) void row_argmax16_kernel(float* dst, const void* src,
+                                                                      int width, float* slot_tokens,
+                                                                      const int* slots, int num_slots,
+                                                                      int* slot_len, int tokens) {
+  static_assert(DT == kF16 || DT == kBF16, "16-bit rows only");
+  constexpr int kInf = DT == kF16 ? 0x7c00 : 0x7f80;  // key of +inf; -inf's is -kInf - 1
+  constexpr int NW = kArgmaxThreads / 64;
+  __shared__ int s_red[2][NW];
+  const int row = blockIdx.x;
+  const uint16_t* p = static_cast<const uint16_t*>(src) + int64_t(row) * width;
+  const int tid = threadIdx.x;
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
+  int head = int(((16 - (addr & 15)) & 15) / 2);
+  if (head > width) head = width;
+  const int nvec = (width - head) / 8;
+  const int tail = head + nvec * 8;
+  const auto* vp = global_view(reinterpret_cast<const u32x4*>(p + head));
+  const bool has_head = tid < head;
+  const int ntail = tail + tid < width ? 1 : 0;  // width - tail < 8 <= threads
+  uint32_t hb = 0, tb = 0;
+  if (has_head) hb = p[tid];
+  if (ntail) tb = p[tail + tid];
+  u32x4 x[kArgmaxBatch];
+#pragma unroll
+  for (int u = 0; u < kArgmaxBatch; ++u) {
+    const int j = tid + u * kArgmaxThreads;
+    if (j < nvec) x[u] = vp[j];
+  }
+  // pass 1: packed key extremes of each vector, and of the thread's elements
+  s16x2 kmax = {SHRT_MIN, SHRT_MIN}, kmin = {SHRT_MAX, SHRT_MAX};
+  if (has_head) { const s16x2 k = key16x2(hb * 0x10001u); kmax = k; kmin = k; }
+  if (ntail) {
+    const s16x2 k = key16x2(tb * 0x10001u);
+    kmax = __builtin_elementwise_max(kmax, k);
+    kmin = __builtin_elementwise_min(kmin, k);
+  }
+  s16x2 vmax[kArgmaxBatch], vmin[kArgmaxBatch];
+#pragma unroll
+  for (int u = 0; u < kArgmaxBatch; ++u) {
+    if (tid + u * kArgmaxThreads < nvec) {
+      const s16x2 k0 = key16x2(x[u].x), k1 = key16x2(x[u].y), k2 = key16x2(x[u].z), k3 = key16x2(x[u].w);
+      vmax[u] = __builtin_elementwise_max(__builtin_elementwise_max(k0, k1), __builtin_elementwise_max(k2, k3));
+      vmin[u] = __builtin_elementwise_min(__builtin_elementwise_min(k0, k1), __builtin_elementwise_min(k2, k3));
+      kmax = __builtin_elementwise_max(kmax, vmax[u]);
+      kmin = __builtin_elementwise_min(kmin, vmin[u]);
+    }
+  }
+  auto nan_in = [&](s16x2 hi, s16x2 lo) {
+    return max(int(hi.x), int(hi.y)) > kInf || min(int(lo.x), int(lo.y)) < -kInf - 1;
+  };
+  const int summary = nan_in(kmax, kmin) ? INT_MAX : max(int(kmax.x), int(kmax.y));
+  const int wave = tid >> 6;
+  int r = wave_max(summary);
+  if ((tid & 63) == 0) s_red[0][wave] = r;
+  __syncthreads();
+  int target = s_red[0][0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) target = max(target, s_red[0][w]);
+  // pass 2: the first matching element of the candidate threads
+  int first = INT_MAX;
+  if (summary == target || (target == 0 && summary == -1)) {
+    auto match = [&](uint32_t h) {
+      if (target == INT_MAX) return int(h & 0x7fffu) > kInf;
+      const int k = key16(h);
+      return k == target || (target == 0 && k == -1);
+    };
+    // a vector holds a match iff its extremes do: its max key is the target
+    // (or -1 when the target is 0), or it holds a NaN
+    auto holds = [&](int u) {
+      if (target == INT_MAX) return nan_in(vmax[u], vmin[u]);
+      const int m = max(int(vmax[u].x), int(vmax[u].y));
+      return m == target || (target == 0 && m == -1);
+    };
+    if (has_head && match(hb)) {
+      first = tid;
+    } else {
+      int hit = -1;
+#pragma unroll
+      for (int u = 0; u < kArgmaxBatch; ++u)
+        if (hit < 0 && tid + u * kArgmaxThreads < nvec && holds(u)) hit = u;
+      if (hit >= 0) {
+#pragma unroll
+        for (int u = 0; u < kArgmaxBatch; ++u) {
+          if (u == hit) {
+            const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+            int e_first = 8;
+#pragma unroll
+            for (int e = 7; e >= 0; --e)
+              if (match((w[e >> 1] >> (16 * (e & 1))) & 0xffffu)) e_first = e;
+            first = head + (tid + u * kArgmaxThreads) * 8 + e_first;
+          }
+        }
+      } else if (ntail && match(tb)) {
+        first = tail + tid;
+      }
+    }
+  }
+  r = wave_min(first);
+  if ((tid & 63) == 0) s_red[1][wave] = r;
+  __syncthreads();
+  if (tid == 0) {
+    int best = s_red[1][0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) best = min(best, s_red[1][w]);
+    dst[row] = float(best);
+    if (slot_tokens) {
+      const int s = slots[row];
+      if (s >= 0 && s < num_slots) {
+        slot_tokens[s] = float(best);
+        if (slot_len) slot_len[s] += tokens;
+      }
+    }
+  }
+}
+
 // ids[r] = slot_tokens[slots[r]]; a slot outside the table gives a NaN id,
 // which the embedding gather turns into a NaN row.
 __global__ __launch_bounds__(256) void gather_slot_tokens_kernel(float* ids, const float* slot_tokens,
@@ -267,11 +425,17 @@ int mt_row_argmax_commit(float* dst, float* slot_tokens, const int* slots, int n
     return hipErrorInvalidValue;
   if (!dst || !src || (slot_tokens && (!slots || num_slots < 1)) || (slot_len && !slot_tokens))
     return hipErrorInvalidValue;
-#define MT_ARGMAX(DT) \
-  row_argmax_kernel<DT><<<rows, kArgmaxThreads>>>(dst, src, width, slot_tokens, slots, num_slots, slot_len, tokens)
-  if (dtype == kF32) MT_ARGMAX(kF32);
-  else if (dtype == kF16) MT_ARGMAX(kF16);
-  else if (dtype == kBF16) MT_ARGMAX(kBF16);
+  // 16-bit rows of element-aligned address that one round trip reads (the
+  // head and tail are under 8 elements each) take the two-pass kernel
+  const bool two_pass = (reinterpret_cast<uintptr_t>(src) & 1) == 0 &&
+                        width <= kArgmaxThreads * kArgmaxBatch * 8;
+#define MT_ARGMAX(K, DT) \
+  K<DT><<<rows, kArgmaxThreads>>>(dst, src, width, slot_tokens, slots, num_slots, slot_len, tokens)
+  if (dtype == kF32) MT_ARGMAX(row_argmax_kernel, kF32);
+  else if (dtype == kF16 && two_pass) MT_ARGMAX(row_argmax16_kernel, kF16);
+  else if (dtype == kBF16 && two_pass) MT_ARGMAX(row_argmax16_kernel, kBF16);
+  else if (dtype == kF16) MT_ARGMAX(row_argmax_kernel, kF16);
+  else if (dtype == kBF16) MT_ARGMAX(row_argmax_kernel, kBF16);
   else return hipErrorInvalidValue;
 #undef MT_ARGMAX
   return hipGetLastError();

@@ -88,6 +88,52 @@ def test_row_argmax_row_counts_and_element_positions(rows):
     assert got.tolist() == ref.tolist()
 
 
+@pytest.mark.parametrize('dtype', ['float16', 'bfloat16'])
+@pytest.mark.parametrize('width', [9, 50257, 65536, 65537])
+def test_row_argmax_16bit_bit_patterns(dtype, width):
+    # 16-bit rows written as raw bits: NaNs of either sign and any payload,
+    # signed zeros and infinities, at head, vector and tail positions; the
+    # expected index is numpy.argmax of the decoded values (any NaN wins, the
+    # first one; -0 == +0)
+    code = {'float16': 1, 'bfloat16': 2}[dtype]
+    inf, qnan = (0x7c00, 0x7e00) if dtype == 'float16' else (0x7f80, 0x7fc0)
+    neg = 0x8000
+    rng = np.random.default_rng([width, code])
+    rows = 12
+    # finite negatives below -1 everywhere (magnitude bits of 2.0 .. 4.0)
+    lo, hi = (0x4000, 0x4400) if dtype == 'float16' else (0x4000, 0x4080)
+    bits = (neg | rng.integers(lo, hi, (rows, width))).astype(np.uint16)
+    last = width - 1
+    mid = width // 2
+    cases = [
+        {3: neg | inf + 1},                              # negative NaN with a payload
+        {mid: neg | qnan, 5: inf},                       # negative NaN beats +inf at a lower index
+        {last: inf | 0x1ff, 0: neg},                     # positive NaN in the tail beats -0
+        {4: neg, last: 0},                               # -0 first, +0 later: -0's index
+        {last - 1: 0, 2: neg},                           # +0 later, -0 first
+        {mid: 0, mid + 1: neg},                          # +0 first
+        {1: neg | inf},                                  # only -inf and finite negatives: largest finite
+        {0: inf, last: inf},                             # +inf tie: first
+        {last: neg},                                     # -0 alone in the tail
+        {min(7, last): 0x3c00 if dtype == 'float16' else 0x3f80},  # 1.0 at the head/vector boundary
+        {},                                              # all finite negatives
+        {mid: neg | inf + 1, 6: neg | qnan},             # two negative NaNs: the first
+    ]
+    for r, spots in enumerate(cases):
+        for j, b in spots.items():
+            bits[r, min(j, last)] = b
+    if dtype == 'float16':
+        values = bits.view(np.float16).astype(np.float32)
+        stored = bits.view(np.float16)
+    else:
+        values = po.decode(bits, code)
+        stored = bits
+    t = DeviceTensor((rows, 1, width), dtype)
+    runtime().h2d(t.ptr, np.ascontiguousarray(stored.reshape(rows, 1, width)))
+    got = greedy_token(t).to_numpy()[:, 0]
+    assert got.tolist() == np.argmax(values, axis=-1).astype(np.float32).tolist()
+
+
 @pytest.mark.parametrize('dtype,width', [('float16', 200003), ('float32', 50257), ('float32', 70001)])
 def test_row_argmax_rows_longer_than_one_round_trip(dtype, width):
     # rows longer than the 128 KiB one workgroup loads per round trip: the
