@@ -314,6 +314,98 @@ def bench_entries(args):
     return {'entries': out, 'pools_rotated': args.pools, 'steps': args.steps}
 
 
+# Compile-time variants of the decode kernel: (name, lanes per token,
+# non-temporal K/V loads). The product build is 8 lanes, non-temporal.
+DECODE_VARIANTS = (
+    ('4_lanes_cached', 4, False),
+    ('4_lanes_nt', 4, True),
+    ('8_lanes_cached', 8, False),
+    ('8_lanes_nt', 8, True),
+)
+VARIANT_DIR = os.path.join(ROOT, 'build', 'decode_variants')
+
+
+def build_decode_variants():
+    """Builds paged_attention_kernel.so once per DECODE_VARIANTS entry from
+    the committed source with its MT_DECODE_GROUP / MT_DECODE_NT_LOADS
+    switches, into build/decode_variants/<name>/ (four hipcc processes)."""
+    import subprocess
+    from minitorch_amd import _build
+    src = os.path.join(str(_build.SRC), 'paged_attention_kernel.hip')
+    procs = []
+    for name, group, nt in DECODE_VARIANTS:
+        out = os.path.join(VARIANT_DIR, name, 'paged_attention_kernel.so')
+        os.makedirs(os.path.dirname(out), exist_ok=True)
+        cmd = [_build.hipcc(), *_build.HIPCC_FLAGS, f'-DMT_DECODE_GROUP={group}',
+               f'-DMT_DECODE_NT_LOADS={int(nt)}', f'-I{_build.SRC}', src, '-o', out]
+        procs.append((name, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    for name, proc in procs:
+        _, err = proc.communicate()
+        if proc.returncode:
+            raise RuntimeError(f'hipcc failed for decode variant {name}:\n{err}')
+        print(f'built decode variant {name}', flush=True)
+
+
+def bench_variants(args):
+    """The decode kernel's compile-time variants (DECODE_VARIANTS) x waves per
+    workgroup (4, 8) x stream unroll (1, 2, 4), each through its own
+    library's mt_paged_decode_split with the host work list: config 2 over
+    rotated pools, config 4's layer shape (4 pools) and config 5 at P = 16.
+    Mean launch time from HIP events; libraries from build_decode_variants."""
+    from minitorch_amd.runtime import RawDeviceBuffer
+    from minitorch_amd.dtypes import dtype_code
+    from minitorch_amd.e2e import config4_lengths
+    from minitorch_amd.workloads import config5_lengths, DeviceRaggedCase
+    rt = runtime()
+    fns = {}
+    for name, _, _ in DECODE_VARIANTS:
+        path = os.path.join(VARIANT_DIR, name, 'paged_attention_kernel.so')
+        if not os.path.exists(path):
+            raise SystemExit(f'{path} is missing: run `python bench.py --build-variants` first')
+        fn = ct.CDLL(path).mt_paged_decode_split
+        fn.argtypes, fn.restype = paged_ops.SPLIT_ARGTYPES, I
+        fns[name] = fn
+    l4 = config4_lengths(np.random.default_rng([args.seed, 4]), 128)
+    l5 = config5_lengths(args.seed, 512)
+    cases = {
+        'config2': lambda: [DevicePagedCase(config2_case(args.seed)) for _ in range(args.pools)],
+        'config4_layer': lambda: [DeviceRaggedCase(args.seed + i, batch=128, heads=16, dim=64, page_size=16,
+                                                   lengths=l4, dtype='bfloat16') for i in range(4)],
+        'config5_p16': lambda: [DeviceRaggedCase(args.seed, batch=512, heads=25, dim=64, page_size=16,
+                                                 lengths=l5, dtype='bfloat16')],
+    }
+    out = {}
+    for shape, make in cases.items():
+        devs = make()
+        case = getattr(devs[0], 'case', devs[0])
+        kw = devs[0].kwargs()
+        split = paged_ops.split_tokens_for(page_size=case.page_size, columns=case.columns)
+        work, items, merges = paged_ops.decode_work_list(case.lengths, case.heads, split, rt.compute_units())
+        order = RawDeviceBuffer(4 * len(work))
+        order.upload(work)
+        ws_bytes = paged_ops.decode_workspace_bytes(b=case.batch, h=case.heads, page_size=case.page_size,
+                                                    columns=case.columns, split_tokens=split)
+        ws = RawDeviceBuffer(max(ws_bytes, 4))
+        nbytes = algorithmic_bytes(case)
+        steps = args.steps if case.batch < 512 else min(args.steps, 50)
+        out[shape] = {}
+        for name, fn in fns.items():
+            for waves in (4, 8):
+                for unroll in (1, 2, 4):
+                    calls = [(d.out.ptr, d.q.ptr, d.k.ptr, d.v.ptr, d.slab_table.ptr, d.block_table.ptr,
+                              d.offsets.ptr, kw['b'], kw['h'], kw['d'], kw['page_size'], kw['pages_per_slab'],
+                              kw['num_slabs'], kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype']),
+                              split, unroll, waves, 0, order.ptr, items, merges, ws.ptr, ws_bytes) for d in devs]
+                    t = time_launches(fn, calls, steps, args.warmup)
+                    out[shape][f'{name}/w{waves}/u{unroll}'] = dict(us_per_launch=round(t * 1e6, 2),
+                                                                   frac=round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4))
+            print(f'{shape} {name}: ' + ' '.join(f'{k.split("/", 1)[1]} {v["us_per_launch"]:.2f}'
+                                                 for k, v in out[shape].items() if k.startswith(name + '/')),
+                  file=sys.stderr, flush=True)
+        del devs, order, ws
+    return {'decode_variants': out, 'pools_rotated': args.pools, 'steps': args.steps}
+
+
 def bench_config5(args):
     """Config 5: B=512, H=25, D=64, bf16, contexts lognormal(ln 256, 1.2)
     clipped to [1, 8192], page 16 and 32; contexts over 1024 tokens take the
@@ -928,6 +1020,12 @@ def main():
     ap.add_argument('--concurrent', type=int, default=128, help='config 4: requests decoded every step')
     ap.add_argument('--projections', action='store_true',
                     help='time the decode projections (projection kernel vs hipBLASLt) at several batch sizes')
+    ap.add_argument('--build-variants', action='store_true',
+                    help='build the decode kernel variants (lanes per token x non-temporal loads) into '
+                         'build/decode_variants/ and exit')
+    ap.add_argument('--variants', action='store_true',
+                    help='time the decode kernel variants x waves (4, 8) x unroll (1, 2, 4) on config 2, '
+                         "config 4's layer and config 5 (P = 16)")
     ap.add_argument('--entries', action='store_true',
                     help='time the decode entries (work list, batch order, mt_paged_decode_batch) on config 2 '
                          'and on one-page rows of the same shape')
@@ -944,7 +1042,13 @@ def main():
               '(request/head sharding is a design note); run with --gpus 1.', file=sys.stderr)
         sys.exit(2)
 
+    if args.build_variants:
+        build_decode_variants()
+        return
     rt = runtime()
+    if args.variants:
+        print(json.dumps(bench_variants(args)), flush=True)
+        return
     if args.calibrate_copy:
         from minitorch_amd.runtime import RawDeviceBuffer
         nbytes = args.calibrate_copy << 20

@@ -43,7 +43,7 @@
 
 // The decode kernel streams every K/V byte of a launch exactly once, so its
 // loads are non-temporal (streamed past the caches). Measured on MI355X
-// (config 2, cold pools): 24.1 -> 21.0 us together with 8 lanes per token.
+// (config 2, cold pools): 24.5 -> 21.2 us together with 8 lanes per token.
 #ifndef MT_DECODE_NT_LOADS
 #define MT_DECODE_NT_LOADS 1
 #endif
