@@ -576,13 +576,21 @@ class DecoderLM:
     def _decode_batch(self, idx, caches, greedy):
         from .paged_decode import PagedDecodeBatch
         with PagedDecodeBatch(self, idx, caches) as batch:
-            batch.prepare()
             dtype = batch.dtype
             w = self._weights(dtype)
             b, d = batch.batch_size, self.n_embd
             pool = batch.pool
-            feedback = (pool, batch.device_slots.ptr) if idx is None else None
-            x = self._embed(w, idx, batch.position_ids, rows=b, feedback=feedback)
+            # A sync-free greedy step fuses as the captured step does: the
+            # metadata launch also embeds each slot's last token, and the
+            # greedy selection also commits the lengths.
+            fused = idx is None and greedy
+            if fused:
+                x = DeviceTensor((b, d), 'float32')
+                batch.prepare(embed=(x.ptr, w.wte.ptr, w.wpe.ptr, self.n_vocab, self.n_positions, d))
+            else:
+                batch.prepare()
+                feedback = (pool, batch.device_slots.ptr) if idx is None else None
+                x = self._embed(w, idx, batch.position_ids, rows=b, feedback=feedback)
             h = DeviceTensor((b, d), dtype)
             lib = model_library()
             scratch_bytes = _scratch_bytes(lib, b, d, dtype)
@@ -594,6 +602,12 @@ class DecoderLM:
                  w.ln_f[1].ptr, w.head.ptr, logits.ptr, self.n_vocab, b, d, self.n_head, self.ln_eps,
                  dtype_code(dtype), 1 if FUSED_GELU else 0, scratch.ptr, scratch_bytes, ct.byref(att))
             batch.mark_layers_written()
+            if fused:
+                ids = DeviceTensor((b, 1), 'float32')
+                paged_ops.row_argmax_commit(ids.ptr, pool.slot_tokens.ptr, batch.device_slots.ptr, pool.max_slots,
+                                            pool.slot_len_ptr, 1, logits.ptr, b, self.n_vocab, dtype)
+                batch.commit(device=False)  # the lengths were committed by the selection
+                return ids
             if greedy:
                 ids = DeviceTensor((b, 1), 'float32')
                 paged_ops.row_argmax_feedback(ids.ptr, pool.slot_tokens.ptr, batch.device_slots.ptr,

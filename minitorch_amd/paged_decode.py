@@ -137,9 +137,10 @@ class PagedDecodeBatch:
         ws.ensure(rows or self.batch_size, self.columns, work_len)
         return ws
 
-    def prepare(self, *, graph=False):
+    def prepare(self, *, graph=False, embed=None):
         """Upload the batch's slots and work list, then build the step's
-        metadata on the device and update the host mirrors.
+        metadata on the device (with ``embed``, and the rows' embeddings: see
+        ``prepare_device``) and update the host mirrors.
 
         With ``graph`` the metadata takes the fixed shapes a captured step
         replays with: the table is [B, pool.max_cols] (the split length
@@ -181,7 +182,7 @@ class PagedDecodeBatch:
         self._ws = ws
         self._limit = -1 if graph else avail
         if not graph:
-            self.prepare_device()
+            self.prepare_device(embed)
         self.table = _DeviceView(ws.buffer, int(ws.offsets[6]), 4 * b * self.columns)
         self.device_slots = _DeviceView(ws.buffer, int(ws.offsets[0]), 4 * b)
         self.device_offsets = _DeviceView(ws.buffer, int(ws.offsets[2]), 4 * b)
