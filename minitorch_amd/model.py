@@ -443,11 +443,15 @@ class DecoderLM:
             prompt_pages = sum(-(-n // ps) for n in tokens)
             if decode_pages > free or decode_pages - returned + prompt_pages > free:
                 raise MemoryError('KV page budget exhausted')
-            batch.prepare()
             b, dtype, d = batch.batch_size, batch.dtype, self.n_embd
             w = self._weights(dtype)
+            # the decode rows' embeddings come from the metadata launch (the
+            # slots' last tokens at their committed lengths), the prompts'
+            # from their IDs below
+            x = DeviceTensor((b + sum(tokens), d), 'float32')
+            batch.prepare(embed=(x.ptr, w.wte.ptr, w.wpe.ptr, self.n_vocab, self.n_positions, d))
             datt = batch.attention_metadata()
-            slots, positions = batch.device_slots, batch.position_ids
+            slots = batch.device_slots
             # the decode half's lengths are committed before any page changes
             # hands; its kernels read the step's own table and offsets
             batch.mark_layers_written()
@@ -465,10 +469,6 @@ class DecoderLM:
         try:
             pool.prepare_appends(new_caches, tokens, blob.ptr)
             prepared = list(new_caches)
-            x = DeviceTensor((b + total, d), 'float32')
-            paged_ops.embed_tokens(x.ptr, w.wte.ptr, w.wpe.ptr, None, positions.ptr, b, self.n_vocab,
-                                   self.n_positions, d, slot_tokens=pool.slot_tokens.ptr, slots=slots.ptr,
-                                   num_slots=pool.max_slots)
             paged_ops.embed_tokens(x.ptr + 4 * b * d, w.wte.ptr, w.wpe.ptr, prompt_ids, prompt_positions, total,
                                    self.n_vocab, self.n_positions, d)
             h = DeviceTensor((b + total, d), dtype)
