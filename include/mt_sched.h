@@ -97,7 +97,7 @@ int mt_sched_decode_prepare(MT_POOL_ARGS, const int* slots, int b, int columns, 
 
 /* mt_sched_decode_prepare and the step's token embeddings in one launch:
  * also x[i, :] = wte[id_i, :] + wpe[pos_i, :] (fp32, [b, dim]) with id_i =
- * slot_tokens[slots[i]] (the slot's last token, num_slots entries) and
+ * slot_tokens[slots[i]] (the slot's last token, num_slots <= max_slots entries) and
  * pos_i = its committed length, as mt_embed_tokens computes them from the
  * positions this call writes (same NaN rule: an id or position that is
  * non-finite, negative, too large or not integral, or a slot outside the

@@ -730,7 +730,7 @@ int mt_sched_decode_prepare_embed(MT_POOL_ARGS, const int* slots, int b, int col
   if (!slots || b < 1 || columns < 1 || columns > max_cols || limit < -1 || !table || !offsets ||
       !positions || !cu_seqlens || !new_page || !(page_size == 8 || page_size == 16 || page_size == 32) ||
       int64_t(b) * columns > INT32_MAX || !x || !wte || !wpe || !slot_tokens || num_slots < 1 ||
-      vocab < 1 || n_positions < 1 || dim < 4 || dim % 4 || !a16(x) || !a16(wte) || !a16(wpe) ||
+      num_slots > max_slots || vocab < 1 || n_positions < 1 || dim < 4 || dim % 4 || !a16(x) || !a16(wte) || !a16(wpe) ||
       int64_t(b) * dim > INT32_MAX || int64_t(vocab) * dim > INT32_MAX || int64_t(n_positions) * dim > INT32_MAX)
     return hipErrorInvalidValue;
   EmbedArgs e{};

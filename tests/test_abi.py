@@ -251,7 +251,7 @@ def test_token_feedback_entries_reject_invalid_arguments():
 def test_fused_prepare_embed_rejects_invalid_arguments():
     # mt_sched_decode_prepare_embed refuses before any launch: pool geometry,
     # metadata arguments and the embedding's (null, unaligned, width not a
-    # multiple of 4, no slot table)
+    # multiple of 4, no slot table or one longer than the pool's slots)
     f = library('sched_kernels').mt_sched_decode_prepare_embed
     f.argtypes, f.restype = [P, I, I, I, I, I, ct.c_uint64, ct.c_uint64] + [P, I, I, I, I, P, P, P, P, P,
                                                                         P, P, P, P, I, I, I, I], I
@@ -261,7 +261,7 @@ def test_fused_prepare_embed_rejects_invalid_arguments():
     # the valid shape passes validation (without a GPU the launch itself fails with another status)
     assert f(*pool, *ok) != 1
     for i, bad in [(1, 0), (2, 0), (2, 2000), (3, 12), (4, -2), (5, None), (10, None), (11, 8), (13, None),
-                   (14, 0), (15, 0), (16, 0), (17, 6), (17, 0)]:
+                   (14, 0), (14, 1025), (15, 0), (16, 0), (17, 6), (17, 0)]:
         args = list(ok)
         args[i] = bad
         assert f(*pool, *args) == 1, (i, bad)
