@@ -36,7 +36,8 @@ int mt_gather_slot_tokens(float* ids, const float* slot_tokens, const int* slots
                           int rows);
 /* mt_row_argmax_feedback that also commits the decode step of each row whose
  * slot is in the table: slot_len[slots[r]] += tokens, where slot_len is the
- * page pool's per-slot committed lengths (device, mt_pool_layout offset 5).
+ * page pool's per-slot committed lengths (device, mt_pool_layout offset 5;
+ * at least num_slots entries, so num_slots must not exceed the pool's slots).
  * The same launch thus replaces mt_row_argmax_feedback followed by
  * mt_sched_add_length. slot_len NULL commits nothing; a non-null slot_len
  * needs slot_tokens. No reference counterpart (the reference commits each
