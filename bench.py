@@ -328,16 +328,19 @@ VARIANT_DIR = os.path.join(ROOT, 'build', 'decode_variants')
 def build_decode_variants():
     """Builds paged_attention_kernel.so once per DECODE_VARIANTS entry from
     the committed source with its MT_DECODE_GROUP / MT_DECODE_NT_LOADS
-    switches, into build/decode_variants/<name>/ (four hipcc processes)."""
+    switches, and once with MT_DECODE_TIMELINE (bench_timeline), into
+    build/decode_variants/<name>/ (five hipcc processes)."""
     import subprocess
     from minitorch_amd import _build
     src = os.path.join(str(_build.SRC), 'paged_attention_kernel.hip')
     procs = []
-    for name, group, nt in DECODE_VARIANTS:
+    builds = [(name, [f'-DMT_DECODE_GROUP={group}', f'-DMT_DECODE_NT_LOADS={int(nt)}'])
+              for name, group, nt in DECODE_VARIANTS]
+    builds.append(('timeline', ['-DMT_DECODE_TIMELINE']))  # the product kernel plus per-workgroup stamps
+    for name, flags in builds:
         out = os.path.join(VARIANT_DIR, name, 'paged_attention_kernel.so')
         os.makedirs(os.path.dirname(out), exist_ok=True)
-        cmd = [_build.hipcc(), *_build.HIPCC_FLAGS, f'-DMT_DECODE_GROUP={group}',
-               f'-DMT_DECODE_NT_LOADS={int(nt)}', f'-I{_build.SRC}', src, '-o', out]
+        cmd = [_build.hipcc(), *_build.HIPCC_FLAGS, *flags, f'-I{_build.SRC}', src, '-o', out]
         procs.append((name, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
     for name, proc in procs:
         _, err = proc.communicate()
@@ -404,6 +407,77 @@ def bench_variants(args):
                   file=sys.stderr, flush=True)
         del devs, order, ws
     return {'decode_variants': out, 'pools_rotated': args.pools, 'steps': args.steps}
+
+
+def bench_timeline(args):
+    """Per-workgroup timeline of one cold config-2 launch of the headline path
+    (host work list, automatic waves and unroll), from the MT_DECODE_TIMELINE
+    build of the decode kernel: each workgroup's start, the start of its K/V
+    stream (wave 0, after the prologue's dependent loads) and its end, in µs
+    from the launch's first start, with its XCD and compute unit. Summarized
+    as: the start spread; stream starts and ends per residency slot
+    (workgroups i, i + CUs, i + 2 CUs share a compute unit in a fully resident
+    grid); how many workgroups stream over time; the K/V tokens per µs of the
+    first slot per XCD; per-CU token loads and their correlation with the
+    CU's end time."""
+    from minitorch_amd.runtime import RawDeviceBuffer
+    from minitorch_amd.dtypes import dtype_code
+    path = os.path.join(VARIANT_DIR, 'timeline', 'paged_attention_kernel.so')
+    if not os.path.exists(path):
+        raise SystemExit(f'{path} is missing: run `python bench.py --build-variants` first')
+    lib = ct.CDLL(path)
+    fn = lib.mt_paged_decode_split
+    fn.argtypes, fn.restype = paged_ops.SPLIT_ARGTYPES, I
+    read = lib.mt_decode_timeline
+    read.argtypes, read.restype = [ct.POINTER(ct.c_ulonglong), I], I
+    rt = runtime()
+    case = config2_case(args.seed)
+    devs = [DevicePagedCase(case) for _ in range(args.pools)]
+    kw = devs[0].kwargs()
+    split = paged_ops.split_tokens_for(page_size=case.page_size, columns=case.columns)
+    cus = rt.compute_units()
+    work, items, merges = paged_ops.decode_work_list(case.lengths, case.heads, split, cus)
+    order = RawDeviceBuffer(4 * len(work))
+    order.upload(work)
+    ws_bytes = paged_ops.decode_workspace_bytes(b=case.batch, h=case.heads, page_size=case.page_size,
+                                                columns=case.columns, split_tokens=split)
+    ws = RawDeviceBuffer(max(ws_bytes, 4))
+    calls = [(d.out.ptr, d.q.ptr, d.k.ptr, d.v.ptr, d.slab_table.ptr, d.block_table.ptr, d.offsets.ptr,
+              kw['b'], kw['h'], kw['d'], kw['page_size'], kw['pages_per_slab'], kw['num_slabs'],
+              kw['columns'], kw['layer'], kw['layers'], dtype_code(kw['dtype']), split, 0, 0, 0,
+              order.ptr, items, merges, ws.ptr, ws_bytes) for d in devs]
+    for i in range(args.warmup + len(calls)):  # the last launch reads a pool untouched for len(calls) - 1 launches
+        rt.check(fn(*calls[i % len(calls)]))
+    n = items * case.heads
+    buf = (ct.c_ulonglong * (5 * n))()
+    rt.check(read(buf, n))
+    rec = np.frombuffer(buf, np.uint64).reshape(n, 5).astype(np.int64)
+    t0 = rec[:, 0].min()
+    start, stream, end = [(rec[:, j] - t0) / 100.0 for j in range(3)]  # 100 MHz ticks -> µs
+    xcc = rec[:, 4] & 0xF
+    cu_key = (xcc << 16) | ((rec[:, 3] >> 8) & 0xFF)  # XCD, SE, SH, CU
+    rows = work[0:2 * items:2][np.arange(n) // case.heads]
+    tokens = case.lengths[rows] - 1  # K/V tokens read from pages (the new one comes from the inputs)
+    slot = np.arange(n) // cus
+    q = lambda x: [round(float(v), 2) for v in np.quantile(x, [0, 0.5, 1])]
+    span = float(end.max())
+    grid = np.arange(0, span + 0.25, 0.25)
+    streaming = [[round(float(t), 2), int(((stream <= t) & (end > t)).sum())] for t in grid]
+    first = slot == 0
+    rate = tokens[first] / np.maximum(end[first] - stream[first], 1e-3)
+    per_xcd = {int(x): round(float(np.median(rate[xcc[first] == x])), 1) for x in np.unique(xcc[first])}
+    keys = np.unique(cu_key)
+    cu_tokens = np.array([tokens[cu_key == k].sum() for k in keys])
+    cu_end = np.array([end[cu_key == k].max() for k in keys])
+    return {'decode_timeline': {
+        'workgroups': n, 'compute_units_seen': int(len(keys)), 'span_us': round(span, 2),
+        'start_spread_us': round(float(start.max()), 2),
+        'stream_start_us_by_slot': {int(k): q(stream[slot == k]) for k in np.unique(slot)},
+        'end_us_by_slot': {int(k): q(end[slot == k]) for k in np.unique(slot)},
+        'first_slot_tokens_per_us_by_xcd': per_xcd,
+        'cu_tokens': q(cu_tokens), 'cu_end_us': q(cu_end),
+        'corr_cu_tokens_end': round(float(np.corrcoef(cu_tokens, cu_end)[0, 1]), 3),
+        'streaming_workgroups': streaming}}
 
 
 def bench_config5(args):
@@ -1026,6 +1100,9 @@ def main():
     ap.add_argument('--variants', action='store_true',
                     help='time the decode kernel variants x waves (4, 8) x unroll (1, 2, 4) on config 2, '
                          "config 4's layer and config 5 (P = 16)")
+    ap.add_argument('--timeline', action='store_true',
+                    help='per-workgroup timeline of one config-2 launch from the MT_DECODE_TIMELINE build '
+                         '(build it with --build-variants)')
     ap.add_argument('--entries', action='store_true',
                     help='time the decode entries (work list, batch order, mt_paged_decode_batch) on config 2 '
                          'and on one-page rows of the same shape')
@@ -1048,6 +1125,9 @@ def main():
     rt = runtime()
     if args.variants:
         print(json.dumps(bench_variants(args)), flush=True)
+        return
+    if args.timeline:
+        print(json.dumps(bench_timeline(args)), flush=True)
         return
     if args.calibrate_copy:
         from minitorch_amd.runtime import RawDeviceBuffer

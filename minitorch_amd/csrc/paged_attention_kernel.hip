@@ -83,6 +83,15 @@ constexpr bool kDecodeNT = MT_DECODE_NT_LOADS != 0;
 // read instead of a second dependent global load.
 constexpr int kLdsSlabs = 512;
 
+#ifdef MT_DECODE_TIMELINE
+// Measurement builds only (bench.py --timeline): wall-clock stamps of each
+// decode workgroup's first item, 100 MHz (s_memrealtime): [start, K/V stream
+// start of wave 0, end, HW_ID register, XCC_ID register], workgroups below
+// kTimelineMax. The product build has none of this.
+constexpr int kTimelineMax = 8192;
+__device__ uint64_t g_decode_timeline[kTimelineMax * 5];
+#endif
+
 struct Geometry {
   int heads, dim, page_size, log2_page, pps, num_slabs, columns, layer;
   int64_t kind_stride;  // elements between the K and V planes of one layer
@@ -584,6 +593,10 @@ void decode_kernel(DecodeArgs a) {
   __shared__ uint64_t s_slabs[kLdsSlabs];
   __shared__ __align__(16) T s_new[2][D];  // the new token's K and V rows
 
+#ifdef MT_DECODE_TIMELINE
+  const uint64_t tl_start = wall_clock64();
+  uint64_t tl_stream = 0;
+#endif
   const Geometry& g = a.g;
   const int dim = VEC ? D : g.dim;
   const int tid = threadIdx.x;
@@ -757,6 +770,9 @@ void decode_kernel(DecodeArgs a) {
 
     Softmax<DL, G> st;
     st.init();
+#ifdef MT_DECODE_TIMELINE
+    if (item == blockIdx.x) tl_stream = wall_clock64();
+#endif
     stream_wave<DT, D, VEC, U, STAGES, G>(st, qv, reinterpret_cast<uint64_t>(my_page), ntok_paged,
                                            wave, WAVES, g, dim);
 
@@ -848,6 +864,16 @@ void decode_kernel(DecodeArgs a) {
     }
     __syncthreads();  // LDS is reused by the next item
   }
+#ifdef MT_DECODE_TIMELINE
+  if (tid == 0 && blockIdx.x < unsigned(kTimelineMax)) {
+    uint64_t* rec = g_decode_timeline + 5 * blockIdx.x;
+    rec[0] = tl_start;
+    rec[1] = tl_stream;
+    rec[2] = wall_clock64();
+    rec[3] = __builtin_amdgcn_s_getreg(4 | (31 << 11));   // HW_ID: wave, SIMD, CU, SH, SE
+    rec[4] = __builtin_amdgcn_s_getreg(20 | (15 << 11));  // XCC_ID
+  }
+#endif
 }
 
 // Split-context reduction: for every (request, head) whose context spans more
@@ -2571,6 +2597,18 @@ int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, in
   *bytes = nsplit_max > 1 ? workspace_bytes_for(int64_t(b) * h, int(nsplit_max)) : 0;
   return hipSuccess;
 }
+
+#ifdef MT_DECODE_TIMELINE
+// Measurement builds only: copies the first `count` workgroups' stamps
+// (5 x uint64 each, see g_decode_timeline) of the last decode launch to host
+// memory `dst`, after the calling thread's stream has drained.
+int mt_decode_timeline(unsigned long long* dst, int count) {
+  if (!dst || count < 1 || count > kTimelineMax) return hipErrorInvalidValue;
+  hipError_t e = hipStreamSynchronize(hipStreamPerThread);
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_timeline), size_t(count) * 5 * 8);
+  return e;
+}
+#endif
 
 int mt_paged_decode_split_tokens(int page_size, int columns, int requested, int* split_tokens) {
   if (!split_tokens || columns < 1 || requested < 0 ||
