@@ -283,8 +283,9 @@ class PagedDecodeBatch:
         self.pool._call('mt_sched_add_length', [P, I, I], self._ws.ptr(0), self.batch_size, 1)
 
     def commit(self, *, device=True):
-        """Commit every cache; ``device=False`` when the device half
-        (``commit_device``) ran already, inside a captured step."""
+        """Commit every cache; ``device=False`` when the device half (every
+        row's length + 1) ran already: in the greedy selection
+        (``mt_row_argmax_commit``) of a sync-free or captured step."""
         if len(self._written_layers) != len(self.layout):
             raise ValueError('Cannot commit incomplete decode batch')
         if any(c._pending_tokens != 1 or len(c._written_layers) != len(c.layout) for c in self.caches):
