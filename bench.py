@@ -412,10 +412,11 @@ def bench_variants(args):
 def bench_timeline(args):
     """Per-workgroup timeline of one cold config-2 launch of the headline path
     (host work list, automatic waves and unroll), from the MT_DECODE_TIMELINE
-    build of the decode kernel: each workgroup's start, the start of its K/V
-    stream (wave 0, after the prologue's dependent loads) and its end, in µs
-    from the launch's first start, with its XCD and compute unit. Summarized
-    as: the start spread; stream starts and ends per residency slot
+    build of the decode kernel: each workgroup's start, the arrival of its
+    work entry and of its table/query/offset loads, the end of its staging
+    barrier, the start of its K/V stream (wave 0) and its end, in µs from the
+    launch's first start, with its XCD and compute unit. Summarized as: the
+    start spread; prologue steps, stream starts and ends per residency slot
     (workgroups i, i + CUs, i + 2 CUs share a compute unit in a fully resident
     grid); how many workgroups stream over time; the K/V tokens per µs of the
     first slot per XCD; per-CU token loads and their correlation with the
@@ -449,13 +450,15 @@ def bench_timeline(args):
     for i in range(args.warmup + len(calls)):  # the last launch reads a pool untouched for len(calls) - 1 launches
         rt.check(fn(*calls[i % len(calls)]))
     n = items * case.heads
-    buf = (ct.c_ulonglong * (5 * n))()
+    fields = 8
+    buf = (ct.c_ulonglong * (fields * n))()
     rt.check(read(buf, n))
-    rec = np.frombuffer(buf, np.uint64).reshape(n, 5).astype(np.int64)
+    rec = np.frombuffer(buf, np.uint64).reshape(n, fields).astype(np.int64)
     t0 = rec[:, 0].min()
-    start, stream, end = [(rec[:, j] - t0) / 100.0 for j in range(3)]  # 100 MHz ticks -> µs
-    xcc = rec[:, 4] & 0xF
-    cu_key = (xcc << 16) | ((rec[:, 3] >> 8) & 0xFF)  # XCD, SE, SH, CU
+    # 100 MHz ticks -> µs from the first start
+    start, entry, loads, barrier, stream, end = [(rec[:, j] - t0) / 100.0 for j in range(6)]
+    xcc = rec[:, 7] & 0xF
+    cu_key = (xcc << 16) | ((rec[:, 6] >> 8) & 0xFF)  # XCD, SE, SH, CU
     rows = work[0:2 * items:2][np.arange(n) // case.heads]
     tokens = case.lengths[rows] - 1  # K/V tokens read from pages (the new one comes from the inputs)
     slot = np.arange(n) // cus
@@ -472,6 +475,10 @@ def bench_timeline(args):
     return {'decode_timeline': {
         'workgroups': n, 'compute_units_seen': int(len(keys)), 'span_us': round(span, 2),
         'start_spread_us': round(float(start.max()), 2),
+        'prologue_us_by_slot': {int(k): {name: q(v[slot == k]) for name, v in
+                                         (('work_entry', entry), ('table_query_offset', loads),
+                                          ('staging_barrier', barrier))}
+                                for k in np.unique(slot)},
         'stream_start_us_by_slot': {int(k): q(stream[slot == k]) for k in np.unique(slot)},
         'end_us_by_slot': {int(k): q(end[slot == k]) for k in np.unique(slot)},
         'first_slot_tokens_per_us_by_xcd': per_xcd,

@@ -85,11 +85,21 @@ constexpr int kLdsSlabs = 512;
 
 #ifdef MT_DECODE_TIMELINE
 // Measurement builds only (bench.py --timeline): wall-clock stamps of each
-// decode workgroup's first item, 100 MHz (s_memrealtime): [start, K/V stream
-// start of wave 0, end, HW_ID register, XCC_ID register], workgroups below
-// kTimelineMax. The product build has none of this.
+// decode workgroup's first item, taken by thread 0 at 100 MHz
+// (s_memrealtime), workgroups below kTimelineMax. Record: [start, work entry
+// returned, table/query/offset returned, past the staging barrier, K/V
+// stream start, end, HW_ID register, XCC_ID register]. A stamp that follows
+// a load takes that load's value as an operand, so it waits for the data.
+// The product build has none of this.
 constexpr int kTimelineMax = 8192;
-__device__ uint64_t g_decode_timeline[kTimelineMax * 5];
+constexpr int kTimelineFields = 8;
+__device__ uint64_t g_decode_timeline[kTimelineMax * kTimelineFields];
+template <class T>
+__device__ __forceinline__ uint64_t stamp_after(T dep) {
+  uint64_t t;
+  asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t) : "v"(dep) : "memory");
+  return t;
+}
 #endif
 
 struct Geometry {
@@ -595,7 +605,7 @@ void decode_kernel(DecodeArgs a) {
 
 #ifdef MT_DECODE_TIMELINE
   const uint64_t tl_start = wall_clock64();
-  uint64_t tl_stream = 0;
+  uint64_t tl_entry = 0, tl_loads = 0, tl_barrier = 0, tl_stream = 0;
 #endif
   const Geometry& g = a.g;
   const int dim = VEC ? D : g.dim;
@@ -691,6 +701,9 @@ void decode_kernel(DecodeArgs a) {
       const uint64_t e = (a.work_count && item == blockIdx.x) ? first_entry : work64[w];
       b = int(uint32_t(e));
       split = int(uint32_t(e >> 32));
+#ifdef MT_DECODE_TIMELINE
+      if (item == blockIdx.x) tl_entry = stamp_after(b);
+#endif
       if (!((unsigned(b) < unsigned(a.batch)) & (unsigned(split) < unsigned(a.nsplit_max)))) continue;
     } else if constexpr (MODE == kVisitRank) {
       // item = (visiting position, head); one split per row
@@ -725,6 +738,9 @@ void decode_kernel(DecodeArgs a) {
     T new_k{}, new_v{};
     if (tid < dim) { new_k = kin[qrow + tid]; new_v = vin[qrow + tid]; }
     const int offset = MODE == kVisitRank ? s_len[b] : a.offsets[b];
+#ifdef MT_DECODE_TIMELINE
+    if (item == blockIdx.x) tl_loads = stamp_after(offset + physical);
+#endif
 
     const int64_t L = offset < 0 ? 0 : int64_t(offset) + 1;
     T* orow = out + bh * dim;
@@ -752,6 +768,9 @@ void decode_kernel(DecodeArgs a) {
     if (tid < dim) { s_new[0][tid] = new_k; s_new[1][tid] = new_v; }
     __syncthreads();
     slabs_staged = true;
+#ifdef MT_DECODE_TIMELINE
+    if (item == blockIdx.x) tl_barrier = wall_clock64();
+#endif
     auto slab_of = [&](int physical) -> uint64_t {
       return lds_slabs ? s_slabs[slab_index(physical, g)] : a.slabs[slab_index(physical, g)];
     };
@@ -866,12 +885,15 @@ void decode_kernel(DecodeArgs a) {
   }
 #ifdef MT_DECODE_TIMELINE
   if (tid == 0 && blockIdx.x < unsigned(kTimelineMax)) {
-    uint64_t* rec = g_decode_timeline + 5 * blockIdx.x;
+    uint64_t* rec = g_decode_timeline + kTimelineFields * blockIdx.x;
     rec[0] = tl_start;
-    rec[1] = tl_stream;
-    rec[2] = wall_clock64();
-    rec[3] = __builtin_amdgcn_s_getreg(4 | (31 << 11));   // HW_ID: wave, SIMD, CU, SH, SE
-    rec[4] = __builtin_amdgcn_s_getreg(20 | (15 << 11));  // XCC_ID
+    rec[1] = tl_entry;
+    rec[2] = tl_loads;
+    rec[3] = tl_barrier;
+    rec[4] = tl_stream;
+    rec[5] = wall_clock64();
+    rec[6] = __builtin_amdgcn_s_getreg(4 | (31 << 11));   // HW_ID: wave, SIMD, CU, SH, SE
+    rec[7] = __builtin_amdgcn_s_getreg(20 | (15 << 11));  // XCC_ID
   }
 #endif
 }
@@ -2599,13 +2621,14 @@ int mt_paged_decode_workspace_bytes(int b, int h, int page_size, int columns, in
 }
 
 #ifdef MT_DECODE_TIMELINE
-// Measurement builds only: copies the first `count` workgroups' stamps
-// (5 x uint64 each, see g_decode_timeline) of the last decode launch to host
-// memory `dst`, after the calling thread's stream has drained.
+// Measurement builds only: copies the first `count` workgroups' records
+// (kTimelineFields x uint64 each, see g_decode_timeline) of the last decode
+// launch to host memory `dst`, after the calling thread's stream has drained.
 int mt_decode_timeline(unsigned long long* dst, int count) {
   if (!dst || count < 1 || count > kTimelineMax) return hipErrorInvalidValue;
   hipError_t e = hipStreamSynchronize(hipStreamPerThread);
-  if (e == hipSuccess) e = hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_timeline), size_t(count) * 5 * 8);
+  if (e == hipSuccess)
+    e = hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_timeline), size_t(count) * kTimelineFields * 8);
   return e;
 }
 #endif
