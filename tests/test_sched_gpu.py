@@ -313,7 +313,10 @@ def test_decode_batch_table_paths_match_oracle(rows, capacity):
     assert_same_pool(pool, oracle)
 
 
-def test_decode_budget_exhaustion_aborts_like_reference():
+@pytest.mark.parametrize('fused', [False, True])
+def test_decode_budget_exhaustion_aborts_like_reference(fused):
+    # fused: the metadata launch also embeds the rows (mt_sched_decode_prepare_embed),
+    # as the sync-free step issues it; the abort must leave the same pool
     model = StubModel(layers=1, heads=1, dim=64, n_positions=128)
     page_bytes = 2 * 1 * 1 * 64 * 16 * 4
     pool, oracle = pool_pair(model, page_size=16, max_bytes=6 * page_bytes, pages_per_slab=2)
@@ -328,10 +331,13 @@ def test_decode_budget_exhaustion_aborts_like_reference():
         oc.commit_append()
         pairs.append((c, oc))
     # rows 0, 1, 2 sit on page boundaries and need a page each: only one is left
-    idx = DeviceTensor.from_numpy(np.zeros((4, 1), np.float32))
+    idx = None if fused else DeviceTensor.from_numpy(np.zeros((4, 1), np.float32))
+    wte = DeviceTensor.from_numpy(np.ones((8, 64), np.float32))
+    wpe = DeviceTensor.from_numpy(np.ones((128, 64), np.float32))
+    x = DeviceTensor((4, 64), 'float32')
     with pytest.raises(MemoryError):
         with PagedDecodeBatch(model, idx, [c for c, _ in pairs]) as batch:
-            batch.prepare()
+            batch.prepare(embed=(x.ptr, wte.ptr, wpe.ptr, 8, 128, 64) if fused else None)
     with pytest.raises(MemoryError):
         decode_batch_metadata_with_abort([oc for _, oc in pairs])
     runtime().synchronize()
@@ -464,15 +470,16 @@ def test_fused_prepare_embed_equals_prepare_then_embed(rows):
             assert a[key] == b[key], key
 
 
+@pytest.mark.parametrize('dtype', ['float32', 'bfloat16', 'float16'])
 @pytest.mark.parametrize('rows', [1, 3, 64])
-def test_argmax_commit_equals_feedback_then_add_length(rows):
+def test_argmax_commit_equals_feedback_then_add_length(rows, dtype):
     # mt_row_argmax_commit against mt_row_argmax_feedback followed by
     # mt_sched_add_length: the ids, the slot tokens and every slot's committed
     # length (rows in a shuffled slot order)
     from minitorch_amd import paged_ops
     rng = np.random.default_rng([4, rows])
     width = 50257
-    logits = DeviceTensor.from_numpy(rng.standard_normal((rows, 1, width)).astype(np.float32))
+    logits = DeviceTensor.from_numpy(rng.standard_normal((rows, 1, width)).astype(np.float32), dtype)
     results = []
     for fused in (True, False):
         model, pool, caches = _pool_with_rows(rows + 11, rows)
@@ -483,10 +490,10 @@ def test_argmax_commit_equals_feedback_then_add_length(rows):
         ids = DeviceTensor((rows, 1), 'float32')
         if fused:
             paged_ops.row_argmax_commit(ids.ptr, pool.slot_tokens.ptr, slots.ptr, pool.max_slots, pool.slot_len_ptr,
-                                        1, logits.ptr, rows, width, 'float32')
+                                        1, logits.ptr, rows, width, dtype)
         else:
             paged_ops.row_argmax_feedback(ids.ptr, pool.slot_tokens.ptr, slots.ptr, pool.max_slots, logits.ptr,
-                                          rows, width, 'float32')
+                                          rows, width, dtype)
             pool._call('mt_sched_add_length', [P, I, I], slots.ptr, rows, 1)
         runtime().synchronize()
         results.append((ids.to_numpy().ravel(), pool.slot_tokens.download(np.float32, pool.max_slots),
