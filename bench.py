@@ -432,8 +432,17 @@ def bench_timeline(args):
     read = lib.mt_decode_timeline
     read.argtypes, read.restype = [ct.POINTER(ct.c_ulonglong), I], I
     rt = runtime()
-    case = config2_case(args.seed)
-    devs = [DevicePagedCase(case) for _ in range(args.pools)]
+    if args.config == 4:
+        # config 4's layer shape: 128 rows x 16 heads, bf16, more workgroups than one residency round
+        from minitorch_amd.e2e import config4_lengths
+        from minitorch_amd.workloads import DeviceRaggedCase
+        l4 = config4_lengths(np.random.default_rng([args.seed, 4]), 128)
+        devs = [DeviceRaggedCase(args.seed + i, batch=128, heads=16, dim=64, page_size=16, lengths=l4,
+                                 dtype='bfloat16') for i in range(4)]
+        case = devs[0]
+    else:
+        case = config2_case(args.seed)
+        devs = [DevicePagedCase(case) for _ in range(args.pools)]
     kw = devs[0].kwargs()
     split = paged_ops.split_tokens_for(page_size=case.page_size, columns=case.columns)
     cus = rt.compute_units()
@@ -472,7 +481,17 @@ def bench_timeline(args):
     keys = np.unique(cu_key)
     cu_tokens = np.array([tokens[cu_key == k].sum() for k in keys])
     cu_end = np.array([end[cu_key == k].max() for k in keys])
+    # workgroups dispatched when the launch starts, and those that take a
+    # slot freed later (grids of several residency rounds)
+    late = start > start.min() + 1.0
+    slot_time = float((end - start).sum())
     return {'decode_timeline': {
+        'config': 4 if args.config == 4 else 2, 'late_dispatched_workgroups': int(late.sum()),
+        'prologue_us_first_dispatch': q(stream[~late] - start[~late]),
+        'prologue_us_late_dispatch': q(stream[late] - start[late]) if late.any() else None,
+        'stream_us': q(end - stream),
+        'prologue_share_of_slot_time': round(float((stream - start).sum()) / slot_time, 3),
+        'mean_streaming_workgroups': round(float((end - stream).sum()) / span, 1),
         'workgroups': n, 'compute_units_seen': int(len(keys)), 'span_us': round(span, 2),
         'start_spread_us': round(float(start.max()), 2),
         'prologue_us_by_slot': {int(k): {name: q(v[slot == k]) for name, v in
@@ -1108,8 +1127,8 @@ def main():
                     help='time the decode kernel variants x waves (4, 8) x unroll (1, 2, 4) on config 2, '
                          "config 4's layer and config 5 (P = 16)")
     ap.add_argument('--timeline', action='store_true',
-                    help='per-workgroup timeline of one config-2 launch from the MT_DECODE_TIMELINE build '
-                         '(build it with --build-variants)')
+                    help="per-workgroup timeline of one config-2 launch (--config 4: config 4's layer shape) "
+                         'from the MT_DECODE_TIMELINE build (build it with --build-variants)')
     ap.add_argument('--entries', action='store_true',
                     help='time the decode entries (work list, batch order, mt_paged_decode_batch) on config 2 '
                          'and on one-page rows of the same shape')
