@@ -427,12 +427,13 @@ def _pool_with_rows(seed, rows, n_positions=512):
     return model, pool, caches
 
 
-@pytest.mark.parametrize('rows', [1, 2, 37, 128])
-def test_fused_prepare_embed_equals_prepare_then_embed(rows):
+@pytest.mark.parametrize('rows,n_pos', [(1, 512), (2, 512), (37, 512), (128, 512), (37, 200)])
+def test_fused_prepare_embed_equals_prepare_then_embed(rows, n_pos):
     # mt_sched_decode_prepare_embed against mt_sched_decode_prepare followed by
     # mt_embed_tokens on two identically built pools: the step's metadata,
-    # the pool state and the embeddings bit for bit, including a NaN token and
-    # an id past the vocabulary (NaN rows)
+    # the pool state and the embeddings bit for bit, including a NaN token, an
+    # id past the vocabulary and (n_pos 200) positions past the position table
+    # (NaN rows)
     from minitorch_amd import paged_ops
     vocab, dim = 300, 64
     rng = np.random.default_rng([3, rows])
@@ -448,10 +449,10 @@ def test_fused_prepare_embed_equals_prepare_then_embed(rows):
         batch = PagedDecodeBatch(model, None, caches)
         batch.prepare(graph=True)
         if fused:
-            batch.prepare_device(embed=(x.ptr, wte.ptr, wpe.ptr, vocab, 512, dim))
+            batch.prepare_device(embed=(x.ptr, wte.ptr, wpe.ptr, vocab, n_pos, dim))
         else:
             batch.prepare_device()
-            paged_ops.embed_tokens(x.ptr, wte.ptr, wpe.ptr, None, batch.position_ids.ptr, rows, vocab, 512, dim,
+            paged_ops.embed_tokens(x.ptr, wte.ptr, wpe.ptr, None, batch.position_ids.ptr, rows, vocab, n_pos, dim,
                                    slot_tokens=pool.slot_tokens.ptr, slots=batch.device_slots.ptr,
                                    num_slots=pool.max_slots)
         runtime().synchronize()
@@ -468,6 +469,10 @@ def test_fused_prepare_embed_equals_prepare_then_embed(rows):
             assert np.array_equal(a[key], b[key]), key
         else:
             assert a[key] == b[key], key
+    if n_pos < 512:
+        # rows at or past the position table are NaN, the others are not all NaN
+        nan_rows = np.isnan(a['x'].view(np.float32)).all(axis=1)
+        assert nan_rows.any() and not nan_rows.all()
 
 
 @pytest.mark.parametrize('dtype', ['float32', 'bfloat16', 'float16'])
